@@ -1,0 +1,166 @@
+/*
+ * litemind_moe.h -- C ABI of the MI355X (gfx950) mixture-of-experts feed-forward path.
+ *
+ * This is the drop-in boundary for LiteMind's MoE block.  Every entry point names
+ * the LiteMind interface it replaces (paths relative to the LiteMind source tree).
+ * The C++20 wrappers in litemind_amd/host/ restore LiteMind's own class and
+ * function signatures (MoeRouter, gemm::, ExpertCache) on top of this ABI.
+ *
+ * Conventions
+ *   - Every function returns an int status: LM_OK (0) or a negative LM_E* code.
+ *     No exception ever crosses this boundary.  lm_last_error() returns a
+ *     thread-local message for the last failure on the calling thread.
+ *   - Pointers named *_dev are device (HBM) pointers; *_host are host pointers.
+ *     lm_alloc / lm_copy_* let a caller without its own HIP runtime manage them.
+ *   - Work is enqueued on the context's stream and is asynchronous unless the
+ *     function says otherwise; lm_synchronize() waits for it.  One context is
+ *     driven from one host thread at a time (LiteMind's runner is single-threaded,
+ *     and MoeRouter / ExpertCache are not reentrant either).
+ *   - Weights are BF16 bit patterns (uint16_t), row-major, exactly as LiteMind's
+ *     WeightView::as_bf16() hands them out (include/WeightStore.hpp:38-41).
+ */
+#ifndef LITEMIND_MOE_H
+#define LITEMIND_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LM_OK 0
+#define LM_EINVAL (-1)   /* bad argument, shape or state */
+#define LM_EHIP (-2)     /* a HIP runtime call failed */
+#define LM_ENOMEM (-3)   /* device or host allocation failed */
+#define LM_ENOTRES (-4)  /* a weight the call needs is not resident in HBM */
+#define LM_EKERNEL (-5)  /* a kernel reported an error through its status word */
+
+typedef struct lm_context lm_context;
+
+/* The MoE subset of LiteMind's Config (include/Config.hpp:211-241, :271-273). */
+typedef struct lm_moe_config {
+    int32_t hidden_size;            /* 2048 for DeepSeek-V2-Lite */
+    int32_t moe_intermediate_size;  /* 1408 */
+    int32_t n_routed_experts;       /* 64 (at most 256) */
+    int32_t num_experts_per_tok;    /* 6 (at most 16) */
+    int32_t n_shared_experts;       /* 2 -> one fused shared FFN of width 1408*2 */
+    int32_t intermediate_size;      /* dense layers: 10944 */
+    int32_t norm_topk_prob;         /* 0 */
+    float routed_scaling_factor;    /* 1.0 */
+    int32_t group_limited;          /* topk_method == "group_limited_greedy" */
+    int32_t n_group;                /* 1 */
+    int32_t topk_group;             /* 1 */
+    float rms_norm_eps;             /* 1e-6 */
+    int32_t num_layers;             /* layers the context can hold (ids 0..num_layers-1) */
+} lm_moe_config;
+
+/* Expert-path selection for lm_moe_forward. */
+#define LM_PATH_AUTO 0  /* GEMV below the crossover token count, MFMA above */
+#define LM_PATH_GEMV 1  /* fp32-activation weight-streaming kernels */
+#define LM_PATH_MFMA 2  /* fp16-operand MFMA grouped GEMM, fp32 accumulate */
+
+/* ---- errors, context ---- */
+const char* lm_last_error(void);
+int lm_version(int32_t* major, int32_t* minor);
+/* Replaces DeepSeekRunner::load's MoeRouter(config) / ExpertCache::configure
+ * (src/DeepSeekRunner.cpp:361-362): one context per GPU owns the resident weights. */
+int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** out);
+int lm_context_destroy(lm_context* ctx);
+int lm_synchronize(lm_context* ctx);
+
+/* ---- device memory plumbing (no LiteMind counterpart: LiteMind has one address space) ---- */
+int lm_alloc(lm_context* ctx, size_t bytes, void** out_dev);
+int lm_free(lm_context* ctx, void* dev);
+int lm_copy_h2d(lm_context* ctx, void* dst_dev, const void* src_host, size_t bytes);  /* synchronous */
+int lm_copy_d2h(lm_context* ctx, void* dst_host, const void* src_dev, size_t bytes);  /* synchronous */
+int lm_memset(lm_context* ctx, void* dst_dev, int32_t value, size_t bytes);           /* async */
+
+/* ---- HBM residency: replaces ExpertCache + WeightView paging ----
+ * (src/ExpertCache.cpp:9-47, src/DeepSeekRunner.cpp:200-222).  Host buffers are
+ * copied once into HBM; LiteMind's mmap/madvise paging leaves the hot loop. */
+/* Router gate [n_routed_experts, hidden] fp32, as LayerWeights.router holds it
+ * after WeightStore::read_float32 (src/DeepSeekRunner.cpp:31, :200-203). */
+int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host);
+/* One routed expert: gate, up [I, H] and down [H, I] (src/DeepSeekRunner.cpp:205-215). */
+int lm_upload_expert(lm_context* ctx, int32_t layer, int32_t expert, const uint16_t* gate_host,
+                     const uint16_t* up_host, const uint16_t* down_host);
+/* The fused shared experts: gate, up [S, H], down [H, S], S = I * n_shared (:217-222). */
+int lm_upload_shared(lm_context* ctx, int32_t layer, const uint16_t* gate_host, const uint16_t* up_host,
+                     const uint16_t* down_host);
+/* A dense SwiGLU layer (layer < first_k_dense_replace): [D, H], [D, H], [H, D] (:192-195). */
+int lm_upload_dense(lm_context* ctx, int32_t layer, const uint16_t* gate_host, const uint16_t* up_host,
+                    const uint16_t* down_host);
+/* post_attention_layernorm weight [H] fp32, used by lm_stack_forward (:265-267). */
+int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host);
+/* Finishes a layer's upload: builds the fp16 shadow copy the MFMA path reads.
+ * Must be called after the layer's experts and shared expert are uploaded. */
+int lm_finalize_layer(lm_context* ctx, int32_t layer);
+/* Bytes resident in HBM for weights (all layers). */
+int lm_resident_bytes(lm_context* ctx, uint64_t* out);
+
+/* ---- the MoE block: replaces src/DeepSeekRunner.cpp:273-288 for T tokens at once ----
+ * matvec_f32 router -> MoeRouter::select -> 6 x feed_forward(expert, weight) ->
+ * feed_forward(shared, 1.0), with the routed experts grouped across tokens.
+ *   x_dev        [T, H] fp32, the post-attention RMSNorm output ("normalised")
+ *   y_dev        [T, H] fp32, the feed-forward output (feed_forward_output; no residual)
+ *   logit_bias_dev  NULL or [E] fp32 added to each logit after the router dot product
+ *                   (not in LiteMind; used to construct skewed routing)
+ *   topk_index_dev  NULL or [T, k] int32: the selected experts in rank order
+ *   topk_weight_dev NULL or [T, k] fp32: their weights
+ *   logits_dev      NULL or [T, E] fp32: router logits (after the bias)
+ *   path            LM_PATH_* */
+int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
+                   const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev,
+                   float* logits_dev, int32_t path);
+
+/* ---- stage entry points (for tests; each is one step of lm_moe_forward) ---- */
+/* gemm::matvec_f32 + MoeRouter::select for T tokens (src/Gemm.cpp:132-137,
+ * src/MoeRouter.cpp:54-107).  Bit-exact with LiteMind for hidden % 8 == 0. */
+int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, const float* logit_bias_dev,
+              float* logits_dev, int32_t* topk_index_dev, float* topk_weight_dev);
+/* MoeRouter::select alone on given logits [T, E] (src/MoeRouter.cpp:54-107). */
+int lm_router_select(lm_context* ctx, const float* logits_dev, int64_t tokens, int32_t* topk_index_dev,
+                     float* topk_weight_dev);
+/* Canonical expert-major permutation of the T*k selections (no LiteMind
+ * counterpart: LiteMind visits one token's selections in rank order,
+ * src/DeepSeekRunner.cpp:277-284).  counts [E], offsets [E+1], perm [T*k]
+ * (assignment t*k+r at each permuted position), slot_of [T*k] (its inverse). */
+int lm_permute(lm_context* ctx, const int32_t* topk_index_dev, int64_t tokens, int32_t* counts_dev,
+               int32_t* offsets_dev, int32_t* perm_dev, int32_t* slot_of_dev);
+
+/* ---- stack glue for the 27-layer FFN chain (src/DeepSeekRunner.cpp:264-290) ----
+ * For each layer l in [first, last]: xn = rms_norm(h, norm[l]); h += FFN_l(xn),
+ * FFN_l = dense SwiGLU or the MoE block.  hidden_dev [T, H] fp32 is updated in place. */
+int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
+                     int32_t path);
+/* gemm::rms_norm over T rows (src/Gemm.cpp:197-207); out may equal in. */
+int lm_rms_norm(lm_context* ctx, const float* in_dev, const float* weight_dev, float* out_dev, int64_t tokens,
+                int32_t hidden, float epsilon);
+/* Dense SwiGLU FFN of a resident dense layer: y = feed_forward(dense, x, scale 1)
+ * into a zeroed output (src/DeepSeekRunner.cpp:228-240, :270-271). */
+int lm_dense_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
+                     int32_t path);
+
+/* ---- per-call gemm compatibility (src/Gemm.cpp:139-175) ----
+ * out = W x (accumulate = 0) or out += scale * W x (accumulate = 1), W [out_dim,
+ * in_dim] BF16.  W_host is looked up in a pointer-keyed HBM cache and uploaded on
+ * first use; x and out are host buffers.  Synchronous. */
+int lm_gemm_matvec_bf16(lm_context* ctx, const uint16_t* w_host, const float* x_host, float* out_host,
+                        size_t out_dim, size_t in_dim, float scale, int32_t accumulate);
+
+/* ---- timing: hipEvents on the context stream ---- */
+int lm_event_create(lm_context* ctx, void** out_event);
+int lm_event_destroy(lm_context* ctx, void* event);
+int lm_event_record(lm_context* ctx, void* event);
+int lm_event_elapsed_ms(lm_context* ctx, void* start, void* stop, float* out_ms);
+/* Per-stage timing of lm_moe_forward: when enabled, each stage is bracketed by
+ * events on the context stream and its durations accumulate.  Stage ids:
+ * 0 router, 1 permute, 2 gate/up, 3 down, 4 combine. */
+int lm_stage_timing(lm_context* ctx, int32_t enable);
+int lm_stage_times(lm_context* ctx, double* out_ms, int32_t* out_calls, int32_t stages);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,275 @@
+"""litemind_amd -- MI355X (gfx950) mixture-of-experts feed-forward path for LiteMind.
+
+The product is the native library ``liblitemind_moe.so`` (HIP kernels + the C ABI
+declared in ``include/litemind_moe.h``).  This module binds that ABI with ctypes
+for Python callers (tests, the benchmark); it never falls back to a CPU path:
+if the library is missing or a GPU call fails, it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblitemind_moe.so")
+
+LM_OK = 0
+PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+STAGES = ("router", "permute", "gate_up", "down", "combine")
+
+
+class LmError(RuntimeError):
+    """A litemind_amd C ABI call returned a non-zero status."""
+
+
+class MoeConfig(C.Structure):
+    """lm_moe_config: the MoE subset of LiteMind's Config (include/Config.hpp:211-241)."""
+
+    _fields_ = [
+        ("hidden_size", C.c_int32),
+        ("moe_intermediate_size", C.c_int32),
+        ("n_routed_experts", C.c_int32),
+        ("num_experts_per_tok", C.c_int32),
+        ("n_shared_experts", C.c_int32),
+        ("intermediate_size", C.c_int32),
+        ("norm_topk_prob", C.c_int32),
+        ("routed_scaling_factor", C.c_float),
+        ("group_limited", C.c_int32),
+        ("n_group", C.c_int32),
+        ("topk_group", C.c_int32),
+        ("rms_norm_eps", C.c_float),
+        ("num_layers", C.c_int32),
+    ]
+
+
+_P = C.c_void_p
+_I32 = C.c_int32
+_I64 = C.c_int64
+_SZ = C.c_size_t
+_F = C.c_float
+
+# name -> argtypes (all return int status unless listed in _RESTYPE)
+PROTOTYPES = {
+    "lm_last_error": [],
+    "lm_version": [_P, _P],
+    "lm_context_create": [_I32, _P, _P],
+    "lm_context_destroy": [_P],
+    "lm_synchronize": [_P],
+    "lm_alloc": [_P, _SZ, _P],
+    "lm_free": [_P, _P],
+    "lm_copy_h2d": [_P, _P, _P, _SZ],
+    "lm_copy_d2h": [_P, _P, _P, _SZ],
+    "lm_memset": [_P, _P, _I32, _SZ],
+    "lm_upload_router": [_P, _I32, _P],
+    "lm_upload_expert": [_P, _I32, _I32, _P, _P, _P],
+    "lm_upload_shared": [_P, _I32, _P, _P, _P],
+    "lm_upload_dense": [_P, _I32, _P, _P, _P],
+    "lm_upload_norm": [_P, _I32, _P],
+    "lm_finalize_layer": [_P, _I32],
+    "lm_resident_bytes": [_P, _P],
+    "lm_moe_forward": [_P, _I32, _P, _I64, _P, _P, _P, _P, _P, _I32],
+    "lm_router": [_P, _I32, _P, _I64, _P, _P, _P, _P],
+    "lm_router_select": [_P, _P, _I64, _P, _P],
+    "lm_permute": [_P, _P, _I64, _P, _P, _P, _P],
+    "lm_stack_forward": [_P, _I32, _I32, _P, _I64, _I32],
+    "lm_rms_norm": [_P, _P, _P, _P, _I64, _I32, _F],
+    "lm_dense_forward": [_P, _I32, _P, _I64, _P, _I32],
+    "lm_gemm_matvec_bf16": [_P, _P, _P, _P, _SZ, _SZ, _F, _I32],
+    "lm_event_create": [_P, _P],
+    "lm_event_destroy": [_P, _P],
+    "lm_event_record": [_P, _P],
+    "lm_event_elapsed_ms": [_P, _P, _P, _P],
+    "lm_stage_timing": [_P, _I32],
+    "lm_stage_times": [_P, _P, _P, _I32],
+}
+_RESTYPE = {"lm_last_error": C.c_char_p}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Loads liblitemind_moe.so, raising if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise LmError(f"{path} is missing: build it with `python -m litemind_amd.build`")
+    lib = C.CDLL(path)
+    for name, args in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, C.c_int)
+    _lib = lib
+    return lib
+
+
+def _ptr(a) -> C.c_void_p:
+    if a is None:
+        return None
+    if isinstance(a, DeviceBuffer):
+        return C.c_void_p(a.ptr)
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("array must be C-contiguous")
+        return a.ctypes.data_as(C.c_void_p)
+    if isinstance(a, int):
+        return C.c_void_p(a)
+    raise TypeError(f"cannot pass {type(a)} as a pointer")
+
+
+class DeviceBuffer:
+    """An HBM allocation owned by a Context (freed on close or context destroy)."""
+
+    def __init__(self, ctx: "Context", nbytes: int, dtype=np.float32, shape=None):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = shape if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        out = C.c_void_p()
+        ctx._check(ctx.lib.lm_alloc(ctx.handle, max(self.nbytes, 1), C.byref(out)))
+        self.ptr = out.value
+
+    def upload(self, host: np.ndarray) -> "DeviceBuffer":
+        host = np.ascontiguousarray(host)
+        if host.nbytes > self.nbytes:
+            raise ValueError("host array larger than the device buffer")
+        self.ctx._check(self.ctx.lib.lm_copy_h2d(self.ctx.handle, C.c_void_p(self.ptr), _ptr(host), host.nbytes))
+        return self
+
+    def download(self, shape=None, dtype=None) -> np.ndarray:
+        dtype = np.dtype(dtype) if dtype is not None else self.dtype
+        shape = shape if shape is not None else self.shape
+        out = np.empty(shape, dtype=dtype)
+        self.ctx._check(self.ctx.lib.lm_copy_d2h(self.ctx.handle, _ptr(out), C.c_void_p(self.ptr), out.nbytes))
+        return out
+
+    def zero(self) -> "DeviceBuffer":
+        self.ctx._check(self.ctx.lib.lm_memset(self.ctx.handle, C.c_void_p(self.ptr), 0, self.nbytes))
+        return self
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx._check(self.ctx.lib.lm_free(self.ctx.handle, C.c_void_p(self.ptr)))
+            self.ptr = 0
+
+
+class Context:
+    """One GPU's resident MoE weights and stream (lm_context)."""
+
+    def __init__(self, config: MoeConfig, device: int = 0):
+        self.lib = load_library()
+        self.config = config
+        handle = C.c_void_p()
+        self._check(self.lib.lm_context_create(device, C.byref(config), C.byref(handle)))
+        self.handle = handle
+        self._buffers: list[DeviceBuffer] = []
+
+    def _check(self, status: int) -> None:
+        if status != LM_OK:
+            msg = self.lib.lm_last_error().decode(errors="replace")
+            raise LmError(f"litemind_amd status {status}: {msg}")
+
+    def close(self) -> None:
+        if self.handle:
+            self._check(self.lib.lm_context_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- memory ----
+    def empty(self, shape, dtype=np.float32) -> DeviceBuffer:
+        shape = tuple(int(s) for s in np.atleast_1d(shape))
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        return DeviceBuffer(self, n, dtype, shape)
+
+    def to_device(self, host: np.ndarray) -> DeviceBuffer:
+        host = np.ascontiguousarray(host)
+        return DeviceBuffer(self, host.nbytes, host.dtype, host.shape).upload(host)
+
+    def synchronize(self) -> None:
+        self._check(self.lib.lm_synchronize(self.handle))
+
+    # ---- residency ----
+    def upload_router(self, layer: int, gate: np.ndarray) -> None:
+        gate = np.ascontiguousarray(gate, dtype=np.float32)
+        self._check(self.lib.lm_upload_router(self.handle, layer, _ptr(gate)))
+
+    def upload_expert(self, layer: int, expert: int, gate, up, down) -> None:
+        self._check(self.lib.lm_upload_expert(self.handle, layer, expert, _ptr(gate), _ptr(up), _ptr(down)))
+
+    def upload_shared(self, layer: int, gate, up, down) -> None:
+        self._check(self.lib.lm_upload_shared(self.handle, layer, _ptr(gate), _ptr(up), _ptr(down)))
+
+    def upload_dense(self, layer: int, gate, up, down) -> None:
+        self._check(self.lib.lm_upload_dense(self.handle, layer, _ptr(gate), _ptr(up), _ptr(down)))
+
+    def upload_norm(self, layer: int, weight: np.ndarray) -> None:
+        weight = np.ascontiguousarray(weight, dtype=np.float32)
+        self._check(self.lib.lm_upload_norm(self.handle, layer, _ptr(weight)))
+
+    def finalize_layer(self, layer: int) -> None:
+        self._check(self.lib.lm_finalize_layer(self.handle, layer))
+
+    def resident_bytes(self) -> int:
+        out = C.c_uint64()
+        self._check(self.lib.lm_resident_bytes(self.handle, C.byref(out)))
+        return out.value
+
+    # ---- compute (device buffers; asynchronous) ----
+    def moe_forward(self, layer, x, tokens, y, bias=None, idx=None, w=None, logits=None, path=PATH_AUTO) -> None:
+        self._check(self.lib.lm_moe_forward(self.handle, layer, _ptr(x), tokens, _ptr(y), _ptr(bias), _ptr(idx),
+                                            _ptr(w), _ptr(logits), path))
+
+    def router(self, layer, x, tokens, idx, w, bias=None, logits=None) -> None:
+        self._check(self.lib.lm_router(self.handle, layer, _ptr(x), tokens, _ptr(bias), _ptr(logits), _ptr(idx),
+                                       _ptr(w)))
+
+    def router_select(self, logits, tokens, idx, w) -> None:
+        self._check(self.lib.lm_router_select(self.handle, _ptr(logits), tokens, _ptr(idx), _ptr(w)))
+
+    def permute(self, idx, tokens, counts, offsets, perm, slot_of) -> None:
+        self._check(self.lib.lm_permute(self.handle, _ptr(idx), tokens, _ptr(counts), _ptr(offsets), _ptr(perm),
+                                        _ptr(slot_of)))
+
+    def stack_forward(self, first, last, hidden, tokens, path=PATH_AUTO) -> None:
+        self._check(self.lib.lm_stack_forward(self.handle, first, last, _ptr(hidden), tokens, path))
+
+    def rms_norm(self, x, weight, out, tokens, hidden, eps) -> None:
+        self._check(self.lib.lm_rms_norm(self.handle, _ptr(x), _ptr(weight), _ptr(out), tokens, hidden, eps))
+
+    def dense_forward(self, layer, x, tokens, y, path=PATH_AUTO) -> None:
+        self._check(self.lib.lm_dense_forward(self.handle, layer, _ptr(x), tokens, _ptr(y), path))
+
+    def gemm_matvec_bf16(self, w: np.ndarray, x: np.ndarray, out: np.ndarray, scale=1.0, accumulate=False) -> None:
+        out_dim, in_dim = w.shape
+        self._check(self.lib.lm_gemm_matvec_bf16(self.handle, _ptr(w), _ptr(x), _ptr(out), out_dim, in_dim,
+                                                 scale, 1 if accumulate else 0))
+
+    # ---- timing ----
+    def event(self):
+        out = C.c_void_p()
+        self._check(self.lib.lm_event_create(self.handle, C.byref(out)))
+        return out
+
+    def record(self, event) -> None:
+        self._check(self.lib.lm_event_record(self.handle, event))
+
+    def elapsed_ms(self, start, stop) -> float:
+        out = C.c_float()
+        self._check(self.lib.lm_event_elapsed_ms(self.handle, start, stop, C.byref(out)))
+        return out.value
+
+    def stage_timing(self, enable: bool) -> None:
+        self._check(self.lib.lm_stage_timing(self.handle, 1 if enable else 0))
+
+    def stage_times(self) -> dict:
+        ms = (C.c_double * len(STAGES))()
+        calls = (C.c_int32 * len(STAGES))()
+        self._check(self.lib.lm_stage_times(self.handle, ms, calls, len(STAGES)))
+        return {name: (ms[i], calls[i]) for i, name in enumerate(STAGES)}

@@ -1,0 +1,1158 @@
+// lm_capi.hip -- the C ABI declared in include/litemind_moe.h.
+//
+// Host orchestration for the gfx950 MoE path: context and stream, HBM residency
+// of every layer's weights (replacing LiteMind's SSD-paged ExpertCache,
+// src/ExpertCache.cpp:9-47), and the per-layer pipeline
+//   router -> permute -> gate/up -> down -> combine
+// enqueued asynchronously on the context stream.  No exception crosses the ABI;
+// every entry point returns a status and records a thread-local message.
+#include "litemind_moe.h"
+#include "lm_internal.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& message) {
+    g_error = message;
+    return code;
+}
+
+#define LM_HIP(call)                                                                                         \
+    do {                                                                                                     \
+        const hipError_t lm_status_ = (call);                                                                \
+        if (lm_status_ != hipSuccess) {                                                                      \
+            return fail(LM_EHIP, std::string(#call) + ": " + hipGetErrorString(lm_status_));                 \
+        }                                                                                                    \
+    } while (0)
+
+#define LM_GUARD_BEGIN try {
+#define LM_GUARD_END                                                                                         \
+    }                                                                                                        \
+    catch (const std::bad_alloc&) {                                                                          \
+        return fail(LM_ENOMEM, "host allocation failed");                                                    \
+    }                                                                                                        \
+    catch (const std::exception& e) {                                                                        \
+        return fail(LM_EINVAL, e.what());                                                                    \
+    }                                                                                                        \
+    catch (...) {                                                                                            \
+        return fail(LM_EINVAL, "unknown exception");                                                         \
+    }
+
+constexpr int kStages = 5;
+constexpr int kEventRing = 256;
+// Token count above which LM_PATH_AUTO switches from weight-streaming GEMV to
+// the MFMA grouped GEMM (the GEMV's fp32 VALU work reaches the HBM time of the
+// expert weights at roughly 100 tokens).
+constexpr int64_t kMfmaCrossover = 64;
+
+struct Layer {
+    bool allocated = false;
+    bool dense = false;
+    bool finalized = false;
+    float* router_t = nullptr;         // [H, E]
+    float* norm = nullptr;             // [H]
+    void* slab = nullptr;              // all FFN matrices of the layer (bf16 then fp16 shadow)
+    size_t slab_bytes = 0;
+    std::vector<lm::FfnDev> experts;   // E routed
+    lm::FfnDev shared;
+    lm::FfnDev dense_ffn;
+    std::vector<unsigned char> expert_present;
+    bool shared_present = false;
+    void** table = nullptr;            // device: gu[E+1], down[E+1], gu_h[E+1], down_h[E+1]
+};
+
+struct Workspace {
+    int64_t tokens = 0;
+    int32_t* idx = nullptr;
+    float* wts = nullptr;
+    int32_t* counts = nullptr;
+    int32_t* offsets = nullptr;
+    int32_t* active = nullptr;
+    int32_t* perm = nullptr;
+    int32_t* slot_of = nullptr;
+    void* act = nullptr;          // fp32 (GEMV) or fp16 (MFMA) activations
+    _Float16* x16 = nullptr;
+    float* down_out = nullptr;
+    float* xnorm = nullptr;       // stack: normalised input
+    float* ffn = nullptr;         // stack / dense: FFN output
+    int32_t* zero = nullptr;      // a device int holding 0 (dense layers have no routed experts)
+};
+
+struct EventSet {
+    hipEvent_t ev[kStages + 1];
+};
+
+}  // namespace
+
+struct lm_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    lm_moe_config cfg{};
+    int H = 0, Hp = 0, I = 0, Ip = 0, E = 0, K = 0, S = 0, Sp = 0, D = 0, Dp = 0;
+    std::vector<Layer> layers;
+    Workspace ws;
+    uint16_t* staging = nullptr;   // pinned host buffer for repacking uploads
+    size_t staging_bytes = 0;
+    int* d_overflow = nullptr;
+    uint64_t resident = 0;
+    // per-call gemm compatibility cache, keyed by host pointer
+    struct Cached {
+        uint16_t* dev;
+        size_t elems;
+    };
+    std::unordered_map<const void*, Cached> gemm_cache;
+    float* gemm_x = nullptr;
+    float* gemm_out = nullptr;
+    size_t gemm_cap = 0;
+    // stage timing
+    bool timing = false;
+    std::vector<EventSet> ring;
+    int ring_next = 0;
+    int ring_pending = 0;
+    double stage_ms[kStages] = {};
+    int32_t stage_calls[kStages] = {};
+};
+
+namespace {
+
+int set_device(lm_context* ctx) {
+    LM_HIP(hipSetDevice(ctx->device));
+    return LM_OK;
+}
+
+size_t ffn_bytes(int64_t inter_p, int64_t hidden, int64_t hidden_p) {
+    // gu [2*inter_p, hidden_p] + down [hidden, inter_p], BF16
+    return static_cast<size_t>((2 * inter_p * hidden_p + hidden * inter_p) * 2);
+}
+
+int check_layer(lm_context* ctx, int32_t layer) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (layer < 0 || layer >= static_cast<int32_t>(ctx->layers.size())) {
+        return fail(LM_EINVAL, "layer " + std::to_string(layer) + " out of range");
+    }
+    return LM_OK;
+}
+
+int ensure_staging(lm_context* ctx, size_t bytes) {
+    if (ctx->staging_bytes >= bytes) {
+        return LM_OK;
+    }
+    if (ctx->staging != nullptr) {
+        LM_HIP(hipHostFree(ctx->staging));
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+    }
+    LM_HIP(hipHostMalloc(reinterpret_cast<void**>(&ctx->staging), bytes, hipHostMallocDefault));
+    ctx->staging_bytes = bytes;
+    return LM_OK;
+}
+
+// Allocates the layer's slab: E routed experts + shared (MoE layer) or one dense FFN,
+// bf16 copies first, then fp16 shadows of the same size.
+int allocate_layer(lm_context* ctx, int32_t layer, bool dense) {
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (L.allocated) {
+        if (L.dense != dense) {
+            return fail(LM_EINVAL, "layer " + std::to_string(layer) + " already holds a different FFN kind");
+        }
+        return LM_OK;
+    }
+    const int64_t H = ctx->H, Hp = ctx->Hp;
+    std::vector<std::pair<lm::FfnDev*, int64_t>> ffns;  // (ffn, inter)
+    if (dense) {
+        ffns.push_back({&L.dense_ffn, ctx->D});
+    } else {
+        L.experts.assign(static_cast<size_t>(ctx->E), lm::FfnDev{});
+        L.expert_present.assign(static_cast<size_t>(ctx->E), 0);
+        for (int e = 0; e < ctx->E; ++e) {
+            ffns.push_back({&L.experts[static_cast<size_t>(e)], ctx->I});
+        }
+        if (ctx->S > 0) {
+            ffns.push_back({&L.shared, ctx->S});
+        }
+    }
+    size_t total = 0;
+    for (auto& f : ffns) {
+        total += ffn_bytes(lm::round_up(f.second, lm::kPad), H, Hp);
+    }
+    void* slab = nullptr;
+    LM_HIP(hipMalloc(&slab, 2 * total));
+    LM_HIP(hipMemsetAsync(slab, 0, 2 * total, ctx->stream));
+    char* bf = static_cast<char*>(slab);
+    char* fh = bf + total;
+    for (auto& f : ffns) {
+        const int64_t ip = lm::round_up(f.second, lm::kPad);
+        lm::FfnDev& d = *f.first;
+        d.inter = static_cast<int32_t>(f.second);
+        d.inter_p = static_cast<int32_t>(ip);
+        const size_t gu_bytes = static_cast<size_t>(2 * ip * Hp * 2);
+        d.gu = reinterpret_cast<uint16_t*>(bf);
+        d.down = reinterpret_cast<uint16_t*>(bf + gu_bytes);
+        d.gu_h = reinterpret_cast<_Float16*>(fh);
+        d.down_h = reinterpret_cast<_Float16*>(fh + gu_bytes);
+        const size_t n = ffn_bytes(ip, H, Hp);
+        bf += n;
+        fh += n;
+    }
+    L.slab = slab;
+    L.slab_bytes = 2 * total;
+    L.allocated = true;
+    L.dense = dense;
+    ctx->resident += 2 * total;
+    return LM_OK;
+}
+
+// Repacks one FFN into the resident layout (gate/up interleaved in 32-row groups,
+// zero padding) in pinned staging memory and copies it to HBM.
+int upload_ffn(lm_context* ctx, const lm::FfnDev& d, const uint16_t* gate, const uint16_t* up, const uint16_t* down) {
+    const int64_t H = ctx->H, Hp = ctx->Hp, I = d.inter, Ip = d.inter_p;
+    const size_t n = ffn_bytes(Ip, H, Hp);
+    int rc = ensure_staging(ctx, n);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));  // the previous upload may still read the staging buffer
+    uint16_t* gu = ctx->staging;
+    std::memset(gu, 0, n);
+    for (int64_t j = 0; j < I; ++j) {
+        const int64_t gate_row = (j / lm::kGroupRows) * (2 * lm::kGroupRows) + (j % lm::kGroupRows);
+        std::memcpy(gu + gate_row * Hp, gate + j * H, static_cast<size_t>(H) * 2);
+        std::memcpy(gu + (gate_row + lm::kGroupRows) * Hp, up + j * H, static_cast<size_t>(H) * 2);
+    }
+    uint16_t* dn = gu + 2 * Ip * Hp;
+    for (int64_t h = 0; h < H; ++h) {
+        std::memcpy(dn + h * Ip, down + h * I, static_cast<size_t>(I) * 2);
+    }
+    LM_HIP(hipMemcpyAsync(d.gu, gu, n, hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+}
+
+int ensure_workspace(lm_context* ctx, int64_t tokens) {
+    Workspace& w = ctx->ws;
+    if (w.tokens >= tokens && w.idx != nullptr) {
+        return LM_OK;
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    void** ptrs[] = {reinterpret_cast<void**>(&w.idx),     reinterpret_cast<void**>(&w.wts),
+                     reinterpret_cast<void**>(&w.counts),  reinterpret_cast<void**>(&w.offsets),
+                     reinterpret_cast<void**>(&w.active),  reinterpret_cast<void**>(&w.perm),
+                     reinterpret_cast<void**>(&w.slot_of), reinterpret_cast<void**>(&w.act),
+                     reinterpret_cast<void**>(&w.x16),     reinterpret_cast<void**>(&w.down_out),
+                     reinterpret_cast<void**>(&w.xnorm),   reinterpret_cast<void**>(&w.ffn),
+                     reinterpret_cast<void**>(&w.zero)};
+    for (void** p : ptrs) {
+        if (*p != nullptr) {
+            LM_HIP(hipFree(*p));
+            *p = nullptr;
+        }
+    }
+    const int64_t T = std::max<int64_t>(tokens, 1);
+    const int64_t TK = T * ctx->K;
+    const int64_t E = ctx->E;
+    const int64_t widest = std::max<int64_t>({ctx->Ip, ctx->Sp, ctx->Dp});
+    const size_t act_elems = static_cast<size_t>(TK * ctx->Ip + T * widest);
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.idx), sizeof(int32_t) * static_cast<size_t>(TK)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.wts), sizeof(float) * static_cast<size_t>(TK)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.counts), sizeof(int32_t) * static_cast<size_t>(E + 1)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.offsets), sizeof(int32_t) * static_cast<size_t>(E + 2)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.active), sizeof(int32_t) * static_cast<size_t>(E + 2)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.perm), sizeof(int32_t) * static_cast<size_t>(TK)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.slot_of), sizeof(int32_t) * static_cast<size_t>(TK)));
+    LM_HIP(hipMalloc(&w.act, sizeof(float) * act_elems));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.x16), sizeof(_Float16) * static_cast<size_t>(T * ctx->Hp)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.down_out), sizeof(float) * static_cast<size_t>((TK + T) * ctx->H)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.xnorm), sizeof(float) * static_cast<size_t>(T * ctx->H)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ffn), sizeof(float) * static_cast<size_t>(T * ctx->H)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.zero), sizeof(int32_t) * 4));
+    LM_HIP(hipMemsetAsync(w.zero, 0, sizeof(int32_t) * 4, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    w.tokens = T;
+    return LM_OK;
+}
+
+// Stage timing: records event `i` of the current ring slot.
+void stage_mark(lm_context* ctx, int i) {
+    if (ctx->timing) {
+        (void)hipEventRecord(ctx->ring[static_cast<size_t>(ctx->ring_next)].ev[i], ctx->stream);
+    }
+}
+
+int stage_collect(lm_context* ctx) {
+    if (ctx->ring_pending == 0) {
+        return LM_OK;
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    const int n = ctx->ring_pending;
+    for (int k = 0; k < n; ++k) {
+        const int slot = (ctx->ring_next - n + k + kEventRing) % kEventRing;
+        EventSet& es = ctx->ring[static_cast<size_t>(slot)];
+        for (int s = 0; s < kStages; ++s) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, es.ev[s], es.ev[s + 1]) == hipSuccess) {
+                ctx->stage_ms[s] += ms;
+                ctx->stage_calls[s] += 1;
+            }
+        }
+    }
+    ctx->ring_pending = 0;
+    return LM_OK;
+}
+
+int stage_finish(lm_context* ctx) {
+    if (!ctx->timing) {
+        return LM_OK;
+    }
+    ctx->ring_next = (ctx->ring_next + 1) % kEventRing;
+    ctx->ring_pending += 1;
+    if (ctx->ring_pending >= kEventRing - 1) {
+        return stage_collect(ctx);
+    }
+    return LM_OK;
+}
+
+lm::RouteBufs route_bufs(lm_context* ctx, int32_t* idx, float* wts) {
+    lm::RouteBufs rb{};
+    rb.idx = idx;
+    rb.wt = wts;
+    rb.counts = ctx->ws.counts;
+    rb.offsets = ctx->ws.offsets;
+    rb.perm = ctx->ws.perm;
+    rb.slot_of = ctx->ws.slot_of;
+    rb.active = ctx->ws.active;
+    return rb;
+}
+
+// Expert kernels + combine for a layer whose routing is in rb (or a dense FFN).
+int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, int64_t T, const lm::RouteBufs& rb,
+                float* y, const float* residual, bool mfma) {
+    lm::ExpertArgs ea{};
+    ea.groups.gu = reinterpret_cast<const uint16_t* const*>(L.table);
+    const int ng = L.dense ? 1 : ctx->E + 1;
+    ea.groups.down = reinterpret_cast<const uint16_t* const*>(L.table + ng);
+    ea.groups.gu_h = reinterpret_cast<const _Float16* const*>(L.table + 2 * ng);
+    ea.groups.down_h = reinterpret_cast<const _Float16* const*>(L.table + 3 * ng);
+    ea.rb = rb;
+    ea.x = x;
+    ea.x16 = x16;
+    ea.act = static_cast<float*>(ctx->ws.act);
+    ea.act16 = static_cast<_Float16*>(ctx->ws.act);
+    ea.down_out = ctx->ws.down_out;
+    ea.tokens = T;
+    ea.hidden = ctx->H;
+    ea.hidden_p = ctx->Hp;
+    if (L.dense) {
+        ea.experts = 0;
+        ea.top_k = 0;
+        ea.inter_p = 0;
+        ea.shared_inter_p = L.dense_ffn.inter_p;
+        ea.has_shared = 1;
+    } else {
+        ea.experts = ctx->E;
+        ea.top_k = ctx->K;
+        ea.inter_p = ctx->Ip;
+        ea.shared_inter_p = L.shared_present ? ctx->Sp : 0;
+        ea.has_shared = L.shared_present ? 1 : 0;
+    }
+    const int64_t max_active = L.dense ? 0 : std::min<int64_t>(ctx->E, T * ctx->K);
+    stage_mark(ctx, 2);
+    if (mfma) {
+        LM_HIP(lm::launch_mfma_gateup(ea, 0, ctx->stream));
+        stage_mark(ctx, 3);
+        LM_HIP(lm::launch_mfma_down(ea, 0, ctx->stream));
+    } else {
+        const int64_t gu_items = max_active * (ea.inter_p / 16) + (ea.has_shared ? ea.shared_inter_p / 16 : 0);
+        LM_HIP(lm::launch_gemv_gateup(ea, gu_items, ctx->stream));
+        stage_mark(ctx, 3);
+        const int64_t down_items = (max_active + ea.has_shared) * (ctx->H / 16);
+        LM_HIP(lm::launch_gemv_down(ea, down_items, ctx->stream));
+    }
+    stage_mark(ctx, 4);
+    lm::CombineArgs ca{};
+    ca.down_out = ctx->ws.down_out;
+    ca.slot_of = rb.slot_of;
+    ca.wts = rb.wt;
+    ca.y = y;
+    ca.residual = residual;
+    ca.tokens = T;
+    ca.hidden = ctx->H;
+    ca.top_k = ea.top_k;
+    ca.has_shared = ea.has_shared;
+    LM_HIP(lm::launch_combine(ca, ctx->stream));
+    stage_mark(ctx, 5);
+    return LM_OK;
+}
+
+bool want_mfma(int32_t path, int64_t tokens) {
+    return path == LM_PATH_MFMA || (path == LM_PATH_AUTO && tokens > kMfmaCrossover);
+}
+
+int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
+              const float* bias, int32_t* idx_out, float* w_out, float* logits_out, int32_t path) {
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.allocated || L.dense || L.router_t == nullptr) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no resident MoE weights");
+    }
+    if (!L.finalized) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " is not finalized (lm_finalize_layer)");
+    }
+    const bool mfma = want_mfma(path, T);
+    int rc = ensure_workspace(ctx, T);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    int32_t* idx = idx_out != nullptr ? idx_out : ctx->ws.idx;
+    float* wts = w_out != nullptr ? w_out : ctx->ws.wts;
+
+    lm::RouterArgs ra{};
+    ra.x = x;
+    ra.wt = L.router_t;
+    ra.bias = bias;
+    ra.logits = logits_out;
+    ra.idx = idx;
+    ra.wts = wts;
+    ra.x16 = mfma ? ctx->ws.x16 : nullptr;
+    ra.tokens = T;
+    ra.hidden = ctx->H;
+    ra.hidden_p = ctx->Hp;
+    ra.experts = ctx->E;
+    ra.top_k = ctx->K;
+    ra.normalize = ctx->cfg.norm_topk_prob;
+    ra.group_limited = ctx->cfg.group_limited;
+    ra.n_group = ctx->cfg.n_group;
+    ra.topk_group = ctx->cfg.topk_group;
+    ra.scale = ctx->cfg.routed_scaling_factor;
+    ra.do_matvec = 1;
+    stage_mark(ctx, 0);
+    LM_HIP(lm::launch_router(ra, ctx->stream));
+    stage_mark(ctx, 1);
+
+    lm::PermuteArgs pa{};
+    pa.idx = idx;
+    pa.tokens = T;
+    pa.top_k = ctx->K;
+    pa.experts = ctx->E;
+    pa.rb = route_bufs(ctx, idx, wts);
+    LM_HIP(lm::launch_permute(pa, ctx->stream));
+
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    return stage_finish(ctx);
+}
+
+int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
+                int32_t path) {
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.allocated || !L.dense || !L.finalized) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no finalized dense FFN");
+    }
+    const bool mfma = want_mfma(path, T);
+    int rc = ensure_workspace(ctx, T);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (mfma) {
+        // fp16 copy of x via the router kernel's conversion is not available without
+        // routing, so convert with a select-free pass: reuse rms-free conversion below.
+        return fail(LM_EINVAL, "dense MFMA path is not built yet");
+    }
+    lm::RouteBufs rb{};
+    rb.counts = ctx->ws.zero;
+    rb.offsets = ctx->ws.zero;
+    rb.active = ctx->ws.zero;
+    rb.perm = ctx->ws.perm;
+    rb.slot_of = ctx->ws.slot_of;
+    rb.idx = ctx->ws.idx;
+    rb.wt = ctx->ws.wts;
+    stage_mark(ctx, 0);
+    stage_mark(ctx, 1);
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, rb, y, residual, false);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    return stage_finish(ctx);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lm_last_error(void) { return g_error.c_str(); }
+
+int lm_version(int32_t* major, int32_t* minor) {
+    if (major != nullptr) {
+        *major = 0;
+    }
+    if (minor != nullptr) {
+        *minor = 1;
+    }
+    return LM_OK;
+}
+
+int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** out) {
+    LM_GUARD_BEGIN
+    if (config == nullptr || out == nullptr) {
+        return fail(LM_EINVAL, "null config or output pointer");
+    }
+    *out = nullptr;
+    const lm_moe_config& c = *config;
+    if (c.hidden_size <= 0 || c.hidden_size % 8 != 0) {
+        return fail(LM_EINVAL, "hidden_size must be a positive multiple of 8");
+    }
+    if (c.n_routed_experts <= 0 || c.n_routed_experts > lm::kMaxExperts) {
+        return fail(LM_EINVAL, "n_routed_experts must be in [1, 64]");
+    }
+    if (c.num_experts_per_tok <= 0 || c.num_experts_per_tok > lm::kMaxTopK ||
+        c.num_experts_per_tok > c.n_routed_experts) {
+        return fail(LM_EINVAL, "num_experts_per_tok must be in [1, min(16, n_routed_experts)]");
+    }
+    if (c.moe_intermediate_size <= 0 || c.n_shared_experts < 0 || c.intermediate_size < 0 || c.num_layers <= 0) {
+        return fail(LM_EINVAL, "invalid intermediate sizes or layer count");
+    }
+    if (c.hidden_size % 16 != 0) {
+        return fail(LM_EINVAL, "hidden_size must be a multiple of 16 (GEMV item rows)");
+    }
+    int count = 0;
+    LM_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) {
+        return fail(LM_EINVAL, "device " + std::to_string(device) + " not present");
+    }
+    auto* ctx = new lm_context();
+    ctx->device = device;
+    ctx->cfg = c;
+    ctx->H = c.hidden_size;
+    ctx->Hp = static_cast<int>(lm::round_up(c.hidden_size, lm::kPad));
+    ctx->I = c.moe_intermediate_size;
+    ctx->Ip = static_cast<int>(lm::round_up(ctx->I, lm::kPad));
+    ctx->E = c.n_routed_experts;
+    ctx->K = c.num_experts_per_tok;
+    ctx->S = c.moe_intermediate_size * c.n_shared_experts;
+    ctx->Sp = static_cast<int>(lm::round_up(ctx->S, lm::kPad));
+    ctx->D = c.intermediate_size;
+    ctx->Dp = static_cast<int>(lm::round_up(ctx->D, lm::kPad));
+    ctx->layers.resize(static_cast<size_t>(c.num_layers));
+    int rc = set_device(ctx);
+    if (rc == LM_OK && hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        rc = fail(LM_EHIP, "hipStreamCreateWithFlags failed");
+    }
+    if (rc == LM_OK && hipMalloc(reinterpret_cast<void**>(&ctx->d_overflow), sizeof(int)) != hipSuccess) {
+        rc = fail(LM_ENOMEM, "hipMalloc failed");
+    }
+    if (rc != LM_OK) {
+        delete ctx;
+        return rc;
+    }
+    *out = ctx;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_context_destroy(lm_context* ctx) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return LM_OK;
+    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (Layer& L : ctx->layers) {
+        (void)hipFree(L.router_t);
+        (void)hipFree(L.norm);
+        (void)hipFree(L.slab);
+        (void)hipFree(L.table);
+    }
+    Workspace& w = ctx->ws;
+    void* ptrs[] = {w.idx, w.wts, w.counts, w.offsets, w.active, w.perm, w.slot_of,
+                    w.act, w.x16, w.down_out, w.xnorm, w.ffn, w.zero};
+    for (void* p : ptrs) {
+        (void)hipFree(p);
+    }
+    for (auto& kv : ctx->gemm_cache) {
+        (void)hipFree(kv.second.dev);
+    }
+    (void)hipFree(ctx->gemm_x);
+    (void)hipFree(ctx->gemm_out);
+    (void)hipFree(ctx->d_overflow);
+    if (ctx->staging != nullptr) {
+        (void)hipHostFree(ctx->staging);
+    }
+    for (EventSet& es : ctx->ring) {
+        for (hipEvent_t e : es.ev) {
+            (void)hipEventDestroy(e);
+        }
+    }
+    if (ctx->stream != nullptr) {
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_synchronize(lm_context* ctx) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+}
+
+int lm_alloc(lm_context* ctx, size_t bytes, void** out_dev) {
+    if (ctx == nullptr || out_dev == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    *out_dev = nullptr;
+    if (hipMalloc(out_dev, bytes == 0 ? 1 : bytes) != hipSuccess) {
+        return fail(LM_ENOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    return LM_OK;
+}
+
+int lm_free(lm_context* ctx, void* dev) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    LM_HIP(hipFree(dev));
+    return LM_OK;
+}
+
+int lm_copy_h2d(lm_context* ctx, void* dst_dev, const void* src_host, size_t bytes) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+}
+
+int lm_copy_d2h(lm_context* ctx, void* dst_host, const void* src_dev, size_t bytes) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+}
+
+int lm_memset(lm_context* ctx, void* dst_dev, int32_t value, size_t bytes) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipMemsetAsync(dst_dev, value, bytes, ctx->stream));
+    return LM_OK;
+}
+
+int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (gate_host == nullptr) {
+        return fail(LM_EINVAL, "null router gate");
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    const size_t n = static_cast<size_t>(ctx->H) * static_cast<size_t>(ctx->E);
+    if (L.router_t == nullptr) {
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), n * sizeof(float)));
+        ctx->resident += n * sizeof(float);
+    }
+    std::vector<float> t(n);
+    for (int e = 0; e < ctx->E; ++e) {
+        for (int i = 0; i < ctx->H; ++i) {
+            t[static_cast<size_t>(i) * ctx->E + e] = gate_host[static_cast<size_t>(e) * ctx->H + i];
+        }
+    }
+    LM_HIP(hipMemcpyAsync(L.router_t, t.data(), n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_upload_expert(lm_context* ctx, int32_t layer, int32_t expert, const uint16_t* gate_host,
+                     const uint16_t* up_host, const uint16_t* down_host) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (expert < 0 || expert >= ctx->E || gate_host == nullptr || up_host == nullptr || down_host == nullptr) {
+        return fail(LM_EINVAL, "bad expert index or null weights");
+    }
+    rc = set_device(ctx);
+    if (rc == LM_OK) {
+        rc = allocate_layer(ctx, layer, false);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    rc = upload_ffn(ctx, L.experts[static_cast<size_t>(expert)], gate_host, up_host, down_host);
+    if (rc == LM_OK) {
+        L.expert_present[static_cast<size_t>(expert)] = 1;
+        L.finalized = false;
+    }
+    return rc;
+    LM_GUARD_END
+}
+
+int lm_upload_shared(lm_context* ctx, int32_t layer, const uint16_t* gate_host, const uint16_t* up_host,
+                     const uint16_t* down_host) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (ctx->S == 0) {
+        return fail(LM_EINVAL, "the configuration has no shared experts");
+    }
+    if (gate_host == nullptr || up_host == nullptr || down_host == nullptr) {
+        return fail(LM_EINVAL, "null shared-expert weights");
+    }
+    rc = set_device(ctx);
+    if (rc == LM_OK) {
+        rc = allocate_layer(ctx, layer, false);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    rc = upload_ffn(ctx, L.shared, gate_host, up_host, down_host);
+    if (rc == LM_OK) {
+        L.shared_present = true;
+        L.finalized = false;
+    }
+    return rc;
+    LM_GUARD_END
+}
+
+int lm_upload_dense(lm_context* ctx, int32_t layer, const uint16_t* gate_host, const uint16_t* up_host,
+                    const uint16_t* down_host) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (ctx->D == 0) {
+        return fail(LM_EINVAL, "the configuration has no dense intermediate size");
+    }
+    if (gate_host == nullptr || up_host == nullptr || down_host == nullptr) {
+        return fail(LM_EINVAL, "null dense weights");
+    }
+    rc = set_device(ctx);
+    if (rc == LM_OK) {
+        rc = allocate_layer(ctx, layer, true);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    rc = upload_ffn(ctx, L.dense_ffn, gate_host, up_host, down_host);
+    if (rc == LM_OK) {
+        L.finalized = false;
+    }
+    return rc;
+    LM_GUARD_END
+}
+
+int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (weight_host == nullptr) {
+        return fail(LM_EINVAL, "null norm weight");
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (L.norm == nullptr) {
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.norm), sizeof(float) * static_cast<size_t>(ctx->H)));
+    }
+    LM_HIP(hipMemcpyAsync(L.norm, weight_host, sizeof(float) * static_cast<size_t>(ctx->H), hipMemcpyHostToDevice,
+                          ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_finalize_layer(lm_context* ctx, int32_t layer) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.allocated) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no uploaded FFN weights");
+    }
+    if (!L.dense) {
+        for (int e = 0; e < ctx->E; ++e) {
+            if (!L.expert_present[static_cast<size_t>(e)]) {
+                return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " expert " + std::to_string(e) +
+                                            " was not uploaded");
+            }
+        }
+        if (L.router_t == nullptr) {
+            return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no router gate");
+        }
+    }
+    // fp16 shadow of the whole slab (bf16 half first, fp16 half second, same layout).
+    const size_t half_bytes = L.slab_bytes / 2;
+    LM_HIP(hipMemsetAsync(ctx->d_overflow, 0, sizeof(int), ctx->stream));
+    LM_HIP(lm::launch_bf16_to_f16(static_cast<const uint16_t*>(L.slab),
+                                  reinterpret_cast<_Float16*>(static_cast<char*>(L.slab) + half_bytes),
+                                  static_cast<int64_t>(half_bytes / 2), ctx->d_overflow, ctx->stream));
+    int overflow = 0;
+    LM_HIP(hipMemcpyAsync(&overflow, ctx->d_overflow, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    if (overflow != 0) {
+        return fail(LM_EINVAL, "layer " + std::to_string(layer) + ": " + std::to_string(overflow) +
+                                   " weights exceed the fp16 range of the MFMA path");
+    }
+    // Group pointer table: gu, down, gu_h, down_h, each [groups].
+    const int ng = L.dense ? 1 : ctx->E + 1;
+    std::vector<void*> table(static_cast<size_t>(4 * ng), nullptr);
+    for (int g = 0; g < ng; ++g) {
+        const lm::FfnDev* f = L.dense ? &L.dense_ffn : (g < ctx->E ? &L.experts[static_cast<size_t>(g)] : &L.shared);
+        if (!L.dense && g == ctx->E && !L.shared_present) {
+            continue;
+        }
+        table[static_cast<size_t>(g)] = f->gu;
+        table[static_cast<size_t>(ng + g)] = f->down;
+        table[static_cast<size_t>(2 * ng + g)] = f->gu_h;
+        table[static_cast<size_t>(3 * ng + g)] = f->down_h;
+    }
+    if (L.table == nullptr) {
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.table), sizeof(void*) * table.size()));
+    }
+    LM_HIP(hipMemcpyAsync(L.table, table.data(), sizeof(void*) * table.size(), hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    L.finalized = true;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_resident_bytes(lm_context* ctx, uint64_t* out) {
+    if (ctx == nullptr || out == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    *out = ctx->resident;
+    return LM_OK;
+}
+
+int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
+                   const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev, float* logits_dev,
+                   int32_t path) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (tokens < 0 || (tokens > 0 && (x_dev == nullptr || y_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null x / y");
+    }
+    if (path < LM_PATH_AUTO || path > LM_PATH_MFMA) {
+        return fail(LM_EINVAL, "unknown path");
+    }
+    if (tokens == 0) {
+        return LM_OK;
+    }
+    return moe_layer(ctx, layer, x_dev, tokens, y_dev, nullptr, logit_bias_dev, topk_index_dev, topk_weight_dev,
+                     logits_dev, path);
+    LM_GUARD_END
+}
+
+int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, const float* logit_bias_dev,
+              float* logits_dev, int32_t* topk_index_dev, float* topk_weight_dev) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (L.router_t == nullptr) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no router gate");
+    }
+    if (tokens < 0 || (tokens > 0 && (x_dev == nullptr || topk_index_dev == nullptr || topk_weight_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null buffers");
+    }
+    lm::RouterArgs ra{};
+    ra.x = x_dev;
+    ra.wt = L.router_t;
+    ra.bias = logit_bias_dev;
+    ra.logits = logits_dev;
+    ra.idx = topk_index_dev;
+    ra.wts = topk_weight_dev;
+    ra.tokens = tokens;
+    ra.hidden = ctx->H;
+    ra.hidden_p = ctx->Hp;
+    ra.experts = ctx->E;
+    ra.top_k = ctx->K;
+    ra.normalize = ctx->cfg.norm_topk_prob;
+    ra.group_limited = ctx->cfg.group_limited;
+    ra.n_group = ctx->cfg.n_group;
+    ra.topk_group = ctx->cfg.topk_group;
+    ra.scale = ctx->cfg.routed_scaling_factor;
+    ra.do_matvec = 1;
+    LM_HIP(lm::launch_router(ra, ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_router_select(lm_context* ctx, const float* logits_dev, int64_t tokens, int32_t* topk_index_dev,
+                     float* topk_weight_dev) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (tokens < 0 || (tokens > 0 && (logits_dev == nullptr || topk_index_dev == nullptr || topk_weight_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null buffers");
+    }
+    lm::RouterArgs ra{};
+    ra.x = logits_dev;
+    ra.idx = topk_index_dev;
+    ra.wts = topk_weight_dev;
+    ra.tokens = tokens;
+    ra.hidden = ctx->H;
+    ra.hidden_p = ctx->Hp;
+    ra.experts = ctx->E;
+    ra.top_k = ctx->K;
+    ra.normalize = ctx->cfg.norm_topk_prob;
+    ra.group_limited = ctx->cfg.group_limited;
+    ra.n_group = ctx->cfg.n_group;
+    ra.topk_group = ctx->cfg.topk_group;
+    ra.scale = ctx->cfg.routed_scaling_factor;
+    ra.do_matvec = 0;
+    LM_HIP(lm::launch_router(ra, ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_permute(lm_context* ctx, const int32_t* topk_index_dev, int64_t tokens, int32_t* counts_dev,
+               int32_t* offsets_dev, int32_t* perm_dev, int32_t* slot_of_dev) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (tokens < 0 || (tokens > 0 && (topk_index_dev == nullptr || counts_dev == nullptr || offsets_dev == nullptr ||
+                                      perm_dev == nullptr || slot_of_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null buffers");
+    }
+    int rc = ensure_workspace(ctx, tokens);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    lm::PermuteArgs pa{};
+    pa.idx = topk_index_dev;
+    pa.tokens = tokens;
+    pa.top_k = ctx->K;
+    pa.experts = ctx->E;
+    pa.rb.idx = const_cast<int32_t*>(topk_index_dev);
+    pa.rb.counts = counts_dev;
+    pa.rb.offsets = offsets_dev;
+    pa.rb.perm = perm_dev;
+    pa.rb.slot_of = slot_of_dev;
+    pa.rb.active = ctx->ws.active;
+    LM_HIP(lm::launch_permute(pa, ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_rms_norm(lm_context* ctx, const float* in_dev, const float* weight_dev, float* out_dev, int64_t tokens,
+                int32_t hidden, float epsilon) {
+    if (ctx == nullptr || in_dev == nullptr || weight_dev == nullptr || out_dev == nullptr || hidden <= 0) {
+        return fail(LM_EINVAL, "null argument or bad hidden size");
+    }
+    LM_HIP(lm::launch_rms_norm(in_dev, weight_dev, out_dev, tokens, hidden, epsilon, ctx->stream));
+    return LM_OK;
+}
+
+int lm_dense_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev, int32_t path) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (tokens <= 0) {
+        return tokens == 0 ? LM_OK : fail(LM_EINVAL, "negative token count");
+    }
+    return dense_layer(ctx, layer, x_dev, tokens, y_dev, nullptr, path);
+    LM_GUARD_END
+}
+
+int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
+                     int32_t path) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, first_layer);
+    if (rc == LM_OK) {
+        rc = check_layer(ctx, last_layer);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (tokens <= 0 || hidden_dev == nullptr) {
+        return tokens == 0 ? LM_OK : fail(LM_EINVAL, "bad token count or null hidden state");
+    }
+    rc = ensure_workspace(ctx, tokens);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    for (int32_t l = first_layer; l <= last_layer; ++l) {
+        Layer& L = ctx->layers[static_cast<size_t>(l)];
+        if (L.norm == nullptr) {
+            return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no norm weight");
+        }
+        // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290, attention omitted).
+        LM_HIP(lm::launch_rms_norm(hidden_dev, L.norm, ctx->ws.xnorm, tokens, ctx->H, ctx->cfg.rms_norm_eps,
+                                   ctx->stream));
+        if (L.dense) {
+            rc = dense_layer(ctx, l, ctx->ws.xnorm, tokens, hidden_dev, hidden_dev, path);
+        } else {
+            rc = moe_layer(ctx, l, ctx->ws.xnorm, tokens, hidden_dev, hidden_dev, nullptr, nullptr, nullptr, nullptr,
+                           path);
+        }
+        if (rc != LM_OK) {
+            return rc;
+        }
+    }
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_gemm_matvec_bf16(lm_context* ctx, const uint16_t* w_host, const float* x_host, float* out_host,
+                        size_t out_dim, size_t in_dim, float scale, int32_t accumulate) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || w_host == nullptr || x_host == nullptr || out_host == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    if (out_dim == 0) {
+        return LM_OK;
+    }
+    const size_t elems = out_dim * in_dim;
+    auto it = ctx->gemm_cache.find(w_host);
+    if (it != ctx->gemm_cache.end() && it->second.elems != elems) {
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        LM_HIP(hipFree(it->second.dev));
+        ctx->gemm_cache.erase(it);
+        it = ctx->gemm_cache.end();
+    }
+    if (it == ctx->gemm_cache.end()) {
+        uint16_t* dev = nullptr;
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&dev), std::max<size_t>(elems, 1) * 2));
+        LM_HIP(hipMemcpyAsync(dev, w_host, elems * 2, hipMemcpyHostToDevice, ctx->stream));
+        it = ctx->gemm_cache.emplace(w_host, lm_context::Cached{dev, elems}).first;
+    }
+    const size_t need = std::max(out_dim, in_dim);
+    if (ctx->gemm_cap < need) {
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        (void)hipFree(ctx->gemm_x);
+        (void)hipFree(ctx->gemm_out);
+        ctx->gemm_x = nullptr;
+        ctx->gemm_out = nullptr;
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_x), need * sizeof(float)));
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_out), need * sizeof(float)));
+        ctx->gemm_cap = need;
+    }
+    LM_HIP(hipMemcpyAsync(ctx->gemm_x, x_host, in_dim * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    if (accumulate) {
+        LM_HIP(hipMemcpyAsync(ctx->gemm_out, out_host, out_dim * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    }
+    LM_HIP(lm::launch_gemv_plain(it->second.dev, ctx->gemm_x, ctx->gemm_out, static_cast<int64_t>(out_dim),
+                                 static_cast<int64_t>(in_dim), scale, accumulate, ctx->stream));
+    LM_HIP(hipMemcpyAsync(out_host, ctx->gemm_out, out_dim * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_event_create(lm_context* ctx, void** out_event) {
+    if (ctx == nullptr || out_event == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    hipEvent_t e = nullptr;
+    LM_HIP(hipEventCreate(&e));
+    *out_event = e;
+    return LM_OK;
+}
+
+int lm_event_destroy(lm_context* ctx, void* event) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    LM_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+    return LM_OK;
+}
+
+int lm_event_record(lm_context* ctx, void* event) {
+    if (ctx == nullptr || event == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    LM_HIP(hipEventRecord(static_cast<hipEvent_t>(event), ctx->stream));
+    return LM_OK;
+}
+
+int lm_event_elapsed_ms(lm_context* ctx, void* start, void* stop, float* out_ms) {
+    if (ctx == nullptr || start == nullptr || stop == nullptr || out_ms == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    LM_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+    LM_HIP(hipEventElapsedTime(out_ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+    return LM_OK;
+}
+
+int lm_stage_timing(lm_context* ctx, int32_t enable) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (enable && ctx->ring.empty()) {
+        ctx->ring.resize(kEventRing);
+        for (EventSet& es : ctx->ring) {
+            for (hipEvent_t& e : es.ev) {
+                LM_HIP(hipEventCreate(&e));
+            }
+        }
+    }
+    int rc = stage_collect(ctx);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    ctx->timing = enable != 0;
+    for (int s = 0; s < kStages; ++s) {
+        ctx->stage_ms[s] = 0.0;
+        ctx->stage_calls[s] = 0;
+    }
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_stage_times(lm_context* ctx, double* out_ms, int32_t* out_calls, int32_t stages) {
+    if (ctx == nullptr || out_ms == nullptr || out_calls == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    int rc = stage_collect(ctx);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    for (int s = 0; s < stages && s < kStages; ++s) {
+        out_ms[s] = ctx->stage_ms[s];
+        out_calls[s] = ctx->stage_calls[s];
+    }
+    return LM_OK;
+}
+
+}  // extern "C"

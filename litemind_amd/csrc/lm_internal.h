@@ -1,0 +1,119 @@
+// lm_internal.h -- shared definitions of the gfx950 MoE library (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lm_math.h"
+
+namespace lm {
+
+// Weight rows are stored with gate and up interleaved in groups of kGroupRows:
+// rows [2*g*G, 2*g*G + G) are gate rows [g*G, (g+1)*G) and the next G rows are
+// the matching up rows.  One 32-wide MFMA column block therefore holds only gate
+// or only up, and its partner block holds the same output columns.
+constexpr int kGroupRows = 32;
+// Padding granularity of the intermediate (reduction) and hidden dimensions in
+// the resident layout; padded rows and columns are zero.
+constexpr int kPad = 64;
+constexpr int kMaxExperts = 64;   // router kernel: one lane per expert
+constexpr int kMaxTopK = 16;
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// One FFN (routed expert, the fused shared expert or a dense layer) resident in HBM.
+//   gu:   [2 * inter_p, hidden_p] BF16, gate/up interleaved as above
+//   down: [hidden, inter_p] BF16 (columns >= inter are zero)
+//   *_h:  the same matrices re-encoded as fp16 for the MFMA path
+struct FfnDev {
+    uint16_t* gu = nullptr;
+    uint16_t* down = nullptr;
+    _Float16* gu_h = nullptr;
+    _Float16* down_h = nullptr;
+    int32_t inter = 0;    // logical intermediate width
+    int32_t inter_p = 0;  // padded to kPad
+};
+
+// Per-group tables the expert kernels index by group id: group g < E is routed
+// expert g, group E is the shared expert.  Device arrays of pointers.
+struct GroupTable {
+    const uint16_t* const* gu;       // [E+1]
+    const uint16_t* const* down;     // [E+1]
+    const _Float16* const* gu_h;     // [E+1]
+    const _Float16* const* down_h;   // [E+1]
+};
+
+// Routing results and the permutation, in device memory.
+struct RouteBufs {
+    int32_t* idx;        // [T*K]
+    float* wt;           // [T*K]
+    int32_t* counts;     // [E]
+    int32_t* offsets;    // [E+1]
+    int32_t* perm;       // [T*K]   assignment id at each permuted slot
+    int32_t* slot_of;    // [T*K]   permuted slot of each assignment
+    int32_t* active;     // [E+1]   routed experts with tokens, ascending; [E] = their number
+};
+
+struct RouterArgs {
+    const float* x;          // [T, H]
+    const float* wt;         // [H, E] router gate, transposed
+    const float* bias;       // [E] or null
+    float* logits;           // [T, E] or null
+    int32_t* idx;            // [T, K]
+    float* wts;              // [T, K]
+    _Float16* x16;           // [T, Hp] or null
+    int64_t tokens;
+    int32_t hidden, hidden_p, experts, top_k;
+    int32_t normalize, group_limited, n_group, topk_group;
+    float scale;
+    int32_t do_matvec;       // 0: x holds logits [T, E] already (select only)
+};
+
+struct PermuteArgs {
+    const int32_t* idx;
+    int64_t tokens;
+    int32_t top_k, experts;
+    RouteBufs rb;
+};
+
+// Grouped expert kernels.  Slot space: routed slots [0, T*K) in permuted order,
+// shared slots [T*K, T*K + T) in token order.
+struct ExpertArgs {
+    GroupTable groups;
+    RouteBufs rb;
+    const float* x;          // [T, H] fp32 (GEMV path)
+    const _Float16* x16;     // [T, Hp] fp16 (MFMA path)
+    float* act;              // GEMV: activations fp32, routed [T*K, Ip] then shared [T, Sp]
+    _Float16* act16;         // MFMA: activations fp16, same layout
+    float* down_out;         // [T*K + T, H] fp32 down-projection per slot
+    int64_t tokens;
+    int32_t hidden, hidden_p, experts, top_k;
+    int32_t inter_p, shared_inter_p;   // padded widths (shared 0 = none)
+    int32_t has_shared;
+};
+
+struct CombineArgs {
+    const float* down_out;   // [T*K + T, H]
+    const int32_t* slot_of;  // [T*K]
+    const float* wts;        // [T*K]
+    float* y;                // [T, H]
+    const float* residual;   // [T, H] or null: y = residual + ffn
+    int64_t tokens;
+    int32_t hidden, top_k, has_shared;
+};
+
+// Kernel launchers (implemented in the .hip files).
+hipError_t launch_router(const RouterArgs& a, hipStream_t s);
+hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
+hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_items, hipStream_t s);
+hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_items, hipStream_t s);
+hipError_t launch_mfma_gateup(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
+hipError_t launch_mfma_down(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
+hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
+hipError_t launch_bf16_to_f16(const uint16_t* src, _Float16* dst, int64_t n, int* overflow, hipStream_t s);
+hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
+                           hipStream_t s);
+hipError_t launch_gemv_plain(const uint16_t* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
+                             float scale, int32_t accumulate, hipStream_t s);
+
+}  // namespace lm

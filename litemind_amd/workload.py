@@ -1,0 +1,260 @@
+"""Seeded synthetic workloads for the MoE feed-forward path (DeepSeek-V2-Lite shapes).
+
+All tensors are pure functions of (seed, stream, element index) produced by
+``libsynth.so`` (counter-based SplitMix64 + Box-Muller in double, rounded to fp32
+and then BF16 with round-to-nearest-even).  The same bits are uploaded to the GPU
+and handed to the CPU checker.
+
+Workloads (sizes of DeepSeek-V2-Lite: hidden 2048, 64 routed experts of width
+1408, top-6, 2 shared experts fused to width 2816, dense layer 0 of width 10944):
+  decode_t1        T=1 decode
+  decode_t32       T=32 batched decode, random routing (1-4 tokens per expert)
+  prefill_t512     T=512, router gate scaled by 1e-2 so routing is near-uniform
+  prefill_t2048_skewed  T=2048, per-expert logit bias: 8 hot experts take ~70% of
+                   the 12288 assignments, the rest follow a Zipf(1.1) tail
+  stack            dense layer 0 + 26 MoE layers chained through RMSNorm, T=1 and T=4096
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SYNTH_PATH = os.path.join(HERE, "libsynth.so")
+
+MASTER_SEED = 0x4C4D3335  # "LM35"
+
+# Stream ids of the tensors of one layer.
+S_ROUTER, S_GATE, S_UP, S_DOWN, S_SH_GATE, S_SH_UP, S_SH_DOWN, S_D_GATE, S_D_UP, S_D_DOWN = range(10)
+S_TOKENS = 1000
+
+
+@dataclasses.dataclass(frozen=True)
+class Dims:
+    hidden: int = 2048
+    inter: int = 1408
+    experts: int = 64
+    top_k: int = 6
+    n_shared: int = 2
+    dense_inter: int = 10944
+    layers: int = 27
+    norm_topk_prob: bool = False
+    routed_scaling_factor: float = 1.0
+    rms_norm_eps: float = 1e-6
+
+    @property
+    def shared_inter(self) -> int:
+        return self.inter * self.n_shared
+
+    def expert_bytes(self) -> int:
+        return 3 * self.inter * self.hidden * 2
+
+    def moe_config(self, num_layers: int | None = None):
+        from . import MoeConfig
+
+        return MoeConfig(
+            hidden_size=self.hidden, moe_intermediate_size=self.inter, n_routed_experts=self.experts,
+            num_experts_per_tok=self.top_k, n_shared_experts=self.n_shared, intermediate_size=self.dense_inter,
+            norm_topk_prob=1 if self.norm_topk_prob else 0, routed_scaling_factor=self.routed_scaling_factor,
+            group_limited=0, n_group=1, topk_group=1, rms_norm_eps=self.rms_norm_eps,
+            num_layers=num_layers if num_layers is not None else self.layers)
+
+
+V2_LITE = Dims()
+
+_synth = None
+
+
+def synth() -> C.CDLL:
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_PATH):
+            raise RuntimeError(f"{SYNTH_PATH} is missing: build it with `python -m litemind_amd.build`")
+        lib = C.CDLL(SYNTH_PATH)
+        lib.lms_normal_f32.argtypes = [C.c_uint64, C.c_uint64, C.c_float, C.c_void_p, C.c_size_t, C.c_int]
+        lib.lms_normal_bf16.argtypes = [C.c_uint64, C.c_uint64, C.c_float, C.c_void_p, C.c_size_t, C.c_int]
+        lib.lms_rms_rows.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_int]
+        lib.lms_expf_ref.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        lib.lms_expf_sweep.argtypes = [C.c_uint32, C.c_float, C.c_float, C.c_void_p]
+        lib.lms_expf_sweep.restype = C.c_uint64
+        for f in (lib.lms_normal_f32, lib.lms_normal_bf16, lib.lms_rms_rows, lib.lms_expf_ref):
+            f.restype = None
+        _synth = lib
+    return _synth
+
+
+def stream_id(layer: int, kind: int, index: int = 0) -> int:
+    return (layer * 64 + kind) * 4096 + index
+
+
+def normal_f32(seed: int, stream: int, sigma: float, shape, threads: int = 0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    synth().lms_normal_f32(seed, stream, sigma, out.ctypes.data, out.size, threads)
+    return out
+
+
+def normal_bf16(seed: int, stream: int, sigma: float, shape, threads: int = 0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint16)
+    synth().lms_normal_bf16(seed, stream, sigma, out.ctypes.data, out.size, threads)
+    return out
+
+
+def tokens(seed: int, count: int, hidden: int, stream: int = S_TOKENS, threads: int = 0) -> np.ndarray:
+    """x ~ N(0,1) per element, then RMSNorm with unit weight (the MoE block's input)."""
+    x = normal_f32(seed, stream_id(0, 0, 0) + stream, 1.0, (count, hidden), threads)
+    synth().lms_rms_rows(x.ctypes.data, count, hidden, 1e-6, threads)
+    return x
+
+
+@dataclasses.dataclass
+class MoeLayer:
+    dims: Dims
+    router: np.ndarray                 # [E, H] fp32
+    gate: list                         # E x [I, H] uint16 (BF16 bits)
+    up: list
+    down: list                         # E x [H, I]
+    shared_gate: np.ndarray | None     # [S, H]
+    shared_up: np.ndarray | None
+    shared_down: np.ndarray | None     # [H, S]
+
+
+def moe_layer(seed: int, layer: int, dims: Dims = V2_LITE, router_scale: float = 1.0, threads: int = 0) -> MoeLayer:
+    """Router ~N(0, 0.02) fp32 (times router_scale), experts and shared ~N(0, 0.02) BF16."""
+    H, I, E, S = dims.hidden, dims.inter, dims.experts, dims.shared_inter
+    router = normal_f32(seed, stream_id(layer, S_ROUTER), 0.02, (E, H), threads)
+    if router_scale != 1.0:
+        router = (router.astype(np.float64) * router_scale).astype(np.float32)
+    gate = [normal_bf16(seed, stream_id(layer, S_GATE, e), 0.02, (I, H), threads) for e in range(E)]
+    up = [normal_bf16(seed, stream_id(layer, S_UP, e), 0.02, (I, H), threads) for e in range(E)]
+    down = [normal_bf16(seed, stream_id(layer, S_DOWN, e), 0.02, (H, I), threads) for e in range(E)]
+    sg = su = sd = None
+    if S > 0:
+        sg = normal_bf16(seed, stream_id(layer, S_SH_GATE), 0.02, (S, H), threads)
+        su = normal_bf16(seed, stream_id(layer, S_SH_UP), 0.02, (S, H), threads)
+        sd = normal_bf16(seed, stream_id(layer, S_SH_DOWN), 0.02, (H, S), threads)
+    return MoeLayer(dims, router, gate, up, down, sg, su, sd)
+
+
+def dense_ffn(seed: int, layer: int, dims: Dims = V2_LITE, threads: int = 0):
+    H, D = dims.hidden, dims.dense_inter
+    return (normal_bf16(seed, stream_id(layer, S_D_GATE), 0.02, (D, H), threads),
+            normal_bf16(seed, stream_id(layer, S_D_UP), 0.02, (D, H), threads),
+            normal_bf16(seed, stream_id(layer, S_D_DOWN), 0.02, (H, D), threads))
+
+
+def upload_moe_layer(ctx, layer_id: int, L: MoeLayer) -> None:
+    ctx.upload_router(layer_id, L.router)
+    for e in range(L.dims.experts):
+        ctx.upload_expert(layer_id, e, L.gate[e], L.up[e], L.down[e])
+    if L.shared_gate is not None:
+        ctx.upload_shared(layer_id, L.shared_gate, L.shared_up, L.shared_down)
+    ctx.finalize_layer(layer_id)
+
+
+def skew_targets(dims: Dims = V2_LITE, hot: int = 8, hot_share: float = 0.70, zipf: float = 1.1) -> np.ndarray:
+    """Target share of the T*k assignments per expert: hot experts split hot_share
+    evenly; the remaining experts follow Zipf(zipf) by rank."""
+    E = dims.experts
+    tail = np.array([1.0 / (r ** zipf) for r in range(1, E - hot + 1)])
+    tail = tail / tail.sum() * (1.0 - hot_share)
+    return np.concatenate([np.full(hot, hot_share / hot), tail])
+
+
+def _topk_counts(logits: np.ndarray, k: int) -> np.ndarray:
+    top = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    return np.bincount(top.ravel(), minlength=logits.shape[1])
+
+
+def calibrate_skew_bias(router: np.ndarray, x: np.ndarray, dims: Dims = V2_LITE, iters: int = 200) -> np.ndarray:
+    """Per-expert bias so top-k routing of x matches skew_targets (float64 model of the router)."""
+    logits = x.astype(np.float64) @ router.astype(np.float64).T
+    target = skew_targets(dims) * x.shape[0] * dims.top_k
+    bias = np.zeros(dims.experts)
+    for _ in range(iters):
+        counts = _topk_counts(logits + bias, dims.top_k).astype(np.float64)
+        bias += 0.5 * (np.log(target + 0.5) - np.log(counts + 0.5))
+        bias -= bias.mean()
+    return bias.astype(np.float32)
+
+
+@dataclasses.dataclass(frozen=True)
+class Workload:
+    name: str
+    tokens: int
+    router_scale: float = 1.0
+    skewed: bool = False
+    description: str = ""
+
+
+WORKLOADS = {
+    "decode_t1": Workload("decode_t1", 1, description="DeepSeek-V2-Lite MoE layer, decode T=1"),
+    "decode_t32": Workload("decode_t32", 32, description="batched decode T=32, random routing"),
+    "prefill_t512": Workload("prefill_t512", 512, router_scale=1e-2,
+                             description="prefill T=512, router gate x1e-2 (near-uniform routing)"),
+    "prefill_t2048_skewed": Workload("prefill_t2048_skewed", 2048, skewed=True,
+                                     description="prefill T=2048, 8 hot experts take ~70% + Zipf(1.1) tail"),
+}
+
+
+def skew_bias(dims: Dims = V2_LITE, seed: int = MASTER_SEED) -> np.ndarray:
+    """The committed bias of the skewed workload (recomputed only if absent)."""
+    path = os.path.join(HERE, "data", "skew_bias_v2lite.npy")
+    if os.path.exists(path):
+        return np.load(path, allow_pickle=False)
+    router = normal_f32(seed, stream_id(0, S_ROUTER), 0.02, (dims.experts, dims.hidden))
+    x = tokens(seed, 2048, dims.hidden)
+    return calibrate_skew_bias(router, x, dims)
+
+
+def tiny_model_layers(layer: int = 1):
+    """A MoE layer of LiteMind's tiny test checkpoint (tools/make_test_model.py:29-70,
+    :73-93, :101-173), restated: the same LCG (seed 20240816, Numerical Recipes
+    constants), the same tensor order, values (s / 0xFFFFFFFF) * 2 - 1 scaled by
+    0.08 and truncated to BF16.  Returns (dims, MoeLayer) for `layer` >= 1."""
+    cfg = dict(hidden=32, layers=3, heads=2, vocab=300, kv_rank=16, qk_nope=8, qk_rope=4, v_head=8, inter=64,
+               moe_inter=16, experts=4, shared=1, top_k=2)
+    state = [20240816 & 0xFFFFFFFF]
+
+    def tensor(count):
+        out = np.empty(count, dtype=np.uint16)
+        s = state[0]
+        for i in range(count):
+            s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+            f = np.float32(((s / 0xFFFFFFFF) * 2.0 - 1.0) * 0.08)  # struct.pack('<f') rounds to fp32
+            out[i] = np.array([f], dtype=np.float32).view(np.uint32)[0] >> 16
+        state[0] = s
+        return out
+
+    H = cfg["hidden"]
+    qk_head = cfg["qk_nope"] + cfg["qk_rope"]
+    tensor(cfg["vocab"] * H)
+    result = None
+    for lyr in range(cfg["layers"]):
+        tensor(cfg["heads"] * qk_head * H)
+        tensor((cfg["kv_rank"] + cfg["qk_rope"]) * H)
+        tensor(cfg["heads"] * (cfg["qk_nope"] + cfg["v_head"]) * cfg["kv_rank"])
+        tensor(H * cfg["heads"] * cfg["v_head"])
+        if lyr < 1:
+            for _ in range(3):
+                tensor(cfg["inter"] * H)
+            continue
+        E, I = cfg["experts"], cfg["moe_inter"]
+        router = tensor(E * H)
+        gate, up, down = [], [], []
+        for _ in range(E):
+            gate.append(tensor(I * H).reshape(I, H))
+            up.append(tensor(I * H).reshape(I, H))
+            down.append(tensor(H * I).reshape(H, I))
+        S = I * cfg["shared"]
+        sg = tensor(S * H).reshape(S, H)
+        su = tensor(S * H).reshape(S, H)
+        sd = tensor(H * S).reshape(H, S)
+        if lyr == layer:
+            router_f32 = (router.astype(np.uint32) << 16).view(np.float32).reshape(E, H)
+            dims = Dims(hidden=H, inter=I, experts=E, top_k=cfg["top_k"], n_shared=cfg["shared"],
+                        dense_inter=cfg["inter"], layers=cfg["layers"])
+            result = (dims, MoeLayer(dims, router_f32, gate, up, down, sg, su, sd))
+    return result
