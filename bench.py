@@ -1,0 +1,227 @@
+"""Benchmark of the MI355X MoE feed-forward path (DeepSeek-V2-Lite MoE layer).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_t1] [--no-cpu]
+
+A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
+experts, combine) over one batch of T synthetic tokens whose inputs are already
+resident in HBM.  The headline workload is decode at T=1; it rotates through 8
+independently seeded layers (1.15 GB each) so the 139 MB active set of a step
+cannot be served from the 256 MB Infinity Cache.  The T=2048 skewed prefill
+workload is measured in the same run and reported under "t2048".
+
+Prints ONE JSON line (rank 0) with the throughput, the dominant kernel's
+roofline fraction measured with HIP events on the library's stream, and
+LiteMind's own CPU path (its kernels compiled from its sources) timed on a
+bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tokens/sec at T=1 and T=2048; % HBM BW (T=1) / % bf16 MFMA (T=2048)"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2516.6  # dense bf16/fp16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk/CU
+
+EXPERT_BYTES = 3 * 1408 * 2048 * 2          # 17,301,504
+GATEUP_EXPERT_BYTES = 2 * 1408 * 2048 * 2   # 11,534,336
+DOWN_EXPERT_BYTES = 1408 * 2048 * 2         # 5,767,168
+SHARED_BYTES = 3 * 2816 * 2048 * 2          # 34,603,008
+ROUTER_BYTES = 64 * 2048 * 4                # 524,288
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic(tokens: int, distinct_experts: int) -> dict:
+    """Bytes and flops of one MoE layer step (weights read once, activations in/out)."""
+    T, U = tokens, distinct_experts
+    H, I, S, K = 2048, 1408, 2816, 6
+    layer_bytes = U * EXPERT_BYTES + SHARED_BYTES + ROUTER_BYTES + T * H * 4 * 2
+    gate_up_bytes = U * GATEUP_EXPERT_BYTES + 2 * S * H * 2 + T * H * 4 + (T * K * I + T * S) * 4
+    down_bytes = U * DOWN_EXPERT_BYTES + S * H * 2 + (T * K * I + T * S) * 4 + (T * K + T) * H * 4
+    flops_assign = 6 * H * I
+    layer_flops = T * K * flops_assign + T * 6 * H * S + T * 2 * 64 * H
+    gate_up_flops = T * K * 4 * H * I + T * 4 * H * S
+    down_flops = T * K * 2 * H * I + T * 2 * H * S
+    return dict(layer_bytes=layer_bytes, gate_up_bytes=gate_up_bytes, down_bytes=down_bytes,
+                layer_flops=layer_flops, gate_up_flops=gate_up_flops, down_flops=down_flops)
+
+
+def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int):
+    from litemind_amd import STAGES, Context
+    from litemind_amd import workload as wl
+
+    w = wl.WORKLOADS[workload_name]
+    dims = wl.V2_LITE
+    T = w.tokens
+    log(f"{workload_name}: generating {rotate} layer(s) and uploading")
+    ctx = Context(dims.moe_config(num_layers=rotate))
+    layers = []
+    for l in range(rotate):
+        L = wl.moe_layer(wl.MASTER_SEED + l, 0, dims, router_scale=w.router_scale)
+        wl.upload_moe_layer(ctx, l, L)
+        layers.append(L)
+    x = wl.tokens(wl.MASTER_SEED + 7, T, dims.hidden)
+    bias = wl.skew_bias() if w.skewed else None
+    dx = ctx.to_device(x)
+    dy = ctx.empty((T, dims.hidden))
+    didx = ctx.empty((rotate, T, dims.top_k), np.int32)
+    dw = ctx.empty((rotate, T, dims.top_k))
+    db = ctx.to_device(bias) if bias is not None else None
+    idx_stride = T * dims.top_k * 4
+
+    def step(i):
+        l = i % rotate
+        ctx.moe_forward(l, dx, T, dy, bias=db, idx=didx.ptr + l * idx_stride, w=dw.ptr + l * idx_stride, path=path)
+
+    log(f"{workload_name}: warmup {warmup}")
+    for i in range(warmup):
+        step(i)
+    ctx.synchronize()
+    start_ev, stop_ev = ctx.event(), ctx.event()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    ctx.record(start_ev)
+    for i in range(steps):
+        step(i)
+    ctx.record(stop_ev)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ctx.elapsed_ms(start_ev, stop_ev)
+    log(f"{workload_name}: {steps} steps wall {wall * 1e3:.3f} ms, events {gpu_ms:.3f} ms")
+
+    # Per-stage durations with HIP events between the stages, in a second timed pass.
+    ctx.stage_timing(True)
+    for i in range(steps):
+        step(i)
+    stages = ctx.stage_times()
+    ctx.stage_timing(False)
+
+    idx_all = didx.download()
+    distinct = [len(np.unique(idx_all[l])) for l in range(min(rotate, steps))]
+    U = float(np.mean(distinct))
+    ctx.close()
+    return dict(T=T, wall_s=wall, gpu_ms=gpu_ms, steps=steps, stages=stages, distinct=U, layers=layers, x=x,
+                bias=bias)
+
+
+def cpu_baseline(layer, x, bias, budget_s: float, max_tokens: int):
+    """LiteMind's CPU MoE path (its own Gemm/MoeRouter/ThreadPool, compiled from its
+    sources into oracle/_ref) on the first tokens of the workload, one token at a
+    time as its runner does, with hardware_concurrency() threads."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+
+    if not ol.have_ref():
+        return None
+    threads = int(ol.ref().ref_hardware_threads())
+    ol.ref_moe_layer(layer, x[:1], bias, workers=0)  # warm-up (pool start, page-in)
+    done, t0 = 0, time.perf_counter()
+    while done < max_tokens and time.perf_counter() - t0 < budget_s:
+        n = min(4, max_tokens - done)
+        rows = [(done + j) % x.shape[0] for j in range(n)]
+        ol.ref_moe_layer(layer, np.ascontiguousarray(x[rows]), bias, workers=0)
+        done += n
+    dt = time.perf_counter() - t0
+    return dict(value=done / dt, unit="tokens/s", cores=threads, kind="reference",
+                sample=f"first {done} tokens of the workload, sequential per-token MoE block "
+                       f"(LiteMind gemm/MoeRouter/ThreadPool, {threads} threads), {dt:.1f} s")
+
+
+def roofline(res: dict, mfma: bool) -> dict:
+    """Dominant kernel's achieved rate: algorithmic bytes (or flops) / event-timed duration."""
+    alg = algorithmic(res["T"], int(round(res["distinct"])))
+    stages = res["stages"]
+    per = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
+    dominant = max(("gate_up", "down"), key=lambda k: per[k])
+    dur_s = per[dominant] / 1e3
+    if mfma:
+        fl = alg[f"{dominant}_flops"]
+        achieved = fl / dur_s / 1e12
+        return {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_us": round(per[dominant] * 1e3, 2), "algorithmic_flops": fl}
+    by = alg[f"{dominant}_bytes"]
+    achieved = by / dur_s / 1e9
+    return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(per[dominant] * 1e3, 2),
+            "algorithmic_bytes": by}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="decode_t1")
+    ap.add_argument("--second", default="prefill_t2048_skewed", help="second workload ('' to skip)")
+    ap.add_argument("--rotate", type=int, default=8, help="layers rotated through at T=1")
+    ap.add_argument("--path", type=int, default=0, help="0 auto, 1 GEMV, 2 MFMA")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    from litemind_amd import workload as wl
+
+    main_w = wl.WORKLOADS[args.workload]
+    rotate = args.rotate if main_w.tokens <= 64 else 1
+    res = run_gpu(args.workload, args.steps, args.warmup, rotate, args.path)
+    T = res["T"]
+    ms = res["wall_s"] * 1e3 / res["steps"]
+    mfma_main = T > 64 if args.path == 0 else args.path == 2
+    line = {
+        "metric": METRIC, "value": round(T / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-normalised tokens)",
+        "config": {"workload": args.workload, "tokens": T, "hidden": 2048, "experts": 64, "top_k": 6,
+                   "moe_intermediate": 1408, "shared_intermediate": 2816, "layers_rotated": rotate,
+                   "expert_path": "mfma-fp16" if mfma_main else "gemv-fp32",
+                   "distinct_experts_per_step": res["distinct"]},
+        "roofline": roofline(res, mfma_main),
+        "layer_gpu_us": round(res["gpu_ms"] * 1e3 / res["steps"], 2),
+        "stage_us": {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res["stages"].items()},
+    }
+    alg = algorithmic(T, int(round(res["distinct"])))
+    line["layer_hbm_frac"] = round(alg["layer_bytes"] / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+
+    if not args.no_cpu:
+        log("cpu baseline (LiteMind's own kernels)")
+        cb = cpu_baseline(res["layers"][0], res["x"], res["bias"], args.cpu_seconds, max_tokens=T if T > 1 else 10**6)
+        if cb is None:
+            cb = {"value": None, "unit": "tokens/s", "cores": os.cpu_count(), "kind": "reference",
+                  "sample": "oracle/_ref/libref.so not built"}
+        line["cpu_baseline"] = cb
+
+    if args.second:
+        w2 = wl.WORKLOADS[args.second]
+        res2 = run_gpu(args.second, max(10, args.steps // 10), max(3, args.warmup // 4), 1, args.path)
+        ms2 = res2["wall_s"] * 1e3 / res2["steps"]
+        mfma2 = w2.tokens > 64 if args.path == 0 else args.path == 2
+        line["t2048" if w2.tokens == 2048 else args.second] = {
+            "workload": args.second, "tokens": w2.tokens, "value": round(w2.tokens / (ms2 / 1e3), 1),
+            "unit": "tokens/s", "ms_per_step": round(ms2, 4), "steps": res2["steps"],
+            "expert_path": "mfma-fp16" if mfma2 else "gemv-fp32",
+            "roofline": roofline(res2, mfma2),
+            "stage_us": {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res2["stages"].items()},
+        }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

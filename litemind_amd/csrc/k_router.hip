@@ -16,15 +16,6 @@ namespace {
 
 constexpr int kWaves = 4;
 
-__device__ inline float wave_max_f32(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float other = __shfl_xor(v, o);
-        v = other > v ? other : v;
-    }
-    return v;
-}
-
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -34,15 +25,34 @@ __device__ inline uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+__device__ inline float lane_value(float v, int e) {
+    return bits_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(float_bits(v)), e)));
+}
+
 // MoeRouter::select for one token whose logit for expert `lane` is `logit`.
+// Values are broadcast with v_readlane so the sequential reductions LiteMind
+// performs (max, left-to-right sum) run on uniform registers without LDS
+// round trips; the top-k order is found by counting, in every lane, how many
+// keys beat its own.
 __device__ void route_token(float logit, bool valid, int lane, int64_t t, const RouterArgs& a) {
     const int E = a.experts;
-    // softmax (src/Gemm.cpp:209-223): max, exp(v - max), left-to-right sum, reciprocal.
-    const float maximum = wave_max_f32(valid ? logit : -__builtin_inff());
+    // softmax (src/Gemm.cpp:209-223): max (std::max_element keeps the first of
+    // equal values; only the value matters), exp(v - max), left-to-right sum.
+    float maximum = lane_value(logit, 0);
+#pragma unroll
+    for (int e = 1; e < kMaxExperts; ++e) {
+        if (e < E) {
+            const float v = lane_value(logit, e);
+            maximum = maximum < v ? v : maximum;
+        }
+    }
     const float s = valid ? expf_ref(logit - maximum) : 0.0f;
     float total = 0.0f;
-    for (int e = 0; e < E; ++e) {
-        total = total + __shfl(s, e);
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) {
+        if (e < E) {
+            total = total + lane_value(s, e);
+        }
     }
     const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
     const float score = s * inverse;
@@ -65,47 +75,41 @@ __device__ void route_token(float logit, bool valid, int lane, int64_t t, const 
         uint64_t gkey = lane < a.n_group
                             ? ((static_cast<uint64_t>(float_bits(gmax)) << 8) | static_cast<uint64_t>(255 - lane))
                             : 0;
-        uint64_t chosen_groups_lo = 0, chosen_groups_hi = 0;  // bitset over 128 groups
+        uint64_t chosen_groups = 0;  // n_group <= 64
         for (int r = 0; r < take; ++r) {
             const uint64_t best = wave_max_u64(gkey);
             const int gsel = 255 - static_cast<int>(best & 255u);
             if (lane == gsel) {
                 gkey = 0;
             }
-            if (gsel < 64) {
-                chosen_groups_lo |= 1ull << gsel;
-            } else {
-                chosen_groups_hi |= 1ull << (gsel - 64);
-            }
+            chosen_groups |= 1ull << gsel;
         }
-        allowed = my_group < 64 ? ((chosen_groups_lo >> my_group) & 1u) != 0
-                                : ((chosen_groups_hi >> (my_group - 64)) & 1u) != 0;
+        allowed = ((chosen_groups >> my_group) & 1u) != 0;
     }
 
     // top_k_indices (src/MoeRouter.cpp:14-34): allowed first, then score
     // descending, then index ascending.  Scores are non-negative, so their bit
-    // patterns order like the values.
-    uint64_t key = valid ? ((static_cast<uint64_t>(allowed ? 1u : 0u) << 40) |
-                            (static_cast<uint64_t>(float_bits(score)) << 8) | static_cast<uint64_t>(255 - lane))
-                         : 0;
+    // patterns order like the values; keys are unique through the index.
+    const uint32_t key_hi = valid ? ((allowed ? 0x80000000u : 0u) | (float_bits(score) >> 1)) : 0u;
+    const uint32_t key_lo = valid ? ((float_bits(score) << 31) | static_cast<uint32_t>(255 - lane)) : 0u;
+    int rank = 0;
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) {
+        if (e < E) {
+            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_hi), e));
+            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_lo), e));
+            rank += (hi > key_hi || (hi == key_hi && lo > key_lo)) ? 1 : 0;
+        }
+    }
     const int K = a.top_k < E ? a.top_k : E;
-    // Lane r keeps the r-th selection; the running sum is wave-uniform.
-    int my_idx = 0;
-    float my_w = 0.0f;
+    // Weights in rank order; the selected sum runs left to right as in :91-94.
     float selected_sum = 0.0f;
     for (int r = 0; r < K; ++r) {
-        const uint64_t best = wave_max_u64(key);
-        const int e = 255 - static_cast<int>(best & 255u);
-        if (lane == e) {
-            key = 0;
-        }
-        const float w = __shfl(score, e);
-        if (lane == r) {
-            my_idx = e;
-            my_w = w;
-        }
-        selected_sum = selected_sum + w;
+        const uint64_t who = __ballot(valid && rank == r);
+        const int src = static_cast<int>(__builtin_ctzll(who));
+        selected_sum = selected_sum + lane_value(score, src);
     }
+    float my_w = score;
     // Normalise XOR scale (src/MoeRouter.cpp:96-106).
     if (a.top_k > 1 && a.normalize) {
         const float denominator = selected_sum + 1e-20f;
@@ -113,9 +117,9 @@ __device__ void route_token(float logit, bool valid, int lane, int64_t t, const 
     } else if (a.scale != 1.0f) {
         my_w = my_w * a.scale;
     }
-    if (lane < K) {
-        a.idx[t * a.top_k + lane] = my_idx;
-        a.wts[t * a.top_k + lane] = my_w;
+    if (valid && rank < K) {
+        a.idx[t * a.top_k + rank] = lane;
+        a.wts[t * a.top_k + rank] = my_w;
     }
 }
 
@@ -123,14 +127,20 @@ __device__ void route_token(float logit, bool valid, int lane, int64_t t, const 
 // component j of entry (q, e) holding gate row i0 + 4q + j of expert e.
 constexpr int kChunk = 64;
 
+// One workgroup routes kWaves * TPW tokens.  All threads stage the next chunk
+// of the transposed gate and of the tokens' activations into LDS while the
+// waves run the current chunk; each wave reads a whole chunk into registers
+// before its dependent add chain starts, so the chain runs at VALU issue rate.
 template <int TPW>
 __global__ __launch_bounds__(kWaves * 64) void router_kernel(RouterArgs a, const float* __restrict__ x,
                                                              const float* __restrict__ wt) {
-    __shared__ float4 stage[2][kChunk / 4][64];
+    __shared__ float4 wstage[2][kChunk / 4][64];
+    __shared__ float4 xstage[2][kWaves * TPW][kChunk / 4];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * TPW;
-    const bool active = t0 < a.tokens;  // wave-uniform; idle waves still help stage the gate
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * kWaves * TPW;  // first token of the block
+    const int64_t t0 = tb0 + static_cast<int64_t>(wave) * TPW;
+    const bool active = t0 < a.tokens;  // wave-uniform; idle waves still help stage
     const int E = a.experts;
     const int H = a.hidden;
     const bool valid = lane < E;
@@ -141,62 +151,99 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(RouterArgs a, const
         acc[k] = 0.0f;
     }
     if (a.do_matvec) {
-        const float* xr[TPW];
-#pragma unroll
-        for (int k = 0; k < TPW; ++k) {
-            const int64_t t = t0 + k < a.tokens ? t0 + k : a.tokens - 1;
-            xr[k] = x + t * H;
-        }
-        // Each thread stages 16 values per chunk: row r = idx / 64, expert e = idx % 64.
-        constexpr int kPer = kChunk * 64 / (kWaves * 64);
-        float pre[kPer];
+        // Per chunk each thread stages 16 gate values (row r = idx / 64, expert
+        // e = idx % 64) and TPW activation values (token idx / 64, row idx % 64).
+        constexpr int kPerW = kChunk * 64 / (kWaves * 64);
+        float wpre[kPerW];
+        float xpre[TPW];
         auto fetch = [&](int i0) {
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
+            for (int j = 0; j < kPerW; ++j) {
                 const int idx = threadIdx.x + j * kWaves * 64;
                 const int r = idx >> 6, e = idx & 63;
-                pre[j] = (i0 + r < H && e < E) ? wt[static_cast<int64_t>(i0 + r) * E + e] : 0.0f;
+                wpre[j] = (i0 + r < H && e < E) ? wt[static_cast<int64_t>(i0 + r) * E + e] : 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+                const int idx = threadIdx.x + k * kWaves * 64;
+                const int tk = idx >> 6, r = idx & 63;
+                const int64_t t = tb0 + tk;
+                xpre[k] = (t < a.tokens && i0 + r < H) ? x[t * H + i0 + r] : 0.0f;
             }
         };
         auto store = [&](int buf) {
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) {
+            for (int j = 0; j < kPerW; ++j) {
                 const int idx = threadIdx.x + j * kWaves * 64;
                 const int r = idx >> 6, e = idx & 63;
-                reinterpret_cast<float*>(&stage[buf][r >> 2][e])[r & 3] = pre[j];
+                reinterpret_cast<float*>(&wstage[buf][r >> 2][e])[r & 3] = wpre[j];
+            }
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+                const int idx = threadIdx.x + k * kWaves * 64;
+                const int tk = idx >> 6, r = idx & 63;
+                reinterpret_cast<float*>(&xstage[buf][tk][r >> 2])[r & 3] = xpre[k];
             }
         };
         const int nchunks = (H + kChunk - 1) / kChunk;
         fetch(0);
         store(0);
-        __syncthreads();
+        lds_barrier();
         for (int c = 0; c < nchunks; ++c) {
             const int i0 = c * kChunk;
+            const int b = c & 1;
             if (c + 1 < nchunks) {
                 fetch(i0 + kChunk);
             }
             if (active) {
-                const int rows = H - i0 < kChunk ? H - i0 : kChunk;  // H % 4 == 0
-                for (int q = 0; q < rows / 4; ++q) {
-                    const float4 w = stage[c & 1][q][lane];
-                    const int i = i0 + 4 * q;
+                if (H - i0 >= kChunk) {
+                    float4 w[kChunk / 4];
+#pragma unroll
+                    for (int q = 0; q < kChunk / 4; ++q) {
+                        w[q] = wstage[b][q][lane];
+                    }
 #pragma unroll
                     for (int k = 0; k < TPW; ++k) {
-                        float p = w.x * xr[k][i];
-                        acc[k] = acc[k] + p;
-                        p = w.y * xr[k][i + 1];
-                        acc[k] = acc[k] + p;
-                        p = w.z * xr[k][i + 2];
-                        acc[k] = acc[k] + p;
-                        p = w.w * xr[k][i + 3];
-                        acc[k] = acc[k] + p;
+                        float4 xv[kChunk / 4];
+#pragma unroll
+                        for (int q = 0; q < kChunk / 4; ++q) {
+                            xv[q] = xstage[b][wave * TPW + k][q];
+                        }
+#pragma unroll
+                        for (int q = 0; q < kChunk / 4; ++q) {
+                            float p = w[q].x * xv[q].x;
+                            acc[k] = acc[k] + p;
+                            p = w[q].y * xv[q].y;
+                            acc[k] = acc[k] + p;
+                            p = w[q].z * xv[q].z;
+                            acc[k] = acc[k] + p;
+                            p = w[q].w * xv[q].w;
+                            acc[k] = acc[k] + p;
+                        }
+                    }
+                } else {
+                    const int quads = (H - i0) / 4;  // H % 4 == 0
+                    for (int q = 0; q < quads; ++q) {
+                        const float4 w = wstage[b][q][lane];
+#pragma unroll
+                        for (int k = 0; k < TPW; ++k) {
+                            const float4 xv = xstage[b][wave * TPW + k][q];
+                            float p = w.x * xv.x;
+                            acc[k] = acc[k] + p;
+                            p = w.y * xv.y;
+                            acc[k] = acc[k] + p;
+                            p = w.z * xv.z;
+                            acc[k] = acc[k] + p;
+                            p = w.w * xv.w;
+                            acc[k] = acc[k] + p;
+                        }
                     }
                 }
             }
             if (c + 1 < nchunks) {
                 store((c + 1) & 1);
             }
-            __syncthreads();
+            lds_barrier();
         }
     } else if (active) {
         // Select-only mode: x holds logits [T, E].
@@ -236,11 +283,272 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(RouterArgs a, const
     }
 }
 
+// Decode router (T <= 4): one workgroup of 16 waves.  The tokens' activations
+// are staged in LDS once; all 1024 threads stream the transposed gate with a
+// kDepth-chunk register prefetch (one float4 per thread per chunk) into a
+// double-buffered LDS ring, and wave t runs token t's sequential chains.
+constexpr int kDecodeThreads = 1024;
+constexpr int kDecodeMaxTokens = 4;
+constexpr int kDepth = 4;
+
+__global__ __launch_bounds__(kDecodeThreads) void router_decode_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                        const float* __restrict__ wt) {
+    __shared__ float4 wstage[2][kChunk / 4][64];                    // 32 KB
+    extern __shared__ float4 xs[];                                   // [T][H / 4]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int E = a.experts;
+    const int H = a.hidden;
+    const int T = static_cast<int>(a.tokens);
+    const bool valid = lane < E;
+    const bool chain = wave < T;
+
+    for (int i = tid; i < T * (H / 4); i += kDecodeThreads) {
+        const int t = i / (H / 4), q = i - t * (H / 4);
+        xs[i] = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(t) * H + 4 * q);
+    }
+    // Thread tid owns float4 slot tid of a chunk: gate row r = tid / 16 of the
+    // chunk, experts 4 * (tid % 16) .. +3 (all of them below E or zero).
+    const int r = tid >> 4;
+    const int e4 = (tid & 15) * 4;
+    // Straight-line fetch with a clamped address and no masking: rows past H
+    // are never read by the chains (a partial chunk reads only its valid
+    // quads) and lanes past E are discarded.  Branches or selects here would
+    // make the compiler wait for every outstanding prefetch.
+    const int e_load = e4 < E ? e4 : 0;  // E % 4 == 0 for this kernel
+    auto fetch = [&](int c) -> float4 {
+        const int i = c * kChunk + r;
+        const int i_load = i < H ? i : H - 1;
+        return *reinterpret_cast<const float4*>(wt + static_cast<int64_t>(i_load) * E + e_load);
+    };
+    auto store = [&](int buf, float4 v) {
+        float* base = reinterpret_cast<float*>(&wstage[buf][r >> 2][0]);
+        base[(e4 + 0) * 4 + (r & 3)] = v.x;
+        base[(e4 + 1) * 4 + (r & 3)] = v.y;
+        base[(e4 + 2) * 4 + (r & 3)] = v.z;
+        base[(e4 + 3) * 4 + (r & 3)] = v.w;
+    };
+    // H % (kChunk * kDepth) == 0 for this kernel: the pipeline below has no
+    // conditionals, so the compiler can wait for exactly the oldest prefetch.
+    // Fetches past the last chunk are clamped to row H - 1 and never used.
+    const int nchunks = H / kChunk;
+    float4 pre[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        pre[d] = fetch(d);
+    }
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const int c = c0 + d;
+            store(c & 1, pre[d]);
+            pre[d] = fetch(c + kDepth);
+            lds_barrier();
+            if (chain) {
+                const int i0 = c * kChunk;
+                constexpr int kHalf = kChunk / 8;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float4 w[kHalf], xv[kHalf];
+#pragma unroll
+                    for (int q = 0; q < kHalf; ++q) {
+                        w[q] = wstage[c & 1][h * kHalf + q][lane];
+                        xv[q] = xs[wave * (H / 4) + i0 / 4 + h * kHalf + q];
+                    }
+#pragma unroll
+                    for (int q = 0; q < kHalf; ++q) {
+                        float p = w[q].x * xv[q].x;
+                        acc = acc + p;
+                        p = w[q].y * xv[q].y;
+                        acc = acc + p;
+                        p = w[q].z * xv[q].z;
+                        acc = acc + p;
+                        p = w[q].w * xv[q].w;
+                        acc = acc + p;
+                    }
+                }
+            }
+        }
+    }
+    if (!chain) {
+        return;
+    }
+    const int64_t t = wave;
+    float logit = acc;
+    if (a.bias != nullptr && valid) {
+        logit = logit + a.bias[lane];
+    }
+    if (a.logits != nullptr && valid) {
+        a.logits[t * E + lane] = logit;
+    }
+    route_token(logit, valid, lane, t, a);
+    if (a.x16 != nullptr) {
+        _Float16* dst = a.x16 + t * a.hidden_p;
+        for (int c = lane; c < a.hidden_p; c += 64) {
+            dst[c] = c < H ? static_cast<_Float16>(x[t * H + c]) : static_cast<_Float16>(0.0f);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Single-token router (T = 1): the experts are split over kSplit workgroups so
+// each one loads its whole slice of the transposed gate (H x 8 fp32, 64 KB at
+// H = 2048) at once, forms every product fl(w * x) in parallel into LDS, and
+// leaves only the ordered additions to the chain lanes (one lane per expert,
+// 4 rows per ds_read_b128).  A second single-workgroup launch performs the
+// selection and the (trivial) permutation.
+// ---------------------------------------------------------------------------
+constexpr int kSplitExperts = 8;
+constexpr int kSplitThreads = 256;
+
+__device__ void permute_one_token(const RouterArgs& a) {
+    // Canonical permutation for T = 1: the k selections, bucketed by expert.
+    const int E = a.experts, K = a.top_k;
+    const int tid = threadIdx.x;
+    if (tid < E) {
+        int count = 0;
+        for (int r = 0; r < K; ++r) {
+            count += a.idx[r] == tid ? 1 : 0;
+        }
+        a.rb.counts[tid] = count;
+        int offset = 0;
+        for (int r = 0; r < K; ++r) {
+            offset += a.idx[r] < tid ? 1 : 0;
+        }
+        a.rb.offsets[tid] = offset;
+        if (tid == 0) {
+            a.rb.offsets[E] = K;
+            a.rb.active[E] = K;
+        }
+    }
+    if (tid < K) {
+        const int e = a.idx[tid];
+        int pos = 0;
+        for (int r = 0; r < K; ++r) {
+            pos += a.idx[r] < e ? 1 : 0;  // experts are distinct within a token
+        }
+        a.rb.perm[pos] = tid;
+        a.rb.slot_of[tid] = pos;
+        a.rb.active[pos] = e;
+    }
+}
+
+__global__ __launch_bounds__(kSplitThreads) void router_single_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                       const float* __restrict__ wt) {
+    extern __shared__ float4 prod[];  // [H / 4][kSplitExperts] float4: 4 consecutive rows of one expert
+    const int tid = threadIdx.x;
+    const int H = a.hidden;
+    const int E = a.experts;
+    const int e0 = blockIdx.x * kSplitExperts;
+    // float4 f covers row f / 2, experts e0 + 4 (f % 2) .. +3 of the slice.
+    const int nf = H * (kSplitExperts / 4);
+    for (int f0 = 0; f0 < nf; f0 += kSplitThreads * 8) {
+        float4 w[8];
+        float xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int f = f0 + j * kSplitThreads + tid;
+            const int fl = f < nf ? f : nf - 1;
+            const int i = fl >> 1;
+            w[j] = *reinterpret_cast<const float4*>(wt + static_cast<int64_t>(i) * E + e0 + 4 * (fl & 1));
+            xv[j] = x[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int f = f0 + j * kSplitThreads + tid;
+            if (f < nf) {
+                const int i = f >> 1;
+                const int el = 4 * (f & 1);
+                float* base = reinterpret_cast<float*>(&prod[(i >> 2) * kSplitExperts]);
+                base[(el + 0) * 4 + (i & 3)] = w[j].x * xv[j];
+                base[(el + 1) * 4 + (i & 3)] = w[j].y * xv[j];
+                base[(el + 2) * 4 + (i & 3)] = w[j].z * xv[j];
+                base[(el + 3) * 4 + (i & 3)] = w[j].w * xv[j];
+            }
+        }
+    }
+    lds_barrier();
+    if (tid < kSplitExperts) {
+        // LiteMind's dot: the rounded products added strictly left to right.
+        float acc = 0.0f;
+        const int quads = H / 4;
+        int q = 0;
+        for (; q + 8 <= quads; q += 8) {
+            float4 p[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                p[u] = prod[(q + u) * kSplitExperts + tid];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc = acc + p[u].x;
+                acc = acc + p[u].y;
+                acc = acc + p[u].z;
+                acc = acc + p[u].w;
+            }
+        }
+        for (; q < quads; ++q) {
+            const float4 p = prod[q * kSplitExperts + tid];
+            acc = acc + p.x;
+            acc = acc + p.y;
+            acc = acc + p.z;
+            acc = acc + p.w;
+        }
+        const int e = e0 + tid;
+        if (a.bias != nullptr) {
+            acc = acc + a.bias[e];
+        }
+        a.logits_scratch[e] = acc;
+        if (a.logits != nullptr) {
+            a.logits[e] = acc;
+        }
+    }
+}
+
+// Selection and permutation for one token from the logits of router_single_kernel
+// (a separate launch: the kernel boundary orders the hand-off across XCDs).
+__global__ __launch_bounds__(64) void select_single_kernel(RouterArgs a) {
+    const int lane = threadIdx.x;
+    const bool valid = lane < a.experts;
+    const float logit = valid ? a.logits_scratch[lane] : 0.0f;
+    route_token(logit, valid, lane, 0, a);
+    if (a.rb.counts != nullptr) {
+        __syncthreads();
+        permute_one_token(a);
+    }
+    if (a.x16 != nullptr) {
+        for (int c = lane; c < a.hidden_p; c += 64) {
+            a.x16[c] = c < a.hidden ? static_cast<_Float16>(a.x[c]) : static_cast<_Float16>(0.0f);
+        }
+    }
+}
+
 }  // namespace
 
-hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
+hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
+    if (permuted != nullptr) {
+        *permuted = false;
+    }
     if (a.tokens <= 0) {
         return hipSuccess;
+    }
+    const size_t split_lds = sizeof(float) * static_cast<size_t>(a.hidden) * kSplitExperts;
+    if (a.do_matvec && a.tokens == 1 && a.experts % kSplitExperts == 0 && a.logits_scratch != nullptr &&
+        split_lds <= 65536) {
+        hipLaunchKernelGGL(router_single_kernel, dim3(a.experts / kSplitExperts), dim3(kSplitThreads), split_lds, s,
+                           a, a.x, a.wt);
+        hipLaunchKernelGGL(select_single_kernel, dim3(1), dim3(64), 0, s, a);
+        if (permuted != nullptr) {
+            *permuted = a.rb.counts != nullptr;
+        }
+        return hipGetLastError();
+    }
+    if (a.do_matvec && a.tokens <= kDecodeMaxTokens && a.experts % 4 == 0 && a.hidden % (kChunk * kDepth) == 0) {
+        const size_t lds = sizeof(float) * static_cast<size_t>(a.tokens) * a.hidden;
+        hipLaunchKernelGGL(router_decode_kernel, dim3(1), dim3(kDecodeThreads), lds, s, a, a.x, a.wt);
+        return hipGetLastError();
     }
     int tpw = 1;
     if (a.do_matvec) {

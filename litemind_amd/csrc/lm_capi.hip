@@ -86,6 +86,8 @@ struct Workspace {
     float* xnorm = nullptr;       // stack: normalised input
     float* ffn = nullptr;         // stack / dense: FFN output
     int32_t* zero = nullptr;      // a device int holding 0 (dense layers have no routed experts)
+    float* logit_scratch = nullptr;  // [E] single-token router hand-off
+    uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
 };
 
 struct EventSet {
@@ -252,7 +254,8 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
                      reinterpret_cast<void**>(&w.slot_of), reinterpret_cast<void**>(&w.act),
                      reinterpret_cast<void**>(&w.x16),     reinterpret_cast<void**>(&w.down_out),
                      reinterpret_cast<void**>(&w.xnorm),   reinterpret_cast<void**>(&w.ffn),
-                     reinterpret_cast<void**>(&w.zero)};
+                     reinterpret_cast<void**>(&w.zero),    reinterpret_cast<void**>(&w.logit_scratch),
+                     reinterpret_cast<void**>(&w.ticket)};
     for (void** p : ptrs) {
         if (*p != nullptr) {
             LM_HIP(hipFree(*p));
@@ -278,6 +281,9 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ffn), sizeof(float) * static_cast<size_t>(T * ctx->H)));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.zero), sizeof(int32_t) * 4));
     LM_HIP(hipMemsetAsync(w.zero, 0, sizeof(int32_t) * 4, ctx->stream));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.logit_scratch), sizeof(float) * static_cast<size_t>(E)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ticket), sizeof(uint32_t) * 4));
+    LM_HIP(hipMemsetAsync(w.ticket, 0, sizeof(uint32_t) * 4, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     w.tokens = T;
     return LM_OK;
@@ -373,11 +379,9 @@ int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, 
         stage_mark(ctx, 3);
         LM_HIP(lm::launch_mfma_down(ea, 0, ctx->stream));
     } else {
-        const int64_t gu_items = max_active * (ea.inter_p / 16) + (ea.has_shared ? ea.shared_inter_p / 16 : 0);
-        LM_HIP(lm::launch_gemv_gateup(ea, gu_items, ctx->stream));
+        LM_HIP(lm::launch_gemv_gateup(ea, max_active, ctx->stream));
         stage_mark(ctx, 3);
-        const int64_t down_items = (max_active + ea.has_shared) * (ctx->H / 16);
-        LM_HIP(lm::launch_gemv_down(ea, down_items, ctx->stream));
+        LM_HIP(lm::launch_gemv_down(ea, max_active, ctx->stream));
     }
     stage_mark(ctx, 4);
     lm::CombineArgs ca{};
@@ -435,8 +439,12 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     ra.topk_group = ctx->cfg.topk_group;
     ra.scale = ctx->cfg.routed_scaling_factor;
     ra.do_matvec = 1;
+    ra.logits_scratch = ctx->ws.logit_scratch;
+    ra.ticket = ctx->ws.ticket;
+    ra.rb = route_bufs(ctx, idx, wts);
     stage_mark(ctx, 0);
-    LM_HIP(lm::launch_router(ra, ctx->stream));
+    bool permuted = false;
+    LM_HIP(lm::launch_router(ra, ctx->stream, &permuted));
     stage_mark(ctx, 1);
 
     lm::PermuteArgs pa{};
@@ -444,8 +452,10 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     pa.tokens = T;
     pa.top_k = ctx->K;
     pa.experts = ctx->E;
-    pa.rb = route_bufs(ctx, idx, wts);
-    LM_HIP(lm::launch_permute(pa, ctx->stream));
+    pa.rb = ra.rb;
+    if (!permuted) {
+        LM_HIP(lm::launch_permute(pa, ctx->stream));
+    }
 
     rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma);
     if (rc != LM_OK) {
@@ -575,8 +585,8 @@ int lm_context_destroy(lm_context* ctx) {
         (void)hipFree(L.table);
     }
     Workspace& w = ctx->ws;
-    void* ptrs[] = {w.idx, w.wts, w.counts, w.offsets, w.active, w.perm, w.slot_of,
-                    w.act, w.x16, w.down_out, w.xnorm, w.ffn, w.zero};
+    void* ptrs[] = {w.idx, w.wts, w.counts, w.offsets, w.active, w.perm, w.slot_of, w.act, w.x16,
+                    w.down_out, w.xnorm, w.ffn, w.zero, w.logit_scratch, w.ticket};
     for (void* p : ptrs) {
         (void)hipFree(p);
     }
@@ -890,9 +900,15 @@ int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens
     if (tokens < 0 || (tokens > 0 && (x_dev == nullptr || topk_index_dev == nullptr || topk_weight_dev == nullptr))) {
         return fail(LM_EINVAL, "bad token count or null buffers");
     }
+    rc = ensure_workspace(ctx, tokens);
+    if (rc != LM_OK) {
+        return rc;
+    }
     lm::RouterArgs ra{};
     ra.x = x_dev;
     ra.wt = L.router_t;
+    ra.logits_scratch = ctx->ws.logit_scratch;
+    ra.ticket = ctx->ws.ticket;
     ra.bias = logit_bias_dev;
     ra.logits = logits_dev;
     ra.idx = topk_index_dev;
@@ -908,7 +924,7 @@ int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens
     ra.topk_group = ctx->cfg.topk_group;
     ra.scale = ctx->cfg.routed_scaling_factor;
     ra.do_matvec = 1;
-    LM_HIP(lm::launch_router(ra, ctx->stream));
+    LM_HIP(lm::launch_router(ra, ctx->stream, nullptr));
     return LM_OK;
     LM_GUARD_END
 }
@@ -937,7 +953,7 @@ int lm_router_select(lm_context* ctx, const float* logits_dev, int64_t tokens, i
     ra.topk_group = ctx->cfg.topk_group;
     ra.scale = ctx->cfg.routed_scaling_factor;
     ra.do_matvec = 0;
-    LM_HIP(lm::launch_router(ra, ctx->stream));
+    LM_HIP(lm::launch_router(ra, ctx->stream, nullptr));
     return LM_OK;
     LM_GUARD_END
 }

@@ -21,6 +21,26 @@ constexpr int kMaxTopK = 16;
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations
+// (lgkmcnt(0); vmcnt and expcnt left at their maxima) and then s_barrier.
+// __syncthreads() also fences global memory, which makes every wave wait for
+// its outstanding global loads and defeats register prefetching across it.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+}
+
+// 16-byte load of streamed weights: global address space (pointers read from a
+// table would otherwise compile to flat loads) and non-temporal, since every
+// weight byte is used once per step.
+__device__ inline uint4 load_stream16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load((global_u32x4*)(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // One FFN (routed expert, the fused shared expert or a dense layer) resident in HBM.
 //   gu:   [2 * inter_p, hidden_p] BF16, gate/up interleaved as above
 //   down: [hidden, inter_p] BF16 (columns >= inter are zero)
@@ -67,6 +87,10 @@ struct RouterArgs {
     int32_t normalize, group_limited, n_group, topk_group;
     float scale;
     int32_t do_matvec;       // 0: x holds logits [T, E] already (select only)
+    // Single-token path: fused selection and permutation by the last workgroup.
+    float* logits_scratch;   // [E] logits handed to the last workgroup
+    uint32_t* ticket;        // arrival counter, 0 between launches (the last workgroup resets it)
+    RouteBufs rb;            // permutation outputs (counts, offsets, perm, slot_of, active)
 };
 
 struct PermuteArgs {
@@ -103,10 +127,10 @@ struct CombineArgs {
 };
 
 // Kernel launchers (implemented in the .hip files).
-hipError_t launch_router(const RouterArgs& a, hipStream_t s);
+hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted);
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
-hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_items, hipStream_t s);
-hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_items, hipStream_t s);
+hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
+hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
 hipError_t launch_mfma_gateup(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
 hipError_t launch_mfma_down(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
