@@ -312,8 +312,10 @@ __global__ __launch_bounds__(kThreads) void gemv_down_kernel(ExpertArgs a) {
 
 template <int NTB>
 hipError_t gateup_dispatch(const ExpertArgs& a, int64_t items, hipStream_t s) {
-    const size_t lds = NTB > 1 ? sizeof(float) * NTB * a.hidden : 0;
     const int iters = (a.hidden + 511) / 512;
+    // Activations are staged in LDS unless one token is held in registers.
+    const bool staged = NTB > 1 || iters > 4;
+    const size_t lds = staged ? sizeof(float) * NTB * a.hidden : 0;
     const dim3 grid(static_cast<unsigned>(items)), block(kThreads);
     switch (iters) {
         case 1: hipLaunchKernelGGL((gemv_gateup_kernel<1, NTB>), grid, block, lds, s, a); break;
@@ -328,8 +330,9 @@ hipError_t gateup_dispatch(const ExpertArgs& a, int64_t items, hipStream_t s) {
 template <int NTB>
 hipError_t down_dispatch(const ExpertArgs& a, int64_t items, hipStream_t s) {
     const int widest = a.shared_inter_p > a.inter_p ? a.shared_inter_p : a.inter_p;
-    const size_t lds = NTB > 1 ? sizeof(float) * NTB * widest : 0;
     const int iters = (widest + 511) / 512;
+    const bool staged = NTB > 1 || iters > 8;
+    const size_t lds = staged ? sizeof(float) * NTB * widest : 0;
     const dim3 grid(static_cast<unsigned>(items)), block(kThreads);
     switch (iters) {
         case 1: hipLaunchKernelGGL((gemv_down_kernel<1, NTB>), grid, block, lds, s, a); break;

@@ -132,7 +132,30 @@ __global__ __launch_bounds__(256) void gemv_plain_kernel(const uint16_t* __restr
     }
 }
 
+// x16[t, c] = fp16(x[t, c]) for c < cols, 0 for cols <= c < cols_p.
+__global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restrict__ x, _Float16* __restrict__ x16,
+                                                          int64_t rows, int32_t cols, int32_t cols_p) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * cols_p) {
+        return;
+    }
+    const int64_t r = i / cols_p;
+    const int c = static_cast<int>(i - r * cols_p);
+    x16[i] = c < cols ? static_cast<_Float16>(x[r * cols + c]) : static_cast<_Float16>(0.0f);
+}
+
 }  // namespace
+
+hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
+                              hipStream_t s) {
+    const int64_t n = rows * cols_p;
+    if (n <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, x16,
+                       rows, cols, cols_p);
+    return hipGetLastError();
+}
 
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {

@@ -476,9 +476,7 @@ int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float
         return rc;
     }
     if (mfma) {
-        // fp16 copy of x via the router kernel's conversion is not available without
-        // routing, so convert with a select-free pass: reuse rms-free conversion below.
-        return fail(LM_EINVAL, "dense MFMA path is not built yet");
+        LM_HIP(lm::launch_to_f16_rows(x, ctx->ws.x16, T, ctx->H, ctx->Hp, ctx->stream));
     }
     lm::RouteBufs rb{};
     rb.counts = ctx->ws.zero;
@@ -490,7 +488,7 @@ int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float
     rb.wt = ctx->ws.wts;
     stage_mark(ctx, 0);
     stage_mark(ctx, 1);
-    rc = run_experts(ctx, L, x, ctx->ws.x16, T, rb, y, residual, false);
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, rb, y, residual, mfma);
     if (rc != LM_OK) {
         return rc;
     }

@@ -135,6 +135,8 @@ hipError_t launch_mfma_gateup(const ExpertArgs& a, int64_t max_tiles, hipStream_
 hipError_t launch_mfma_down(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* src, _Float16* dst, int64_t n, int* overflow, hipStream_t s);
+hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
+                              hipStream_t s);
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
                            hipStream_t s);
 hipError_t launch_gemv_plain(const uint16_t* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,

@@ -56,3 +56,53 @@ def test_layer_gemv_tiny(tiny_ctx):
     assert np.array_equal(idx, oidx)
     max_abs, mean_rel = layer_error(y, oy)
     assert max_abs <= 1e-5 and mean_rel <= 1e-5
+
+
+@pytest.mark.parametrize("case", ["t48_forced", "t512_uniform", "t2048_skewed"])
+def test_layer_mfma_v2lite(v2_ctx, case):
+    """fp16-operand MFMA path: routing still bit-exact, outputs within tolerance."""
+    from litemind_amd import PATH_AUTO, PATH_MFMA
+    from litemind_amd import workload as wl
+
+    ctx, layers = v2_ctx
+    T = {"t48_forced": 48, "t512_uniform": 512, "t2048_skewed": 2048}[case]
+    layer_id = 1 if case == "t512_uniform" else 0
+    bias = wl.skew_bias() if case == "t2048_skewed" else None
+    path = PATH_MFMA if case == "t48_forced" else PATH_AUTO
+    x = wl.tokens(wl.MASTER_SEED + 200 + T, T, 2048)
+    announce(f"layer MFMA {case} T={T}")
+    y, idx, w = _gpu_layer(ctx, layer_id, x, path, bias=bias)
+    oy, oidx, ow, _ = ol.oracle_moe_layer(layers[layer_id], x, bias=bias)
+    assert np.array_equal(idx, oidx)
+    assert np.array_equal(w.view(np.uint32), ow.view(np.uint32))
+    max_abs, mean_rel = layer_error(y, oy)
+    print(f"{case} max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+
+
+def test_layer_mfma_tiny(tiny_ctx):
+    from litemind_amd import PATH_MFMA
+    from litemind_amd import workload as wl
+
+    ctx, layer = tiny_ctx
+    x = wl.tokens(23, 300, layer.dims.hidden)
+    announce("layer MFMA tiny model T=300")
+    y, idx, w = _gpu_layer(ctx, 0, x, PATH_MFMA)
+    oy, oidx, ow, _ = ol.oracle_moe_layer(layer, x)
+    assert np.array_equal(idx, oidx)
+    max_abs, mean_rel = layer_error(y, oy)
+    assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+
+
+def test_gemv_and_mfma_agree(v2_ctx):
+    from litemind_amd import PATH_GEMV, PATH_MFMA
+    from litemind_amd import workload as wl
+
+    ctx, _ = v2_ctx
+    x = wl.tokens(wl.MASTER_SEED + 300, 64, 2048)
+    announce("layer GEMV vs MFMA T=64")
+    yg, ig, wg = _gpu_layer(ctx, 0, x, PATH_GEMV)
+    ym, im, wm = _gpu_layer(ctx, 0, x, PATH_MFMA)
+    assert np.array_equal(ig, im)
+    max_abs, mean_rel = layer_error(ym, yg)
+    assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
