@@ -18,11 +18,13 @@
 #include "Threading.hpp"
 
 #include <algorithm>
+#include <bit>
 #include <cstdint>
 #include <cstring>
 #include <map>
 #include <memory>
 #include <mutex>
+#include <random>
 #include <stdexcept>
 #include <vector>
 
@@ -125,6 +127,21 @@ int ref_router_select_top_k(const float* logits, std::int32_t logit_count, std::
         return static_cast<int>(selection.size());
     } catch (const std::invalid_argument&) {
         return -1;
+    }
+}
+
+// The inputs of LiteMind's matvec test (tests/KernelTest.cpp:28-48): mt19937(12345),
+// uniform(-1, 1) floats, weights rounded to BF16 with round-to-nearest-even,
+// drawn in the same order (all weights, then the input vector).
+void ref_kerneltest_inputs(std::uint16_t* weights_bf16, float* input, std::size_t out_dim, std::size_t in_dim) {
+    std::mt19937 generator(12345U);
+    std::uniform_real_distribution<float> distribution(-1.0F, 1.0F);
+    for (std::size_t i = 0; i < out_dim * in_dim; ++i) {
+        const std::uint32_t bits = std::bit_cast<std::uint32_t>(distribution(generator));
+        weights_bf16[i] = static_cast<std::uint16_t>((bits + 0x7fffU + ((bits >> 16U) & 1U)) >> 16U);
+    }
+    for (std::size_t i = 0; i < in_dim; ++i) {
+        input[i] = distribution(generator);
     }
 }
 

@@ -97,6 +97,7 @@ def ref() -> C.CDLL:
         lib.ref_router_select.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P]
         lib.ref_router_select_top_k.argtypes = [_P, _I32, _I32, _I32, _I32, _P, _P]
         lib.ref_parallel_for_visit.argtypes = [_SZ, _SZ, _P]
+        lib.ref_kerneltest_inputs.argtypes = [_P, _P, _SZ, _SZ]
         lib.ref_cache_create.argtypes = [C.c_uint64]
         lib.ref_cache_create.restype = C.c_void_p
         lib.ref_cache_destroy.argtypes = [_P]
