@@ -149,6 +149,38 @@ int lm_dense_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t
 int lm_gemm_matvec_bf16(lm_context* ctx, const uint16_t* w_host, const float* x_host, float* out_host,
                         size_t out_dim, size_t in_dim, float scale, int32_t accumulate);
 
+/* out = W x for a row-major fp32 matrix with LiteMind's dot semantics (each
+ * product rounded, then added left to right): gemm::matvec_f32
+ * (src/Gemm.cpp:132-137, :183-189).  W is cached in HBM by host pointer.  Synchronous. */
+int lm_gemm_matvec_f32(lm_context* ctx, const float* w_host, const float* x_host, float* out_host, size_t out_dim,
+                       size_t in_dim);
+
+/* Vector helpers of namespace gemm (src/Gemm.cpp:177-231), computed on the GPU with
+ * LiteMind's rounding.  Synchronous; host buffers.
+ *   LM_OP_DOT       out[0] = dot(a, b)                         (gemm::dot)
+ *   LM_OP_AXPY      out += scalar * a                          (gemm::axpy)
+ *   LM_OP_SOFTMAX   out = softmax(a)                           (gemm::softmax)
+ *   LM_OP_SILU_MUL  out = silu(a) * b                          (gemm::silu_multiply)
+ *   LM_OP_RMS_NORM  out = rms_norm(a, weight b, eps scalar)    (gemm::rms_norm)
+ *   LM_OP_WIDEN     out = widen((const uint16_t*)a)            (gemm::widen_bf16) */
+#define LM_OP_DOT 0
+#define LM_OP_AXPY 1
+#define LM_OP_SOFTMAX 2
+#define LM_OP_SILU_MUL 3
+#define LM_OP_RMS_NORM 4
+#define LM_OP_WIDEN 5
+int lm_vector_op(lm_context* ctx, int32_t op, const void* a_host, const float* b_host, float* out_host, size_t n,
+                 float scalar);
+
+/* Per-pointer HBM residency: replaces WeightView::prefetch / release
+ * (src/WeightStore.cpp:40-50), which ExpertCache::touch / evict_oldest call
+ * (src/ExpertCache.cpp:33-35, :53-55).  prefetch copies `bytes` from host_ptr
+ * into HBM (no-op if resident); release frees the copy.  The per-call gemm
+ * entry points use a resident copy when one exists for their weight pointer. */
+int lm_weight_prefetch(lm_context* ctx, const void* host_ptr, size_t bytes);
+int lm_weight_release(lm_context* ctx, const void* host_ptr);
+int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resident);
+
 /* ---- timing: hipEvents on the context stream ---- */
 int lm_event_create(lm_context* ctx, void** out_event);
 int lm_event_destroy(lm_context* ctx, void* event);

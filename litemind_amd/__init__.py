@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "liblitemind_moe.so")
 
 LM_OK = 0
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+OP_DOT, OP_AXPY, OP_SOFTMAX, OP_SILU_MUL, OP_RMS_NORM, OP_WIDEN = range(6)
 STAGES = ("router", "permute", "gate_up", "down", "combine")
 
 
@@ -77,6 +78,11 @@ PROTOTYPES = {
     "lm_rms_norm": [_P, _P, _P, _P, _I64, _I32, _F],
     "lm_dense_forward": [_P, _I32, _P, _I64, _P, _I32],
     "lm_gemm_matvec_bf16": [_P, _P, _P, _P, _SZ, _SZ, _F, _I32],
+    "lm_gemm_matvec_f32": [_P, _P, _P, _P, _SZ, _SZ],
+    "lm_vector_op": [_P, _I32, _P, _P, _P, _SZ, _F],
+    "lm_weight_prefetch": [_P, _P, _SZ],
+    "lm_weight_release": [_P, _P],
+    "lm_weight_resident": [_P, _P, _P],
     "lm_event_create": [_P, _P],
     "lm_event_destroy": [_P, _P],
     "lm_event_record": [_P, _P],
@@ -250,6 +256,13 @@ class Context:
         out_dim, in_dim = w.shape
         self._check(self.lib.lm_gemm_matvec_bf16(self.handle, _ptr(w), _ptr(x), _ptr(out), out_dim, in_dim,
                                                  scale, 1 if accumulate else 0))
+
+    def gemm_matvec_f32(self, w: np.ndarray, x: np.ndarray, out: np.ndarray) -> None:
+        out_dim, in_dim = w.shape
+        self._check(self.lib.lm_gemm_matvec_f32(self.handle, _ptr(w), _ptr(x), _ptr(out), out_dim, in_dim))
+
+    def vector_op(self, op: int, a: np.ndarray, b, out: np.ndarray, scalar: float = 0.0) -> None:
+        self._check(self.lib.lm_vector_op(self.handle, op, _ptr(a), _ptr(b), _ptr(out), a.size, scalar))
 
     # ---- timing ----
     def event(self):

@@ -95,41 +95,56 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* in, const fl
 // out[r] = W[r] . x or out[r] += scale * (W[r] . x) for a plain row-major BF16
 // matrix (gemm::matvec_bf16 / matvec_bf16_accumulate, src/Gemm.cpp:139-175).
 // One wave per row.
+// out[row] = dot_bf16(w[row], x) in LiteMind's association order, bit for bit
+// (src/Gemm.cpp:46-82, AVX2 + FMA branch): 32 fused chains over elements
+// i = c (mod 32), chains 0..7 also take the 8-wide remainder, then
+// (a0+a1)+(a2+a3) per lane, lanes j and j+4 added, (h0+h2)+(h1+h3), and a fused
+// scalar tail.  32 lanes hold one row's chains, so a block takes 8 rows.
+// With `accumulate` the row is folded as fma(scale, dot, out[row])
+// (src/Gemm.cpp:156-175).
 __global__ __launch_bounds__(256) void gemv_plain_kernel(const uint16_t* __restrict__ w, const float* __restrict__ x,
                                                          float* out, int64_t out_dim, int64_t in_dim, float scale,
                                                          int accumulate) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= out_dim) {
+    __shared__ float part[8][33];
+    const int c = threadIdx.x & 31;
+    const int slot = threadIdx.x >> 5;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + slot;
+    const bool live = row < out_dim;
+    const int64_t n32 = in_dim / 32 * 32;
+    const int64_t n8 = n32 + (in_dim - n32) / 8 * 8;
+    const uint16_t* wr = w + (live ? row : 0) * in_dim;
+    float acc = 0.0f;
+    if (live) {
+        for (int64_t i = c; i < n32; i += 32) {
+            acc = __builtin_fmaf(widen_bf16(wr[i]), x[i], acc);
+        }
+        if (c < 8) {
+            for (int64_t i = n32 + c; i < n8; i += 8) {
+                acc = __builtin_fmaf(widen_bf16(wr[i]), x[i], acc);
+            }
+        }
+    }
+    part[slot][c] = acc;
+    __syncthreads();
+    if (!live || c != 0) {
         return;
     }
-    const uint16_t* wr = w + row * in_dim;
-    float acc = 0.0f;
-    if ((in_dim & 7) == 0) {
-        for (int64_t c = lane * 8; c < in_dim; c += 512) {
-            const uint4 q = *reinterpret_cast<const uint4*>(wr + c);
-            const float4 x0 = *reinterpret_cast<const float4*>(x + c);
-            const float4 x1 = *reinterpret_cast<const float4*>(x + c + 4);
-            acc = __builtin_fmaf(bits_float(q.x << 16), x0.x, acc);
-            acc = __builtin_fmaf(bits_float(q.x & 0xffff0000u), x0.y, acc);
-            acc = __builtin_fmaf(bits_float(q.y << 16), x0.z, acc);
-            acc = __builtin_fmaf(bits_float(q.y & 0xffff0000u), x0.w, acc);
-            acc = __builtin_fmaf(bits_float(q.z << 16), x1.x, acc);
-            acc = __builtin_fmaf(bits_float(q.z & 0xffff0000u), x1.y, acc);
-            acc = __builtin_fmaf(bits_float(q.w << 16), x1.z, acc);
-            acc = __builtin_fmaf(bits_float(q.w & 0xffff0000u), x1.w, acc);
-        }
-    } else {
-        for (int64_t c = lane; c < in_dim; c += 64) {
-            acc = __builtin_fmaf(widen_bf16(wr[c]), x[c], acc);
-        }
+    const float* a = part[slot];
+    float lane_sum[8];
+    for (int l = 0; l < 8; ++l) {
+        const float low = a[l] + a[8 + l];
+        const float high = a[16 + l] + a[24 + l];
+        lane_sum[l] = low + high;
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        acc += __shfl_xor(acc, o);
+    const float h0 = lane_sum[0] + lane_sum[4];
+    const float h1 = lane_sum[1] + lane_sum[5];
+    const float h2 = lane_sum[2] + lane_sum[6];
+    const float h3 = lane_sum[3] + lane_sum[7];
+    float total = (h0 + h2) + (h1 + h3);
+    for (int64_t i = n8; i < in_dim; ++i) {
+        total = __builtin_fmaf(widen_bf16(wr[i]), x[i], total);
     }
-    if (lane == 0) {
-        out[row] = accumulate ? __builtin_fmaf(scale, acc, out[row]) : acc;
-    }
+    out[row] = accumulate ? __builtin_fmaf(scale, total, out[row]) : total;
 }
 
 // x16[t, c] = fp16(x[t, c]) for c < cols, 0 for cols <= c < cols_p.
@@ -144,7 +159,115 @@ __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restric
     x16[i] = c < cols ? static_cast<_Float16>(x[r * cols + c]) : static_cast<_Float16>(0.0f);
 }
 
+// gemm::matvec_f32 with LiteMind's dot (src/Gemm.cpp:183-189) as its GCC build
+// runs it: products rounded and added left to right, the last n % 4 elements
+// fused (the scalar epilogue).  One lane per output row.
+__device__ inline float dot_ref(const float* a, const float* b, int64_t n, int64_t stride_a) {
+    const int64_t unfused = n - n % 4;
+    float t = 0.0f;
+    int64_t i = 0;
+    for (; i < unfused; ++i) {
+        const float p = a[i * stride_a] * b[i];
+        t = t + p;
+    }
+    for (; i < n; ++i) {
+        t = __builtin_fmaf(a[i * stride_a], b[i], t);
+    }
+    return t;
+}
+
+__global__ __launch_bounds__(64) void matvec_f32_ref_kernel(const float* w, const float* x, float* out,
+                                                            int64_t out_dim, int64_t in_dim) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (row < out_dim) {
+        out[row] = dot_ref(w + row * in_dim, x, in_dim, 1);
+    }
+}
+
+// The vector helpers of namespace gemm (src/Gemm.cpp:177-231) with LiteMind's
+// rounding: sequential reductions run on one lane, elementwise ops on all.
+__global__ __launch_bounds__(256) void vector_op_kernel(int op, const void* a_raw, const float* b, float* out,
+                                                        int64_t n, float scalar) {
+    const float* a = static_cast<const float*>(a_raw);
+    const int tid = threadIdx.x;
+    switch (op) {
+        case 0:  // dot
+            if (tid == 0) {
+                out[0] = dot_ref(a, b, n, 1);
+            }
+            break;
+        case 1:  // axpy: out += scalar * a, fused as GCC compiles it
+            for (int64_t i = tid; i < n; i += blockDim.x) {
+                out[i] = __builtin_fmaf(scalar, a[i], out[i]);
+            }
+            break;
+        case 2:  // softmax
+            if (tid == 0 && n > 0) {
+                float maximum = a[0];
+                for (int64_t i = 1; i < n; ++i) {
+                    maximum = maximum < a[i] ? a[i] : maximum;
+                }
+                float total = 0.0f;
+                for (int64_t i = 0; i < n; ++i) {
+                    out[i] = expf_ref(a[i] - maximum);
+                    total = total + out[i];
+                }
+                const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
+                for (int64_t i = 0; i < n; ++i) {
+                    out[i] = out[i] * inverse;
+                }
+            }
+            break;
+        case 3:  // silu_multiply
+            for (int64_t i = tid; i < n; i += blockDim.x) {
+                out[i] = silu_mul_ref(a[i], b[i]);
+            }
+            break;
+        case 4: {  // rms_norm, sum of squares in double left to right
+            __shared__ float inverse;
+            if (tid == 0) {
+                double sum = 0.0;
+                for (int64_t i = 0; i < n; ++i) {
+                    const double v = static_cast<double>(a[i]);
+                    sum = sum + v * v;
+                }
+                inverse = static_cast<float>(
+                    1.0 / __builtin_sqrt(sum / static_cast<double>(n) + static_cast<double>(scalar)));
+            }
+            __syncthreads();
+            for (int64_t i = tid; i < n; i += blockDim.x) {
+                const float scaled = a[i] * inverse;
+                out[i] = scaled * b[i];
+            }
+            break;
+        }
+        case 5:  // widen_bf16
+            for (int64_t i = tid; i < n; i += blockDim.x) {
+                out[i] = widen_bf16(static_cast<const uint16_t*>(a_raw)[i]);
+            }
+            break;
+        default:
+            break;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
+                                 hipStream_t s) {
+    if (out_dim <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(matvec_f32_ref_kernel, dim3(static_cast<unsigned>((out_dim + 63) / 64)), dim3(64), 0, s, w, x,
+                       out, out_dim, in_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_vector_op(int op, const void* a, const float* b, float* out, int64_t n, float scalar,
+                            hipStream_t s) {
+    hipLaunchKernelGGL(vector_op_kernel, dim3(1), dim3(256), 0, s, op, a, b, out, n, scalar);
+    return hipGetLastError();
+}
 
 hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
                               hipStream_t s) {
@@ -193,7 +316,7 @@ hipError_t launch_gemv_plain(const uint16_t* w, const float* x, float* out, int6
     if (out_dim <= 0) {
         return hipSuccess;
     }
-    hipLaunchKernelGGL(gemv_plain_kernel, dim3(static_cast<unsigned>((out_dim + 3) / 4)), dim3(256), 0, s, w, x, out,
+    hipLaunchKernelGGL(gemv_plain_kernel, dim3(static_cast<unsigned>((out_dim + 7) / 8)), dim3(256), 0, s, w, x, out,
                        out_dim, in_dim, scale, accumulate);
     return hipGetLastError();
 }

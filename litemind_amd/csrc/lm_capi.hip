@@ -107,15 +107,19 @@ struct lm_context {
     size_t staging_bytes = 0;
     int* d_overflow = nullptr;
     uint64_t resident = 0;
-    // per-call gemm compatibility cache, keyed by host pointer
+    // Per-pointer HBM residency (WeightView::prefetch / release and the per-call
+    // gemm entry points), keyed by host pointer.
     struct Cached {
-        uint16_t* dev;
-        size_t elems;
+        void* dev;
+        size_t bytes;
     };
-    std::unordered_map<const void*, Cached> gemm_cache;
-    float* gemm_x = nullptr;
-    float* gemm_out = nullptr;
-    size_t gemm_cap = 0;
+    std::unordered_map<const void*, Cached> resident_ptrs;
+    void* gemm_w = nullptr;      // per-call upload of a matrix that is not resident
+    size_t gemm_w_cap = 0;
+    float* gemm_x = nullptr;     // per-call scratch: input vector / first operand
+    float* gemm_b = nullptr;     // second operand
+    float* gemm_out = nullptr;   // output
+    size_t gemm_cap = 0;         // floats in each scratch buffer
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -495,6 +499,66 @@ int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float
     return stage_finish(ctx);
 }
 
+// Makes host_ptr[0, bytes) resident: uploads it, or replaces a copy of another
+// size.  The caller promises the range does not change until it is released.
+int resident_copy(lm_context* ctx, const void* host_ptr, size_t bytes, void** dev_out) {
+    auto it = ctx->resident_ptrs.find(host_ptr);
+    if (it != ctx->resident_ptrs.end() && it->second.bytes != bytes) {
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        LM_HIP(hipFree(it->second.dev));
+        ctx->resident_ptrs.erase(it);
+        it = ctx->resident_ptrs.end();
+    }
+    if (it == ctx->resident_ptrs.end()) {
+        void* dev = nullptr;
+        LM_HIP(hipMalloc(&dev, std::max<size_t>(bytes, 1)));
+        LM_HIP(hipMemcpyAsync(dev, host_ptr, bytes, hipMemcpyHostToDevice, ctx->stream));
+        it = ctx->resident_ptrs.emplace(host_ptr, lm_context::Cached{dev, bytes}).first;
+    }
+    *dev_out = it->second.dev;
+    return LM_OK;
+}
+
+// Device view of a matrix for one gemm call: the resident copy when the range was
+// prefetched, otherwise this call's own upload into a reused staging buffer (the
+// host memory is read on every call, as LiteMind's gemm reads it).
+int matrix_for_call(lm_context* ctx, const void* host_ptr, size_t bytes, void** dev_out) {
+    auto it = ctx->resident_ptrs.find(host_ptr);
+    if (it != ctx->resident_ptrs.end() && it->second.bytes >= bytes) {
+        *dev_out = it->second.dev;
+        return LM_OK;
+    }
+    if (ctx->gemm_w_cap < bytes) {
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        LM_HIP(hipFree(ctx->gemm_w));
+        ctx->gemm_w = nullptr;
+        ctx->gemm_w_cap = 0;
+        LM_HIP(hipMalloc(&ctx->gemm_w, bytes));
+        ctx->gemm_w_cap = bytes;
+    }
+    if (bytes > 0) {
+        LM_HIP(hipMemcpyAsync(ctx->gemm_w, host_ptr, bytes, hipMemcpyHostToDevice, ctx->stream));
+    }
+    *dev_out = ctx->gemm_w;
+    return LM_OK;
+}
+
+int ensure_gemm_scratch(lm_context* ctx, size_t floats) {
+    if (ctx->gemm_cap >= floats) {
+        return LM_OK;
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    (void)hipFree(ctx->gemm_x);
+    (void)hipFree(ctx->gemm_b);
+    (void)hipFree(ctx->gemm_out);
+    ctx->gemm_x = ctx->gemm_b = ctx->gemm_out = nullptr;
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_x), floats * sizeof(float)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_b), floats * sizeof(float)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_out), floats * sizeof(float)));
+    ctx->gemm_cap = floats;
+    return LM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -588,10 +652,12 @@ int lm_context_destroy(lm_context* ctx) {
     for (void* p : ptrs) {
         (void)hipFree(p);
     }
-    for (auto& kv : ctx->gemm_cache) {
+    for (auto& kv : ctx->resident_ptrs) {
         (void)hipFree(kv.second.dev);
     }
+    (void)hipFree(ctx->gemm_w);
     (void)hipFree(ctx->gemm_x);
+    (void)hipFree(ctx->gemm_b);
     (void)hipFree(ctx->gemm_out);
     (void)hipFree(ctx->d_overflow);
     if (ctx->staging != nullptr) {
@@ -1056,41 +1122,129 @@ int lm_gemm_matvec_bf16(lm_context* ctx, const uint16_t* w_host, const float* x_
     if (out_dim == 0) {
         return LM_OK;
     }
-    const size_t elems = out_dim * in_dim;
-    auto it = ctx->gemm_cache.find(w_host);
-    if (it != ctx->gemm_cache.end() && it->second.elems != elems) {
-        LM_HIP(hipStreamSynchronize(ctx->stream));
-        LM_HIP(hipFree(it->second.dev));
-        ctx->gemm_cache.erase(it);
-        it = ctx->gemm_cache.end();
+    void* w_dev = nullptr;
+    int rc = matrix_for_call(ctx, w_host, out_dim * in_dim * 2, &w_dev);
+    if (rc == LM_OK) {
+        rc = ensure_gemm_scratch(ctx, std::max(out_dim, in_dim));
     }
-    if (it == ctx->gemm_cache.end()) {
-        uint16_t* dev = nullptr;
-        LM_HIP(hipMalloc(reinterpret_cast<void**>(&dev), std::max<size_t>(elems, 1) * 2));
-        LM_HIP(hipMemcpyAsync(dev, w_host, elems * 2, hipMemcpyHostToDevice, ctx->stream));
-        it = ctx->gemm_cache.emplace(w_host, lm_context::Cached{dev, elems}).first;
-    }
-    const size_t need = std::max(out_dim, in_dim);
-    if (ctx->gemm_cap < need) {
-        LM_HIP(hipStreamSynchronize(ctx->stream));
-        (void)hipFree(ctx->gemm_x);
-        (void)hipFree(ctx->gemm_out);
-        ctx->gemm_x = nullptr;
-        ctx->gemm_out = nullptr;
-        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_x), need * sizeof(float)));
-        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->gemm_out), need * sizeof(float)));
-        ctx->gemm_cap = need;
+    if (rc != LM_OK) {
+        return rc;
     }
     LM_HIP(hipMemcpyAsync(ctx->gemm_x, x_host, in_dim * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     if (accumulate) {
         LM_HIP(hipMemcpyAsync(ctx->gemm_out, out_host, out_dim * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     }
-    LM_HIP(lm::launch_gemv_plain(it->second.dev, ctx->gemm_x, ctx->gemm_out, static_cast<int64_t>(out_dim),
-                                 static_cast<int64_t>(in_dim), scale, accumulate, ctx->stream));
+    LM_HIP(lm::launch_gemv_plain(static_cast<const uint16_t*>(w_dev), ctx->gemm_x, ctx->gemm_out,
+                                 static_cast<int64_t>(out_dim), static_cast<int64_t>(in_dim), scale, accumulate,
+                                 ctx->stream));
     LM_HIP(hipMemcpyAsync(out_host, ctx->gemm_out, out_dim * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     return LM_OK;
     LM_GUARD_END
+}
+
+int lm_gemm_matvec_f32(lm_context* ctx, const float* w_host, const float* x_host, float* out_host, size_t out_dim,
+                       size_t in_dim) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || w_host == nullptr || x_host == nullptr || out_host == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    if (out_dim == 0) {
+        return LM_OK;
+    }
+    void* w_dev = nullptr;
+    int rc = matrix_for_call(ctx, w_host, out_dim * in_dim * sizeof(float), &w_dev);
+    if (rc == LM_OK) {
+        rc = ensure_gemm_scratch(ctx, std::max(out_dim, in_dim));
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    LM_HIP(hipMemcpyAsync(ctx->gemm_x, x_host, in_dim * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(lm::launch_matvec_f32_ref(static_cast<const float*>(w_dev), ctx->gemm_x, ctx->gemm_out,
+                                     static_cast<int64_t>(out_dim), static_cast<int64_t>(in_dim), ctx->stream));
+    LM_HIP(hipMemcpyAsync(out_host, ctx->gemm_out, out_dim * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_vector_op(lm_context* ctx, int32_t op, const void* a_host, const float* b_host, float* out_host, size_t n,
+                 float scalar) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || out_host == nullptr || (n > 0 && a_host == nullptr)) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    if (op < LM_OP_DOT || op > LM_OP_WIDEN) {
+        return fail(LM_EINVAL, "unknown vector op");
+    }
+    const bool needs_b = op == LM_OP_DOT || op == LM_OP_SILU_MUL || op == LM_OP_RMS_NORM;
+    if (needs_b && b_host == nullptr) {
+        return fail(LM_EINVAL, "the operation needs a second operand");
+    }
+    if (n == 0) {
+        if (op == LM_OP_DOT) {
+            out_host[0] = 0.0f;
+        }
+        return LM_OK;
+    }
+    int rc = ensure_gemm_scratch(ctx, n);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const size_t a_bytes = op == LM_OP_WIDEN ? n * sizeof(uint16_t) : n * sizeof(float);
+    LM_HIP(hipMemcpyAsync(ctx->gemm_x, a_host, a_bytes, hipMemcpyHostToDevice, ctx->stream));
+    if (needs_b) {
+        LM_HIP(hipMemcpyAsync(ctx->gemm_b, b_host, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    }
+    if (op == LM_OP_AXPY) {
+        LM_HIP(hipMemcpyAsync(ctx->gemm_out, out_host, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    }
+    LM_HIP(lm::launch_vector_op(op, ctx->gemm_x, ctx->gemm_b, ctx->gemm_out, static_cast<int64_t>(n), scalar,
+                                ctx->stream));
+    const size_t out_n = op == LM_OP_DOT ? 1 : n;
+    LM_HIP(hipMemcpyAsync(out_host, ctx->gemm_out, out_n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_weight_prefetch(lm_context* ctx, const void* host_ptr, size_t bytes) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || host_ptr == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    void* dev = nullptr;
+    int rc = resident_copy(ctx, host_ptr, bytes, &dev);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_weight_release(lm_context* ctx, const void* host_ptr) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    auto it = ctx->resident_ptrs.find(host_ptr);
+    if (it != ctx->resident_ptrs.end()) {
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        LM_HIP(hipFree(it->second.dev));
+        ctx->resident_ptrs.erase(it);
+    }
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resident) {
+    if (ctx == nullptr || out_resident == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    *out_resident = ctx->resident_ptrs.count(host_ptr) != 0 ? 1 : 0;
+    return LM_OK;
 }
 
 int lm_event_create(lm_context* ctx, void** out_event) {

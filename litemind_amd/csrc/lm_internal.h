@@ -139,6 +139,10 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
                               hipStream_t s);
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
                            hipStream_t s);
+hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
+                                 hipStream_t s);
+hipError_t launch_vector_op(int op, const void* a, const float* b, float* out, int64_t n, float scalar,
+                            hipStream_t s);
 hipError_t launch_gemv_plain(const uint16_t* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
                              float scale, int32_t accumulate, hipStream_t s);
 
