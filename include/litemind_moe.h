@@ -38,11 +38,11 @@ extern "C" {
 
 typedef struct lm_context lm_context;
 
-/* The MoE subset of LiteMind's Config (include/Config.hpp:211-241, :271-273). */
+/* The MoE subset of LiteMind's Config (include/Config.hpp:48, :58-71, :101-103). */
 typedef struct lm_moe_config {
     int32_t hidden_size;            /* 2048 for DeepSeek-V2-Lite */
     int32_t moe_intermediate_size;  /* 1408 */
-    int32_t n_routed_experts;       /* 64 (at most 256) */
+    int32_t n_routed_experts;       /* 64 (at most 64) */
     int32_t num_experts_per_tok;    /* 6 (at most 16) */
     int32_t n_shared_experts;       /* 2 -> one fused shared FFN of width 1408*2 */
     int32_t intermediate_size;      /* dense layers: 10944 */
@@ -143,15 +143,18 @@ int lm_dense_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t
                      int32_t path);
 
 /* ---- per-call gemm compatibility (src/Gemm.cpp:139-175) ----
- * out = W x (accumulate = 0) or out += scale * W x (accumulate = 1), W [out_dim,
- * in_dim] BF16.  W_host is looked up in a pointer-keyed HBM cache and uploaded on
- * first use; x and out are host buffers.  Synchronous. */
+ * gemm::matvec_bf16 / _serial (accumulate = 0): out = W x, and
+ * gemm::matvec_bf16_accumulate (accumulate = 1): out = fma(scale, W x, out), with
+ * W [out_dim, in_dim] BF16, each row reduced in dot_bf16's association order
+ * (src/Gemm.cpp:46-82), so the result is bit-identical to LiteMind's.  W is read
+ * from its HBM copy when lm_weight_prefetch made it resident, otherwise uploaded
+ * for this call; x and out are host buffers.  Synchronous. */
 int lm_gemm_matvec_bf16(lm_context* ctx, const uint16_t* w_host, const float* x_host, float* out_host,
                         size_t out_dim, size_t in_dim, float scale, int32_t accumulate);
 
 /* out = W x for a row-major fp32 matrix with LiteMind's dot semantics (each
  * product rounded, then added left to right): gemm::matvec_f32
- * (src/Gemm.cpp:132-137, :183-189).  W is cached in HBM by host pointer.  Synchronous. */
+ * (src/Gemm.cpp:132-137, :183-189).  W as for lm_gemm_matvec_bf16.  Synchronous. */
 int lm_gemm_matvec_f32(lm_context* ctx, const float* w_host, const float* x_host, float* out_host, size_t out_dim,
                        size_t in_dim);
 
@@ -175,8 +178,9 @@ int lm_vector_op(lm_context* ctx, int32_t op, const void* a_host, const float* b
 /* Per-pointer HBM residency: replaces WeightView::prefetch / release
  * (src/WeightStore.cpp:40-50), which ExpertCache::touch / evict_oldest call
  * (src/ExpertCache.cpp:33-35, :53-55).  prefetch copies `bytes` from host_ptr
- * into HBM (no-op if resident); release frees the copy.  The per-call gemm
- * entry points use a resident copy when one exists for their weight pointer. */
+ * into HBM (no-op if resident with the same size); release frees the copy.  The
+ * per-call gemm entry points use a resident copy when one exists for their weight
+ * pointer, so a prefetched range must not change until it is released. */
 int lm_weight_prefetch(lm_context* ctx, const void* host_ptr, size_t bytes);
 int lm_weight_release(lm_context* ctx, const void* host_ptr);
 int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resident);

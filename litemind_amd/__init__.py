@@ -26,7 +26,7 @@ class LmError(RuntimeError):
 
 
 class MoeConfig(C.Structure):
-    """lm_moe_config: the MoE subset of LiteMind's Config (include/Config.hpp:211-241)."""
+    """lm_moe_config: the MoE subset of LiteMind's Config (include/Config.hpp:48, :58-71, :101-103)."""
 
     _fields_ = [
         ("hidden_size", C.c_int32),

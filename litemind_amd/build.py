@@ -74,16 +74,17 @@ def build_synth() -> str:
 
 
 def build_dropin() -> str | None:
-    """C++20 drop-in wrappers (MoeRouter / gemm / ExpertCache) and their demo program."""
+    """C++20 drop-in wrappers (MoeRouter / gemm / ExpertCache / MoeBlockGpu) and their demo program."""
     demo_src = os.path.join(HOST, "dropin_demo.cpp")
     if not os.path.exists(demo_src):
         return None
-    srcs = [os.path.join(HOST, f) for f in sorted(os.listdir(HOST)) if f.endswith(".cpp")]
+    src_dir = os.path.join(HOST, "src")
+    srcs = [os.path.join(src_dir, f) for f in sorted(os.listdir(src_dir)) if f.endswith(".cpp")]
     bindir = os.path.join(HERE, "bin")
     os.makedirs(bindir, exist_ok=True)
     exe = os.path.join(bindir, "dropin_demo")
-    _run(["g++", *HOST_FLAGS, "-I", HOST, "-I", INCLUDE, "-o", exe + ".tmp", *srcs,
-          "-L", HERE, "-llitemind_moe", f"-Wl,-rpath,$ORIGIN/..", "-ldl"])
+    _run(["g++", *HOST_FLAGS, "-I", os.path.join(HOST, "include"), "-I", INCLUDE, "-o", exe + ".tmp", demo_src,
+          *srcs, "-L", HERE, "-llitemind_moe", "-Wl,-rpath,$ORIGIN/..", "-pthread"])
     os.replace(exe + ".tmp", exe)
     return exe
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-/* Routing policy, the MoE subset of Config (include/Config.hpp:228-241). */
+/* Routing policy, the MoE subset of Config (include/Config.hpp:66-71). */
 typedef struct orc_router_cfg {
     int32_t expert_count;        /* n_routed_experts */
     int32_t top_k;               /* num_experts_per_tok */
@@ -36,7 +36,7 @@ typedef struct orc_router_cfg {
     float routed_scaling_factor; /* routed_scaling_factor */
 } orc_router_cfg;
 
-/* Shapes of one MoE layer (include/Config.hpp:229-233, :271-273). */
+/* Shapes of one MoE layer (include/Config.hpp:58-64, :101-103). */
 typedef struct orc_layer_dims {
     int32_t hidden;        /* hidden_size, H */
     int32_t inter;         /* moe_intermediate_size, I */
