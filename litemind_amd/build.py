@@ -5,6 +5,7 @@
   litemind_amd/bin/dropin_demo      C++20 drop-in wrappers exercised like LiteMind's runner
   oracle/liboracle.so               CPU oracle (test infrastructure)
   oracle/_ref/libref.so             LiteMind's own sources, where the source tree is present
+  oracle/_ref/*_gpu                 LiteMind's own unit tests linked against the GPU drop-in
 
 Every call recompiles.  Run:  python -m litemind_amd.build
 """
@@ -68,7 +69,7 @@ def build_hip(jobs: int = 6) -> str:
 def build_synth() -> str:
     lib = os.path.join(HERE, "libsynth.so")
     tmp = lib + ".tmp"
-    _run(["g++", *HOST_FLAGS, "-shared", "-I", CSRC, "-o", tmp, os.path.join(CSRC, "synth.cpp")])
+    _run(["g++", *HOST_FLAGS, "-fopenmp", "-shared", "-I", CSRC, "-o", tmp, os.path.join(CSRC, "synth.cpp")])
     os.replace(tmp, lib)
     return lib
 
@@ -83,7 +84,10 @@ def build_dropin() -> str | None:
     bindir = os.path.join(HERE, "bin")
     os.makedirs(bindir, exist_ok=True)
     exe = os.path.join(bindir, "dropin_demo")
-    _run(["g++", *HOST_FLAGS, "-I", os.path.join(HOST, "include"), "-I", INCLUDE, "-o", exe + ".tmp", demo_src,
+    # host/include: what the drop-in adds; host/litemind_api: LiteMind's interfaces
+    # (inside LiteMind its own include/ takes this place)
+    _run(["g++", *HOST_FLAGS, "-I", os.path.join(HOST, "include"), "-I", os.path.join(HOST, "litemind_api"),
+          "-I", INCLUDE, "-o", exe + ".tmp", demo_src,
           *srcs, "-L", HERE, "-llitemind_moe", "-Wl,-rpath,$ORIGIN/..", "-pthread"])
     os.replace(exe + ".tmp", exe)
     return exe
@@ -95,11 +99,18 @@ def build_oracle() -> None:
         _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-B", "ref", f"REF={REFERENCE}"])
 
 
+def build_ref_tests() -> None:
+    """LiteMind's own KernelTest / MoeRouterSamplerTest linked against the GPU drop-in."""
+    if os.path.isdir(os.path.join(REFERENCE, "tests")):
+        _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-B", "ref-tests", f"REF={REFERENCE}"])
+
+
 def build_all() -> None:
     build_oracle()
     build_synth()
     build_hip()
     build_dropin()
+    build_ref_tests()
 
 
 if __name__ == "__main__":

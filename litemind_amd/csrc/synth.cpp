@@ -120,8 +120,10 @@ void lms_expf_ref(const float* in, float* out, std::size_t n) {
 // [lo, hi], how often lm::expf_ref differs from the C library's expf.
 uint64_t lms_expf_sweep(uint32_t stride, float lo, float hi, uint64_t* checked) {
     uint64_t bad = 0, n = 0;
-    for (uint64_t u = 0; u < 0x100000000ull; u += stride) {
-        const float x = lm::bits_float(static_cast<uint32_t>(u));
+    const int64_t steps = static_cast<int64_t>((0x100000000ull + stride - 1) / stride);
+#pragma omp parallel for schedule(static, 1 << 16) reduction(+ : bad, n)
+    for (int64_t i = 0; i < steps; ++i) {
+        const float x = lm::bits_float(static_cast<uint32_t>(static_cast<uint64_t>(i) * stride));
         if (!(x >= lo && x <= hi)) {
             continue;
         }
