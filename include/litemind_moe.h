@@ -185,6 +185,13 @@ int lm_weight_prefetch(lm_context* ctx, const void* host_ptr, size_t bytes);
 int lm_weight_release(lm_context* ctx, const void* host_ptr);
 int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resident);
 
+/* Testing hook, no counterpart in LiteMind.  The single-token forward starts the
+ * routed experts from a speculative selection (a fast, reassociated logit sum)
+ * and recomputes any rank where it disagrees with the exact selection.  mode 1
+ * makes every speculative rank wrong so that tests exercise the recomputation;
+ * outputs must not change.  mode 0 (the default) restores normal operation. */
+int lm_decode_speculation_test(lm_context* ctx, int32_t mode);
+
 /* ---- timing: hipEvents on the context stream ---- */
 int lm_event_create(lm_context* ctx, void** out_event);
 int lm_event_destroy(lm_context* ctx, void* event);

@@ -39,16 +39,19 @@ constexpr int log2c() {
 
 // Reduces V per-lane partial sums (V a power of two, <= 64) across the wave.
 // Afterwards every lane holds the full sum of value index lane >> (6 - log2 V).
+// The halves are exchanged with a bit mask rather than `upper ? v[a] : v[b]`,
+// which the compiler may turn into a dynamically indexed (scratch) array.
 template <int V>
 __device__ inline float transpose_reduce(float (&v)[V], int lane) {
     int off = 32;
 #pragma unroll
     for (int half = V / 2; half >= 1; half >>= 1) {
-        const bool upper = (lane & off) != 0;
+        const uint32_t m = (lane & off) != 0 ? 0xffffffffu : 0u;
 #pragma unroll
         for (int i = 0; i < half; ++i) {
-            const float keep = upper ? v[i + half] : v[i];
-            const float send = upper ? v[i] : v[i + half];
+            const uint32_t lo = float_bits(v[i]), hi = float_bits(v[i + half]);
+            const float keep = bits_float((hi & m) | (lo & ~m));
+            const float send = bits_float((lo & m) | (hi & ~m));
             v[i] = keep + __shfl_xor(send, off);
         }
         off >>= 1;

@@ -1,0 +1,767 @@
+// k_decode.hip -- the MoE block for a single token (decode) in one launch.
+//
+// Reference: the MoE branch of DeepSeekRunner::Impl::forward
+// (src/DeepSeekRunner.cpp:273-290): router matvec_f32, MoeRouter::select,
+// feed_forward for each selected expert in rank order, then the shared expert,
+// accumulated into the layer output.
+//
+// At T = 1 the block streams ~139 MB of weights; what it computes is small.  Its
+// critical path would be the router's 2048-long dependent add chain (~7 us on
+// gfx950: every logit is LiteMind's strictly sequential fp32 sum) followed by
+// the routed experts, which cannot start before the selection is known.  One
+// launch runs every part as a role of its workgroups, ordered so that work
+// waits only on workgroups with lower indices (see decode_fused_kernel), and
+// the routed experts start from a speculative selection while the exact
+// logits are still being summed.
+#include "gemv_items.h"
+#include "lm_select.h"
+
+namespace lm {
+namespace {
+
+using gemv::dot_rows;
+using gemv::fma8;
+using gemv::load_rows;
+using gemv::log2c;
+using gemv::transpose_reduce;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRouterExperts = 4;            // experts per router workgroup
+constexpr int kRpw = 4;                      // gate rows (and as many up rows) per wave
+constexpr int kItemRows = kRpw * kWaves;     // gate rows per gate/up item
+constexpr int kDownRpw = 2;                  // shared down rows per wave
+constexpr int kDownItemRows = kDownRpw * kWaves;
+
+struct DecodeArgs {
+    const float* x;            // [H] the token
+    const float* wq;           // [E/4][H][4] router gate, four experts per contiguous slice
+    const float* bias;         // [E] or null
+    float* logits;             // [E] exact logits (hand-off to the selecting workgroup)
+    float* logits_out;         // [E] or null
+    int32_t* idx;              // [K] selection in rank order
+    float* wts;                // [K]
+    const uint16_t* routed;    // expert 0's FFN; expert e at routed + e * routed_stride
+    int64_t routed_stride;     // elements between consecutive experts
+    const uint16_t* shared_gu;
+    const uint16_t* shared_down;
+    float* act;                // [K, Ip] routed activations in rank order, then [Sp] shared
+    float* shared_out;         // [H] shared expert's down projection
+    float* y;                  // [H]
+    const float* residual;     // [H] or null
+    int32_t hidden, hidden_p, experts, top_k, inter_p, shared_inter_p, has_shared;
+    SelectPolicy policy;
+};
+
+// Device-scope accesses (`sc1`): stores write through the XCD's L2 to memory
+// and loads bypass it, so a value written by a workgroup on one XCD is seen by
+// a workgroup on another within the same launch without an L2 writeback or
+// invalidate.  Everything one workgroup hands to another goes through these.
+__device__ inline void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void store_coherent(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int32_t load_coherent(const int32_t* p) {
+    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float4 load_coherent4(const float* p) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(bits_float(static_cast<uint32_t>(lo)), bits_float(static_cast<uint32_t>(lo >> 32)),
+                       bits_float(static_cast<uint32_t>(hi)), bits_float(static_cast<uint32_t>(hi >> 32)));
+}
+
+// Activations of lane columns of one row (device-scope loads): zero past the end.
+template <int ITERS>
+__device__ inline void load_act_coherent(const float* row, int width, int lane, float4 (&x)[ITERS][2]) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int c = it * 512 + lane * 8;
+        const int cc = c < width ? c : width - 8;
+        x[it][0] = load_coherent4(row + cc);
+        x[it][1] = load_coherent4(row + cc + 4);
+        if (c >= width) {
+            x[it][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+            x[it][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+}
+
+// ---- roles -------------------------------------------------------------------
+
+// Logits of experts [e0, e0 + 4) with LiteMind's dot (src/Gemm.cpp:183-189):
+// all threads form the rounded products into LDS ([H/4][4] float4, four
+// consecutive rows of one expert per float4) from the slice's contiguous
+// [H][4] weights; then lane e adds its expert's products strictly left to
+// right, at raised wave priority (the chain shares its SIMD with streaming
+// waves).  after_load runs on every thread once the products are in LDS.
+template <typename AfterLoad>
+__device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4* prod, AfterLoad after_load) {
+    const int tid = threadIdx.x;
+    const int H = a.hidden;
+    const float4* slice = reinterpret_cast<const float4*>(a.wq) + static_cast<int64_t>(e0 / 4) * H;
+    float* pf = reinterpret_cast<float*>(prod);
+    for (int hb = 0; hb < H; hb += kThreads * 8) {
+        float4 w[8];
+        float xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int h = hb + j * kThreads + tid;
+            const int hc = h < H ? h : H - 1;
+            w[j] = slice[hc];
+            xv[j] = a.x[hc];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int h = hb + j * kThreads + tid;
+            if (h < H) {
+                float* q = pf + (h >> 2) * 16 + (h & 3);
+                q[0] = w[j].x * xv[j];
+                q[4] = w[j].y * xv[j];
+                q[8] = w[j].z * xv[j];
+                q[12] = w[j].w * xv[j];
+            }
+        }
+    }
+    lds_barrier();
+    after_load();
+    if (tid >= kRouterExperts) {
+        return;
+    }
+    __builtin_amdgcn_s_setprio(3);
+    const int quads = H / 4;
+    float acc = 0.0f;
+    int q = 0;
+    if (quads >= 16) {
+        float4 A[8], B[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            A[u] = prod[u * kRouterExperts + tid];
+        }
+        for (; q + 16 <= quads; q += 16) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                B[u] = prod[(q + 8 + u) * kRouterExperts + tid];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc = acc + A[u].x;
+                acc = acc + A[u].y;
+                acc = acc + A[u].z;
+                acc = acc + A[u].w;
+            }
+            const int nq = q + 16 + 8 <= quads ? q + 16 : q;  // next A batch (re-read harmlessly at the end)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                A[u] = prod[(nq + u) * kRouterExperts + tid];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc = acc + B[u].x;
+                acc = acc + B[u].y;
+                acc = acc + B[u].z;
+                acc = acc + B[u].w;
+            }
+        }
+    }
+    for (; q < quads; ++q) {
+        const float4 p = prod[q * kRouterExperts + tid];
+        acc = acc + p.x;
+        acc = acc + p.y;
+        acc = acc + p.z;
+        acc = acc + p.w;
+    }
+    __builtin_amdgcn_s_setprio(0);
+    const int e = e0 + tid;
+    if (a.bias != nullptr) {
+        acc = acc + a.bias[e];
+    }
+    store_coherent(a.logits + e, acc);
+    if (a.logits_out != nullptr) {
+        a.logits_out[e] = acc;
+    }
+}
+
+// Gate/up rows [16 chunk, 16 chunk + 16) of one FFN for the token, act =
+// silu(gate) * up (src/Gemm.cpp:225-231), four gate rows and the matching up
+// rows per wave.  The token's activations are staged once per workgroup in LDS
+// (xs, hidden floats) rather than held by every wave, which leaves the registers
+// to weight rows in flight; their loads are issued before the weights' so that
+// waiting for them does not wait for the weights.
+template <int GI>
+__device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs& a, int chunk, float* act_row,
+                                            float* xs) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    constexpr int R = 2 * kRpw;
+    const uint16_t* rows[R];
+    const int j0 = chunk * kItemRows + wave * kRpw;
+#pragma unroll
+    for (int r = 0; r < kRpw; ++r) {
+        const int j = j0 + r;
+        const int64_t gate_row = static_cast<int64_t>(j / kGroupRows) * (2 * kGroupRows) + (j % kGroupRows);
+        rows[r] = gu + gate_row * a.hidden_p;
+        rows[kRpw + r] = gu + (gate_row + kGroupRows) * a.hidden_p;
+    }
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        acc[i] = 0.0f;
+    }
+    uint4 w[R][GI];
+    constexpr int XS = (GI * 128 + kThreads - 1) / kThreads;  // float4 per thread
+    const int n4 = a.hidden / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    float4 xv[XS];
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+        xv[i] = x4[f < n4 ? f : n4 - 1];
+    }
+    load_rows<R, GI>(rows, a.hidden, lane, w);
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+        if (f < n4) {
+            xs4[f] = xv[i];
+        }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int it = 0; it < GI; ++it) {
+        const int c = it * 512 + lane * 8;
+        const bool in = c < a.hidden;
+        const int cc = in ? c : 0;
+        float4 x0 = xs4[cc / 4];
+        float4 x1 = xs4[cc / 4 + 1];
+        if (!in) {
+            x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+            x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            fma8(acc[r], w[r][it], x0, x1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float sum = transpose_reduce<R>(acc, lane);
+    constexpr int L = log2c<R>();
+    const int vi = lane >> (6 - L);
+    const float up = __shfl_xor(sum, kRpw << (6 - L));
+    if ((lane & ((1 << (6 - L)) - 1)) == 0 && (vi & kRpw) == 0) {
+        store_coherent(act_row + j0 + (vi & (kRpw - 1)), silu_mul_ref(sum, up));
+    }
+}
+
+// Shared expert's down rows [8 item, 8 item + 8): shared_out[h] = W_d[h] . act_shared.
+template <int SI>
+__device__ __forceinline__ void shared_down_item(const DecodeArgs& a, int item) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int W = a.shared_inter_p;
+    constexpr int R = kDownRpw;
+    const int h0 = item * kDownItemRows + wave * R;
+    const uint16_t* rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rows[r] = a.shared_down + static_cast<int64_t>(h0 + r) * W;
+    }
+    uint4 w[R][SI];
+    load_rows<R, SI>(rows, W, lane, w);
+    float4 hr[1][SI][2];
+    load_act_coherent<SI>(a.act + a.top_k * a.inter_p, W, lane, hr[0]);
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        acc[i] = 0.0f;
+    }
+    dot_rows<R, SI, 1>(w, hr, acc);
+    const float sum = transpose_reduce<R>(acc, lane);
+    constexpr int L = log2c<R>();
+    if ((lane & ((1 << (6 - L)) - 1)) == 0) {
+        store_coherent(a.shared_out + h0 + (lane >> (6 - L)), sum);
+    }
+}
+
+// ---- the single launch --------------------------------------------------------
+//
+// One grid, roles by workgroup index, in dependency order:
+//   [routers | shared gate/up | routed gate/up | shared down | down + combine]
+// A workgroup waits only for workgroups with lower indices.  The dispatcher
+// places workgroups on the GPU in index order, so when one waits, everything it
+// waits for is resident or finished, and every wait ends; each wait is bounded
+// all the same and reports a timeout through the error word.  Counters come in
+// two sets used by alternating launches; each launch clears the set the next one
+// uses (the launch before it, which used that set, has completed).
+constexpr uint32_t kMaxSpins = 1u << 16;  // ~50 ms of polling
+// Each logical counter is spread over kLanes slots, one 64-byte line apart, so
+// hundreds of workgroups neither add to nor poll one address.
+constexpr int kLanes = 16;
+constexpr int kSlotStride = 16;  // words
+enum : int {
+    kRouterLoaded = 0, kApproxDone, kSpecReady, kRouterDone, kSelectReady, kSharedGuDone, kSharedDownDone,
+    kRoutedDone, kCounters
+};
+constexpr int kSetWords = kCounters * kLanes * kSlotStride;
+constexpr int kFusedRows = kWaves;  // down + combine: one output row per wave
+
+struct FusedArgs {
+    DecodeArgs a;
+    uint32_t* sync;     // [2][kSetWords] counters, then the error word
+    float* approx;      // [E] fast (reassociated) logits for the speculative selection
+    int32_t* spec;      // [K] speculative experts by rank
+    uint32_t* mask;     // ranks whose speculative expert differs from the exact one
+    int32_t parity;
+    int32_t perturb;    // testing: make the speculation disagree with every rank
+    int32_t n_router, n_shared_gu, n_shared_down, n_routed;
+};
+
+__device__ inline uint32_t* counter_slot(uint32_t* set, int counter, int slot) {
+    return set + (counter * kLanes + slot) * kSlotStride;
+}
+
+// Counts this workgroup done once every wave's stores are acknowledged; returns
+// the slot's previous value.
+__device__ inline uint32_t signal_done(uint32_t* set, int counter) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    __shared__ uint32_t previous;
+    if (threadIdx.x == 0) {
+        previous = __hip_atomic_fetch_add(counter_slot(set, counter, blockIdx.x % kLanes), 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return previous;
+}
+
+// Waits until the counter's slots sum to `target` (wave 0 polls all slots at
+// once, backing off while far from done), then releases the workgroup.
+__device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, uint32_t* error) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        uint32_t spins = 0;
+        for (;;) {
+            uint32_t v = lane < kLanes ? __hip_atomic_load(counter_slot(set, counter, lane), __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0u;
+            // every lane of the wave must see the total, or the lanes would leave
+            // the loop at different times
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                v += __shfl_xor(v, o);
+            }
+            if (v >= target) {
+                break;
+            }
+            if (++spins > kMaxSpins) {
+                if (lane == 0) {
+                    __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                break;
+            }
+            if (target - v > target / 4) {
+                __builtin_amdgcn_s_sleep(32);
+            } else {
+                __builtin_amdgcn_s_sleep(4);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Router workgroups, once their products are in LDS: count the router's loads
+// done and publish the approximate logits of the slice.
+__device__ __forceinline__ void speculate(const FusedArgs& f, uint32_t* sync, int e0, int b, const float4* lds) {
+    const DecodeArgs& a = f.a;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(counter_slot(sync, kRouterLoaded, b % kLanes), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Approximate logit of expert e0 + wave: the same products, tree order.
+    const int quads = a.hidden / 4;
+    float t = 0.0f;
+    for (int q = lane; q < quads; q += 64) {
+        const float4 p = lds[q * kRouterExperts + wave];
+        t += (p.x + p.y) + (p.z + p.w);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        t += __shfl_xor(t, o);
+    }
+    if (lane == 0) {
+        store_coherent(f.approx + e0 + wave, a.bias != nullptr ? t + a.bias[e0 + wave] : t);
+    }
+    signal_done(sync, kApproxDone);
+}
+
+// Recomputes, in LDS, the activation row of rank r for expert e (rare path:
+// the speculative selection put another expert at this rank).  Plain loops,
+// few registers: it runs once in tens of thousands of tokens.
+__device__ void repair_act_row(const DecodeArgs& a, int e, float* act_row) {
+    const uint16_t* gu = a.routed + static_cast<int64_t>(e) * a.routed_stride;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    for (int j = threadIdx.x; j < a.inter_p; j += blockDim.x) {
+        const int64_t gate_row = static_cast<int64_t>(j / kGroupRows) * (2 * kGroupRows) + (j % kGroupRows);
+        const uint16_t* g = gu + gate_row * a.hidden_p;
+        const uint16_t* u = g + static_cast<int64_t>(kGroupRows) * a.hidden_p;
+        float gate = 0.0f, up = 0.0f;
+        for (int c = 0; c < a.hidden; c += 8) {
+            const uint4 wg = *reinterpret_cast<const uint4*>(g + c);
+            const uint4 wu = *reinterpret_cast<const uint4*>(u + c);
+            const float4 x0 = x4[c / 4], x1 = x4[c / 4 + 1];
+            fma8(gate, wg, x0, x1);
+            fma8(up, wu, x0, x1);
+        }
+        act_row[j] = silu_mul_ref(gate, up);
+    }
+}
+
+// Down projection and combine for output row h (one per wave) in the single
+// launch.  The down rows are fetched for the speculative experts as soon as
+// those are known; the exact selection then decides: ranks it confirms use the
+// rows in registers and the activations the routed workgroups wrote, the others
+// (rare) are recomputed here from the exact expert's weights.
+template <int KM, int DI>
+__device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, uint32_t* error, int h,
+                                           float* acts) {
+    constexpr int KP = KM <= 2 ? 2 : (KM <= 4 ? 4 : 8);  // reduction width (power of two)
+    __shared__ float fixed_dot[kWaves][kMaxTopK];
+    const DecodeArgs& a = f.a;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int K = a.top_k;
+    const int W = a.inter_p;
+    const int64_t down_off = static_cast<int64_t>(2) * W * a.hidden_p + static_cast<int64_t>(h) * W;
+    wait_count(sync, kSpecReady, 1, error);
+    uint4 w[KM][DI];
+    {
+        int ex[KM];
+#pragma unroll
+        for (int r = 0; r < KM; ++r) {
+            ex[r] = load_coherent(f.spec + (r < K ? r : 0));
+        }
+#pragma unroll
+        for (int it = 0; it < DI; ++it) {
+            const int c = it * 512 + lane * 8;
+            const int cc = c < W ? c : W - 8;
+#pragma unroll
+            for (int r = 0; r < KM; ++r) {
+                w[r][it] = load_stream16(a.routed + static_cast<int64_t>(ex[r]) * a.routed_stride + down_off + cc);
+            }
+        }
+    }
+    wait_count(sync, kRoutedDone, f.n_routed, error);
+    wait_count(sync, kSharedDownDone, f.n_shared_down, error);
+    wait_count(sync, kSelectReady, 1, error);
+    const uint32_t m = __hip_atomic_load(f.mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float wk[KM];
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+        wk[r] = load_coherent(a.wts + (r < K ? r : 0));
+    }
+    // The activations of the confirmed ranks, once per workgroup, into LDS.
+    const int n4 = K * W / 4;
+    for (int f0 = threadIdx.x; f0 < n4; f0 += 4 * kThreads) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = f0 + u * kThreads;
+            v[u] = load_coherent4(a.act + 4 * (g < n4 ? g : n4 - 1));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = f0 + u * kThreads;
+            if (g < n4 && ((m >> (4 * g / W)) & 1u) == 0) {
+                *reinterpret_cast<float4*>(acts + 4 * g) = v[u];
+            }
+        }
+    }
+    const float shared_h = a.has_shared ? load_coherent(a.shared_out + h) : 0.0f;
+    const float residual_h = a.residual != nullptr ? a.residual[h] : 0.0f;
+    lds_barrier();
+    float acc[KP];
+#pragma unroll
+    for (int r = 0; r < KP; ++r) {
+        acc[r] = 0.0f;
+    }
+#pragma unroll
+    for (int it = 0; it < DI; ++it) {
+        const int c = it * 512 + lane * 8;
+        if (c < W) {
+#pragma unroll
+            for (int r = 0; r < KM; ++r) {
+                const int rr = r < K ? r : 0;  // ranks past K read valid data and are never combined
+                const float4 x0 = *reinterpret_cast<const float4*>(acts + rr * W + c);
+                const float4 x1 = *reinterpret_cast<const float4*>(acts + rr * W + c + 4);
+                fma8(acc[r], w[r][it], x0, x1);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float sum = transpose_reduce<KP>(acc, lane);
+    if (m != 0) {
+        // Ranks the speculation got wrong: their activation rows and down dot
+        // products from the exact experts (the sums above are discarded).
+        for (int r = 0; r < K; ++r) {
+            if (((m >> r) & 1u) == 0) {
+                continue;
+            }
+            const int e = load_coherent(a.idx + r);
+            lds_barrier();
+            repair_act_row(a, e, acts + r * W);
+            lds_barrier();
+            const uint16_t* down = a.routed + static_cast<int64_t>(e) * a.routed_stride + down_off;
+            float d = 0.0f;
+            for (int c = lane * 8; c < W; c += 512) {
+                const float4 x0 = *reinterpret_cast<const float4*>(acts + r * W + c);
+                const float4 x1 = *reinterpret_cast<const float4*>(acts + r * W + c + 4);
+                fma8(d, *reinterpret_cast<const uint4*>(down + c), x0, x1);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                d += __shfl_xor(d, o);
+            }
+            if (lane == 0) {
+                fixed_dot[wave][r] = d;
+            }
+        }
+        lds_barrier();
+    }
+    constexpr int L = log2c<KP>();
+    float out = 0.0f;
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+        if (r < K) {
+            const float d = ((m >> r) & 1u) != 0 ? fixed_dot[wave][r] : lane_value(sum, r << (6 - L));
+            out = __builtin_fmaf(wk[r], d, out);
+        }
+    }
+    if (a.has_shared) {
+        out = out + shared_h;
+    }
+    if (a.residual != nullptr) {
+        out = residual_h + out;
+    }
+    if (lane == 0) {
+        a.y[h] = out;
+    }
+}
+
+// The routed experts start from a speculative selection: each router workgroup
+// first sums its products in a fast tree order (approximate logits), the last
+// one to finish selects from those, and the routed gate/up rows of the
+// speculated experts stream while the exact, strictly sequential logits are
+// still being added.  The exact selection decides everything that is output;
+// ranks where the speculation picked another expert are recomputed by the fix-up
+// workgroups (almost never: only a near-tie between two experts' scores can
+// order them differently), and the down projection reads those rows instead.
+template <int GI, int SI, int KM, int DI>
+__global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
+    extern __shared__ float4 lds[];  // router products or the down stage's activations
+    __shared__ __align__(16) float sel[kSelectScratch];
+    __shared__ int expert_of_rank[kMaxTopK];
+    __shared__ uint32_t arrived;
+    const DecodeArgs& a = f.a;
+    uint32_t* sync = f.sync + f.parity * kSetWords;
+    uint32_t* error = f.sync + kDecodeErrorWord;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int b = blockIdx.x;
+    if (b == static_cast<int>(gridDim.x) - 1) {
+        // the last workgroup, off the critical path, clears the next launch's counters
+        uint32_t* next = f.sync + (1 - f.parity) * kSetWords;
+        for (int i = threadIdx.x; i < kCounters * kLanes; i += kThreads) {
+            __hip_atomic_store(next + i * kSlotStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (b < f.n_router) {
+        const int e0 = b * kRouterExperts;
+        router_slice(a, e0, lds, [&] { speculate(f, sync, e0, b, lds); });
+        // The last router workgroup to finish its exact logits selects for the output.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            arrived = __hip_atomic_fetch_add(counter_slot(sync, kRouterDone, 0), 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (arrived != static_cast<uint32_t>(f.n_router - 1)) {
+            return;
+        }
+        if (threadIdx.x < 64) {
+            const bool valid = lane < a.experts;
+            const float logit = valid ? load_coherent(a.logits + lane) : 0.0f;
+            int rank;
+            float weight;
+            select_token_lds(logit, valid, lane, a.policy, sel, rank, weight);
+            const bool chosen = valid && rank < a.top_k;
+            if (chosen) {
+                store_coherent(a.idx + rank, lane);
+                store_coherent(a.wts + rank, weight);
+            }
+            const uint64_t wrong = __ballot(chosen && load_coherent(f.spec + rank) != lane);
+            // bit r of the mask: rank r must be recomputed
+            uint32_t m = 0;
+            if (chosen && ((wrong >> lane) & 1u) != 0) {
+                m = 1u << rank;
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                m |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), o));
+            }
+            if (lane == 0) {
+                __hip_atomic_store(f.mask, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        signal_done(sync, kSelectReady);
+        return;
+    }
+    b -= f.n_router;
+    if (b < f.n_shared_gu) {
+        // Streams only once the router's weights are in: the router's loads are
+        // the block's critical path and would otherwise queue behind these.
+        wait_count(sync, kRouterLoaded, f.n_router, error);
+        gateup_item<GI>(a.shared_gu, a, b, a.act + a.top_k * a.inter_p, reinterpret_cast<float*>(lds));
+        signal_done(sync, kSharedGuDone);
+        return;
+    }
+    b -= f.n_shared_gu;
+    const int chunks = a.inter_p / kItemRows;
+    if (b < f.n_routed) {
+        if (b == 0) {
+            // The first routed workgroup selects speculatively from the
+            // approximate logits, for itself and the others.
+            wait_count(sync, kApproxDone, f.n_router, error);
+            if (threadIdx.x < 64) {
+                const bool valid = lane < a.experts;
+                const float logit = valid ? load_coherent(f.approx + lane) : 0.0f;
+                int rank;
+                float weight;
+                select_token_lds(logit, valid, lane, a.policy, sel, rank, weight);
+                if (valid && rank < a.top_k) {
+                    store_coherent(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), lane);
+                }
+            }
+            signal_done(sync, kSpecReady);
+        } else {
+            wait_count(sync, kSpecReady, 1, error);
+        }
+    }
+    b -= f.n_routed;
+    if (b >= 0 && b < f.n_shared_down) {
+        wait_count(sync, kSharedGuDone, f.n_shared_gu, error);
+        shared_down_item<SI>(a, b);
+        signal_done(sync, kSharedDownDone);
+        return;
+    }
+    b -= f.n_shared_down;
+    if (b < 0) {
+        // Routed gate/up of the speculative experts.
+        const int item = b + f.n_routed + f.n_shared_down;
+        const int r = item / chunks;
+        if (threadIdx.x == 0) {
+            expert_of_rank[0] = load_coherent(f.spec + r);
+        }
+        __syncthreads();
+        gateup_item<GI>(a.routed + static_cast<int64_t>(expert_of_rank[0]) * a.routed_stride, a,
+                                    item - r * chunks, a.act + static_cast<int64_t>(r) * a.inter_p,
+                                    reinterpret_cast<float*>(lds));
+        signal_done(sync, kRoutedDone);
+        return;
+    }
+    down_fused<KM, DI>(f, sync, error, b * kFusedRows + wave, reinterpret_cast<float*>(lds));
+}
+
+int iters_of(int width) { return (width + 511) / 512; }
+
+int km_of(int top_k) { return top_k <= 2 ? 2 : (top_k <= 4 ? 4 : (top_k <= 6 ? 6 : 8)); }
+
+// (GI, SI, KM, DI) instantiations: DeepSeek-V2-Lite (hidden 2048, routed 1408,
+// shared 2816, k 6) and LiteMind's tiny test model (hidden 32, routed 16,
+// shared 16, k 2).  Other shapes take the general path.
+int fused_shape(int hidden, int top_k, int inter_p, int shared_inter_p) {
+    const int gi = iters_of(hidden), si = iters_of(shared_inter_p), km = km_of(top_k), di = iters_of(inter_p);
+    if (gi == 4 && si == 6 && km == 6 && di == 3) {
+        return 0;
+    }
+    if (gi == 1 && si == 1 && km == 2 && di == 1) {
+        return 1;
+    }
+    return -1;
+}
+
+}  // namespace
+
+bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p) {
+    return experts % kRouterExperts == 0 && experts >= 2 && experts <= kMaxExperts && top_k >= 1 &&
+           top_k <= 8 && top_k <= experts && shared_inter_p > 0 && hidden % kDownItemRows == 0 &&
+           hidden % kWaves == 0 && hidden * 16 <= 65536 && top_k * inter_p * 4 <= 65536 &&
+           inter_p % kItemRows == 0 && shared_inter_p % kItemRows == 0 &&
+           fused_shape(hidden, top_k, inter_p, shared_inter_p) >= 0;
+}
+
+hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
+    const int hidden = d.hidden, top_k = d.policy.top_k, inter_p = d.inter_p;
+    if (d.sync == nullptr || d.shared_gu == nullptr ||
+        !decode_supported(hidden, d.policy.experts, top_k, inter_p, d.shared_inter_p)) {
+        return hipErrorInvalidValue;
+    }
+    FusedArgs f{};
+    DecodeArgs& a = f.a;
+    a.x = d.x;
+    a.wq = d.wq;
+    a.bias = d.bias;
+    a.logits = d.logits;
+    a.logits_out = d.logits_out;
+    a.idx = d.idx;
+    a.wts = d.wts;
+    a.routed = d.routed;
+    a.routed_stride = d.routed_stride;
+    a.shared_gu = d.shared_gu;
+    a.shared_down = d.shared_down;
+    a.act = d.act;
+    a.shared_out = d.shared_out;
+    a.y = d.y;
+    a.residual = d.residual;
+    a.hidden = hidden;
+    a.hidden_p = d.hidden_p;
+    a.experts = d.policy.experts;
+    a.top_k = top_k;
+    a.inter_p = inter_p;
+    a.shared_inter_p = d.shared_inter_p;
+    a.has_shared = 1;
+    a.policy = d.policy;
+    static_assert(2 * kSetWords == kDecodeCounterWords, "decode scratch layout");
+    f.sync = d.sync;
+    f.approx = reinterpret_cast<float*>(d.sync + kDecodeApproxWord);
+    f.spec = reinterpret_cast<int32_t*>(d.sync + kDecodeSpecWord);
+    f.mask = d.sync + kDecodeMaskWord;
+    f.parity = d.parity & 1;
+    f.perturb = d.perturb;
+    f.n_router = a.experts / kRouterExperts;
+    f.n_shared_gu = a.shared_inter_p / kItemRows;
+    f.n_shared_down = hidden / kDownItemRows;
+    f.n_routed = top_k * (inter_p / kItemRows);
+    const int n_down = hidden / kFusedRows;
+    const dim3 grid(static_cast<unsigned>(f.n_router + f.n_shared_gu + f.n_shared_down + f.n_routed + n_down));
+    const size_t router_lds = sizeof(float) * static_cast<size_t>(hidden) * kRouterExperts;
+    const size_t down_lds = sizeof(float) * static_cast<size_t>(top_k) * inter_p;
+    const size_t lds = router_lds > down_lds ? router_lds : down_lds;
+    if (fused_shape(hidden, top_k, inter_p, d.shared_inter_p) == 0) {
+        hipLaunchKernelGGL((decode_fused_kernel<4, 6, 6, 3>), grid, dim3(kThreads), lds, s, f);
+    } else {
+        hipLaunchKernelGGL((decode_fused_kernel<1, 1, 2, 1>), grid, dim3(kThreads), lds, s, f);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lm

@@ -9,117 +9,23 @@
 // so neither the products nor the additions are fused.  The router gate is
 // stored transposed ([H, E]) so the 64 lanes read one 256-byte row per step;
 // the token's activations are wave-uniform scalar loads.
-#include "lm_internal.h"
+#include "lm_select.h"
 
 namespace lm {
 namespace {
 
 constexpr int kWaves = 4;
 
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint64_t other = __shfl_xor(v, o);
-        v = other > v ? other : v;
-    }
-    return v;
-}
-
-__device__ inline float lane_value(float v, int e) {
-    return bits_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(float_bits(v)), e)));
-}
-
-// MoeRouter::select for one token whose logit for expert `lane` is `logit`.
-// Values are broadcast with v_readlane so the sequential reductions LiteMind
-// performs (max, left-to-right sum) run on uniform registers without LDS
-// round trips; the top-k order is found by counting, in every lane, how many
-// keys beat its own.
+// Selects for token t and writes its experts and weights in rank order.
 __device__ void route_token(float logit, bool valid, int lane, int64_t t, const RouterArgs& a) {
-    const int E = a.experts;
-    // softmax (src/Gemm.cpp:209-223): max (std::max_element keeps the first of
-    // equal values; only the value matters), exp(v - max), left-to-right sum.
-    float maximum = lane_value(logit, 0);
-#pragma unroll
-    for (int e = 1; e < kMaxExperts; ++e) {
-        if (e < E) {
-            const float v = lane_value(logit, e);
-            maximum = maximum < v ? v : maximum;
-        }
-    }
-    const float s = valid ? expf_ref(logit - maximum) : 0.0f;
-    float total = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kMaxExperts; ++e) {
-        if (e < E) {
-            total = total + lane_value(s, e);
-        }
-    }
-    const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
-    const float score = s * inverse;
-
-    // Group-limited mask (src/MoeRouter.cpp:67-84), with the constructor's
-    // fallback to greedy when the groups do not divide the experts (:46-51).
-    bool allowed = true;
-    if (a.group_limited && a.n_group > 1 && E % a.n_group == 0) {
-        const int per_group = E / a.n_group;
-        const int my_group = lane / per_group;
-        // Lane j < n_group computes the maximum score of group j.
-        float gmax = -__builtin_inff();
-        for (int q = 0; q < per_group; ++q) {
-            const int src = (lane < a.n_group ? lane : 0) * per_group + q;
-            const float v = __shfl(score, src);
-            gmax = v > gmax ? v : gmax;
-        }
-        // top_k_indices over the group scores (no mask): higher score, then lower index.
-        const int take = a.topk_group < a.n_group ? a.topk_group : a.n_group;
-        uint64_t gkey = lane < a.n_group
-                            ? ((static_cast<uint64_t>(float_bits(gmax)) << 8) | static_cast<uint64_t>(255 - lane))
-                            : 0;
-        uint64_t chosen_groups = 0;  // n_group <= 64
-        for (int r = 0; r < take; ++r) {
-            const uint64_t best = wave_max_u64(gkey);
-            const int gsel = 255 - static_cast<int>(best & 255u);
-            if (lane == gsel) {
-                gkey = 0;
-            }
-            chosen_groups |= 1ull << gsel;
-        }
-        allowed = ((chosen_groups >> my_group) & 1u) != 0;
-    }
-
-    // top_k_indices (src/MoeRouter.cpp:14-34): allowed first, then score
-    // descending, then index ascending.  Scores are non-negative, so their bit
-    // patterns order like the values; keys are unique through the index.
-    const uint32_t key_hi = valid ? ((allowed ? 0x80000000u : 0u) | (float_bits(score) >> 1)) : 0u;
-    const uint32_t key_lo = valid ? ((float_bits(score) << 31) | static_cast<uint32_t>(255 - lane)) : 0u;
-    int rank = 0;
-#pragma unroll
-    for (int e = 0; e < kMaxExperts; ++e) {
-        if (e < E) {
-            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_hi), e));
-            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_lo), e));
-            rank += (hi > key_hi || (hi == key_hi && lo > key_lo)) ? 1 : 0;
-        }
-    }
-    const int K = a.top_k < E ? a.top_k : E;
-    // Weights in rank order; the selected sum runs left to right as in :91-94.
-    float selected_sum = 0.0f;
-    for (int r = 0; r < K; ++r) {
-        const uint64_t who = __ballot(valid && rank == r);
-        const int src = static_cast<int>(__builtin_ctzll(who));
-        selected_sum = selected_sum + lane_value(score, src);
-    }
-    float my_w = score;
-    // Normalise XOR scale (src/MoeRouter.cpp:96-106).
-    if (a.top_k > 1 && a.normalize) {
-        const float denominator = selected_sum + 1e-20f;
-        my_w = my_w / denominator;
-    } else if (a.scale != 1.0f) {
-        my_w = my_w * a.scale;
-    }
+    const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
+    int rank;
+    float weight;
+    select_token(logit, valid, lane, p, rank, weight);
+    const int K = a.top_k < a.experts ? a.top_k : a.experts;
     if (valid && rank < K) {
         a.idx[t * a.top_k + rank] = lane;
-        a.wts[t * a.top_k + rank] = my_w;
+        a.wts[t * a.top_k + rank] = weight;
     }
 }
 

@@ -59,7 +59,7 @@ struct Layer {
     bool allocated = false;
     bool dense = false;
     bool finalized = false;
-    float* router_t = nullptr;         // [H, E]
+    float* router_t = nullptr;         // [H, E], then [E/4][H][4]
     float* norm = nullptr;             // [H]
     void* slab = nullptr;              // all FFN matrices of the layer (bf16 then fp16 shadow)
     size_t slab_bytes = 0;
@@ -87,6 +87,7 @@ struct Workspace {
     float* ffn = nullptr;         // stack / dense: FFN output
     int32_t* zero = nullptr;      // a device int holding 0 (dense layers have no routed experts)
     float* logit_scratch = nullptr;  // [E] single-token router hand-off
+    uint32_t* decode_sync = nullptr;  // single-launch decode counters (zeroed once) + error word
     uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
 };
 
@@ -114,6 +115,9 @@ struct lm_context {
         size_t bytes;
     };
     std::unordered_map<const void*, Cached> resident_ptrs;
+    int32_t decode_parity = 0;   // alternates between single-launch decodes
+    int32_t decode_perturb = 0;  // testing: force the speculative selection to disagree
+    bool decode_pending = false; // a single-launch decode ran since the last error check
     void* gemm_w = nullptr;      // per-call upload of a matrix that is not resident
     size_t gemm_w_cap = 0;
     float* gemm_x = nullptr;     // per-call scratch: input vector / first operand
@@ -407,6 +411,57 @@ bool want_mfma(int32_t path, int64_t tokens) {
     return path == LM_PATH_MFMA || (path == LM_PATH_AUTO && tokens > kMfmaCrossover);
 }
 
+bool decode_eligible(const lm_context* ctx, const Layer& L) {
+    return L.shared_present && lm::decode_supported(ctx->H, ctx->E, ctx->K, ctx->Ip, ctx->Sp);
+}
+
+// One token through the single-launch decode kernel (k_decode.hip).  Routed
+// experts sit back to back in the layer slab, so expert e's FFN is found by
+// offset.  Stage timing sees one launch, attributed to the gate/up stage.
+int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const float* residual, const float* bias,
+                 int32_t* idx, float* wts, float* logits_out) {
+    if (ctx->ws.decode_sync == nullptr) {
+        const size_t bytes = sizeof(uint32_t) * lm::kDecodeSyncWords;
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_sync), bytes));
+        LM_HIP(hipMemsetAsync(ctx->ws.decode_sync, 0, bytes, ctx->stream));
+    }
+    lm::DecodeLaunch d{};
+    d.x = x;
+    d.wq = L.router_t + static_cast<size_t>(ctx->H) * ctx->E;
+    d.bias = bias;
+    d.logits = ctx->ws.logit_scratch;
+    d.logits_out = logits_out;
+    d.idx = idx;
+    d.wts = wts;
+    d.routed = L.experts[0].gu;
+    d.routed_stride = static_cast<int64_t>(L.experts[1].gu - L.experts[0].gu);
+    d.shared_gu = L.shared.gu;
+    d.shared_down = L.shared.down;
+    d.act = static_cast<float*>(ctx->ws.act);
+    d.shared_out = ctx->ws.down_out;
+    d.y = y;
+    d.residual = residual;
+    d.hidden = ctx->H;
+    d.hidden_p = ctx->Hp;
+    d.inter_p = ctx->Ip;
+    d.shared_inter_p = ctx->Sp;
+    d.policy = lm::SelectPolicy{ctx->E, ctx->K, ctx->cfg.norm_topk_prob, ctx->cfg.group_limited, ctx->cfg.n_group,
+                                ctx->cfg.topk_group, ctx->cfg.routed_scaling_factor};
+    d.sync = ctx->ws.decode_sync;
+    d.parity = ctx->decode_parity;
+    d.perturb = ctx->decode_perturb;
+    ctx->decode_parity ^= 1;
+    ctx->decode_pending = true;
+    stage_mark(ctx, 0);
+    stage_mark(ctx, 1);
+    stage_mark(ctx, 2);
+    LM_HIP(lm::launch_decode(d, ctx->stream));
+    stage_mark(ctx, 3);
+    stage_mark(ctx, 4);
+    stage_mark(ctx, 5);
+    return stage_finish(ctx);
+}
+
 int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
               const float* bias, int32_t* idx_out, float* w_out, float* logits_out, int32_t path) {
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
@@ -423,6 +478,10 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     }
     int32_t* idx = idx_out != nullptr ? idx_out : ctx->ws.idx;
     float* wts = w_out != nullptr ? w_out : ctx->ws.wts;
+
+    if (T == 1 && !mfma && decode_eligible(ctx, L)) {
+        return decode_layer(ctx, L, x, y, residual, bias, idx, wts, logits_out);
+    }
 
     lm::RouterArgs ra{};
     ra.x = x;
@@ -660,6 +719,7 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->gemm_b);
     (void)hipFree(ctx->gemm_out);
     (void)hipFree(ctx->d_overflow);
+    (void)hipFree(w.decode_sync);
     if (ctx->staging != nullptr) {
         (void)hipHostFree(ctx->staging);
     }
@@ -681,6 +741,17 @@ int lm_synchronize(lm_context* ctx) {
         return fail(LM_EINVAL, "null context");
     }
     LM_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->decode_pending) {
+        // A bounded wait inside a single-launch decode that ran out reports here.
+        ctx->decode_pending = false;
+        uint32_t error = 0;
+        uint32_t* word = ctx->ws.decode_sync + lm::kDecodeErrorWord;
+        LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
+        if (error != 0) {
+            LM_HIP(hipMemset(word, 0, sizeof error));
+            return fail(LM_EKERNEL, "a single-token decode wait timed out; its outputs are invalid");
+        }
+    }
     return LM_OK;
 }
 
@@ -742,16 +813,20 @@ int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host) {
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
     const size_t n = static_cast<size_t>(ctx->H) * static_cast<size_t>(ctx->E);
     if (L.router_t == nullptr) {
-        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), n * sizeof(float)));
-        ctx->resident += n * sizeof(float);
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), 2 * n * sizeof(float)));
+        ctx->resident += 2 * n * sizeof(float);
     }
-    std::vector<float> t(n);
+    // [H, E] for the batched router, then [E/4][H][4] (four experts' weights of
+    // one row side by side, each slice contiguous) for the single-token router.
+    std::vector<float> t(2 * n, 0.0f);
     for (int e = 0; e < ctx->E; ++e) {
         for (int i = 0; i < ctx->H; ++i) {
-            t[static_cast<size_t>(i) * ctx->E + e] = gate_host[static_cast<size_t>(e) * ctx->H + i];
+            const float v = gate_host[static_cast<size_t>(e) * ctx->H + i];
+            t[static_cast<size_t>(i) * ctx->E + e] = v;
+            t[n + (static_cast<size_t>(e / 4) * ctx->H + i) * 4 + e % 4] = v;
         }
     }
-    LM_HIP(hipMemcpyAsync(L.router_t, t.data(), n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipMemcpyAsync(L.router_t, t.data(), 2 * n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     return LM_OK;
     LM_GUARD_END
@@ -1244,6 +1319,14 @@ int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resid
         return fail(LM_EINVAL, "null argument");
     }
     *out_resident = ctx->resident_ptrs.count(host_ptr) != 0 ? 1 : 0;
+    return LM_OK;
+}
+
+int lm_decode_speculation_test(lm_context* ctx, int32_t mode) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    ctx->decode_perturb = mode != 0 ? 1 : 0;
     return LM_OK;
 }
 

@@ -126,8 +126,51 @@ struct CombineArgs {
     int32_t hidden, top_k, has_shared;
 };
 
+// The routing policy of MoeRouter (src/MoeRouter.cpp:38-52).
+struct SelectPolicy {
+    int32_t experts, top_k;
+    int32_t normalize, group_limited, n_group, topk_group;
+    float scale;
+};
+
+// The single-token MoE block (k_decode.hip).
+struct DecodeLaunch {
+    const float* x;             // [H]
+    const float* wq;            // [E/4][H][4] router gate, four experts per contiguous slice
+    const float* bias;          // [E] or null
+    float* logits;              // [E] scratch
+    float* logits_out;          // [E] or null
+    int32_t* idx;               // [K] out, rank order
+    float* wts;                 // [K] out
+    const uint16_t* routed;     // expert 0's resident FFN (gate/up then down)
+    int64_t routed_stride;      // elements from one expert's FFN to the next
+    const uint16_t* shared_gu;  // shared expert (null: none)
+    const uint16_t* shared_down;
+    float* act;                 // [K * Ip + Sp]
+    float* shared_out;          // [H]
+    float* y;                   // [H]
+    const float* residual;      // [H] or null
+    int32_t hidden, hidden_p, inter_p, shared_inter_p;
+    SelectPolicy policy;
+    uint32_t* sync;             // kDecodeSyncWords words, zeroed once
+    int32_t parity;             // alternates between consecutive launches
+    int32_t perturb;            // testing: the speculative selection disagrees with every rank
+};
+
 // Kernel launchers (implemented in the .hip files).
 hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted);
+// True when the single-token forward has a one-launch kernel for this shape.
+bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p);
+hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s);
+// Single-launch decode scratch, in 32-bit words: two sets of 8 counters x 16
+// slots x 64 B, the error word, approximate logits [64], speculative experts
+// [16] and the mask of ranks the speculation got wrong.
+constexpr int kDecodeCounterWords = 2 * 8 * 16 * 16;
+constexpr int kDecodeErrorWord = kDecodeCounterWords;
+constexpr int kDecodeApproxWord = kDecodeErrorWord + 16;
+constexpr int kDecodeSpecWord = kDecodeApproxWord + kMaxExperts;
+constexpr int kDecodeMaskWord = kDecodeSpecWord + kMaxTopK;
+constexpr int kDecodeSyncWords = kDecodeMaskWord + 16;
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
 hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t s);

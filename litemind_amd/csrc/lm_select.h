@@ -1,0 +1,206 @@
+// lm_select.h -- MoeRouter::select on one wavefront (one lane per expert).
+//
+// Reference: gemm::softmax (src/Gemm.cpp:209-223) and MoeRouter::select /
+// top_k_indices (src/MoeRouter.cpp:14-107).
+#pragma once
+
+#include "lm_internal.h"
+
+namespace lm {
+
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t other = __shfl_xor(v, o);
+        v = other > v ? other : v;
+    }
+    return v;
+}
+
+__device__ inline float lane_value(float v, int e) {
+    return bits_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(float_bits(v)), e)));
+}
+
+// MoeRouter::select for one token whose logit for expert `lane` is `logit`
+// (lanes >= experts pass valid = false).  On return `rank` is the lane's place
+// in the selection (>= top_k when not selected) and `weight` its routing weight.
+// Values are broadcast with v_readlane so the sequential reductions LiteMind
+// performs (max, left-to-right sum) run on uniform registers without LDS
+// round trips; the top-k order is found by counting, in every lane, how many
+// keys beat its own.
+__device__ inline void select_token(float logit, bool valid, int lane, const SelectPolicy& a, int& rank,
+                                    float& weight) {
+    const int E = a.experts;
+    // softmax (src/Gemm.cpp:209-223): max (std::max_element keeps the first of
+    // equal values; only the value matters), exp(v - max), left-to-right sum.
+    float maximum = lane_value(logit, 0);
+#pragma unroll
+    for (int e = 1; e < kMaxExperts; ++e) {
+        if (e < E) {
+            const float v = lane_value(logit, e);
+            maximum = maximum < v ? v : maximum;
+        }
+    }
+    const float s = valid ? expf_ref(logit - maximum) : 0.0f;
+    float total = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) {
+        if (e < E) {
+            total = total + lane_value(s, e);
+        }
+    }
+    const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
+    const float score = s * inverse;
+
+    // Group-limited mask (src/MoeRouter.cpp:67-84), with the constructor's
+    // fallback to greedy when the groups do not divide the experts (:46-51).
+    bool allowed = true;
+    if (a.group_limited && a.n_group > 1 && E % a.n_group == 0) {
+        const int per_group = E / a.n_group;
+        const int my_group = lane / per_group;
+        // Lane j < n_group computes the maximum score of group j.
+        float gmax = -__builtin_inff();
+        for (int q = 0; q < per_group; ++q) {
+            const int src = (lane < a.n_group ? lane : 0) * per_group + q;
+            const float v = __shfl(score, src);
+            gmax = v > gmax ? v : gmax;
+        }
+        // top_k_indices over the group scores (no mask): higher score, then lower index.
+        const int take = a.topk_group < a.n_group ? a.topk_group : a.n_group;
+        uint64_t gkey = lane < a.n_group
+                            ? ((static_cast<uint64_t>(float_bits(gmax)) << 8) | static_cast<uint64_t>(255 - lane))
+                            : 0;
+        uint64_t chosen_groups = 0;  // n_group <= 64
+        for (int r = 0; r < take; ++r) {
+            const uint64_t best = wave_max_u64(gkey);
+            const int gsel = 255 - static_cast<int>(best & 255u);
+            if (lane == gsel) {
+                gkey = 0;
+            }
+            chosen_groups |= 1ull << gsel;
+        }
+        allowed = ((chosen_groups >> my_group) & 1u) != 0;
+    }
+
+    // top_k_indices (src/MoeRouter.cpp:14-34): allowed first, then score
+    // descending, then index ascending.  Scores are non-negative, so their bit
+    // patterns order like the values; keys are unique through the index.
+    const uint32_t key_hi = valid ? ((allowed ? 0x80000000u : 0u) | (float_bits(score) >> 1)) : 0u;
+    const uint32_t key_lo = valid ? ((float_bits(score) << 31) | static_cast<uint32_t>(255 - lane)) : 0u;
+    rank = 0;
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; ++e) {
+        if (e < E) {
+            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_hi), e));
+            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key_lo), e));
+            rank += (hi > key_hi || (hi == key_hi && lo > key_lo)) ? 1 : 0;
+        }
+    }
+    const int K = a.top_k < E ? a.top_k : E;
+    // Weights in rank order; the selected sum runs left to right as in :91-94.
+    float selected_sum = 0.0f;
+    for (int r = 0; r < K; ++r) {
+        const uint64_t who = __ballot(valid && rank == r);
+        const int src = static_cast<int>(__builtin_ctzll(who));
+        selected_sum = selected_sum + lane_value(score, src);
+    }
+    float my_w = score;
+    // Normalise XOR scale (src/MoeRouter.cpp:96-106).
+    if (a.top_k > 1 && a.normalize) {
+        const float denominator = selected_sum + 1e-20f;
+        my_w = my_w / denominator;
+    } else if (a.scale != 1.0f) {
+        my_w = my_w * a.scale;
+    }
+    weight = my_w;
+}
+
+
+// Per-wave LDS scratch of select_token_lds, in floats (16-byte aligned).
+constexpr int kSelectScratch = 64 + 128 + kMaxTopK;
+
+// The same selection as select_token, with the all-to-all steps done through
+// the wave's own LDS scratch instead of v_readlane chains: each lane reads the
+// 64 values with broadcast loads and reduces them in registers.  Identical
+// results (max is exact in any order; the sum runs left to right over experts,
+// invalid lanes adding +0; the rank counts beating keys).  Group-limited
+// routing takes select_token.
+__device__ inline void select_token_lds(float logit, bool valid, int lane, const SelectPolicy& a, float* sh,
+                                        int& rank, float& weight) {
+    if (a.group_limited && a.n_group > 1 && a.experts % a.n_group == 0) {
+        select_token(logit, valid, lane, a, rank, weight);
+        return;
+    }
+    float4* sh4 = reinterpret_cast<float4*>(sh);
+    // max over valid logits (lanes past E repeat expert 0's logit)
+    const float first = lane_value(logit, 0);
+    sh[lane] = valid ? logit : first;
+    __builtin_amdgcn_wave_barrier();
+    float m[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 v = sh4[i];
+        const float a01 = v.x < v.y ? v.y : v.x;
+        const float a23 = v.z < v.w ? v.w : v.z;
+        m[i] = a01 < a23 ? a23 : a01;
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int i = 0; i < w; ++i) {
+            m[i] = m[i] < m[i + w] ? m[i + w] : m[i];
+        }
+    }
+    const float maximum = m[0];
+    const float s = valid ? expf_ref(logit - maximum) : 0.0f;
+    __builtin_amdgcn_wave_barrier();
+    sh[lane] = s;
+    __builtin_amdgcn_wave_barrier();
+    // LiteMind's left-to-right total (src/Gemm.cpp:216-218); +0 for lanes past E.
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 v = sh4[i];
+        total = total + v.x;
+        total = total + v.y;
+        total = total + v.z;
+        total = total + v.w;
+    }
+    const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
+    const float score = s * inverse;
+    // top_k_indices order: score descending, then index ascending (all allowed).
+    const uint64_t key = valid ? ((static_cast<uint64_t>(float_bits(score)) << 8) | static_cast<uint64_t>(255 - lane))
+                               : 0ull;
+    uint64_t* keys = reinterpret_cast<uint64_t*>(sh + 64);
+    keys[lane] = key;
+    __builtin_amdgcn_wave_barrier();
+    int beaten = 0;
+    const ulonglong2* keys2 = reinterpret_cast<const ulonglong2*>(keys);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const ulonglong2 k2 = keys2[i];
+        beaten += k2.x > key ? 1 : 0;
+        beaten += k2.y > key ? 1 : 0;
+    }
+    rank = beaten;
+    const int K = a.top_k < a.experts ? a.top_k : a.experts;
+    float* picked = sh + 192;
+    if (valid && rank < K) {
+        picked[rank] = score;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float selected_sum = 0.0f;
+    for (int r = 0; r < K; ++r) {
+        selected_sum = selected_sum + picked[r];
+    }
+    float my_w = score;
+    if (a.top_k > 1 && a.normalize) {
+        const float denominator = selected_sum + 1e-20f;
+        my_w = my_w / denominator;
+    } else if (a.scale != 1.0f) {
+        my_w = my_w * a.scale;
+    }
+    weight = my_w;
+}
+
+}  // namespace lm
