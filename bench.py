@@ -37,6 +37,11 @@ DOWN_EXPERT_BYTES = 1408 * 2048 * 2         # 5,767,168
 SHARED_BYTES = 3 * 2816 * 2048 * 2          # 34,603,008
 ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over
+# this benchmark, scaled by the counters' readings for a conversion kernel of
+# known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md).
+MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 140_252_864}
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -100,19 +105,22 @@ def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int)
     gpu_ms = ctx.elapsed_ms(start_ev, stop_ev)
     log(f"{workload_name}: {steps} steps wall {wall * 1e3:.3f} ms, events {gpu_ms:.3f} ms")
 
-    # Per-stage durations with HIP events between the stages, in a second timed pass.
-    ctx.stage_timing(True)
-    for i in range(steps):
-        step(i)
-    stages = ctx.stage_times()
-    ctx.stage_timing(False)
+    # Per-stage durations with HIP events between the stages, in a second timed
+    # pass (a single token is one kernel per step: nothing to split).
+    stages = {}
+    if T > 1:
+        ctx.stage_timing(True)
+        for i in range(steps):
+            step(i)
+        stages = ctx.stage_times()
+        ctx.stage_timing(False)
 
     idx_all = didx.download()
     distinct = [len(np.unique(idx_all[l])) for l in range(min(rotate, steps))]
     U = float(np.mean(distinct))
     ctx.close()
     return dict(T=T, wall_s=wall, gpu_ms=gpu_ms, steps=steps, stages=stages, distinct=U, layers=layers, x=x,
-                bias=bias)
+                bias=bias, workload=workload_name)
 
 
 def cpu_baseline(layer, x, bias, budget_s: float, max_tokens: int):
@@ -141,6 +149,16 @@ def cpu_baseline(layer, x, bias, budget_s: float, max_tokens: int):
 def roofline(res: dict, mfma: bool) -> dict:
     """Dominant kernel's achieved rate: algorithmic bytes (or flops) / event-timed duration."""
     alg = algorithmic(res["T"], int(round(res["distinct"])))
+    if res["T"] == 1:
+        # The single-token forward is one kernel (decode_fused_kernel) per step:
+        # its average duration is the event-timed span of the timed steps / steps.
+        dur_us = res["gpu_ms"] * 1e3 / res["steps"]
+        by = alg["layer_bytes"]
+        achieved = by / (dur_us * 1e-6) / 1e9
+        return {"bound": "hbm", "kernel": "decode_fused_kernel", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": MEASURED_TRAFFIC.get((res["workload"], "decode_fused_kernel")),
+                "avg_us": round(dur_us, 2), "algorithmic_bytes": by}
     stages = res["stages"]
     per = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
     dominant = max(("gate_up", "down"), key=lambda k: per[k])
@@ -194,8 +212,9 @@ def main() -> int:
                    "distinct_experts_per_step": res["distinct"]},
         "roofline": roofline(res, mfma_main),
         "layer_gpu_us": round(res["gpu_ms"] * 1e3 / res["steps"], 2),
-        "stage_us": {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res["stages"].items()},
     }
+    if res["stages"]:
+        line["stage_us"] = {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res["stages"].items()}
     alg = algorithmic(T, int(round(res["distinct"])))
     line["layer_hbm_frac"] = round(alg["layer_bytes"] / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
 
