@@ -26,8 +26,8 @@ BUILD = os.path.join(HERE, "_build")
 REFERENCE = os.environ.get("LITEMIND_REFERENCE", "/root/reference")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-HIP_SOURCES = ["k_router.hip", "k_permute.hip", "k_gemv.hip", "k_decode.hip", "k_mfma.hip", "k_misc.hip",
-               "lm_capi.hip"]
+HIP_SOURCES = ["k_router.hip", "k_permute.hip", "k_gemv.hip", "k_decode.hip", "k_mfma.hip",
+               "k_misc.hip", "lm_capi.hip"]
 # -ffp-contract=off: every fused multiply-add in the kernels is written out
 # explicitly; the router must not fuse at all to match LiteMind bit for bit.
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 generated from float code.

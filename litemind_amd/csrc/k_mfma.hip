@@ -12,9 +12,22 @@
 //            groups, so a wave's two 32-wide column blocks are the gate and the
 //            up of the same outputs and the epilogue pairs them in registers.
 //   down:    down_out[slot, h] = act16[slot] . Wd[h] (fp32 out, combined later).
-// Block tile 128 x 128, K step 64, 4 waves of 64 x 64 (2 x 2 MFMA blocks).
-// Tiles of one weight column block are consecutive (M fastest) and tile ids
-// are remapped so consecutive tiles run on the same XCD and share its L2.
+//
+// Every operand is stored in panel layout (32-column panels of [rows, 32]), so
+// the K slice of a stage is one contiguous block per operand: 64 bytes per row,
+// consecutive rows adjacent.  Loads go from global memory straight into LDS
+// with global_load_lds_dwordx4 (no staging registers); each wave instruction
+// fills 1 KB of LDS, 16 rows of 64 bytes, lane l writing bytes [16 l, 16 l + 16).
+// The lane chooses which 16-byte chunk of its row it loads, so rows are stored
+// in LDS with their chunks permuted (row_swizzle), which keeps the MFMA fragment
+// reads free of bank conflicts.
+//
+// Per workgroup: WAVES waves of 64 x 128 (2 x 4 MFMA blocks of 32 x 32, 128
+// accumulator registers) over a BM x 256 tile, BM = 32 WAVES, K step 32, and a
+// STAGES-deep pipeline: while stage k is multiplied, stages k + 1 .. k +
+// STAGES - 1 are in flight, each in its own LDS array so the compiler can track
+// the asynchronous writes per buffer.  Rows past the end of a group (tokens) or
+// of a matrix (weight rows) load a clamped row and are never stored.
 #include "lm_internal.h"
 
 namespace lm {
@@ -22,14 +35,29 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(1))) const void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kThreads = 256;
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int BK = 64;
-constexpr int kLdsRow = BK + 8;          // halves per LDS row (16 B padding)
-constexpr int kTileHalves = BM * kLdsRow;
+constexpr int BN = 256;
+constexpr int BK = kPanel;                   // halves: 64-byte rows, 4 chunks of 16 B
+constexpr int kRowBytes = BK * 2;
+constexpr int kBBytes = BN * kRowBytes;      // 16 KB
 constexpr int kXcds = 8;
+
+template <int WAVES, int STAGES>
+struct Shape {
+    static constexpr int kThreads = 64 * WAVES;
+    static constexpr int BM = 32 * WAVES;
+    static constexpr int kABytes = BM * kRowBytes;
+    static constexpr int kALoads = kABytes / 1024 / WAVES;  // wave instructions per stage
+    static constexpr int kBLoads = kBBytes / 1024 / WAVES;
+    static constexpr int kLoadsPerStage = kALoads + kBLoads;
+};
+
+// Tile configuration: 4 waves of 64 x 128 (128 x 256 tiles) with three stages,
+// two workgroups per CU.
+constexpr int kWaves = 4;
+constexpr int kStages = 3;
 
 enum Mode { kGateUp = 0, kDown = 1 };
 
@@ -40,9 +68,14 @@ struct TileInfo {
     int64_t slot0;
 };
 
-// Finds the tile's group from per-group tile counts (routed experts in expert
-// order, then the shared expert).  Wave 0 scans; the result goes through LDS.
-__device__ bool decode_tile(const ExpertArgs& a, int64_t tile, int nt_routed, int nt_shared, TileInfo& ti) {
+// Maps workgroup `blk` to a tile and finds the tile's group from per-group tile
+// counts (routed experts in expert order, then the shared expert); M tiles of
+// one column block are consecutive.  Workgroup b runs on XCD b % 8: XCD x gets
+// the x-th of eight contiguous, equal (within one) ranges of the tiles that
+// exist, so the M tiles of a column block share one L2 and no XCD is left with
+// only the empty tail of the grid.
+__device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_routed, int nt_shared,
+                            TileInfo& ti) {
     __shared__ int s_info[4];
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
@@ -60,6 +93,12 @@ __device__ bool decode_tile(const ExpertArgs& a, int64_t tile, int nt_routed, in
         }
         const int excl = incl - tiles;
         const int routed_total = __shfl(incl, 63);
+        const int mts_s = a.has_shared ? static_cast<int>((a.tokens + BM - 1) / BM) : 0;
+        const int64_t total = routed_total + static_cast<int64_t>(mts_s) * nt_shared;
+        const int64_t per = total / kXcds, extra = total % kXcds;
+        const int64_t xcd = blk % kXcds, idx = blk / kXcds;
+        const int64_t count = per + (xcd < extra ? 1 : 0);
+        const int64_t tile = idx < count ? xcd * per + (xcd < extra ? xcd : extra) + idx : total;
         int found = -1, local = 0, found_mts = 0;
         if (tile < routed_total) {
             const uint64_t hit = __ballot(tile >= excl && tile < incl && tiles > 0);
@@ -67,14 +106,10 @@ __device__ bool decode_tile(const ExpertArgs& a, int64_t tile, int nt_routed, in
             found = gl;
             local = static_cast<int>(tile) - __shfl(excl, gl);
             found_mts = __shfl(mts, gl);
-        } else if (a.has_shared) {
-            const int mts_s = static_cast<int>((a.tokens + BM - 1) / BM);
-            const int64_t l = tile - routed_total;
-            if (l < static_cast<int64_t>(mts_s) * nt_shared) {
-                found = a.experts;
-                local = static_cast<int>(l);
-                found_mts = mts_s;
-            }
+        } else if (tile < total) {
+            found = a.experts;
+            local = static_cast<int>(tile - routed_total);
+            found_mts = mts_s;
         }
         if (lane == 0) {
             s_info[0] = found;
@@ -99,136 +134,183 @@ __device__ bool decode_tile(const ExpertArgs& a, int64_t tile, int nt_routed, in
     return true;
 }
 
-// 16-byte load through the global address space (operand pointers are read
-// from tables, which would otherwise compile to flat loads).
-__device__ inline uint4 load16(const void* p) {
-    const u32x4 v = *(global_u32x4*)(p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 __device__ inline float silu_fast(float g, float u) {
     // The fp16-operand path is checked against a tolerance; the hardware exp
     // and reciprocal are accurate to a few ulp, far below the fp16 rounding.
     return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads) void mfma_kernel(ExpertArgs a, int64_t grid_tiles) {
-    __shared__ _Float16 lds[2][2][kTileHalves];  // [buffer][A, B][row * kLdsRow + k]
+// Chunk permutation of row r (row bits 1..3 only).  A ds_read_b128 serves 16
+// lanes per cycle from 64 banks: lanes 0..15 read rows r0..r0+15 (r0 a
+// multiple of 16) at one logical chunk, and the rows that share a bank phase
+// (r mod 4) get four different chunk positions; the same holds for 8-lane
+// groups over 32 banks.
+__device__ inline int row_swizzle(int r) { return ((r >> 2) & 3) ^ (r & 2); }
+// LDS byte offset of the 16-byte chunk c of row r.
+__device__ inline int chunk_offset(int r, int c) { return r * kRowBytes + ((c ^ row_swizzle(r)) << 4); }
+
+template <int MODE, int WAVES, int STAGES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_grouped_kernel(
+    ExpertArgs a) {
+    using S = Shape<WAVES, STAGES>;
+    constexpr int BM = S::BM;
+    // One LDS array per stage (A tile, then B tile): the compiler tracks the
+    // asynchronous LDS writes per array and only a few arrays individually.
+    constexpr int kA = S::kABytes;
+    constexpr int kStage = kA + kBBytes;
+    constexpr int kStage3 = STAGES > 3 ? kStage : 16;
+    __shared__ __attribute__((aligned(1024))) char s0[kStage], s1[kStage], s2[kStage], s3[kStage3];
+    char* const As[4] = {s0, s1, s2, s3};
+    char* const Bs[4] = {s0 + kA, s1 + kA, s2 + kA, s3 + kA};
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    // XCD-aware remap: workgroup b runs on XCD b % 8; give each XCD a
-    // contiguous range of tiles (grid_tiles is a multiple of 8).
-    const int64_t b = blockIdx.x;
-    const int64_t tile = (b % kXcds) * (grid_tiles / kXcds) + b / kXcds;
-
     const int inter_p = a.inter_p;
-    const int nt_routed = MODE == kGateUp ? 2 * inter_p / BN : (a.hidden + BN - 1) / BN;
-    const int nt_shared = MODE == kGateUp ? 2 * a.shared_inter_p / BN : (a.hidden + BN - 1) / BN;
+    const int n_routed = MODE == kGateUp ? 2 * inter_p : a.hidden;  // weight rows
+    const int n_shared = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
     TileInfo ti;
-    if (!decode_tile(a, tile, nt_routed, nt_shared, ti)) {
+    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, ti)) {
         return;
     }
     const bool shared = ti.g >= a.experts;
     const int width_p = shared ? a.shared_inter_p : inter_p;
+    const int n_rows = shared ? n_shared : n_routed;
     const int K = MODE == kGateUp ? a.hidden_p : width_p;
-    const _Float16* act_base =
-        a.act16 + (shared ? a.tokens * a.top_k * static_cast<int64_t>(inter_p) : ti.slot0 * inter_p);
+    // act16: routed panels [T*K, Ip], then the shared expert's panels [T, Sp].
+    const int64_t TK = a.tokens * a.top_k;
+    const int64_t act_rows = shared ? a.tokens : TK;
+    const int64_t act_slot0 = shared ? 0 : ti.slot0;
+    _Float16* const act_base = a.act16 + (shared ? TK * static_cast<int64_t>(inter_p) : 0);
 
-    // Global -> register staging: each thread moves 4 x 16 B of A and of B per K step.
-    // Chunk c = tid + 256 q (q = 0..3): row c / 8, 16-byte column c % 8.
-    const _Float16* arow[4];
-    const _Float16* brow[4];
+    // Rows this lane loads: A block q covers rows 16 (WAVES q + wave) + lane / 4,
+    // B block q likewise over the 256 B rows.  The chunk follows the permutation.
+    const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);  // the lane's row is 16 k + lane / 4
+    const _Float16* pa[S::kALoads];
+    const _Float16* pb[S::kBLoads];
+    // Halves between consecutive K panels of each operand.
+    const int64_t a_step = (MODE == kGateUp ? a.tokens : act_rows) * kPanel;
+    const int64_t b_step = static_cast<int64_t>(n_rows) * kPanel;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int c = tid + q * kThreads;
-        const int r = c >> 3;
+    for (int q = 0; q < S::kALoads; ++q) {
+        const int r = 16 * (WAVES * q + wave) + (lane >> 2);
         int m = ti.mt * BM + r;
         m = m < ti.rows ? m : ti.rows - 1;  // padding rows repeat the last row; never stored
         if (MODE == kGateUp) {
             const int64_t token = shared ? m : a.rb.perm[ti.slot0 + m] / a.top_k;
-            arow[q] = a.x16 + token * a.hidden_p + (c & 7) * 8;
-            brow[q] = a.groups.gu_h[ti.g] + static_cast<int64_t>(ti.nt * BN + r) * a.hidden_p + (c & 7) * 8;
+            pa[q] = a.x16 + token * kPanel + chunk * 8;
         } else {
-            // Output rows past H (hidden not a multiple of 128) repeat row H - 1; never stored.
-            const int h = ti.nt * BN + r < a.hidden ? ti.nt * BN + r : a.hidden - 1;
-            arow[q] = act_base + static_cast<int64_t>(m) * width_p + (c & 7) * 8;
-            brow[q] = a.groups.down_h[ti.g] + static_cast<int64_t>(h) * width_p + (c & 7) * 8;
+            pa[q] = act_base + (act_slot0 + m) * kPanel + chunk * 8;
         }
     }
-    // Staging registers, written out per chunk so they stay in registers.
-    uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-    const int off0 = ((tid + 0 * kThreads) >> 3) * kLdsRow + (tid & 7) * 8;
-    const int off1 = ((tid + 1 * kThreads) >> 3) * kLdsRow + (tid & 7) * 8;
-    const int off2 = ((tid + 2 * kThreads) >> 3) * kLdsRow + (tid & 7) * 8;
-    const int off3 = ((tid + 3 * kThreads) >> 3) * kLdsRow + (tid & 7) * 8;
-#define LM_MFMA_FETCH(k0)               \
-    ra0 = load16(arow[0] + (k0));       \
-    rb0 = load16(brow[0] + (k0));       \
-    ra1 = load16(arow[1] + (k0));       \
-    rb1 = load16(brow[1] + (k0));       \
-    ra2 = load16(arow[2] + (k0));       \
-    rb2 = load16(brow[2] + (k0));       \
-    ra3 = load16(arow[3] + (k0));       \
-    rb3 = load16(brow[3] + (k0));
-#define LM_MFMA_STORE(buf)                                        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][0][off0]) = ra0;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][1][off0]) = rb0;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][0][off1]) = ra1;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][1][off1]) = rb1;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][0][off2]) = ra2;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][1][off2]) = rb2;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][0][off3]) = ra3;        \
-    *reinterpret_cast<uint4*>(&lds[(buf)][1][off3]) = rb3;
+    const _Float16* const wbase = MODE == kGateUp ? a.groups.gu_h[ti.g] : a.groups.down_h[ti.g];
+#pragma unroll
+    for (int q = 0; q < S::kBLoads; ++q) {
+        const int r = 16 * (WAVES * q + wave) + (lane >> 2);
+        int row = ti.nt * BN + r;
+        row = row < n_rows ? row : n_rows - 1;  // rows past the matrix: never stored
+        pb[q] = wbase + static_cast<int64_t>(row) * kPanel + chunk * 8;
+    }
 
-    floatx16 acc[2][2];
+    auto issue = [&](int ks, char* as, char* bs) {
+#pragma unroll
+        for (int q = 0; q < S::kALoads; ++q) {
+            __builtin_amdgcn_global_load_lds((global_void*)(pa[q] + ks * a_step),
+                                             (lds_void*)(as + (WAVES * q + wave) * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < S::kBLoads; ++q) {
+            __builtin_amdgcn_global_load_lds((global_void*)(pb[q] + ks * b_step),
+                                             (lds_void*)(bs + (WAVES * q + wave) * 1024), 16, 0, 0);
+        }
+    };
+
+    floatx16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 4; ++j) {
             acc[i][j] = floatx16{};
         }
     }
-    const int nk = K / BK;
-    LM_MFMA_FETCH(0)
-    LM_MFMA_STORE(0)
-    lds_barrier();
-    for (int ks = 0; ks < nk; ++ks) {
-        const int buf = ks & 1;
-        if (ks + 1 < nk) {
-            LM_MFMA_FETCH((ks + 1) * BK)
-        }
+    auto compute = [&](const char* as, const char* bs) {
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
-            half8 af[2], bf[2];
+            const int c = 2 * kk + (lane >> 5);
+            half8 af[2], bf[4];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + (lane & 31);
-                af[i] = *reinterpret_cast<const half8*>(&lds[buf][0][row * kLdsRow + kk * 16 + (lane >> 5) * 8]);
+                const int r = wm * 64 + i * 32 + (lane & 31);
+                af[i] = *reinterpret_cast<const half8*>(as + chunk_offset(r, c));
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int row = wn * 64 + j * 32 + (lane & 31);
-                bf[j] = *reinterpret_cast<const half8*>(&lds[buf][1][row * kLdsRow + kk * 16 + (lane >> 5) * 8]);
+            for (int j = 0; j < 4; ++j) {
+                const int r = wn * 128 + j * 32 + (lane & 31);
+                bf[j] = *reinterpret_cast<const half8*>(bs + chunk_offset(r, c));
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
                 }
             }
         }
-        if (ks + 1 < nk) {
-            LM_MFMA_STORE(buf ^ 1)
+    };
+    // Stage ks lives in buffer ks % STAGES and was issued STAGES - 1 steps
+    // earlier.  Before multiplying it, wait for this wave's loads of it (the
+    // loads of the stages after it may remain in flight) and for its own LDS
+    // reads of the previous step; the barrier then makes every wave's part
+    // visible and guarantees that buffer (ks - 1) % STAGES, read in the previous
+    // step, is free for stage ks + STAGES - 1.
+    constexpr int L = S::kLoadsPerStage;
+    const int nk = K / BK;
+    auto step_full = [&](int ks, char* as, char* bs, char* an, char* bn) {
+        __builtin_amdgcn_s_waitcnt(0x0070 | ((STAGES - 2) * L));  // vmcnt((STAGES - 2) L) lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        issue(ks + STAGES - 1, an, bn);
+        compute(as, bs);
+    };
+    // The last steps: fewer stages remain in flight behind stage ks.
+    auto step_tail = [&](int ks, char* as, char* bs, char* an, char* bn) {
+        const int later = nk - 1 - ks;
+        if (STAGES > 3 && later >= 2) {
+            __builtin_amdgcn_s_waitcnt(0x0070 | (2 * L));
+        } else if (later >= 1) {
+            __builtin_amdgcn_s_waitcnt(0x0070 | L);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0070);
         }
-        lds_barrier();
+        __builtin_amdgcn_s_barrier();
+        if (ks + STAGES - 1 < nk) {
+            issue(ks + STAGES - 1, an, bn);
+        }
+        compute(as, bs);
+    };
+    // The prologue always issues STAGES - 1 stages (a stage past the end
+    // reloads the last one into a buffer that is never read), so every path
+    // into the main loop has the same loads in flight and the compiler's own
+    // wait tracking needs no extra vmcnt(0).
+#pragma unroll
+    for (int d = 0; d < STAGES - 1; ++d) {
+        issue(d < nk ? d : nk - 1, As[d], Bs[d]);
     }
-#undef LM_MFMA_FETCH
-#undef LM_MFMA_STORE
+    // Main loop: every step has STAGES - 2 stages behind it and issues one.
+    int ks = 0;
+    for (; ks + 2 * STAGES - 1 <= nk; ks += STAGES) {
+#pragma unroll
+        for (int j = 0; j < STAGES; ++j) {
+            step_full(ks + j, As[j], Bs[j], As[(j + STAGES - 1) % STAGES], Bs[(j + STAGES - 1) % STAGES]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * STAGES - 1; ++j) {
+        if (ks + j < nk) {
+            step_tail(ks + j, As[j % STAGES], Bs[j % STAGES], As[(j + STAGES - 1) % STAGES],
+                      Bs[(j + STAGES - 1) % STAGES]);
+        }
+    }
 
     // Epilogue.  Lane l holds column n = l % 32 of each 32 x 32 block, rows
     // m = 8 (r / 4) + 4 (l / 32) + r % 4 for registers r = 0..15.
@@ -243,15 +325,19 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(ExpertArgs a, int64_t gr
                 continue;
             }
             if (MODE == kGateUp) {
-                // Interleaved columns: block j = 0 is gate, j = 1 the matching up.
-                const int jcol = (ti.nt * BN) / 2 + wn * 32 + n;
-                const float h = silu_fast(acc[i][0][r], acc[i][1][r]);
-                a.act16[(shared ? a.tokens * a.top_k * static_cast<int64_t>(inter_p) : ti.slot0 * inter_p) +
-                        static_cast<int64_t>(m) * width_p + jcol] = static_cast<_Float16>(h);
+                // Blocks (0, 1) and (2, 3) are the gate and up of two 32-column groups.
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const int jcol = (ti.nt * BN) / 2 + wn * 64 + p * 32 + n;
+                    if (jcol < width_p) {
+                        const float h = silu_fast(acc[i][2 * p][r], acc[i][2 * p + 1][r]);
+                        act_base[panel_index(act_slot0 + m, jcol, act_rows)] = static_cast<_Float16>(h);
+                    }
+                }
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int h = ti.nt * BN + wn * 64 + j * 32 + n;
+                for (int j = 0; j < 4; ++j) {
+                    const int h = ti.nt * BN + wn * 128 + j * 32 + n;
                     if (h < a.hidden) {
                         a.down_out[(ti.slot0 + m) * a.hidden + h] = acc[i][j][r];
                     }
@@ -261,7 +347,9 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(ExpertArgs a, int64_t gr
     }
 }
 
-int64_t tile_bound(const ExpertArgs& a, int nt_routed, int nt_shared) {
+// Upper bound of the tile count (the kernel maps workgroups onto the tiles that
+// exist and the rest return at once), rounded to whole XCD rounds.
+int64_t tile_bound(const ExpertArgs& a, int BM, int nt_routed, int nt_shared) {
     const int64_t TK = a.tokens * a.top_k;
     const int64_t groups = a.experts < TK ? a.experts : TK;
     int64_t tiles = ((TK + BM - 1) / BM + groups) * nt_routed;
@@ -271,31 +359,27 @@ int64_t tile_bound(const ExpertArgs& a, int nt_routed, int nt_shared) {
     return (tiles + kXcds - 1) / kXcds * kXcds;
 }
 
+template <int MODE>
+hipError_t launch(const ExpertArgs& a, hipStream_t s) {
+    if (a.tokens <= 0) {
+        return hipSuccess;
+    }
+    if (a.hidden_p % BK != 0 || a.inter_p % BK != 0 || (a.has_shared && a.shared_inter_p % BK != 0)) {
+        return hipErrorInvalidValue;
+    }
+    using S = Shape<kWaves, kStages>;
+    const int nr = MODE == kGateUp ? 2 * a.inter_p : a.hidden;
+    const int ns = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
+    const int64_t grid = tile_bound(a, S::BM, (nr + BN - 1) / BN, (ns + BN - 1) / BN);
+    hipLaunchKernelGGL((mfma_grouped_kernel<MODE, kWaves, kStages>), dim3(static_cast<unsigned>(grid)),
+                       dim3(S::kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_mfma_gateup(const ExpertArgs& a, int64_t, hipStream_t s) {
-    if (a.tokens <= 0) {
-        return hipSuccess;
-    }
-    if (a.hidden_p % BK != 0 || (2 * a.inter_p) % BN != 0 || (2 * a.shared_inter_p) % BN != 0) {
-        return hipErrorInvalidValue;
-    }
-    const int64_t grid = tile_bound(a, 2 * a.inter_p / BN, 2 * a.shared_inter_p / BN);
-    hipLaunchKernelGGL((mfma_kernel<kGateUp>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, a, grid);
-    return hipGetLastError();
-}
+hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s) { return launch<kGateUp>(a, s); }
 
-hipError_t launch_mfma_down(const ExpertArgs& a, int64_t, hipStream_t s) {
-    if (a.tokens <= 0) {
-        return hipSuccess;
-    }
-    if (a.inter_p % BK != 0 || a.shared_inter_p % BK != 0) {
-        return hipErrorInvalidValue;
-    }
-    const int nt = (a.hidden + BN - 1) / BN;
-    const int64_t grid = tile_bound(a, nt, nt);
-    hipLaunchKernelGGL((mfma_kernel<kDown>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, a, grid);
-    return hipGetLastError();
-}
+hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s) { return launch<kDown>(a, s); }
 
 }  // namespace lm

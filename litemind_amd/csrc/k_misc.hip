@@ -44,19 +44,26 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     *reinterpret_cast<float4*>(a.y + t * a.hidden + c) = acc;
 }
 
-// BF16 -> fp16 re-encoding of resident weights for the MFMA path.  Exact for
-// every BF16 value of magnitude in [2^-17, 65504]; smaller ones round to fp16
-// subnormals (absolute error <= 2^-25), larger ones would overflow and are
-// counted so the host can refuse the layer.
-__global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t* __restrict__ src, _Float16* __restrict__ dst,
-                                                          int64_t n, int* overflow) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+// BF16 -> fp16 re-encoding of resident weights for the MFMA path, written in
+// panel layout.  Exact for every BF16 value of magnitude in [2^-17, 65504];
+// smaller ones round to fp16 subnormals (absolute error <= 2^-25), larger ones
+// would overflow and are counted so the host can refuse the layer.  Thread i
+// produces destination element i (coalesced writes; reads within one panel
+// row are contiguous).
+__global__ __launch_bounds__(256) void bf16_to_f16_panels_kernel(const uint16_t* __restrict__ src,
+                                                                 _Float16* __restrict__ dst, int64_t rows,
+                                                                 int64_t cols, int* overflow) {
+    const int64_t n = rows * cols;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     int bad = 0;
-    for (int64_t k = i; k < n; k += stride) {
-        const float v = widen_bf16(src[k]);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t panel = i / (rows * kPanel);
+        const int64_t rem = i - panel * rows * kPanel;
+        const int64_t r = rem / kPanel;
+        const int64_t c = panel * kPanel + (rem - r * kPanel);
+        const float v = widen_bf16(src[r * cols + c]);
         bad += (v > 65504.0f || v < -65504.0f) ? 1 : 0;
-        dst[k] = static_cast<_Float16>(v);
+        dst[i] = static_cast<_Float16>(v);
     }
     if (bad != 0) {
         atomicAdd(overflow, bad);
@@ -147,15 +154,18 @@ __global__ __launch_bounds__(256) void gemv_plain_kernel(const uint16_t* __restr
     out[row] = accumulate ? __builtin_fmaf(scale, total, out[row]) : total;
 }
 
-// x16[t, c] = fp16(x[t, c]) for c < cols, 0 for cols <= c < cols_p.
+// x16 (panel layout, rows x cols_p) = fp16(x[r, c]) for c < cols, 0 for
+// cols <= c < cols_p.  Thread i produces destination element i.
 __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restrict__ x, _Float16* __restrict__ x16,
                                                           int64_t rows, int32_t cols, int32_t cols_p) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= rows * cols_p) {
         return;
     }
-    const int64_t r = i / cols_p;
-    const int c = static_cast<int>(i - r * cols_p);
+    const int64_t panel = i / (rows * kPanel);
+    const int64_t rem = i - panel * rows * kPanel;
+    const int64_t r = rem / kPanel;
+    const int64_t c = panel * kPanel + (rem - r * kPanel);
     x16[i] = c < cols ? static_cast<_Float16>(x[r * cols + c]) : static_cast<_Float16>(0.0f);
 }
 
@@ -275,6 +285,9 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
     if (n <= 0) {
         return hipSuccess;
     }
+    if (cols_p % kPanel != 0) {
+        return hipErrorInvalidValue;
+    }
     hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, x16,
                        rows, cols, cols_p);
     return hipGetLastError();
@@ -289,16 +302,21 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_bf16_to_f16(const uint16_t* src, _Float16* dst, int64_t n, int* overflow, hipStream_t s) {
+hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t rows, int64_t cols, int* overflow,
+                                     hipStream_t s) {
+    const int64_t n = rows * cols;
     if (n <= 0) {
         return hipSuccess;
+    }
+    if (cols % kPanel != 0) {
+        return hipErrorInvalidValue;
     }
     int64_t blocks = (n + 255) / 256;
     if (blocks > 65536) {
         blocks = 65536;
     }
-    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, n,
-                       overflow);
+    hipLaunchKernelGGL(bf16_to_f16_panels_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, rows,
+                       cols, overflow);
     return hipGetLastError();
 }
 

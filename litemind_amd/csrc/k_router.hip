@@ -178,12 +178,12 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(RouterArgs a, const
         }
         route_token(logit, valid, lane, t, a);
 
-        // fp16 copy of the activations for the MFMA path, zero-padded to hidden_p.
+        // fp16 copy of the activations for the MFMA path (panel layout),
+        // zero-padded to hidden_p.
         if (a.x16 != nullptr) {
             const float* xt = x + t * H;
-            _Float16* dst = a.x16 + t * a.hidden_p;
             for (int c = lane; c < a.hidden_p; c += 64) {
-                dst[c] = c < H ? static_cast<_Float16>(xt[c]) : static_cast<_Float16>(0.0f);
+                a.x16[panel_index(t, c, a.tokens)] = c < H ? static_cast<_Float16>(xt[c]) : static_cast<_Float16>(0.0f);
             }
         }
     }
@@ -291,9 +291,8 @@ __global__ __launch_bounds__(kDecodeThreads) void router_decode_kernel(RouterArg
     }
     route_token(logit, valid, lane, t, a);
     if (a.x16 != nullptr) {
-        _Float16* dst = a.x16 + t * a.hidden_p;
         for (int c = lane; c < a.hidden_p; c += 64) {
-            dst[c] = c < H ? static_cast<_Float16>(x[t * H + c]) : static_cast<_Float16>(0.0f);
+            a.x16[panel_index(t, c, a.tokens)] = c < H ? static_cast<_Float16>(x[t * H + c]) : static_cast<_Float16>(0.0f);
         }
     }
 }
@@ -424,7 +423,7 @@ __global__ __launch_bounds__(64) void select_single_kernel(RouterArgs a) {
         __syncthreads();
         permute_one_token(a);
     }
-    if (a.x16 != nullptr) {
+    if (a.x16 != nullptr) {  // one token: the panel layout is the row itself
         for (int c = lane; c < a.hidden_p; c += 64) {
             a.x16[c] = c < a.hidden ? static_cast<_Float16>(a.x[c]) : static_cast<_Float16>(0.0f);
         }

@@ -383,9 +383,9 @@ int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, 
     const int64_t max_active = L.dense ? 0 : std::min<int64_t>(ctx->E, T * ctx->K);
     stage_mark(ctx, 2);
     if (mfma) {
-        LM_HIP(lm::launch_mfma_gateup(ea, 0, ctx->stream));
+        LM_HIP(lm::launch_mfma_gateup(ea, ctx->stream));
         stage_mark(ctx, 3);
-        LM_HIP(lm::launch_mfma_down(ea, 0, ctx->stream));
+        LM_HIP(lm::launch_mfma_down(ea, ctx->stream));
     } else {
         LM_HIP(lm::launch_gemv_gateup(ea, max_active, ctx->stream));
         stage_mark(ctx, 3);
@@ -959,12 +959,24 @@ int lm_finalize_layer(lm_context* ctx, int32_t layer) {
             return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no router gate");
         }
     }
-    // fp16 shadow of the whole slab (bf16 half first, fp16 half second, same layout).
-    const size_t half_bytes = L.slab_bytes / 2;
+    // fp16 shadow of every matrix in panel layout (the MFMA path's operands).
     LM_HIP(hipMemsetAsync(ctx->d_overflow, 0, sizeof(int), ctx->stream));
-    LM_HIP(lm::launch_bf16_to_f16(static_cast<const uint16_t*>(L.slab),
-                                  reinterpret_cast<_Float16*>(static_cast<char*>(L.slab) + half_bytes),
-                                  static_cast<int64_t>(half_bytes / 2), ctx->d_overflow, ctx->stream));
+    std::vector<const lm::FfnDev*> ffns;
+    if (L.dense) {
+        ffns.push_back(&L.dense_ffn);
+    } else {
+        for (const lm::FfnDev& f : L.experts) {
+            ffns.push_back(&f);
+        }
+        if (ctx->S > 0) {
+            ffns.push_back(&L.shared);
+        }
+    }
+    for (const lm::FfnDev* f : ffns) {
+        LM_HIP(lm::launch_bf16_to_f16_panels(f->gu, f->gu_h, 2 * static_cast<int64_t>(f->inter_p), ctx->Hp,
+                                             ctx->d_overflow, ctx->stream));
+        LM_HIP(lm::launch_bf16_to_f16_panels(f->down, f->down_h, ctx->H, f->inter_p, ctx->d_overflow, ctx->stream));
+    }
     int overflow = 0;
     LM_HIP(hipMemcpyAsync(&overflow, ctx->d_overflow, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));

@@ -21,6 +21,15 @@ constexpr int kMaxTopK = 16;
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Panel layout of the fp16 operands of the MFMA path: a [rows, cols] matrix
+// (cols a multiple of kPanel) is stored as cols / kPanel panels of
+// [rows, kPanel], so the 32-column K slice of any run of rows is one contiguous
+// block (rows x 64 bytes).  Element (r, c) sits at panel_index(r, c, rows).
+constexpr int kPanel = 32;
+__host__ __device__ inline int64_t panel_index(int64_t r, int64_t c, int64_t rows) {
+    return (c / kPanel) * rows * kPanel + r * kPanel + (c % kPanel);
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
 
@@ -44,7 +53,7 @@ __device__ inline uint4 load_stream16(const void* p) {
 // One FFN (routed expert, the fused shared expert or a dense layer) resident in HBM.
 //   gu:   [2 * inter_p, hidden_p] BF16, gate/up interleaved as above
 //   down: [hidden, inter_p] BF16 (columns >= inter are zero)
-//   *_h:  the same matrices re-encoded as fp16 for the MFMA path
+//   *_h:  the same matrices re-encoded as fp16 in panel layout for the MFMA path
 struct FfnDev {
     uint16_t* gu = nullptr;
     uint16_t* down = nullptr;
@@ -81,7 +90,7 @@ struct RouterArgs {
     float* logits;           // [T, E] or null
     int32_t* idx;            // [T, K]
     float* wts;              // [T, K]
-    _Float16* x16;           // [T, Hp] or null
+    _Float16* x16;           // [T, Hp] fp16 in panel layout, or null
     int64_t tokens;
     int32_t hidden, hidden_p, experts, top_k;
     int32_t normalize, group_limited, n_group, topk_group;
@@ -106,9 +115,9 @@ struct ExpertArgs {
     GroupTable groups;
     RouteBufs rb;
     const float* x;          // [T, H] fp32 (GEMV path)
-    const _Float16* x16;     // [T, Hp] fp16 (MFMA path)
+    const _Float16* x16;     // [T, Hp] fp16 in panel layout (MFMA path)
     float* act;              // GEMV: activations fp32, routed [T*K, Ip] then shared [T, Sp]
-    _Float16* act16;         // MFMA: activations fp16, same layout
+    _Float16* act16;         // MFMA: fp16 panels, routed [T*K, Ip] then shared [T, Sp]
     float* down_out;         // [T*K + T, H] fp32 down-projection per slot
     int64_t tokens;
     int32_t hidden, hidden_p, experts, top_k;
@@ -174,10 +183,15 @@ constexpr int kDecodeSyncWords = kDecodeMaskWord + 16;
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
 hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
-hipError_t launch_mfma_gateup(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
-hipError_t launch_mfma_down(const ExpertArgs& a, int64_t max_tiles, hipStream_t s);
+// Grouped SwiGLU on MFMA (k_mfma.hip): fp16 panel operands, fp32 accumulation.
+hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
-hipError_t launch_bf16_to_f16(const uint16_t* src, _Float16* dst, int64_t n, int* overflow, hipStream_t s);
+// dst = fp16 panels of the BF16 matrix src [rows, cols] (cols % kPanel == 0);
+// counts values outside the fp16 range into *overflow.
+hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t rows, int64_t cols, int* overflow,
+                                     hipStream_t s);
+// x16 = fp16 panels of x [rows, cols], zero-padded to cols_p columns.
 hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
                               hipStream_t s);
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
