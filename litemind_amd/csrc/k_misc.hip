@@ -155,18 +155,33 @@ __global__ __launch_bounds__(256) void gemv_plain_kernel(const uint16_t* __restr
 }
 
 // x16 (panel layout, rows x cols_p) = fp16(x[r, c]) for c < cols, 0 for
-// cols <= c < cols_p.  Thread i produces destination element i.
+// cols <= c < cols_p.  Thread i converts 8 consecutive columns of one row
+// (one 16-byte store inside a panel row); consecutive threads walk a row.
 __global__ __launch_bounds__(256) void to_f16_rows_kernel(const float* __restrict__ x, _Float16* __restrict__ x16,
                                                           int64_t rows, int32_t cols, int32_t cols_p) {
+    typedef _Float16 half8 __attribute__((ext_vector_type(8)));
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= rows * cols_p) {
+    const int per_row = cols_p / 8;
+    if (i >= rows * per_row) {
         return;
     }
-    const int64_t panel = i / (rows * kPanel);
-    const int64_t rem = i - panel * rows * kPanel;
-    const int64_t r = rem / kPanel;
-    const int64_t c = panel * kPanel + (rem - r * kPanel);
-    x16[i] = c < cols ? static_cast<_Float16>(x[r * cols + c]) : static_cast<_Float16>(0.0f);
+    const int64_t r = i / per_row;
+    const int c = static_cast<int>(i - r * per_row) * 8;
+    const float* src = x + r * cols + c;
+    half8 h;
+    if (c + 8 <= cols && (cols & 3) == 0) {
+        const float4 v0 = *reinterpret_cast<const float4*>(src);
+        const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
+        h = half8{static_cast<_Float16>(v0.x), static_cast<_Float16>(v0.y), static_cast<_Float16>(v0.z),
+                  static_cast<_Float16>(v0.w), static_cast<_Float16>(v1.x), static_cast<_Float16>(v1.y),
+                  static_cast<_Float16>(v1.z), static_cast<_Float16>(v1.w)};
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            h[j] = c + j < cols ? static_cast<_Float16>(src[j]) : static_cast<_Float16>(0.0f);
+        }
+    }
+    *reinterpret_cast<half8*>(x16 + panel_index(r, c, rows)) = h;
 }
 
 // gemm::matvec_f32 with LiteMind's dot (src/Gemm.cpp:183-189) as its GCC build
@@ -288,7 +303,8 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
     if (cols_p % kPanel != 0) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, x, x16,
+    const int64_t units = n / 8;
+    hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0, s, x, x16,
                        rows, cols, cols_p);
     return hipGetLastError();
 }

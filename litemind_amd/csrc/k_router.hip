@@ -298,6 +298,177 @@ __global__ __launch_bounds__(kDecodeThreads) void router_decode_kernel(RouterArg
 }
 
 // ---------------------------------------------------------------------------
+// Batched router for many tokens (E == 64, H % 256 == 0).  A workgroup of 4
+// waves routes 4 * TPW tokens; lane e owns expert e and runs TPW sequential
+// chains.  Each chunk of 64 gate rows (16 KB of the [H/4][E][4] layout: lane e
+// reads four consecutive rows of its expert with one ds_read_b128) and the
+// tokens' activations for those rows go from global memory straight into a
+// 4-deep LDS ring with global_load_lds, so three chunks are always in flight
+// behind the one the chains consume; every step waits for a constant count and
+// always issues (a chunk past the end reloads the last one into a buffer that
+// is never read), so the waits stay exact.  The selection uses the LDS variant.
+// The fp16 copy of the activations (MFMA path) is a separate, fully parallel
+// conversion launch rather than a loop of dependent loads at the end of each
+// wave.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(1))) const void router_global_void;
+typedef __attribute__((address_space(3))) void router_lds_void;
+
+constexpr int kWideRows = 64;
+constexpr int kWideDepth = 4;
+constexpr int kWideWaves = 4;
+constexpr int64_t kWideTpw2Tokens = 2048;  // above this, two tokens per wave
+constexpr int64_t kWideTpw4Tokens = 4096;  // above this, four
+
+template <int TPW>
+struct WideShape {
+    static constexpr int kWBytes = kWideRows * 64 * 4;                   // 16 KB of gate rows
+    static constexpr int kXBytes = kWideWaves * 1024;  // activations: 1 KB per wave (TPW * 256 B used)
+    static constexpr int kStage = kWBytes + kXBytes;
+    static constexpr int kLoads = kWBytes / 1024 / kWideWaves + 1;       // wave instructions per chunk
+};
+
+__device__ inline void route_token_lds(float logit, bool valid, int lane, int64_t t, const RouterArgs& a,
+                                       float* sh) {
+    const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
+    int rank;
+    float weight;
+    select_token_lds(logit, valid, lane, p, sh, rank, weight);
+    const int K = a.top_k < a.experts ? a.top_k : a.experts;
+    if (valid && rank < K) {
+        a.idx[t * a.top_k + rank] = lane;
+        a.wts[t * a.top_k + rank] = weight;
+    }
+}
+
+template <int TPW>
+__global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                       const float* __restrict__ wq4) {
+    using S = WideShape<TPW>;
+    constexpr int kS4 = kWideDepth > 4 ? S::kStage : 16;
+    __shared__ __attribute__((aligned(1024))) char r0[S::kStage], r1[S::kStage], r2[S::kStage], r3[S::kStage];
+    __shared__ __attribute__((aligned(1024))) char r4[kS4], r5[kS4], r6[kS4], r7[kS4];
+    char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int H = a.hidden;
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * kWideWaves * TPW;
+    const int nchunks = H / kWideRows;
+
+    // This lane's activation row segment: token wave * TPW + (lane / 16) % TPW
+    // of the workgroup (clamped to the last token), rows 4 (lane % 16) .. +3.
+    // Every lane loads (lanes past TPW * 16 repeat a token into the unused part
+    // of the wave's slot), so the issue has no divergent branch.
+    int64_t xt = tb0 + wave * TPW + ((lane >> 4) % TPW);
+    xt = xt < a.tokens ? xt : a.tokens - 1;
+    const float* xsrc = x + xt * H + 4 * (lane & 15);
+    const float* wsrc = wq4 + static_cast<int64_t>(wave) * 256 + 4 * lane;
+    auto issue = [&](int c, char* buf) {
+        c = c < nchunks ? c : nchunks - 1;
+        const int64_t i0 = static_cast<int64_t>(c) * kWideRows;
+#pragma unroll
+        for (int j = 0; j < S::kLoads - 1; ++j) {
+            const int n = j * kWideWaves + wave;  // 1 KB block n of the chunk's gate rows
+            __builtin_amdgcn_global_load_lds((router_global_void*)(wsrc + i0 * 64 + j * kWideWaves * 256),
+                                             (router_lds_void*)(buf + n * 1024), 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + i0), (router_lds_void*)(buf + S::kWBytes + wave * 1024),
+                                         16, 0, 0);
+    };
+
+    float acc[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+        acc[k] = 0.0f;
+    }
+    // Rows 4q .. 4q + 3 of a chunk: the four gate values of this lane's expert
+    // (one 16-byte read) and the activations of its tokens (broadcast reads).
+    // The reads of a batch of kBatch rows are issued together and the
+    // additions then run from registers: while LDS-DMA writes are pending the
+    // compiler can only wait for all LDS reads at once, so one wait per batch
+    // is the cheapest arrangement.
+    constexpr int kBatch = 32;
+    auto compute = [&](const char* buf) {
+        const float4* wb = reinterpret_cast<const float4*>(buf);
+        const float* xb = reinterpret_cast<const float*>(buf + S::kWBytes + wave * 1024);
+#pragma unroll
+        for (int r0 = 0; r0 < kWideRows; r0 += kBatch) {
+            float4 w[kBatch / 4];
+            float4 xv[kBatch / 4][TPW];
+#pragma unroll
+            for (int q = 0; q < kBatch / 4; ++q) {
+                w[q] = wb[(r0 / 4 + q) * 64 + lane];
+#pragma unroll
+                for (int k = 0; k < TPW; ++k) {
+                    xv[q][k] = *reinterpret_cast<const float4*>(xb + k * kWideRows + r0 + 4 * q);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kBatch / 4; ++q) {
+                // Products first (independent), then the TPW chains' additions
+                // interleaved so consecutive adds never depend on each other.
+                float p[4][TPW];
+#pragma unroll
+                for (int k = 0; k < TPW; ++k) {
+                    p[0][k] = w[q].x * xv[q][k].x;
+                    p[1][k] = w[q].y * xv[q][k].y;
+                    p[2][k] = w[q].z * xv[q][k].z;
+                    p[3][k] = w[q].w * xv[q][k].w;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int k = 0; k < TPW; ++k) {
+                        acc[k] = acc[k] + p[j][k];
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // Chunk c lives in ring[c % depth]; before consuming it, wait until at
+    // most the depth - 2 chunks issued after it are in flight (and this wave's
+    // LDS reads of the previous chunk are done); the barrier then also frees the
+    // buffer consumed in the previous step for chunk c + depth - 1.
+    constexpr int kVm = (kWideDepth - 2) * S::kLoads;
+    static_assert(kVm < 64, "vmcnt immediate");
+    constexpr int kWait = 0x0070 | (kVm & 15) | ((kVm >> 4) << 14);  // vmcnt(kVm) lgkmcnt(0)
+#pragma unroll
+    for (int d = 0; d < kWideDepth - 1; ++d) {
+        issue(d, ring[d]);
+    }
+    for (int c0 = 0; c0 < nchunks; c0 += kWideDepth) {
+#pragma unroll
+        for (int j = 0; j < kWideDepth; ++j) {
+            __builtin_amdgcn_s_waitcnt(kWait);
+            __builtin_amdgcn_s_barrier();
+            issue(c0 + j + kWideDepth - 1, ring[(j + kWideDepth - 1) % kWideDepth]);
+            compute(ring[j]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);  // drain the clamped reloads
+    __builtin_amdgcn_s_barrier();
+
+    float* sh = reinterpret_cast<float*>(r0) + wave * kSelectScratch;
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+        const int64_t t = tb0 + wave * TPW + k;
+        if (t >= a.tokens) {
+            break;
+        }
+        float logit = acc[k];
+        if (a.bias != nullptr) {
+            logit = logit + a.bias[lane];
+        }
+        if (a.logits != nullptr) {
+            a.logits[t * 64 + lane] = logit;
+        }
+        route_token_lds(logit, true, lane, t, a, sh);
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Single-token router (T = 1): the experts are split over kSplit workgroups so
 // each one loads its whole slice of the transposed gate (H x 8 fp32, 64 KB at
 // H = 2048) at once, forms every product fl(w * x) in parallel into LDS, and
@@ -454,6 +625,22 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         const size_t lds = sizeof(float) * static_cast<size_t>(a.tokens) * a.hidden;
         hipLaunchKernelGGL(router_decode_kernel, dim3(1), dim3(kDecodeThreads), lds, s, a, a.x, a.wt);
         return hipGetLastError();
+    }
+    if (a.do_matvec && a.wq4 != nullptr && a.experts == 64 && a.hidden % (kWideRows * kWideDepth) == 0 &&
+        a.tokens >= 64) {
+        const int tpw = a.tokens > kWideTpw4Tokens ? 4 : (a.tokens > kWideTpw2Tokens ? 2 : 1);
+        const int64_t per_block = static_cast<int64_t>(kWideWaves) * tpw;
+        const dim3 grid(static_cast<unsigned>((a.tokens + per_block - 1) / per_block));
+        switch (tpw) {
+            case 4: hipLaunchKernelGGL(router_wide_kernel<4>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
+            case 2: hipLaunchKernelGGL(router_wide_kernel<2>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
+            default: hipLaunchKernelGGL(router_wide_kernel<1>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
+        }
+        hipError_t err = hipGetLastError();
+        if (err == hipSuccess && a.x16 != nullptr) {
+            err = launch_to_f16_rows(a.x, a.x16, a.tokens, a.hidden, a.hidden_p, s);
+        }
+        return err;
     }
     int tpw = 1;
     if (a.do_matvec) {

@@ -59,7 +59,7 @@ struct Layer {
     bool allocated = false;
     bool dense = false;
     bool finalized = false;
-    float* router_t = nullptr;         // [H, E], then [E/4][H][4]
+    float* router_t = nullptr;         // [H, E], then [E/4][H][4], then [H/4][E][4]
     float* norm = nullptr;             // [H]
     void* slab = nullptr;              // all FFN matrices of the layer (bf16 then fp16 shadow)
     size_t slab_bytes = 0;
@@ -486,6 +486,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     lm::RouterArgs ra{};
     ra.x = x;
     ra.wt = L.router_t;
+    ra.wq4 = L.router_t + 2 * static_cast<size_t>(ctx->H) * ctx->E;
     ra.bias = bias;
     ra.logits = logits_out;
     ra.idx = idx;
@@ -812,21 +813,27 @@ int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host) {
     }
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
     const size_t n = static_cast<size_t>(ctx->H) * static_cast<size_t>(ctx->E);
+    // Three layouts of the gate: [H, E] for the per-wave router; [E/4][H][4]
+    // (four experts' weights of one row side by side, each slice contiguous)
+    // for the single-token router; [H/4][E][4] (four consecutive rows of one
+    // expert side by side) for the wide router.  H is padded to a multiple of
+    // 4 with zero rows in the last one.
+    const size_t n4 = static_cast<size_t>(lm::round_up(ctx->H, 4)) * static_cast<size_t>(ctx->E);
+    const size_t total = 2 * n + n4;
     if (L.router_t == nullptr) {
-        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), 2 * n * sizeof(float)));
-        ctx->resident += 2 * n * sizeof(float);
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), total * sizeof(float)));
+        ctx->resident += total * sizeof(float);
     }
-    // [H, E] for the batched router, then [E/4][H][4] (four experts' weights of
-    // one row side by side, each slice contiguous) for the single-token router.
-    std::vector<float> t(2 * n, 0.0f);
+    std::vector<float> t(total, 0.0f);
     for (int e = 0; e < ctx->E; ++e) {
         for (int i = 0; i < ctx->H; ++i) {
             const float v = gate_host[static_cast<size_t>(e) * ctx->H + i];
             t[static_cast<size_t>(i) * ctx->E + e] = v;
             t[n + (static_cast<size_t>(e / 4) * ctx->H + i) * 4 + e % 4] = v;
+            t[2 * n + (static_cast<size_t>(i / 4) * ctx->E + e) * 4 + i % 4] = v;
         }
     }
-    LM_HIP(hipMemcpyAsync(L.router_t, t.data(), 2 * n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LM_HIP(hipMemcpyAsync(L.router_t, t.data(), total * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     return LM_OK;
     LM_GUARD_END
@@ -1058,6 +1065,7 @@ int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens
     lm::RouterArgs ra{};
     ra.x = x_dev;
     ra.wt = L.router_t;
+    ra.wq4 = L.router_t + 2 * static_cast<size_t>(ctx->H) * ctx->E;
     ra.logits_scratch = ctx->ws.logit_scratch;
     ra.ticket = ctx->ws.ticket;
     ra.bias = logit_bias_dev;

@@ -86,6 +86,7 @@ struct RouteBufs {
 struct RouterArgs {
     const float* x;          // [T, H]
     const float* wt;         // [H, E] router gate, transposed
+    const float* wq4;        // [H/4][E][4] the same gate, four rows of an expert together
     const float* bias;       // [E] or null
     float* logits;           // [T, E] or null
     int32_t* idx;            // [T, K]

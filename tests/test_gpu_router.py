@@ -39,12 +39,17 @@ def _oracle_route(layer, x, bias=None):
     return logits, idx, w
 
 
-@pytest.mark.parametrize("case", ["t1", "t5", "t32", "t512_uniform", "t2048_skewed"])
+@pytest.mark.parametrize("case", ["t1", "t5", "t32", "t100_ragged", "t512_uniform", "t2048_skewed", "t4096",
+                                  "t4100_ragged"])
 def test_router_bit_exact_v2lite(v2_ctx, case):
+    """Every router kernel shape: single token, decode batch, the per-wave
+    kernel, and the wide kernel with one, two and four tokens per wave,
+    including partial last workgroups."""
     from litemind_amd import workload as wl
 
     ctx, layers = v2_ctx
-    T = {"t1": 1, "t5": 5, "t32": 32, "t512_uniform": 512, "t2048_skewed": 2048}[case]
+    T = {"t1": 1, "t5": 5, "t32": 32, "t100_ragged": 100, "t512_uniform": 512, "t2048_skewed": 2048,
+         "t4096": 4096, "t4100_ragged": 4100}[case]
     layer_id = 1 if case == "t512_uniform" else 0
     bias = wl.skew_bias() if case == "t2048_skewed" else None
     x = wl.tokens(wl.MASTER_SEED + T, T, 2048)
