@@ -30,8 +30,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kRouterExperts = 4;            // experts per router workgroup
 constexpr int kRpw = 4;                      // gate rows (and as many up rows) per wave
 constexpr int kItemRows = kRpw * kWaves;     // gate rows per gate/up item
-constexpr int kDownRpw = 2;                  // shared down rows per wave
-constexpr int kDownItemRows = kDownRpw * kWaves;
 
 struct DecodeArgs {
     const float* x;            // [H] the token
@@ -46,7 +44,6 @@ struct DecodeArgs {
     const uint16_t* shared_gu;
     const uint16_t* shared_down;
     float* act;                // [K, Ip] routed activations in rank order, then [Sp] shared
-    float* shared_out;         // [H] shared expert's down projection
     float* y;                  // [H]
     const float* residual;     // [H] or null
     int32_t hidden, hidden_p, experts, top_k, inter_p, shared_inter_p, has_shared;
@@ -260,40 +257,11 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
     }
 }
 
-// Shared expert's down rows [8 item, 8 item + 8): shared_out[h] = W_d[h] . act_shared.
-template <int SI>
-__device__ __forceinline__ void shared_down_item(const DecodeArgs& a, int item) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int W = a.shared_inter_p;
-    constexpr int R = kDownRpw;
-    const int h0 = item * kDownItemRows + wave * R;
-    const uint16_t* rows[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        rows[r] = a.shared_down + static_cast<int64_t>(h0 + r) * W;
-    }
-    uint4 w[R][SI];
-    load_rows<R, SI>(rows, W, lane, w);
-    float4 hr[1][SI][2];
-    load_act_coherent<SI>(a.act + a.top_k * a.inter_p, W, lane, hr[0]);
-    float acc[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        acc[i] = 0.0f;
-    }
-    dot_rows<R, SI, 1>(w, hr, acc);
-    const float sum = transpose_reduce<R>(acc, lane);
-    constexpr int L = log2c<R>();
-    if ((lane & ((1 << (6 - L)) - 1)) == 0) {
-        store_coherent(a.shared_out + h0 + (lane >> (6 - L)), sum);
-    }
-}
-
 // ---- the single launch --------------------------------------------------------
 //
 // One grid, roles by workgroup index, in dependency order:
-//   [routers | shared gate/up | routed gate/up | shared down | down + combine]
+//   [routers | shared gate/up | routed gate/up | down + combine]
+// (the down workgroups also project the shared expert for their rows).
 // A workgroup waits only for workgroups with lower indices.  The dispatcher
 // places workgroups on the GPU in index order, so when one waits, everything it
 // waits for is resident or finished, and every wait ends; each wait is bounded
@@ -306,8 +274,7 @@ constexpr uint32_t kMaxSpins = 1u << 16;  // ~50 ms of polling
 constexpr int kLanes = 16;
 constexpr int kSlotStride = 16;  // words
 enum : int {
-    kRouterLoaded = 0, kApproxDone, kSpecReady, kRouterDone, kSelectReady, kSharedGuDone, kSharedDownDone,
-    kRoutedDone, kCounters
+    kRouterLoaded = 0, kRouterDone, kSelectReady, kSharedGuDone, kRoutedDone, kCounters
 };
 constexpr int kSetWords = kCounters * kLanes * kSlotStride;
 constexpr int kFusedRows = kWaves;  // down + combine: one output row per wave
@@ -315,16 +282,25 @@ constexpr int kFusedRows = kWaves;  // down + combine: one output row per wave
 struct FusedArgs {
     DecodeArgs a;
     uint32_t* sync;     // [2][kSetWords] counters, then the error word
-    float* approx;      // [E] fast (reassociated) logits for the speculative selection
-    int32_t* spec;      // [K] speculative experts by rank
+    uint64_t* approx;   // [E] fast (reassociated) logits for the speculative selection, tagged
+    uint64_t* spec;     // [K] speculative experts by rank, tagged
     uint32_t* mask;     // ranks whose speculative expert differs from the exact one
     int32_t parity;
+    uint32_t seq;       // this launch's tag of the approx / spec words (nonzero, changes every launch)
     int32_t perturb;    // testing: make the speculation disagree with every rank
-    int32_t n_router, n_shared_gu, n_shared_down, n_routed;
+    int32_t n_router, n_shared_gu, n_routed;
 };
 
 __device__ inline uint32_t* counter_slot(uint32_t* set, int counter, int slot) {
     return set + (counter * kLanes + slot) * kSlotStride;
+}
+
+// Counters that at most the 16 router workgroups (or one workgroup) add to live
+// in one slot: a waiter then reads a single line, and the previous value of an
+// add tells the last arriver.  The per-item counters of the streaming roles
+// spread over kLanes slots.
+__device__ constexpr bool single_slot(int counter) {
+    return counter == kRouterLoaded || counter == kRouterDone || counter == kSelectReady;
 }
 
 // Counts this workgroup done once every wave's stores are acknowledged; returns
@@ -334,7 +310,8 @@ __device__ inline uint32_t signal_done(uint32_t* set, int counter) {
     __syncthreads();
     __shared__ uint32_t previous;
     if (threadIdx.x == 0) {
-        previous = __hip_atomic_fetch_add(counter_slot(set, counter, blockIdx.x % kLanes), 1u, __ATOMIC_RELAXED,
+        const int slot = single_slot(counter) ? 0 : static_cast<int>(blockIdx.x % kLanes);
+        previous = __hip_atomic_fetch_add(counter_slot(set, counter, slot), 1u, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
@@ -347,8 +324,9 @@ __device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, u
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         uint32_t spins = 0;
+        const int polled = single_slot(counter) ? 1 : kLanes;
         for (;;) {
-            uint32_t v = lane < kLanes ? __hip_atomic_load(counter_slot(set, counter, lane), __ATOMIC_RELAXED,
+            uint32_t v = lane < polled ? __hip_atomic_load(counter_slot(set, counter, lane), __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_AGENT)
                                        : 0u;
             // every lane of the wave must see the total, or the lanes would leave
@@ -366,7 +344,9 @@ __device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, u
                 }
                 break;
             }
-            if (target - v > target / 4) {
+            if (single_slot(counter)) {
+                __builtin_amdgcn_s_sleep(4);  // one line polled: check often
+            } else if (target - v > target / 4) {
                 __builtin_amdgcn_s_sleep(32);
             } else {
                 __builtin_amdgcn_s_sleep(4);
@@ -376,15 +356,55 @@ __device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, u
     __syncthreads();
 }
 
+// Tagged hand-off words: the value in the low 32 bits, the launch's sequence
+// number in the high 32, written with one 64-bit device-scope store.  A reader
+// knows a word is this launch's from the word itself, so the writer neither
+// waits for its store nor counts it anywhere.
+__device__ inline void publish(uint64_t* p, uint32_t seq, uint32_t bits) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(seq) << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave polls words [0, n) (n <= 64) until all carry `seq`; lane i < n then
+// holds the low 32 bits of word i.  Bounded like wait_count.
+__device__ inline uint32_t wait_tagged(const uint64_t* p, int n, uint32_t seq, uint32_t* error) {
+    const int lane = threadIdx.x & 63;
+    uint32_t spins = 0;
+    for (;;) {
+        const uint64_t v = lane < n ? __hip_atomic_load(const_cast<uint64_t*>(p) + lane, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : static_cast<uint64_t>(seq) << 32;
+        if (__ballot(static_cast<uint32_t>(v >> 32) != seq) == 0) {
+            return static_cast<uint32_t>(v);
+        }
+        if (++spins > kMaxSpins) {
+            if (lane == 0) {
+                __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return static_cast<uint32_t>(v);
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+// Speculative experts of every rank into LDS (all waves read them afterwards).
+__device__ inline void load_spec(const FusedArgs& f, uint32_t* error, int* spec_lds) {
+    if (threadIdx.x < 64) {
+        const uint32_t v = wait_tagged(f.spec, f.a.top_k, f.seq, error);
+        if (static_cast<int>(threadIdx.x) < f.a.top_k) {
+            spec_lds[threadIdx.x] = static_cast<int>(v);
+        }
+    }
+    __syncthreads();
+}
+
 // Router workgroups, once their products are in LDS: count the router's loads
 // done and publish the approximate logits of the slice.
-__device__ __forceinline__ void speculate(const FusedArgs& f, uint32_t* sync, int e0, int b, const float4* lds) {
+__device__ __forceinline__ void speculate(const FusedArgs& f, uint32_t* sync, int e0, const float4* lds) {
     const DecodeArgs& a = f.a;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(counter_slot(sync, kRouterLoaded, b % kLanes), 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(counter_slot(sync, kRouterLoaded, 0), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // Approximate logit of expert e0 + wave: the same products, tree order.
     const int quads = a.hidden / 4;
@@ -398,9 +418,8 @@ __device__ __forceinline__ void speculate(const FusedArgs& f, uint32_t* sync, in
         t += __shfl_xor(t, o);
     }
     if (lane == 0) {
-        store_coherent(f.approx + e0 + wave, a.bias != nullptr ? t + a.bias[e0 + wave] : t);
+        publish(f.approx + e0 + wave, f.seq, float_bits(a.bias != nullptr ? t + a.bias[e0 + wave] : t));
     }
-    signal_done(sync, kApproxDone);
 }
 
 // Recomputes, in LDS, the activation row of rank r for expert e (rare path:
@@ -430,7 +449,7 @@ __device__ void repair_act_row(const DecodeArgs& a, int e, float* act_row) {
 // those are known; the exact selection then decides: ranks it confirms use the
 // rows in registers and the activations the routed workgroups wrote, the others
 // (rare) are recomputed here from the exact expert's weights.
-template <int KM, int DI>
+template <int KM, int DI, int SI>
 __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, uint32_t* error, int h,
                                            float* acts) {
     constexpr int KP = KM <= 2 ? 2 : (KM <= 4 ? 4 : 8);  // reduction width (power of two)
@@ -441,13 +460,25 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     const int K = a.top_k;
     const int W = a.inter_p;
     const int64_t down_off = static_cast<int64_t>(2) * W * a.hidden_p + static_cast<int64_t>(h) * W;
-    wait_count(sync, kSpecReady, 1, error);
+    const int WS = a.shared_inter_p;
+    // The shared expert's down row h does not depend on the selection.
+    uint4 ws[SI];
+    {
+        const uint16_t* srow = a.shared_down + static_cast<int64_t>(h) * WS;
+#pragma unroll
+        for (int it = 0; it < SI; ++it) {
+            const int c = it * 512 + lane * 8;
+            ws[it] = load_stream16(srow + (c < WS ? c : WS - 8));
+        }
+    }
+    __shared__ int spec_lds[kMaxTopK];
+    load_spec(f, error, spec_lds);
     uint4 w[KM][DI];
     {
         int ex[KM];
 #pragma unroll
         for (int r = 0; r < KM; ++r) {
-            ex[r] = load_coherent(f.spec + (r < K ? r : 0));
+            ex[r] = spec_lds[r < K ? r : 0];
         }
 #pragma unroll
         for (int it = 0; it < DI; ++it) {
@@ -459,8 +490,8 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             }
         }
     }
+    wait_count(sync, kSharedGuDone, f.n_shared_gu, error);
     wait_count(sync, kRoutedDone, f.n_routed, error);
-    wait_count(sync, kSharedDownDone, f.n_shared_down, error);
     wait_count(sync, kSelectReady, 1, error);
     const uint32_t m = __hip_atomic_load(f.mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float wk[KM];
@@ -468,8 +499,10 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     for (int r = 0; r < KM; ++r) {
         wk[r] = load_coherent(a.wts + (r < K ? r : 0));
     }
-    // The activations of the confirmed ranks, once per workgroup, into LDS.
-    const int n4 = K * W / 4;
+    // The activations of the confirmed ranks and of the shared expert (stored
+    // right after the routed ones), once per workgroup, into LDS.
+    const int routed4 = K * W / 4;
+    const int n4 = routed4 + WS / 4;
     for (int f0 = threadIdx.x; f0 < n4; f0 += 4 * kThreads) {
         float4 v[4];
 #pragma unroll
@@ -480,14 +513,28 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int g = f0 + u * kThreads;
-            if (g < n4 && ((m >> (4 * g / W)) & 1u) == 0) {
+            if (g < n4 && (g >= routed4 || ((m >> (4 * g / W)) & 1u) == 0)) {
                 *reinterpret_cast<float4*>(acts + 4 * g) = v[u];
             }
         }
     }
-    const float shared_h = a.has_shared ? load_coherent(a.shared_out + h) : 0.0f;
     const float residual_h = a.residual != nullptr ? a.residual[h] : 0.0f;
     lds_barrier();
+    // The shared expert's down projection for row h.
+    float shared_h = 0.0f;
+#pragma unroll
+    for (int it = 0; it < SI; ++it) {
+        const int c = it * 512 + lane * 8;
+        if (c < WS) {
+            const float4 x0 = *reinterpret_cast<const float4*>(acts + K * W + c);
+            const float4 x1 = *reinterpret_cast<const float4*>(acts + K * W + c + 4);
+            fma8(shared_h, ws[it], x0, x1);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        shared_h += __shfl_xor(shared_h, o);
+    }
     float acc[KP];
 #pragma unroll
     for (int r = 0; r < KP; ++r) {
@@ -561,9 +608,9 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
 // one to finish selects from those, and the routed gate/up rows of the
 // speculated experts stream while the exact, strictly sequential logits are
 // still being added.  The exact selection decides everything that is output;
-// ranks where the speculation picked another expert are recomputed by the fix-up
+// ranks where the speculation picked another expert are recomputed by the down
 // workgroups (almost never: only a near-tie between two experts' scores can
-// order them differently), and the down projection reads those rows instead.
+// order them differently).
 template <int GI, int SI, int KM, int DI>
 __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     extern __shared__ float4 lds[];  // router products or the down stage's activations
@@ -585,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     }
     if (b < f.n_router) {
         const int e0 = b * kRouterExperts;
-        router_slice(a, e0, lds, [&] { speculate(f, sync, e0, b, lds); });
+        router_slice(a, e0, lds, [&] { speculate(f, sync, e0, lds); });
         // The last router workgroup to finish its exact logits selects for the output.
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
@@ -608,7 +655,9 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
                 store_coherent(a.idx + rank, lane);
                 store_coherent(a.wts + rank, weight);
             }
-            const uint64_t wrong = __ballot(chosen && load_coherent(f.spec + rank) != lane);
+            const int spec_of_rank = __shfl(static_cast<int>(wait_tagged(f.spec, a.top_k, f.seq, error)),
+                                            chosen ? rank : 0);
+            const uint64_t wrong = __ballot(chosen && spec_of_rank != lane);
             // bit r of the mask: rank r must be recomputed
             uint32_t m = 0;
             if (chosen && ((wrong >> lane) & 1u) != 0) {
@@ -636,49 +685,33 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     }
     b -= f.n_shared_gu;
     const int chunks = a.inter_p / kItemRows;
-    if (b < f.n_routed) {
-        if (b == 0) {
-            // The first routed workgroup selects speculatively from the
-            // approximate logits, for itself and the others.
-            wait_count(sync, kApproxDone, f.n_router, error);
-            if (threadIdx.x < 64) {
-                const bool valid = lane < a.experts;
-                const float logit = valid ? load_coherent(f.approx + lane) : 0.0f;
-                int rank;
-                float weight;
-                select_token_lds(logit, valid, lane, a.policy, sel, rank, weight);
-                if (valid && rank < a.top_k) {
-                    store_coherent(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), lane);
-                }
+    if (b == 0) {
+        // The first routed workgroup selects speculatively from the approximate
+        // logits and publishes the experts for the routed and down workgroups.
+        if (threadIdx.x < 64) {
+            const bool valid = lane < a.experts;
+            const float logit = bits_float(wait_tagged(f.approx, a.experts, f.seq, error));
+            int rank;
+            float weight;
+            select_token_lds(valid ? logit : 0.0f, valid, lane, a.policy, sel, rank, weight);
+            if (valid && rank < a.top_k) {
+                publish(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), f.seq, static_cast<uint32_t>(lane));
             }
-            signal_done(sync, kSpecReady);
-        } else {
-            wait_count(sync, kSpecReady, 1, error);
         }
     }
     b -= f.n_routed;
-    if (b >= 0 && b < f.n_shared_down) {
-        wait_count(sync, kSharedGuDone, f.n_shared_gu, error);
-        shared_down_item<SI>(a, b);
-        signal_done(sync, kSharedDownDone);
-        return;
-    }
-    b -= f.n_shared_down;
     if (b < 0) {
         // Routed gate/up of the speculative experts.
-        const int item = b + f.n_routed + f.n_shared_down;
+        const int item = b + f.n_routed;
         const int r = item / chunks;
-        if (threadIdx.x == 0) {
-            expert_of_rank[0] = load_coherent(f.spec + r);
-        }
-        __syncthreads();
-        gateup_item<GI>(a.routed + static_cast<int64_t>(expert_of_rank[0]) * a.routed_stride, a,
-                                    item - r * chunks, a.act + static_cast<int64_t>(r) * a.inter_p,
-                                    reinterpret_cast<float*>(lds));
+        load_spec(f, error, expert_of_rank);
+        gateup_item<GI>(a.routed + static_cast<int64_t>(expert_of_rank[r]) * a.routed_stride, a,
+                        item - r * chunks, a.act + static_cast<int64_t>(r) * a.inter_p,
+                        reinterpret_cast<float*>(lds));
         signal_done(sync, kRoutedDone);
         return;
     }
-    down_fused<KM, DI>(f, sync, error, b * kFusedRows + wave, reinterpret_cast<float*>(lds));
+    down_fused<KM, DI, SI>(f, sync, error, b * kFusedRows + wave, reinterpret_cast<float*>(lds));
 }
 
 int iters_of(int width) { return (width + 511) / 512; }
@@ -703,8 +736,8 @@ int fused_shape(int hidden, int top_k, int inter_p, int shared_inter_p) {
 
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p) {
     return experts % kRouterExperts == 0 && experts >= 2 && experts <= kMaxExperts && top_k >= 1 &&
-           top_k <= 8 && top_k <= experts && shared_inter_p > 0 && hidden % kDownItemRows == 0 &&
-           hidden % kWaves == 0 && hidden * 16 <= 65536 && top_k * inter_p * 4 <= 65536 &&
+           top_k <= 8 && top_k <= experts && shared_inter_p > 0 && shared_inter_p % 4 == 0 &&
+           hidden % kWaves == 0 && hidden * 16 <= 65536 && (top_k * inter_p + shared_inter_p) * 4 <= 65536 &&
            inter_p % kItemRows == 0 && shared_inter_p % kItemRows == 0 &&
            fused_shape(hidden, top_k, inter_p, shared_inter_p) >= 0;
 }
@@ -729,7 +762,6 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     a.shared_gu = d.shared_gu;
     a.shared_down = d.shared_down;
     a.act = d.act;
-    a.shared_out = d.shared_out;
     a.y = d.y;
     a.residual = d.residual;
     a.hidden = hidden;
@@ -742,19 +774,19 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     a.policy = d.policy;
     static_assert(2 * kSetWords == kDecodeCounterWords, "decode scratch layout");
     f.sync = d.sync;
-    f.approx = reinterpret_cast<float*>(d.sync + kDecodeApproxWord);
-    f.spec = reinterpret_cast<int32_t*>(d.sync + kDecodeSpecWord);
+    f.approx = reinterpret_cast<uint64_t*>(d.sync + kDecodeApproxWord);
+    f.spec = reinterpret_cast<uint64_t*>(d.sync + kDecodeSpecWord);
+    f.seq = d.seq;
     f.mask = d.sync + kDecodeMaskWord;
     f.parity = d.parity & 1;
     f.perturb = d.perturb;
     f.n_router = a.experts / kRouterExperts;
     f.n_shared_gu = a.shared_inter_p / kItemRows;
-    f.n_shared_down = hidden / kDownItemRows;
     f.n_routed = top_k * (inter_p / kItemRows);
     const int n_down = hidden / kFusedRows;
-    const dim3 grid(static_cast<unsigned>(f.n_router + f.n_shared_gu + f.n_shared_down + f.n_routed + n_down));
+    const dim3 grid(static_cast<unsigned>(f.n_router + f.n_shared_gu + f.n_routed + n_down));
     const size_t router_lds = sizeof(float) * static_cast<size_t>(hidden) * kRouterExperts;
-    const size_t down_lds = sizeof(float) * static_cast<size_t>(top_k) * inter_p;
+    const size_t down_lds = sizeof(float) * (static_cast<size_t>(top_k) * inter_p + d.shared_inter_p);
     const size_t lds = router_lds > down_lds ? router_lds : down_lds;
     if (fused_shape(hidden, top_k, inter_p, d.shared_inter_p) == 0) {
         hipLaunchKernelGGL((decode_fused_kernel<4, 6, 6, 3>), grid, dim3(kThreads), lds, s, f);

@@ -116,6 +116,7 @@ struct lm_context {
     };
     std::unordered_map<const void*, Cached> resident_ptrs;
     int32_t decode_parity = 0;   // alternates between single-launch decodes
+    uint32_t decode_seq = 0;     // tag of the single-launch decode's hand-off words (never 0 in a launch)
     int32_t decode_perturb = 0;  // testing: force the speculative selection to disagree
     bool decode_pending = false; // a single-launch decode ran since the last error check
     void* gemm_w = nullptr;      // per-call upload of a matrix that is not resident
@@ -438,7 +439,6 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     d.shared_gu = L.shared.gu;
     d.shared_down = L.shared.down;
     d.act = static_cast<float*>(ctx->ws.act);
-    d.shared_out = ctx->ws.down_out;
     d.y = y;
     d.residual = residual;
     d.hidden = ctx->H;
@@ -451,6 +451,8 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     d.parity = ctx->decode_parity;
     d.perturb = ctx->decode_perturb;
     ctx->decode_parity ^= 1;
+    ctx->decode_seq = ctx->decode_seq == 0xffffffffu ? 1u : ctx->decode_seq + 1u;
+    d.seq = ctx->decode_seq;
     ctx->decode_pending = true;
     stage_mark(ctx, 0);
     stage_mark(ctx, 1);

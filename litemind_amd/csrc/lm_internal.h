@@ -157,13 +157,13 @@ struct DecodeLaunch {
     const uint16_t* shared_gu;  // shared expert (null: none)
     const uint16_t* shared_down;
     float* act;                 // [K * Ip + Sp]
-    float* shared_out;          // [H]
     float* y;                   // [H]
     const float* residual;      // [H] or null
     int32_t hidden, hidden_p, inter_p, shared_inter_p;
     SelectPolicy policy;
     uint32_t* sync;             // kDecodeSyncWords words, zeroed once
     int32_t parity;             // alternates between consecutive launches
+    uint32_t seq;               // nonzero, different in consecutive launches: tags the hand-off words
     int32_t perturb;            // testing: the speculative selection disagrees with every rank
 };
 
@@ -172,14 +172,14 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted);
 // True when the single-token forward has a one-launch kernel for this shape.
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p);
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s);
-// Single-launch decode scratch, in 32-bit words: two sets of 8 counters x 16
-// slots x 64 B, the error word, approximate logits [64], speculative experts
-// [16] and the mask of ranks the speculation got wrong.
-constexpr int kDecodeCounterWords = 2 * 8 * 16 * 16;
+// Single-launch decode scratch, in 32-bit words: two sets of 5 counters x 16
+// slots x 64 B, the error word, approximate logits [64] and speculative experts
+// [16] as tagged 64-bit words, and the mask of ranks the speculation got wrong.
+constexpr int kDecodeCounterWords = 2 * 5 * 16 * 16;
 constexpr int kDecodeErrorWord = kDecodeCounterWords;
 constexpr int kDecodeApproxWord = kDecodeErrorWord + 16;
-constexpr int kDecodeSpecWord = kDecodeApproxWord + kMaxExperts;
-constexpr int kDecodeMaskWord = kDecodeSpecWord + kMaxTopK;
+constexpr int kDecodeSpecWord = kDecodeApproxWord + 2 * kMaxExperts;
+constexpr int kDecodeMaskWord = kDecodeSpecWord + 2 * kMaxTopK;
 constexpr int kDecodeSyncWords = kDecodeMaskWord + 16;
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
