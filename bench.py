@@ -40,7 +40,7 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over
 # this benchmark, scaled by the counters' readings for a conversion kernel of
 # known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md).
-MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 140_252_864}
+MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 140_105_165}
 
 
 def log(msg: str) -> None:
@@ -176,6 +176,17 @@ def roofline(res: dict, mfma: bool) -> dict:
             "algorithmic_bytes": by}
 
 
+def swiglu(res: dict) -> dict:
+    """The grouped SwiGLU (gate/up and down launches together) against dense MFMA peak."""
+    stages = res["stages"]
+    us = sum(stages[k][0] / stages[k][1] * 1e3 for k in ("gate_up", "down") if stages.get(k) and stages[k][1])
+    alg = algorithmic(res["T"], int(round(res["distinct"])))
+    fl = alg["gate_up_flops"] + alg["down_flops"]
+    tf = fl / (us * 1e-6) / 1e12 if us else 0.0
+    return {"us": round(us, 2), "flops": fl, "achieved": round(tf, 2), "unit": "TFLOP/s", "peak": MFMA_PEAK_TFLOPS,
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +249,8 @@ def main() -> int:
             "roofline": roofline(res2, mfma2),
             "stage_us": {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res2["stages"].items()},
         }
+        if mfma2:
+            line["t2048" if w2.tokens == 2048 else args.second]["grouped_swiglu"] = swiglu(res2)
     print(json.dumps(line), flush=True)
     return 0
 
