@@ -1,6 +1,7 @@
 """Benchmark of the MI355X MoE feed-forward path (DeepSeek-V2-Lite MoE layer).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_t1] [--no-cpu]
+    python bench.py --workload stack      # the 27-layer FFN stack at T=1 and T=4096
 
 A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
 experts, combine) over one batch of T synthetic tokens whose inputs are already
@@ -123,6 +124,50 @@ def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int)
                 bias=bias, workload=workload_name)
 
 
+def run_stack(steps_t1: int, steps_big: int, big_tokens: int, moe_layers: int) -> dict:
+    """The full FFN stack: dense layer 0, then `moe_layers` MoE layers (independent
+    seeds), chained through RMSNorm (weights 1) and the residual add, resident in
+    HBM.  A step is one pass of T tokens through every layer.  (Parity of the
+    chain is tests/test_gpu_stack.py.)"""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = wl.V2_LITE
+    n = 1 + moe_layers
+    log(f"stack: generating and uploading dense + {moe_layers} MoE layers")
+    ctx = Context(dims.moe_config(num_layers=n))
+    gate, up, down = wl.dense_ffn(wl.MASTER_SEED, 0, dims)
+    ctx.upload_dense(0, gate, up, down)
+    ctx.finalize_layer(0)
+    del gate, up, down
+    for l in range(1, n):
+        wl.upload_moe_layer(ctx, l, wl.moe_layer(wl.MASTER_SEED, l, dims))
+    ones = np.ones(dims.hidden, np.float32)
+    for l in range(n):
+        ctx.upload_norm(l, ones)
+    resident = ctx.resident_bytes()
+    out = {"layers": n, "resident_gb": round(resident / 1e9, 2)}
+    for T, steps in ((1, steps_t1), (big_tokens, steps_big)):
+        h0 = wl.tokens(wl.MASTER_SEED + 11, T, dims.hidden)
+        dh = ctx.to_device(h0)
+        for _ in range(2):  # warm-up passes (the hidden state keeps evolving; timing only)
+            ctx.stack_forward(0, n - 1, dh, T)
+        ctx.synchronize()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(steps):
+            ctx.stack_forward(0, n - 1, dh, T)
+        ctx.record(e1)
+        ctx.synchronize()
+        ms = ctx.elapsed_ms(e0, e1) / steps
+        out[f"t{T}"] = {"tokens": T, "steps": steps, "ms_per_step": round(ms, 4),
+                        "value": round(T / (ms / 1e3), 1), "unit": "tokens/s"}
+        dh.free()
+        log(f"stack T={T}: {ms:.3f} ms per step")
+    ctx.close()
+    return out
+
+
 def cpu_baseline(layer, x, bias, budget_s: float, max_tokens: int):
     """LiteMind's CPU MoE path (its own Gemm/MoeRouter/ThreadPool, compiled from its
     sources into oracle/_ref) on the first tokens of the workload, one token at a
@@ -199,6 +244,18 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
+    if args.workload == "stack":
+        if args.gpus != 1:
+            print("bench.py measures one GPU.", file=sys.stderr)
+            return 2
+        st = run_stack(args.steps if args.steps != 200 else 20, 5, 4096, 26)
+        line = {"metric": "MoE FFN stack tokens/sec (dense layer 0 + 26 MoE layers, RMSNorm-chained)",
+                "value": st["t1"]["value"], "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+                "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-normalised tokens)",
+                "config": {"workload": "stack", "layers": st["layers"], "resident_gb": st["resident_gb"]},
+                "t1": st["t1"], "t4096": st["t4096"]}
+        print(json.dumps(line), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)

@@ -198,3 +198,27 @@ def oracle_dense(gate, up, down, x: np.ndarray, threads: int = 0):
     y = np.zeros((x.shape[0], H), np.float32)
     oracle().orc_dense_ffn(p(gate), p(up), p(down), H, D, p(x), x.shape[0], p(y), threads)
     return y
+
+
+def oracle_stack(layers, h: np.ndarray, eps: float, every_layer: bool = False):
+    """The FFN chain of LiteMind's runner with attention omitted
+    (src/DeepSeekRunner.cpp:264-290): for each layer, xn = rms_norm(h, 1)
+    (src/Gemm.cpp:197-207), then h += 1 * FFN(xn) with gemm::axpy
+    (src/Gemm.cpp:191-195).  ``layers`` is a list of ("dense", (gate, up, down))
+    or ("moe", MoeLayer); h [T, H] is not modified.  Returns the final h, or
+    with every_layer the hidden state after each layer."""
+    h = np.array(h, dtype=np.float32, copy=True)
+    T, H = h.shape
+    ones = np.ones(H, np.float32)
+    o = oracle()
+    states = []
+    for kind, data in layers:
+        xn = h.copy()
+        for t in range(T):
+            o.orc_rms_norm(p(xn[t]), p(ones), H, eps)
+        y = oracle_dense(*data, xn) if kind == "dense" else oracle_moe_layer(data, xn)[0]
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        for t in range(T):
+            o.orc_axpy(1.0, p(y[t]), p(h[t]), H)
+        states.append(h.copy())
+    return states if every_layer else h
