@@ -32,7 +32,10 @@ constexpr int kRpw = 4;                      // gate rows (and as many up rows) 
 constexpr int kItemRows = kRpw * kWaves;     // gate rows per gate/up item
 
 struct DecodeArgs {
-    const float* x;            // [H] the token
+    const float* x;            // [H] the token (the hidden state when norm is set)
+    const float* norm;         // [H] RMSNorm weight applied to x first, or null (x is already normalised)
+    float eps;
+    float* xnorm;              // [H] the normalised token (written by router workgroup 0 when norm is set)
     const float* wq;           // [E/4][H][4] router gate, four experts per contiguous slice
     const float* bias;         // [E] or null
     float* logits;             // [E] exact logits (hand-off to the selecting workgroup)
@@ -90,6 +93,74 @@ __device__ inline void load_act_coherent(const float* row, int width, int lane, 
     }
 }
 
+// RMSNorm of the token inside the launch (the stack's T = 1 step): the inverse
+// of gemm::rms_norm (src/Gemm.cpp:197-207) with the arithmetic of
+// rms_norm_kernel (thread-strided double sums of exact squares, wave
+// butterfly, then (w0 + w1) + (w2 + w3)), so the normalised token is the same
+// bits as the separate kernel's.  The token's elements are loaded first
+// (norm_load: issue them before any weight stream, so waiting for them waits
+// for nothing else) and reduced by norm_reduce, which every thread of the
+// workgroup calls; its barrier orders LDS only.
+static_assert(kWaves == 4, "norm_reduce combines four wave sums");
+template <int N>
+__device__ inline void norm_load(const DecodeArgs& a, float (&v)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int c = static_cast<int>(threadIdx.x) + k * kThreads;
+        v[k] = c < a.hidden ? a.x[c] : 0.0f;
+    }
+}
+
+template <int N>
+__device__ inline float norm_reduce(const DecodeArgs& a, const float (&v)[N]) {
+    __shared__ double part[kWaves];
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (static_cast<int>(threadIdx.x) + k * kThreads < a.hidden) {
+            const double d = static_cast<double>(v[k]);
+            s = s + d * d;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        s += __shfl_xor(s, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = s;
+    }
+    lds_barrier();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(a.hidden) + static_cast<double>(a.eps)));
+}
+
+// Elements per thread of norm_load for a hidden width covered by GI 512-column steps.
+template <int GI>
+constexpr int norm_elems() { return 2 * GI; }
+
+// Element c of the token as the FFN sees it: normalised when a.norm is set.
+__device__ inline float token_at(const DecodeArgs& a, int c, float inverse) {
+    const float v = a.x[c];
+    if (a.norm == nullptr) {
+        return v;
+    }
+    const float scaled = v * inverse;
+    return scaled * a.norm[c];
+}
+
+__device__ inline float4 token4_at(const DecodeArgs& a, const float4 v, int c, float inverse) {
+    if (a.norm == nullptr) {
+        return v;
+    }
+    const float4 w = *reinterpret_cast<const float4*>(a.norm + c);
+    float4 r;
+    r.x = (v.x * inverse) * w.x;
+    r.y = (v.y * inverse) * w.y;
+    r.z = (v.z * inverse) * w.z;
+    r.w = (v.w * inverse) * w.w;
+    return r;
+}
+
 // ---- roles -------------------------------------------------------------------
 
 // Logits of experts [e0, e0 + 4) with LiteMind's dot (src/Gemm.cpp:183-189):
@@ -98,12 +169,18 @@ __device__ inline void load_act_coherent(const float* row, int width, int lane, 
 // [H][4] weights; then lane e adds its expert's products strictly left to
 // right, at raised wave priority (the chain shares its SIMD with streaming
 // waves).  after_load runs on every thread once the products are in LDS.
-template <typename AfterLoad>
+template <int GI, typename AfterLoad>
 __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4* prod, AfterLoad after_load) {
     const int tid = threadIdx.x;
     const int H = a.hidden;
     const float4* slice = reinterpret_cast<const float4*>(a.wq) + static_cast<int64_t>(e0 / 4) * H;
     float* pf = reinterpret_cast<float*>(prod);
+    float inverse = 1.0f;
+    if (a.norm != nullptr) {
+        float v[norm_elems<GI>()];
+        norm_load(a, v);
+        inverse = norm_reduce(a, v);
+    }
     for (int hb = 0; hb < H; hb += kThreads * 8) {
         float4 w[8];
         float xv[8];
@@ -112,7 +189,12 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
             const int h = hb + j * kThreads + tid;
             const int hc = h < H ? h : H - 1;
             w[j] = slice[hc];
-            xv[j] = a.x[hc];
+            xv[j] = token_at(a, hc, inverse);
+            if (a.norm != nullptr && e0 == 0 && h < H) {
+                // the repair path's copy: y may overwrite x (the stack updates the
+                // hidden state in place) once every router and gate/up item is done
+                store_coherent(a.xnorm + h, xv[j]);
+            }
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -221,13 +303,18 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
         const int f = static_cast<int>(threadIdx.x) + i * kThreads;
         xv[i] = x4[f < n4 ? f : n4 - 1];
     }
+    float nv[norm_elems<GI>()];
+    if (a.norm != nullptr) {
+        norm_load(a, nv);
+    }
     load_rows<R, GI>(rows, a.hidden, lane, w);
+    const float inverse = a.norm != nullptr ? norm_reduce(a, nv) : 1.0f;
     float4* xs4 = reinterpret_cast<float4*>(xs);
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
         const int f = static_cast<int>(threadIdx.x) + i * kThreads;
         if (f < n4) {
-            xs4[f] = xv[i];
+            xs4[f] = token4_at(a, xv[i], 4 * f, inverse);
         }
     }
     lds_barrier();
@@ -436,7 +523,9 @@ __device__ void repair_act_row(const DecodeArgs& a, int e, float* act_row) {
         for (int c = 0; c < a.hidden; c += 8) {
             const uint4 wg = *reinterpret_cast<const uint4*>(g + c);
             const uint4 wu = *reinterpret_cast<const uint4*>(u + c);
-            const float4 x0 = x4[c / 4], x1 = x4[c / 4 + 1];
+            // with the norm fused, the normalised copy (x itself may be overwritten)
+            const float4 x0 = a.norm != nullptr ? load_coherent4(a.xnorm + c) : x4[c / 4];
+            const float4 x1 = a.norm != nullptr ? load_coherent4(a.xnorm + c + 4) : x4[c / 4 + 1];
             fma8(gate, wg, x0, x1);
             fma8(up, wu, x0, x1);
         }
@@ -632,7 +721,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     }
     if (b < f.n_router) {
         const int e0 = b * kRouterExperts;
-        router_slice(a, e0, lds, [&] { speculate(f, sync, e0, lds); });
+        router_slice<GI>(a, e0, lds, [&] { speculate(f, sync, e0, lds); });
         // The last router workgroup to finish its exact logits selects for the output.
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
@@ -744,13 +833,16 @@ bool decode_supported(int hidden, int experts, int top_k, int inter_p, int share
 
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     const int hidden = d.hidden, top_k = d.policy.top_k, inter_p = d.inter_p;
-    if (d.sync == nullptr || d.shared_gu == nullptr ||
+    if (d.sync == nullptr || d.shared_gu == nullptr || (d.norm != nullptr && d.xnorm == nullptr) ||
         !decode_supported(hidden, d.policy.experts, top_k, inter_p, d.shared_inter_p)) {
         return hipErrorInvalidValue;
     }
     FusedArgs f{};
     DecodeArgs& a = f.a;
     a.x = d.x;
+    a.norm = d.norm;
+    a.eps = d.eps;
+    a.xnorm = d.xnorm;
     a.wq = d.wq;
     a.bias = d.bias;
     a.logits = d.logits;

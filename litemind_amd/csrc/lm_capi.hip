@@ -420,7 +420,7 @@ bool decode_eligible(const lm_context* ctx, const Layer& L) {
 // experts sit back to back in the layer slab, so expert e's FFN is found by
 // offset.  Stage timing sees one launch, attributed to the gate/up stage.
 int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const float* residual, const float* bias,
-                 int32_t* idx, float* wts, float* logits_out) {
+                 int32_t* idx, float* wts, float* logits_out, const float* norm) {
     if (ctx->ws.decode_sync == nullptr) {
         const size_t bytes = sizeof(uint32_t) * lm::kDecodeSyncWords;
         LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_sync), bytes));
@@ -428,6 +428,9 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     }
     lm::DecodeLaunch d{};
     d.x = x;
+    d.norm = norm;
+    d.eps = ctx->cfg.rms_norm_eps;
+    d.xnorm = ctx->ws.xnorm;
     d.wq = L.router_t + static_cast<size_t>(ctx->H) * ctx->E;
     d.bias = bias;
     d.logits = ctx->ws.logit_scratch;
@@ -464,8 +467,10 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     return stage_finish(ctx);
 }
 
+// norm: when set, x is the hidden state and the block's input is rms_norm(x, norm).
 int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
-              const float* bias, int32_t* idx_out, float* w_out, float* logits_out, int32_t path) {
+              const float* bias, int32_t* idx_out, float* w_out, float* logits_out, int32_t path,
+              const float* norm = nullptr) {
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
     if (!L.allocated || L.dense || L.router_t == nullptr) {
         return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no resident MoE weights");
@@ -482,7 +487,11 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     float* wts = w_out != nullptr ? w_out : ctx->ws.wts;
 
     if (T == 1 && !mfma && decode_eligible(ctx, L)) {
-        return decode_layer(ctx, L, x, y, residual, bias, idx, wts, logits_out);
+        return decode_layer(ctx, L, x, y, residual, bias, idx, wts, logits_out, norm);
+    }
+    if (norm != nullptr) {
+        LM_HIP(lm::launch_rms_norm(x, norm, ctx->ws.xnorm, T, ctx->H, ctx->cfg.rms_norm_eps, ctx->stream));
+        x = ctx->ws.xnorm;
     }
 
     lm::RouterArgs ra{};
@@ -1193,14 +1202,16 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
         if (L.norm == nullptr) {
             return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no norm weight");
         }
-        // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290, attention omitted).
-        LM_HIP(lm::launch_rms_norm(hidden_dev, L.norm, ctx->ws.xnorm, tokens, ctx->H, ctx->cfg.rms_norm_eps,
-                                   ctx->stream));
+        // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290, attention omitted).  The
+        // MoE block normalises the hidden state itself (inside the single-token
+        // launch, or with rms_norm_kernel before the batched path).
         if (L.dense) {
+            LM_HIP(lm::launch_rms_norm(hidden_dev, L.norm, ctx->ws.xnorm, tokens, ctx->H, ctx->cfg.rms_norm_eps,
+                                       ctx->stream));
             rc = dense_layer(ctx, l, ctx->ws.xnorm, tokens, hidden_dev, hidden_dev, path);
         } else {
-            rc = moe_layer(ctx, l, ctx->ws.xnorm, tokens, hidden_dev, hidden_dev, nullptr, nullptr, nullptr, nullptr,
-                           path);
+            rc = moe_layer(ctx, l, hidden_dev, tokens, hidden_dev, hidden_dev, nullptr, nullptr, nullptr, nullptr,
+                           path, L.norm);
         }
         if (rc != LM_OK) {
             return rc;

@@ -145,7 +145,10 @@ struct SelectPolicy {
 
 // The single-token MoE block (k_decode.hip).
 struct DecodeLaunch {
-    const float* x;             // [H]
+    const float* x;             // [H] the token, or the hidden state when norm is set
+    const float* norm;          // [H] RMSNorm weight applied inside the launch, or null
+    float eps;
+    float* xnorm;               // [H] scratch: the normalised token (needed when norm is set)
     const float* wq;            // [E/4][H][4] router gate, four experts per contiguous slice
     const float* bias;          // [E] or null
     float* logits;              // [E] scratch

@@ -108,3 +108,24 @@ def test_stack_tokens_independent(stack_ctx):
     single = np.stack([_run(ctx, h0[t:t + 1])[0] for t in pick])
     _, mean_rel = layer_error(batch[pick], single)
     assert mean_rel < MEAN_REL
+
+
+def test_stack_t1_speculation_recovery(stack_ctx):
+    """Every speculative rank forced wrong in every MoE layer of the chain: the
+    repair path recomputes the ranks from the normalised token (the hidden
+    state itself is updated in place by the same launch) and the chain still
+    matches the oracle."""
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    h0 = wl.tokens(wl.MASTER_SEED + 703, 1, dims.hidden)
+    announce("stack T=1 with every speculative rank forced wrong")
+    ctx._check(ctx.lib.lm_decode_speculation_test(ctx.handle, 1))
+    try:
+        h = _run(ctx, h0)
+    finally:
+        ctx._check(ctx.lib.lm_decode_speculation_test(ctx.handle, 0))
+    oh = ol.oracle_stack(layers, h0, dims.rms_norm_eps)
+    max_abs, mean_rel = layer_error(h, oh)
+    print(f"stack T=1 forced repair max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert max_abs <= MAX_ABS and mean_rel < 1e-5
