@@ -48,13 +48,15 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic(tokens: int, distinct_experts: int) -> dict:
-    """Bytes and flops of one MoE layer step (weights read once, activations in/out)."""
+def algorithmic(tokens: int, distinct_experts: int, act_bytes: int = 4) -> dict:
+    """Bytes and flops of one MoE layer step (weights read once, activations in/out).
+    act_bytes: width of the expert kernels' input and intermediate activations
+    (fp32 on the GEMV path, fp16 panels on the MFMA path)."""
     T, U = tokens, distinct_experts
     H, I, S, K = 2048, 1408, 2816, 6
     layer_bytes = U * EXPERT_BYTES + SHARED_BYTES + ROUTER_BYTES + T * H * 4 * 2
-    gate_up_bytes = U * GATEUP_EXPERT_BYTES + 2 * S * H * 2 + T * H * 4 + (T * K * I + T * S) * 4
-    down_bytes = U * DOWN_EXPERT_BYTES + S * H * 2 + (T * K * I + T * S) * 4 + (T * K + T) * H * 4
+    gate_up_bytes = U * GATEUP_EXPERT_BYTES + 2 * S * H * 2 + T * H * act_bytes + (T * K * I + T * S) * act_bytes
+    down_bytes = U * DOWN_EXPERT_BYTES + S * H * 2 + (T * K * I + T * S) * act_bytes + (T * K + T) * H * 4
     flops_assign = 6 * H * I
     layer_flops = T * K * flops_assign + T * 6 * H * S + T * 2 * 64 * H
     gate_up_flops = T * K * 4 * H * I + T * 4 * H * S
@@ -208,17 +210,22 @@ def roofline(res: dict, mfma: bool) -> dict:
     per = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
     dominant = max(("gate_up", "down"), key=lambda k: per[k])
     dur_s = per[dominant] / 1e3
+    alg = algorithmic(res["T"], int(round(res["distinct"])), 2 if mfma else 4)
+    by, fl = alg[f"{dominant}_bytes"], alg[f"{dominant}_flops"]
+    gbs, tfs = by / dur_s / 1e9, fl / dur_s / 1e12
+    # The bound is the resource whose peak gives the longer floor for this
+    # launch (the GEMV path's fp32 VALU work never does at its token counts).
+    mfma_bound = mfma and fl / (MFMA_PEAK_TFLOPS * 1e12) > by / (HBM_PEAK_GBS * 1e9)
+    out = {"bound": "mfma" if mfma_bound else "hbm", "kernel": dominant}
+    if mfma_bound:
+        out.update(achieved=round(tfs, 2), peak=MFMA_PEAK_TFLOPS, unit="TFLOP/s", frac=round(tfs / MFMA_PEAK_TFLOPS, 4))
+    else:
+        out.update(achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4))
+    out.update(traffic=None, avg_us=round(per[dominant] * 1e3, 2), algorithmic_bytes=by, algorithmic_flops=fl,
+               hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     if mfma:
-        fl = alg[f"{dominant}_flops"]
-        achieved = fl / dur_s / 1e12
-        return {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                "avg_us": round(per[dominant] * 1e3, 2), "algorithmic_flops": fl}
-    by = alg[f"{dominant}_bytes"]
-    achieved = by / dur_s / 1e9
-    return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_us": round(per[dominant] * 1e3, 2),
-            "algorithmic_bytes": by}
+        out["mfma_frac"] = round(tfs / MFMA_PEAK_TFLOPS, 4)
+    return out
 
 
 def swiglu(res: dict) -> dict:
@@ -261,6 +268,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    import litemind_amd as lm
     from litemind_amd import workload as wl
 
     main_w = wl.WORKLOADS[args.workload]
@@ -268,7 +276,7 @@ def main() -> int:
     res = run_gpu(args.workload, args.steps, args.warmup, rotate, args.path)
     T = res["T"]
     ms = res["wall_s"] * 1e3 / res["steps"]
-    mfma_main = T > 64 if args.path == 0 else args.path == 2
+    mfma_main = T > lm.MFMA_CROSSOVER if args.path == 0 else args.path == 2
     line = {
         "metric": METRIC, "value": round(T / (ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
@@ -298,7 +306,7 @@ def main() -> int:
         w2 = wl.WORKLOADS[args.second]
         res2 = run_gpu(args.second, max(10, args.steps // 10), max(3, args.warmup // 4), 1, args.path)
         ms2 = res2["wall_s"] * 1e3 / res2["steps"]
-        mfma2 = w2.tokens > 64 if args.path == 0 else args.path == 2
+        mfma2 = w2.tokens > lm.MFMA_CROSSOVER if args.path == 0 else args.path == 2
         line["t2048" if w2.tokens == 2048 else args.second] = {
             "workload": args.second, "tokens": w2.tokens, "value": round(w2.tokens / (ms2 / 1e3), 1),
             "unit": "tokens/s", "ms_per_step": round(ms2, 4), "steps": res2["steps"],

@@ -56,9 +56,10 @@ typedef struct lm_moe_config {
 } lm_moe_config;
 
 /* Expert-path selection for lm_moe_forward. */
-#define LM_PATH_AUTO 0  /* GEMV below the crossover token count, MFMA above */
+#define LM_PATH_AUTO 0  /* GEMV up to LM_MFMA_CROSSOVER tokens, MFMA above */
 #define LM_PATH_GEMV 1  /* fp32-activation weight-streaming kernels */
 #define LM_PATH_MFMA 2  /* fp16-operand MFMA grouped GEMM, fp32 accumulate */
+#define LM_MFMA_CROSSOVER 2  /* LM_PATH_AUTO: token counts above this take the MFMA path */
 
 /* ---- errors, context ---- */
 const char* lm_last_error(void);

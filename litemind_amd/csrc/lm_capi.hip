@@ -51,9 +51,12 @@ int fail(int code, const std::string& message) {
 constexpr int kStages = 5;
 constexpr int kEventRing = 256;
 // Token count above which LM_PATH_AUTO switches from weight-streaming GEMV to
-// the MFMA grouped GEMM (the GEMV's fp32 VALU work reaches the HBM time of the
-// expert weights at roughly 100 tokens).
-constexpr int64_t kMfmaCrossover = 64;
+// the MFMA grouped GEMM.  Both stream every active expert's weights once; the
+// MFMA kernel does it through a deep LDS-DMA pipeline and reaches more of the
+// HBM bandwidth from three tokens on (T = 3: 130 us against 137 us per V2-Lite
+// MoE block, T = 32: 257 against 447 us), while two tokens still favour the
+// GEMV's register-held weight rows (114 against 126 us).
+constexpr int64_t kMfmaCrossover = LM_MFMA_CROSSOVER;
 
 struct Layer {
     bool allocated = false;

@@ -42,9 +42,9 @@ def _oracle_route(layer, x, bias=None):
 @pytest.mark.parametrize("case", ["t1", "t5", "t32", "t100_ragged", "t512_uniform", "t2048_skewed", "t4096",
                                   "t4100_ragged"])
 def test_router_bit_exact_v2lite(v2_ctx, case):
-    """Every router kernel shape: single token, decode batch, the per-wave
-    kernel, and the wide kernel with one, two and four tokens per wave,
-    including partial last workgroups."""
+    """Every router kernel of the V2-Lite shape: the single-token split kernel,
+    and the wide kernel from a few tokens (one partly filled workgroup) up to
+    one, two and four tokens per wave, including partial last workgroups."""
     from litemind_amd import workload as wl
 
     ctx, layers = v2_ctx
@@ -59,6 +59,29 @@ def test_router_bit_exact_v2lite(v2_ctx, case):
     assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32)), "logits differ"
     assert np.array_equal(g_idx, o_idx), "selected experts differ"
     assert np.array_equal(g_w.view(np.uint32), o_w.view(np.uint32)), "weights differ"
+
+
+@pytest.mark.parametrize("T", [2, 4, 37])
+def test_router_bit_exact_32_experts(T):
+    """A 32-expert gate (H = 512) is outside the wide kernel's shape, so T <= 4
+    runs the 16-wave few-token kernel and larger batches the per-wave kernel."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = wl.Dims(hidden=512, inter=128, experts=32, top_k=4, n_shared=1, dense_inter=256, layers=1,
+                   norm_topk_prob=True, routed_scaling_factor=2.0)
+    layer = wl.moe_layer(wl.MASTER_SEED + 5, 0, dims)
+    x = wl.tokens(wl.MASTER_SEED + 100 + T, T, dims.hidden)
+    announce(f"router 32 experts H=512 T={T}")
+    ctx = Context(dims.moe_config(num_layers=1))
+    try:
+        wl.upload_moe_layer(ctx, 0, layer)
+        g = _gpu_route(ctx, 0, x)
+    finally:
+        ctx.close()
+    o = _oracle_route(layer, x)
+    for a, b in zip(g, o):
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
 
 
 def test_router_tiny_model(tiny_ctx):
