@@ -175,6 +175,17 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
     const int H = a.hidden;
     const float4* slice = reinterpret_cast<const float4*>(a.wq) + static_cast<int64_t>(e0 / 4) * H;
     float* pf = reinterpret_cast<float*>(prod);
+    auto load_block = [&](int hb, float4 (&w)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int h = hb + j * kThreads + tid;
+            w[j] = slice[h < H ? h : H - 1];
+        }
+    };
+    // The slice's first rows are requested before the norm's token loads, so
+    // the two round trips overlap instead of running one after the other.
+    float4 w[8];
+    load_block(0, w);
     float inverse = 1.0f;
     if (a.norm != nullptr) {
         float v[norm_elems<GI>()];
@@ -182,13 +193,14 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
         inverse = norm_reduce(a, v);
     }
     for (int hb = 0; hb < H; hb += kThreads * 8) {
-        float4 w[8];
+        if (hb > 0) {
+            load_block(hb, w);
+        }
         float xv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int h = hb + j * kThreads + tid;
             const int hc = h < H ? h : H - 1;
-            w[j] = slice[hc];
             xv[j] = token_at(a, hc, inverse);
             if (a.norm != nullptr && e0 == 0 && h < H) {
                 // the repair path's copy: y may overwrite x (the stack updates the
