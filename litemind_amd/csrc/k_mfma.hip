@@ -22,12 +22,16 @@
 // in LDS with their chunks permuted (row_swizzle), which keeps the MFMA fragment
 // reads free of bank conflicts.
 //
-// Per workgroup: WAVES waves of 64 x 128 (2 x 4 MFMA blocks of 32 x 32, 128
-// accumulator registers) over a BM x 256 tile, BM = 32 WAVES, K step 32, and a
-// STAGES-deep pipeline: while stage k is multiplied, stages k + 1 .. k +
-// STAGES - 1 are in flight, each in its own LDS array so the compiler can track
-// the asynchronous writes per buffer.  Rows past the end of a group (tokens) or
-// of a matrix (weight rows) load a clamped row and are never stored.
+// Per workgroup: a WM x WN grid of waves, each computing MI x NJ MFMA blocks of
+// 32 x 32, over a BM x 256 tile (BM = 32 WM MI), K step 32, and a STAGES-deep
+// pipeline: while stage k is multiplied, stages k + 1 .. k + STAGES - 1 are in
+// flight, each in its own LDS array so the compiler can track the asynchronous
+// writes per buffer.  Rows past the end of a group (tokens) or of a matrix
+// (weight rows) load a clamped row and are never stored.  Two shapes:
+//   128 x 256, 2 x 2 waves of 64 x 128, 3 stages (24 KB each): large groups;
+//    64 x 256, 1 x 4 waves of 64 x 64, 4 stages (20 KB each): groups of a few
+//    dozen rows, where the kernel streams weights and the bytes in flight
+//    per CU (two workgroups x (STAGES - 1) x 16 KB of weights) set its rate.
 #include "lm_internal.h"
 
 namespace lm {
@@ -44,20 +48,26 @@ constexpr int kRowBytes = BK * 2;
 constexpr int kBBytes = BN * kRowBytes;      // 16 KB
 constexpr int kXcds = 8;
 
-template <int WAVES, int STAGES>
+template <int WM, int WN, int MI, int NJ, int STAGES>
 struct Shape {
+    static constexpr int WAVES = WM * WN;
     static constexpr int kThreads = 64 * WAVES;
-    static constexpr int BM = 32 * WAVES;
+    static constexpr int BM = 32 * WM * MI;
     static constexpr int kABytes = BM * kRowBytes;
     static constexpr int kALoads = kABytes / 1024 / WAVES;  // wave instructions per stage
     static constexpr int kBLoads = kBBytes / 1024 / WAVES;
     static constexpr int kLoadsPerStage = kALoads + kBLoads;
+    static_assert(32 * WN * NJ == BN, "the waves cover the 256 columns");
+    static_assert(kALoads * 1024 * WAVES == kABytes && kALoads >= 1, "whole A instructions per wave");
+    static_assert(NJ % 2 == 0, "gate/up column blocks come in pairs");
+    static_assert((STAGES - 2) * kLoadsPerStage < 16, "vmcnt immediate");
 };
 
-// Tile configuration: 4 waves of 64 x 128 (128 x 256 tiles) with three stages,
-// two workgroups per CU.
-constexpr int kWaves = 4;
-constexpr int kStages = 3;
+// Launches whose average group fits one 64-row tile (T k <= 64 E) take the
+// 64-row shape.  Measured on V2-Lite (one MoE block, 64 experts, k 6): 8-12%
+// faster from T = 8 to T = 512, 4-13% slower from T = 768 on, where groups
+// span several 64-row tiles and each re-streams the expert's weights.
+constexpr int64_t kNarrowRows = 64;
 
 enum Mode { kGateUp = 0, kDown = 1 };
 
@@ -73,10 +83,11 @@ struct TileInfo {
 // one column block are consecutive.  Workgroup b runs on XCD b % 8: XCD x gets
 // the x-th of eight contiguous, equal (within one) ranges of the tiles that
 // exist, so the M tiles of a column block share one L2 and no XCD is left with
-// only the empty tail of the grid.
+// only the empty tail of the grid.  s_info: 3 ints of LDS for the hand-off
+// from wave 0 (the caller lends a pipeline buffer that no load writes before
+// every wave has passed a later barrier).
 __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_routed, int nt_shared,
-                            TileInfo& ti) {
-    __shared__ int s_info[4];
+                            TileInfo& ti, int* s_info) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
         const int g = lane;
@@ -149,10 +160,11 @@ __device__ inline int row_swizzle(int r) { return ((r >> 2) & 3) ^ (r & 2); }
 // LDS byte offset of the 16-byte chunk c of row r.
 __device__ inline int chunk_offset(int r, int c) { return r * kRowBytes + ((c ^ row_swizzle(r)) << 4); }
 
-template <int MODE, int WAVES, int STAGES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_grouped_kernel(
+template <int MODE, int WM, int WN, int MI, int NJ, int STAGES>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_grouped_kernel(
     ExpertArgs a) {
-    using S = Shape<WAVES, STAGES>;
+    using S = Shape<WM, WN, MI, NJ, STAGES>;
+    constexpr int WAVES = S::WAVES;
     constexpr int BM = S::BM;
     // One LDS array per stage (A tile, then B tile): the compiler tracks the
     // asynchronous LDS writes per array and only a few arrays individually.
@@ -165,13 +177,17 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
     const int inter_p = a.inter_p;
     const int n_routed = MODE == kGateUp ? 2 * inter_p : a.hidden;  // weight rows
     const int n_shared = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
     TileInfo ti;
-    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, ti)) {
+    // The last stage buffer holds the tile hand-off: the prologue never loads
+    // into it, and the first load that does follows the main loop's first
+    // barrier, after every wave has read its tile.
+    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, ti,
+                     reinterpret_cast<int*>(As[STAGES - 1]))) {
         return;
     }
     const bool shared = ti.g >= a.experts;
@@ -226,11 +242,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         }
     };
 
-    floatx16 acc[2][4];
+    floatx16 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MI; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             acc[i][j] = floatx16{};
         }
     }
@@ -238,21 +254,21 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             const int c = 2 * kk + (lane >> 5);
-            half8 af[2], bf[4];
+            half8 af[MI], bf[NJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = wm * 64 + i * 32 + (lane & 31);
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * (32 * MI) + i * 32 + (lane & 31);
                 af[i] = *reinterpret_cast<const half8*>(as + chunk_offset(r, c));
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = wn * 128 + j * 32 + (lane & 31);
+            for (int j = 0; j < NJ; ++j) {
+                const int r = wn * (32 * NJ) + j * 32 + (lane & 31);
                 bf[j] = *reinterpret_cast<const half8*>(bs + chunk_offset(r, c));
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < MI; ++i) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
                 }
             }
@@ -316,19 +332,19 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     // m = 8 (r / 4) + 4 (l / 32) + r % 4 for registers r = 0..15.
     const int n = lane & 31;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MI; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m_local = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int m_local = wm * (32 * MI) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             const int m = ti.mt * BM + m_local;
             if (m >= ti.rows) {
                 continue;
             }
             if (MODE == kGateUp) {
-                // Blocks (0, 1) and (2, 3) are the gate and up of two 32-column groups.
+                // Blocks (2p, 2p + 1) are the gate and up of one 32-column group.
 #pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    const int jcol = (ti.nt * BN) / 2 + wn * 64 + p * 32 + n;
+                for (int p = 0; p < NJ / 2; ++p) {
+                    const int jcol = (ti.nt * BN) / 2 + wn * (16 * NJ) + p * 32 + n;
                     if (jcol < width_p) {
                         const float h = silu_fast(acc[i][2 * p][r], acc[i][2 * p + 1][r]);
                         act_base[panel_index(act_slot0 + m, jcol, act_rows)] = static_cast<_Float16>(h);
@@ -336,8 +352,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int h = ti.nt * BN + wn * 128 + j * 32 + n;
+                for (int j = 0; j < NJ; ++j) {
+                    const int h = ti.nt * BN + wn * (32 * NJ) + j * 32 + n;
                     if (h < a.hidden) {
                         a.down_out[(ti.slot0 + m) * a.hidden + h] = acc[i][j][r];
                     }
@@ -359,6 +375,17 @@ int64_t tile_bound(const ExpertArgs& a, int BM, int nt_routed, int nt_shared) {
     return (tiles + kXcds - 1) / kXcds * kXcds;
 }
 
+template <int MODE, int WM, int WN, int MI, int NJ, int STAGES>
+hipError_t launch_shape(const ExpertArgs& a, hipStream_t s) {
+    using S = Shape<WM, WN, MI, NJ, STAGES>;
+    const int nr = MODE == kGateUp ? 2 * a.inter_p : a.hidden;
+    const int ns = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
+    const int64_t grid = tile_bound(a, S::BM, (nr + BN - 1) / BN, (ns + BN - 1) / BN);
+    hipLaunchKernelGGL((mfma_grouped_kernel<MODE, WM, WN, MI, NJ, STAGES>), dim3(static_cast<unsigned>(grid)),
+                       dim3(S::kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int MODE>
 hipError_t launch(const ExpertArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
@@ -367,13 +394,10 @@ hipError_t launch(const ExpertArgs& a, hipStream_t s) {
     if (a.hidden_p % BK != 0 || a.inter_p % BK != 0 || (a.has_shared && a.shared_inter_p % BK != 0)) {
         return hipErrorInvalidValue;
     }
-    using S = Shape<kWaves, kStages>;
-    const int nr = MODE == kGateUp ? 2 * a.inter_p : a.hidden;
-    const int ns = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
-    const int64_t grid = tile_bound(a, S::BM, (nr + BN - 1) / BN, (ns + BN - 1) / BN);
-    hipLaunchKernelGGL((mfma_grouped_kernel<MODE, kWaves, kStages>), dim3(static_cast<unsigned>(grid)),
-                       dim3(S::kThreads), 0, s, a);
-    return hipGetLastError();
+    if (a.tokens * a.top_k <= kNarrowRows * a.experts) {
+        return launch_shape<MODE, 1, 4, 2, 2, 4>(a, s);
+    }
+    return launch_shape<MODE, 2, 2, 2, 4, 3>(a, s);
 }
 
 }  // namespace
