@@ -34,41 +34,44 @@ LM_HD inline float bits_float(uint32_t u) { return __builtin_bit_cast(float, u);
 LM_HD inline float widen_bf16(uint16_t bits) { return bits_float(static_cast<uint32_t>(bits) << 16); }
 
 // 2^(i/32) as double bits, with i << 47 subtracted so adding k << 47 scales by 2^(k/32).
+// A select tree over the five index bits: on the GPU the index differs from
+// lane to lane, so a switch would compile to a tree of divergent branches that
+// every wave walks in full, and a table in memory would put a load behind the
+// kernel's weight stream in the in-order memory queue.
 LM_HD inline uint64_t exp2_table(uint32_t i) {
-    switch (i & 31u) {
-        case 0: return 0x3ff0000000000000ull;
-        case 1: return 0x3fefd9b0d3158574ull;
-        case 2: return 0x3fefb5586cf9890full;
-        case 3: return 0x3fef9301d0125b51ull;
-        case 4: return 0x3fef72b83c7d517bull;
-        case 5: return 0x3fef54873168b9aaull;
-        case 6: return 0x3fef387a6e756238ull;
-        case 7: return 0x3fef1e9df51fdee1ull;
-        case 8: return 0x3fef06fe0a31b715ull;
-        case 9: return 0x3feef1a7373aa9cbull;
-        case 10: return 0x3feedea64c123422ull;
-        case 11: return 0x3feece086061892dull;
-        case 12: return 0x3feebfdad5362a27ull;
-        case 13: return 0x3feeb42b569d4f82ull;
-        case 14: return 0x3feeab07dd485429ull;
-        case 15: return 0x3feea47eb03a5585ull;
-        case 16: return 0x3feea09e667f3bcdull;
-        case 17: return 0x3fee9f75e8ec5f74ull;
-        case 18: return 0x3feea11473eb0187ull;
-        case 19: return 0x3feea589994cce13ull;
-        case 20: return 0x3feeace5422aa0dbull;
-        case 21: return 0x3feeb737b0cdc5e5ull;
-        case 22: return 0x3feec49182a3f090ull;
-        case 23: return 0x3feed503b23e255dull;
-        case 24: return 0x3feee89f995ad3adull;
-        case 25: return 0x3feeff76f2fb5e47ull;
-        case 26: return 0x3fef199bdd85529cull;
-        case 27: return 0x3fef3720dcef9069ull;
-        case 28: return 0x3fef5818dcfba487ull;
-        case 29: return 0x3fef7c97337b9b5full;
-        case 30: return 0x3fefa4afa2a490daull;
-        default: return 0x3fefd0765b6e4540ull;
-    }
+    const bool b0 = (i & 1u) != 0, b1 = (i & 2u) != 0, b2 = (i & 4u) != 0, b3 = (i & 8u) != 0,
+               b4 = (i & 16u) != 0;
+    const uint64_t v0 = b0 ? 0x3fefd9b0d3158574ull : 0x3ff0000000000000ull;
+    const uint64_t v1 = b0 ? 0x3fef9301d0125b51ull : 0x3fefb5586cf9890full;
+    const uint64_t v2 = b0 ? 0x3fef54873168b9aaull : 0x3fef72b83c7d517bull;
+    const uint64_t v3 = b0 ? 0x3fef1e9df51fdee1ull : 0x3fef387a6e756238ull;
+    const uint64_t v4 = b0 ? 0x3feef1a7373aa9cbull : 0x3fef06fe0a31b715ull;
+    const uint64_t v5 = b0 ? 0x3feece086061892dull : 0x3feedea64c123422ull;
+    const uint64_t v6 = b0 ? 0x3feeb42b569d4f82ull : 0x3feebfdad5362a27ull;
+    const uint64_t v7 = b0 ? 0x3feea47eb03a5585ull : 0x3feeab07dd485429ull;
+    const uint64_t v8 = b0 ? 0x3fee9f75e8ec5f74ull : 0x3feea09e667f3bcdull;
+    const uint64_t v9 = b0 ? 0x3feea589994cce13ull : 0x3feea11473eb0187ull;
+    const uint64_t v10 = b0 ? 0x3feeb737b0cdc5e5ull : 0x3feeace5422aa0dbull;
+    const uint64_t v11 = b0 ? 0x3feed503b23e255dull : 0x3feec49182a3f090ull;
+    const uint64_t v12 = b0 ? 0x3feeff76f2fb5e47ull : 0x3feee89f995ad3adull;
+    const uint64_t v13 = b0 ? 0x3fef3720dcef9069ull : 0x3fef199bdd85529cull;
+    const uint64_t v14 = b0 ? 0x3fef7c97337b9b5full : 0x3fef5818dcfba487ull;
+    const uint64_t v15 = b0 ? 0x3fefd0765b6e4540ull : 0x3fefa4afa2a490daull;
+    const uint64_t w0 = b1 ? v1 : v0;
+    const uint64_t w1 = b1 ? v3 : v2;
+    const uint64_t w2 = b1 ? v5 : v4;
+    const uint64_t w3 = b1 ? v7 : v6;
+    const uint64_t w4 = b1 ? v9 : v8;
+    const uint64_t w5 = b1 ? v11 : v10;
+    const uint64_t w6 = b1 ? v13 : v12;
+    const uint64_t w7 = b1 ? v15 : v14;
+    const uint64_t x0 = b2 ? w1 : w0;
+    const uint64_t x1 = b2 ? w3 : w2;
+    const uint64_t x2 = b2 ? w5 : w4;
+    const uint64_t x3 = b2 ? w7 : w6;
+    const uint64_t y0 = b3 ? x1 : x0;
+    const uint64_t y1 = b3 ? x3 : x2;
+    return b4 ? y1 : y0;
 }
 
 // expf as glibc 2.35 computes it on an FMA-capable x86-64 host (see the header).
