@@ -7,14 +7,19 @@
 // increasing a (token, then rank).  Positions come from ballots and prefix sums,
 // never from atomic arrival order, so the permutation is deterministic.
 //
-// One workgroup of 16 waves.  Wave w owns a contiguous segment of the
-// assignment list, walked in 64-entry steps.  In each step every lane finds the
-// lanes holding the same expert as itself from six ballots (one per bit of the
-// expert id); its rank among them is the number of such lanes below it, and the
-// lowest of them updates the wave's running count for that expert in LDS.
-// Pass 1 counts; the counts are scanned (waves in order within an expert,
-// experts in order) into each wave's first position per expert; pass 2 repeats
-// the walk and places every entry at its running position plus its rank.
+// The assignment list is cut into segments of kSegment entries, one per
+// workgroup of 16 waves, one 64-entry step per wave.  In a step every lane finds
+// the lanes holding the same expert as itself from six ballots (one per bit of
+// the expert id); its rank among them is the number of such lanes below it, and
+// the lowest of them records the step's count for that expert.  Two launches:
+//   count:   every workgroup stores its per-expert counts; the last one to
+//            finish (an arrival ticket, so no workgroup ever waits for another)
+//            scans them into each segment's first position per expert
+//            (segments in order within an expert, experts in order) and writes
+//            counts, offsets and the list of experts with tokens;
+//   scatter: every workgroup recounts its steps, adds the waves before it to
+//            its segment's base, and places every entry at its position plus
+//            its rank.
 #include "lm_internal.h"
 
 namespace lm {
@@ -22,130 +27,177 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
-constexpr int kBatch = 16;  // 64-entry steps per batch of loads
+constexpr int kSegment = kThreads;  // assignments per workgroup, one step per wave
 
-__global__ __launch_bounds__(kThreads) void permute_kernel(PermuteArgs a) {
+// Device-scope accesses: the segment counts cross XCDs within the count launch.
+__device__ inline void store_agent(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int32_t load_agent(const int32_t* p) {
+    return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lanes of this step holding the same (valid) expert as this lane.
+__device__ inline uint64_t same_expert(int v, int E) {
+    const bool valid = v >= 0 && v < E;
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 6; ++bit) {  // experts < 64
+        const uint64_t plane = __ballot(((v >> bit) & 1) != 0);
+        m &= ((v >> bit) & 1) != 0 ? plane : ~plane;
+    }
+    return valid ? m : 0ull;
+}
+
+// This wave's step: its entry (-1 past the end), the lanes sharing its expert,
+// and the step's count per expert into count[] (one LDS row per wave).
+__device__ inline void count_step(const PermuteArgs& a, int64_t i, int lane, int& v, uint64_t& m, int* count) {
+    const int64_t total = a.tokens * a.top_k;
+    v = i < total ? a.idx[i] : -1;
+    m = same_expert(v, a.experts);
+    count[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t below = (1ull << lane) - 1ull;
+    if (m != 0 && (m & below) == 0) {  // lowest lane of its expert in this step
+        count[v] = __popcll(m);
+    }
+}
+
+// scratch: [0] the arrival ticket (0 between launches), [16, 16 + 64 G) the
+// segment counts, replaced by the segment bases.
+constexpr int kTicketWords = 16;
+
+__global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) {
+    __shared__ int wave_count[kWaves][kMaxExperts];
+    __shared__ uint32_t arrived;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int E = a.experts;
+    const int g = blockIdx.x;
+    const int G = gridDim.x;
+    int v;
+    uint64_t m;
+    count_step(a, static_cast<int64_t>(g) * kSegment + wave * 64 + lane, lane, v, m, wave_count[wave]);
+    __syncthreads();
+    int32_t* seg = a.scratch + kTicketWords;
+    if (threadIdx.x < 64) {
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            c += wave_count[w][lane];
+        }
+        if (lane < E) {
+            store_agent(seg + g * kMaxExperts + lane, c);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the counts are out before the ticket
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        arrived = __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(a.scratch), 1u, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (arrived != static_cast<uint32_t>(G - 1) || threadIdx.x >= 64) {
+        return;
+    }
+    // The last workgroup: lane e scans expert e's counts over the segments (in
+    // batches of 8 loads), then the totals over the experts.
+    const bool valid = lane < E;
+    int tot = 0;
+    for (int g0 = 0; g0 < G; g0 += 8) {
+        int c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            c[j] = valid && g0 + j < G ? load_agent(seg + (g0 + j) * kMaxExperts + lane) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (valid && g0 + j < G) {
+                seg[(g0 + j) * kMaxExperts + lane] = tot;  // relative base, offset added below
+                tot += c[j];
+            }
+        }
+    }
+    int incl = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int up = __shfl_up(incl, o);
+        if (lane >= o) {
+            incl += up;
+        }
+    }
+    const int off = incl - tot;
+    if (valid) {
+        for (int s = 0; s < G; ++s) {
+            seg[s * kMaxExperts + lane] += off;
+        }
+        a.rb.counts[lane] = tot;
+        a.rb.offsets[lane] = off;
+    }
+    if (lane == E - 1) {
+        a.rb.offsets[E] = incl;
+    }
+    // Experts with tokens, ascending, and their number.
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint64_t has = __ballot(valid && tot > 0);
+    if (valid && tot > 0) {
+        a.rb.active[__popcll(has & below)] = lane;
+    }
+    if (lane == 0) {
+        a.rb.active[E] = __popcll(has);
+        a.scratch[0] = 0;  // the ticket, for the next launch
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void permute_scatter_kernel(PermuteArgs a) {
     __shared__ int wave_count[kWaves][kMaxExperts];
     __shared__ int wave_base[kWaves][kMaxExperts];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int E = a.experts;
-    const int64_t total = a.tokens * a.top_k;
-    const int64_t steps = (total + 63) / 64;
-    const int64_t per_wave = (steps + kWaves - 1) / kWaves;
-    const int64_t first = per_wave * wave * 64;
-    const int64_t last = first + per_wave * 64 < total ? first + per_wave * 64 : total;
-    const uint64_t below = (1ull << lane) - 1ull;
-
-    // Lanes of this step holding the same (valid) expert as this lane.
-    auto same_expert = [&](int v) -> uint64_t {
-        const bool valid = v >= 0 && v < E;
-        uint64_t m = __ballot(valid);
-#pragma unroll
-        for (int bit = 0; bit < 6; ++bit) {  // experts < 64
-            const uint64_t plane = __ballot(((v >> bit) & 1) != 0);
-            m &= ((v >> bit) & 1) != 0 ? plane : ~plane;
-        }
-        return valid ? m : 0ull;
-    };
-    // The segment is walked in batches of kBatch steps whose loads are all
-    // issued before any is used (one memory latency per batch, not per step).
-    auto load_batch = [&](int64_t b0, int (&v)[kBatch]) {
-#pragma unroll
-        for (int st = 0; st < kBatch; ++st) {
-            const int64_t i = b0 + st * 64 + lane;
-            v[st] = i < last ? a.idx[i] : -1;
-        }
-    };
-    int* const my_count = wave_count[wave];
-    for (int j = lane; j < kMaxExperts; j += 64) {
-        my_count[j] = 0;
-    }
-    __builtin_amdgcn_wave_barrier();
-    for (int64_t b0 = first; b0 < last; b0 += 64 * kBatch) {
-        int v[kBatch];
-        load_batch(b0, v);
-#pragma unroll
-        for (int st = 0; st < kBatch; ++st) {
-            const uint64_t m = same_expert(v[st]);
-            if (m != 0 && (m & below) == 0) {  // lowest lane of its expert in this step
-                my_count[v[st]] += __popcll(m);
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
-    }
+    const int g = blockIdx.x;
+    const int64_t i = static_cast<int64_t>(g) * kSegment + wave * 64 + lane;
+    int v;
+    uint64_t m;
+    count_step(a, i, lane, v, m, wave_count[wave]);
     __syncthreads();
     if (threadIdx.x < 64) {
-        // Lane e: expert e's total, then the exclusive scan over experts.
-        int tot = 0;
-        if (lane < E) {
-            for (int w = 0; w < kWaves; ++w) {
-                tot += wave_count[w][lane];
-            }
-        }
-        int incl = tot;
+        // First position of each expert for every wave of the segment.
+        int run = lane < a.experts ? a.scratch[kTicketWords + g * kMaxExperts + lane] : 0;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int up = __shfl_up(incl, o);
-            if (lane >= o) {
-                incl += up;
-            }
-        }
-        const int off = incl - tot;
-        if (lane < E) {
-            int run = off;
-            for (int w = 0; w < kWaves; ++w) {
-                wave_base[w][lane] = run;
-                run += wave_count[w][lane];
-            }
-            a.rb.counts[lane] = tot;
-            a.rb.offsets[lane] = off;
-        }
-        if (lane == E - 1) {
-            a.rb.offsets[E] = incl;
-        }
-        // Experts with tokens, ascending, and their number.
-        const uint64_t has = __ballot(lane < E && tot > 0);
-        if (lane < E && tot > 0) {
-            a.rb.active[__popcll(has & below)] = lane;
-        }
-        if (lane == 0) {
-            a.rb.active[E] = __popcll(has);
+        for (int w = 0; w < kWaves; ++w) {
+            wave_base[w][lane] = run;
+            run += wave_count[w][lane];
         }
     }
     __syncthreads();
-    int* const my_pos = wave_base[wave];  // next slot of each expert for this wave
-    for (int64_t b0 = first; b0 < last; b0 += 64 * kBatch) {
-        int v[kBatch];
-        load_batch(b0, v);
-#pragma unroll
-        for (int st = 0; st < kBatch; ++st) {
-            const int64_t i = b0 + st * 64 + lane;
-            const uint64_t m = same_expert(v[st]);
-            if (m != 0) {
-                const int at = my_pos[v[st]] + __popcll(m & below);
-                a.rb.perm[at] = static_cast<int32_t>(i);
-                a.rb.slot_of[i] = at;
-            }
-            __builtin_amdgcn_wave_barrier();  // every lane has read its expert's position
-            if (m != 0 && (m & below) == 0) {
-                my_pos[v[st]] += __popcll(m);
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
+    if (m != 0) {
+        const uint64_t below = (1ull << lane) - 1ull;
+        const int at = wave_base[wave][v] + __popcll(m & below);
+        a.rb.perm[at] = static_cast<int32_t>(i);
+        a.rb.slot_of[i] = at;
     }
 }
 
 }  // namespace
 
+int64_t permute_scratch_words(int64_t assignments) {
+    return kTicketWords + (assignments + kSegment - 1) / kSegment * kMaxExperts;
+}
+
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
         return hipSuccess;
     }
-    if (a.experts <= 0 || a.experts > kMaxExperts) {
+    if (a.experts <= 0 || a.experts > kMaxExperts || a.scratch == nullptr) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kThreads), 0, s, a);
+    const int64_t segments = (a.tokens * a.top_k + kSegment - 1) / kSegment;
+    hipLaunchKernelGGL(permute_count_kernel, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

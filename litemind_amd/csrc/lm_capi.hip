@@ -92,6 +92,7 @@ struct Workspace {
     float* logit_scratch = nullptr;  // [E] single-token router hand-off
     uint32_t* decode_sync = nullptr;  // single-launch decode counters (zeroed once) + error word
     uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
+    int32_t* permute_scratch = nullptr;  // segment counts and arrival ticket of the permutation
 };
 
 struct EventSet {
@@ -267,7 +268,7 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
                      reinterpret_cast<void**>(&w.x16),     reinterpret_cast<void**>(&w.down_out),
                      reinterpret_cast<void**>(&w.xnorm),   reinterpret_cast<void**>(&w.ffn),
                      reinterpret_cast<void**>(&w.zero),    reinterpret_cast<void**>(&w.logit_scratch),
-                     reinterpret_cast<void**>(&w.ticket)};
+                     reinterpret_cast<void**>(&w.ticket),  reinterpret_cast<void**>(&w.permute_scratch)};
     for (void** p : ptrs) {
         if (*p != nullptr) {
             LM_HIP(hipFree(*p));
@@ -296,6 +297,9 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.logit_scratch), sizeof(float) * static_cast<size_t>(E)));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ticket), sizeof(uint32_t) * 4));
     LM_HIP(hipMemsetAsync(w.ticket, 0, sizeof(uint32_t) * 4, ctx->stream));
+    const size_t permute_bytes = sizeof(int32_t) * static_cast<size_t>(lm::permute_scratch_words(TK));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.permute_scratch), permute_bytes));
+    LM_HIP(hipMemsetAsync(w.permute_scratch, 0, permute_bytes, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     w.tokens = T;
     return LM_OK;
@@ -531,6 +535,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     pa.top_k = ctx->K;
     pa.experts = ctx->E;
     pa.rb = ra.rb;
+    pa.scratch = ctx->ws.permute_scratch;
     if (!permuted) {
         LM_HIP(lm::launch_permute(pa, ctx->stream));
     }
@@ -722,7 +727,7 @@ int lm_context_destroy(lm_context* ctx) {
     }
     Workspace& w = ctx->ws;
     void* ptrs[] = {w.idx, w.wts, w.counts, w.offsets, w.active, w.perm, w.slot_of, w.act, w.x16,
-                    w.down_out, w.xnorm, w.ffn, w.zero, w.logit_scratch, w.ticket};
+                    w.down_out, w.xnorm, w.ffn, w.zero, w.logit_scratch, w.ticket, w.permute_scratch};
     for (void* p : ptrs) {
         (void)hipFree(p);
     }
@@ -1156,6 +1161,7 @@ int lm_permute(lm_context* ctx, const int32_t* topk_index_dev, int64_t tokens, i
     pa.rb.perm = perm_dev;
     pa.rb.slot_of = slot_of_dev;
     pa.rb.active = ctx->ws.active;
+    pa.scratch = ctx->ws.permute_scratch;
     LM_HIP(lm::launch_permute(pa, ctx->stream));
     return LM_OK;
     LM_GUARD_END

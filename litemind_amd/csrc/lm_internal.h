@@ -108,6 +108,7 @@ struct PermuteArgs {
     int64_t tokens;
     int32_t top_k, experts;
     RouteBufs rb;
+    int32_t* scratch;        // permute_scratch_words(T*K) words, word 0 zero between launches
 };
 
 // Grouped expert kernels.  Slot space: routed slots [0, T*K) in permuted order,
@@ -185,6 +186,8 @@ constexpr int kDecodeSpecWord = kDecodeApproxWord + 2 * kMaxExperts;
 constexpr int kDecodeMaskWord = kDecodeSpecWord + 2 * kMaxTopK;
 constexpr int kDecodeSyncWords = kDecodeMaskWord + 16;
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
+// Words of the permutation's scratch for T*K assignments (zeroed once at allocation).
+int64_t permute_scratch_words(int64_t assignments);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
 hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
 // Grouped SwiGLU on MFMA (k_mfma.hip): fp16 panel operands, fp32 accumulation.
