@@ -376,7 +376,8 @@ enum : int {
     kRouterLoaded = 0, kRouterDone, kSelectReady, kSharedGuDone, kRoutedDone, kCounters
 };
 constexpr int kSetWords = kCounters * kLanes * kSlotStride;
-constexpr int kFusedRows = kWaves;  // down + combine: one output row per wave
+constexpr int kDownRows = 2;                   // down + combine: output rows per wave
+constexpr int kFusedRows = kWaves * kDownRows;  // output rows per down workgroup
 
 struct FusedArgs {
     DecodeArgs a;
@@ -550,31 +551,33 @@ __device__ void repair_act_row(const DecodeArgs& a, int e, float* act_row) {
 // those are known; the exact selection then decides: ranks it confirms use the
 // rows in registers and the activations the routed workgroups wrote, the others
 // (rare) are recomputed here from the exact expert's weights.
-template <int KM, int DI, int SI>
-__device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, uint32_t* error, int h,
+template <int KM, int DI, int SI, int RW>
+__device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, uint32_t* error, int h0,
                                            float* acts) {
-    constexpr int KP = KM <= 2 ? 2 : (KM <= 4 ? 4 : 8);  // reduction width (power of two)
-    __shared__ float fixed_dot[kWaves][kMaxTopK];
+    constexpr int KP = KM <= 2 ? 2 : (KM <= 4 ? 4 : 8);  // reduction width per row (power of two)
+    __shared__ float fixed_dot[kWaves][RW][kMaxTopK];
     const DecodeArgs& a = f.a;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int K = a.top_k;
     const int W = a.inter_p;
-    const int64_t down_off = static_cast<int64_t>(2) * W * a.hidden_p + static_cast<int64_t>(h) * W;
     const int WS = a.shared_inter_p;
-    // The shared expert's down row h does not depend on the selection.
-    uint4 ws[SI];
-    {
-        const uint16_t* srow = a.shared_down + static_cast<int64_t>(h) * WS;
+    // Rows h0 .. h0 + RW - 1 of the output.  The shared expert's down rows do
+    // not depend on the selection.
+    uint4 ws[RW][SI];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const uint16_t* srow = a.shared_down + static_cast<int64_t>(h0 + j) * WS;
 #pragma unroll
         for (int it = 0; it < SI; ++it) {
             const int c = it * 512 + lane * 8;
-            ws[it] = load_stream16(srow + (c < WS ? c : WS - 8));
+            ws[j][it] = load_stream16(srow + (c < WS ? c : WS - 8));
         }
     }
     __shared__ int spec_lds[kMaxTopK];
     load_spec(f, error, spec_lds);
-    uint4 w[KM][DI];
+    const int64_t down_base = static_cast<int64_t>(2) * W * a.hidden_p;
+    uint4 w[RW][KM][DI];
     {
         int ex[KM];
 #pragma unroll
@@ -582,12 +585,16 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             ex[r] = spec_lds[r < K ? r : 0];
         }
 #pragma unroll
-        for (int it = 0; it < DI; ++it) {
-            const int c = it * 512 + lane * 8;
-            const int cc = c < W ? c : W - 8;
+        for (int j = 0; j < RW; ++j) {
 #pragma unroll
-            for (int r = 0; r < KM; ++r) {
-                w[r][it] = load_stream16(a.routed + static_cast<int64_t>(ex[r]) * a.routed_stride + down_off + cc);
+            for (int it = 0; it < DI; ++it) {
+                const int c = it * 512 + lane * 8;
+                const int cc = c < W ? c : W - 8;
+#pragma unroll
+                for (int r = 0; r < KM; ++r) {
+                    w[j][r][it] = load_stream16(a.routed + static_cast<int64_t>(ex[r]) * a.routed_stride + down_base +
+                                                static_cast<int64_t>(h0 + j) * W + cc);
+                }
             }
         }
     }
@@ -619,27 +626,39 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             }
         }
     }
-    const float residual_h = a.residual != nullptr ? a.residual[h] : 0.0f;
-    lds_barrier();
-    // The shared expert's down projection for row h.
-    float shared_h = 0.0f;
+    float residual[RW];
 #pragma unroll
-    for (int it = 0; it < SI; ++it) {
-        const int c = it * 512 + lane * 8;
-        if (c < WS) {
-            const float4 x0 = *reinterpret_cast<const float4*>(acts + K * W + c);
-            const float4 x1 = *reinterpret_cast<const float4*>(acts + K * W + c + 4);
-            fma8(shared_h, ws[it], x0, x1);
+    for (int j = 0; j < RW; ++j) {
+        residual[j] = a.residual != nullptr ? a.residual[h0 + j] : 0.0f;
+    }
+    lds_barrier();
+    // acc[j KP + r]: row j, rank r (ranks past K read valid data and are never
+    // combined); the shared expert's projection of row j is summed separately.
+    float acc[RW * KP];
+    float shared_h[RW];
+#pragma unroll
+    for (int i = 0; i < RW * KP; ++i) {
+        acc[i] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        shared_h[j] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < SI; ++it) {
+            const int c = it * 512 + lane * 8;
+            if (c < WS) {
+                const float4 x0 = *reinterpret_cast<const float4*>(acts + K * W + c);
+                const float4 x1 = *reinterpret_cast<const float4*>(acts + K * W + c + 4);
+                fma8(shared_h[j], ws[j][it], x0, x1);
+            }
         }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-        shared_h += __shfl_xor(shared_h, o);
-    }
-    float acc[KP];
 #pragma unroll
-    for (int r = 0; r < KP; ++r) {
-        acc[r] = 0.0f;
+        for (int j = 0; j < RW; ++j) {
+            shared_h[j] += __shfl_xor(shared_h[j], o);
+        }
     }
 #pragma unroll
     for (int it = 0; it < DI; ++it) {
@@ -647,15 +666,18 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
         if (c < W) {
 #pragma unroll
             for (int r = 0; r < KM; ++r) {
-                const int rr = r < K ? r : 0;  // ranks past K read valid data and are never combined
+                const int rr = r < K ? r : 0;
                 const float4 x0 = *reinterpret_cast<const float4*>(acts + rr * W + c);
                 const float4 x1 = *reinterpret_cast<const float4*>(acts + rr * W + c + 4);
-                fma8(acc[r], w[r][it], x0, x1);
+#pragma unroll
+                for (int j = 0; j < RW; ++j) {
+                    fma8(acc[j * KP + r], w[j][r][it], x0, x1);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    const float sum = transpose_reduce<KP>(acc, lane);
+    const float sum = transpose_reduce<RW * KP>(acc, lane);
     if (m != 0) {
         // Ranks the speculation got wrong: their activation rows and down dot
         // products from the exact experts (the sums above are discarded).
@@ -667,40 +689,47 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             lds_barrier();
             repair_act_row(a, e, acts + r * W);
             lds_barrier();
-            const uint16_t* down = a.routed + static_cast<int64_t>(e) * a.routed_stride + down_off;
-            float d = 0.0f;
-            for (int c = lane * 8; c < W; c += 512) {
-                const float4 x0 = *reinterpret_cast<const float4*>(acts + r * W + c);
-                const float4 x1 = *reinterpret_cast<const float4*>(acts + r * W + c + 4);
-                fma8(d, *reinterpret_cast<const uint4*>(down + c), x0, x1);
-            }
+            for (int j = 0; j < RW; ++j) {
+                const uint16_t* down = a.routed + static_cast<int64_t>(e) * a.routed_stride + down_base +
+                                       static_cast<int64_t>(h0 + j) * W;
+                float d = 0.0f;
+                for (int c = lane * 8; c < W; c += 512) {
+                    const float4 x0 = *reinterpret_cast<const float4*>(acts + r * W + c);
+                    const float4 x1 = *reinterpret_cast<const float4*>(acts + r * W + c + 4);
+                    fma8(d, *reinterpret_cast<const uint4*>(down + c), x0, x1);
+                }
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) {
-                d += __shfl_xor(d, o);
-            }
-            if (lane == 0) {
-                fixed_dot[wave][r] = d;
+                for (int o = 32; o >= 1; o >>= 1) {
+                    d += __shfl_xor(d, o);
+                }
+                if (lane == 0) {
+                    fixed_dot[wave][j][r] = d;
+                }
             }
         }
         lds_barrier();
     }
-    constexpr int L = log2c<KP>();
-    float out = 0.0f;
+    constexpr int L = log2c<RW * KP>();
 #pragma unroll
-    for (int r = 0; r < KM; ++r) {
-        if (r < K) {
-            const float d = ((m >> r) & 1u) != 0 ? fixed_dot[wave][r] : lane_value(sum, r << (6 - L));
-            out = __builtin_fmaf(wk[r], d, out);
+    for (int j = 0; j < RW; ++j) {
+        float out = 0.0f;
+#pragma unroll
+        for (int r = 0; r < KM; ++r) {
+            if (r < K) {
+                const float d =
+                    ((m >> r) & 1u) != 0 ? fixed_dot[wave][j][r] : lane_value(sum, (j * KP + r) << (6 - L));
+                out = __builtin_fmaf(wk[r], d, out);
+            }
         }
-    }
-    if (a.has_shared) {
-        out = out + shared_h;
-    }
-    if (a.residual != nullptr) {
-        out = residual_h + out;
-    }
-    if (lane == 0) {
-        a.y[h] = out;
+        if (a.has_shared) {
+            out = out + shared_h[j];
+        }
+        if (a.residual != nullptr) {
+            out = residual[j] + out;
+        }
+        if (lane == 0) {
+            a.y[h0 + j] = out;
+        }
     }
 }
 
@@ -812,7 +841,8 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         signal_done(sync, kRoutedDone);
         return;
     }
-    down_fused<KM, DI, SI>(f, sync, error, b * kFusedRows + wave, reinterpret_cast<float*>(lds));
+    down_fused<KM, DI, SI, kDownRows>(f, sync, error, b * kFusedRows + wave * kDownRows,
+                                      reinterpret_cast<float*>(lds));
 }
 
 int iters_of(int width) { return (width + 511) / 512; }
@@ -838,7 +868,7 @@ int fused_shape(int hidden, int top_k, int inter_p, int shared_inter_p) {
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p) {
     return experts % kRouterExperts == 0 && experts >= 2 && experts <= kMaxExperts && top_k >= 1 &&
            top_k <= 8 && top_k <= experts && shared_inter_p > 0 && shared_inter_p % 4 == 0 &&
-           hidden % kWaves == 0 && hidden * 16 <= 65536 && (top_k * inter_p + shared_inter_p) * 4 <= 65536 &&
+           hidden % kFusedRows == 0 && hidden * 16 <= 65536 && (top_k * inter_p + shared_inter_p) * 4 <= 65536 &&
            inter_p % kItemRows == 0 && shared_inter_p % kItemRows == 0 &&
            fused_shape(hidden, top_k, inter_p, shared_inter_p) >= 0;
 }

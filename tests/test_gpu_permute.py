@@ -26,7 +26,9 @@ def _distinct_topk(rng, T, E, K, p=None):
     return np.stack([rng.choice(E, size=K, replace=False, p=p) for _ in range(T)]).astype(np.int32)
 
 
-@pytest.mark.parametrize("T", [1, 7, 32, 2048, 4096])
+# Segments of 1,024 assignments: one partial (7, 32), several with a ragged
+# last one (171: 1,026 assignments; 1000), whole ones (2048, 4096).
+@pytest.mark.parametrize("T", [1, 7, 32, 171, 1000, 2048, 4096])
 def test_permute_matches_canonical(v2_ctx, T):
     ctx, _ = v2_ctx
     rng = np.random.default_rng(T)
