@@ -63,8 +63,8 @@ struct Shape {
     static_assert((STAGES - 2) * kLoadsPerStage < 16, "vmcnt immediate");
 };
 
-// Launches whose average group fits one 64-row tile (T k <= 64 E) take the
-// 64-row shape.  Measured on V2-Lite (one MoE block, 64 experts, k 6): 8-12%
+// Launches whose average routed group fits one 64-row tile (T k <= 64 E; a
+// dense layer: T <= 64) take the 64-row shape.  Measured on V2-Lite (one MoE block, 64 experts, k 6): 8-12%
 // faster from T = 8 to T = 512, 4-13% slower from T = 768 on, where groups
 // span several 64-row tiles and each re-streams the expert's weights.
 constexpr int64_t kNarrowRows = 64;
@@ -394,7 +394,9 @@ hipError_t launch(const ExpertArgs& a, hipStream_t s) {
     if (a.hidden_p % BK != 0 || a.inter_p % BK != 0 || (a.has_shared && a.shared_inter_p % BK != 0)) {
         return hipErrorInvalidValue;
     }
-    if (a.tokens * a.top_k <= kNarrowRows * a.experts) {
+    // A layer without routed experts (the dense FFN) is one group of T rows.
+    const bool narrow = a.experts > 0 ? a.tokens * a.top_k <= kNarrowRows * a.experts : a.tokens <= kNarrowRows;
+    if (narrow) {
         return launch_shape<MODE, 1, 4, 2, 2, 4>(a, s);
     }
     return launch_shape<MODE, 2, 2, 2, 4, 3>(a, s);
