@@ -138,29 +138,6 @@ __device__ inline float norm_reduce(const DecodeArgs& a, const float (&v)[N]) {
 template <int GI>
 constexpr int norm_elems() { return 2 * GI; }
 
-// Element c of the token as the FFN sees it: normalised when a.norm is set.
-__device__ inline float token_at(const DecodeArgs& a, int c, float inverse) {
-    const float v = a.x[c];
-    if (a.norm == nullptr) {
-        return v;
-    }
-    const float scaled = v * inverse;
-    return scaled * a.norm[c];
-}
-
-__device__ inline float4 token4_at(const DecodeArgs& a, const float4 v, int c, float inverse) {
-    if (a.norm == nullptr) {
-        return v;
-    }
-    const float4 w = *reinterpret_cast<const float4*>(a.norm + c);
-    float4 r;
-    r.x = (v.x * inverse) * w.x;
-    r.y = (v.y * inverse) * w.y;
-    r.z = (v.z * inverse) * w.z;
-    r.w = (v.w * inverse) * w.w;
-    return r;
-}
-
 // ---- roles -------------------------------------------------------------------
 
 // Logits of experts [e0, e0 + 4) with LiteMind's dot (src/Gemm.cpp:183-189):
@@ -182,18 +159,29 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
             w[j] = slice[h < H ? h : H - 1];
         }
     };
-    // The slice's first rows are requested before the norm's token loads, so
-    // the two round trips overlap instead of running one after the other.
+    // The slice's first rows, the token's elements and their norm weights are
+    // requested together, so their round trips overlap; with the norm fused the
+    // elements the norm reduces are the ones this thread multiplies (element
+    // tid + kThreads k), so nothing is loaded after the reduction.
+    constexpr int kBlocks = (GI + 3) / 4;  // passes of kThreads * 8 rows
+    constexpr int KB = kBlocks * 8;
     float4 w[8];
     load_block(0, w);
+    float v[KB], nw[KB];
     float inverse = 1.0f;
     if (a.norm != nullptr) {
-        float v[norm_elems<GI>()];
         norm_load(a, v);
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int c = tid + k * kThreads;
+            nw[k] = c < H ? a.norm[c] : 0.0f;
+        }
         inverse = norm_reduce(a, v);
     }
-    for (int hb = 0; hb < H; hb += kThreads * 8) {
-        if (hb > 0) {
+#pragma unroll
+    for (int blk = 0; blk < kBlocks; ++blk) {
+        const int hb = blk * kThreads * 8;
+        if (blk > 0) {
             load_block(hb, w);
         }
         float xv[8];
@@ -201,7 +189,12 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
         for (int j = 0; j < 8; ++j) {
             const int h = hb + j * kThreads + tid;
             const int hc = h < H ? h : H - 1;
-            xv[j] = token_at(a, hc, inverse);
+            if (a.norm != nullptr) {
+                const float scaled = v[blk * 8 + j] * inverse;  // rms_norm's (x * inverse) * w
+                xv[j] = scaled * nw[blk * 8 + j];
+            } else {
+                xv[j] = a.x[hc];
+            }
             if (a.norm != nullptr && e0 == 0 && h < H) {
                 // the repair path's copy: y may overwrite x (the stack updates the
                 // hidden state in place) once every router and gate/up item is done
@@ -315,9 +308,19 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
         const int f = static_cast<int>(threadIdx.x) + i * kThreads;
         xv[i] = x4[f < n4 ? f : n4 - 1];
     }
+    // With the norm fused, its elements and the norm weights of this thread's
+    // staging columns are requested before the weight rows too: results return
+    // in issue order, so anything requested after the rows would wait for them.
     float nv[norm_elems<GI>()];
+    float4 nw[XS];
     if (a.norm != nullptr) {
         norm_load(a, nv);
+        const float4* n4w = reinterpret_cast<const float4*>(a.norm);
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+            nw[i] = n4w[f < n4 ? f : n4 - 1];
+        }
     }
     load_rows<R, GI>(rows, a.hidden, lane, w);
     const float inverse = a.norm != nullptr ? norm_reduce(a, nv) : 1.0f;
@@ -326,7 +329,14 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
     for (int i = 0; i < XS; ++i) {
         const int f = static_cast<int>(threadIdx.x) + i * kThreads;
         if (f < n4) {
-            xs4[f] = token4_at(a, xv[i], 4 * f, inverse);
+            float4 t = xv[i];
+            if (a.norm != nullptr) {  // rms_norm's (x * inverse) * w, on the preloaded weights
+                t.x = (t.x * inverse) * nw[i].x;
+                t.y = (t.y * inverse) * nw[i].y;
+                t.z = (t.z * inverse) * nw[i].z;
+                t.w = (t.w * inverse) * nw[i].w;
+            }
+            xs4[f] = t;
         }
     }
     lds_barrier();
