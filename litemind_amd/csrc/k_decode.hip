@@ -532,6 +532,37 @@ __device__ __forceinline__ void speculate(const FusedArgs& f, uint32_t* sync, in
     }
 }
 
+// Speculative rank of expert `lane` from the approximate logits.  A softmax
+// score is non-decreasing in its logit, so ordering by logit (higher first,
+// then lower index) is MoeRouter::select's order unless two different logits
+// round to the same score; the exact selection corrects any such rank.  This
+// skips the exponentials, the sequential total and the weights, which the
+// speculation does not use.  Group-limited routing takes the full selection.
+__device__ inline int speculative_rank(float logit, bool valid, int lane, const SelectPolicy& p, float* sh) {
+    if (p.group_limited && p.n_group > 1 && p.experts % p.n_group == 0) {
+        int rank;
+        float weight;
+        select_token_lds(logit, valid, lane, p, sh, rank, weight);
+        return rank;
+    }
+    // logit bits mapped so unsigned order is float order
+    const uint32_t bits = float_bits(logit);
+    const uint32_t ordered = (bits & 0x80000000u) != 0 ? ~bits : (bits | 0x80000000u);
+    const uint64_t key = valid ? ((static_cast<uint64_t>(ordered) << 8) | static_cast<uint64_t>(255 - lane)) : 0ull;
+    uint64_t* keys = reinterpret_cast<uint64_t*>(sh + 64);
+    keys[lane] = key;
+    __builtin_amdgcn_wave_barrier();
+    const ulonglong2* keys2 = reinterpret_cast<const ulonglong2*>(keys);
+    int beaten = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const ulonglong2 k2 = keys2[i];
+        beaten += k2.x > key ? 1 : 0;
+        beaten += k2.y > key ? 1 : 0;
+    }
+    return beaten;
+}
+
 // Recomputes, in LDS, the activation row of rank r for expert e (rare path:
 // the speculative selection put another expert at this rank).  Plain loops,
 // few registers: it runs once in tens of thousands of tokens.
@@ -831,9 +862,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         if (threadIdx.x < 64) {
             const bool valid = lane < a.experts;
             const float logit = bits_float(wait_tagged(f.approx, a.experts, f.seq, error));
-            int rank;
-            float weight;
-            select_token_lds(valid ? logit : 0.0f, valid, lane, a.policy, sel, rank, weight);
+            const int rank = speculative_rank(valid ? logit : 0.0f, valid, lane, a.policy, sel);
             if (valid && rank < a.top_k) {
                 publish(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), f.seq, static_cast<uint32_t>(lane));
             }
