@@ -176,10 +176,10 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted);
 // True when the single-token forward has a one-launch kernel for this shape.
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p);
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s);
-// Single-launch decode scratch, in 32-bit words: two sets of 5 counters x 16
+// Single-launch decode scratch, in 32-bit words: two sets of 4 counters x 16
 // slots x 64 B, the error word, approximate logits [64] and speculative experts
 // [16] as tagged 64-bit words, and the mask of ranks the speculation got wrong.
-constexpr int kDecodeCounterWords = 2 * 5 * 16 * 16;
+constexpr int kDecodeCounterWords = 2 * 4 * 16 * 16;
 constexpr int kDecodeErrorWord = kDecodeCounterWords;
 constexpr int kDecodeApproxWord = kDecodeErrorWord + 16;
 constexpr int kDecodeSpecWord = kDecodeApproxWord + 2 * kMaxExperts;
