@@ -69,6 +69,8 @@ int lm_version(int32_t* major, int32_t* minor);
 int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** out);
 int lm_context_destroy(lm_context* ctx);
 int lm_synchronize(lm_context* ctx);
+/* The configuration the context was created with. */
+int lm_context_config(lm_context* ctx, lm_moe_config* out);
 
 /* ---- device memory plumbing (no LiteMind counterpart: LiteMind has one address space) ---- */
 int lm_alloc(lm_context* ctx, size_t bytes, void** out_dev);
@@ -97,6 +99,51 @@ int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host);
 /* Finishes a layer's upload: builds the fp16 shadow copy the MFMA path reads.
  * Must be called after the layer's experts and shared expert are uploaded. */
 int lm_finalize_layer(lm_context* ctx, int32_t layer);
+/* ---- SafeTensors checkpoints: replaces WeightStore + SafeTensor ----
+ * (src/WeightStore.cpp:52-185, src/SafeTensor.cpp:30-160).  lm_checkpoint_open maps
+ * every *.safetensors file of a directory read-only (sorted by file name; a tensor
+ * name present in two shards resolves to the first shard's) and validates each
+ * header as SafeTensor::open does; failures return LM_EINVAL with LiteMind's
+ * message in lm_last_error.  Payload pointers stay valid until lm_checkpoint_close.
+ * No call of this group except lm_load_layer touches the GPU. */
+typedef struct lm_checkpoint lm_checkpoint;
+#define LM_DT_BF16 1  /* element types, as SafeTensor::parse_data_type (src/SafeTensor.cpp:15-27) */
+#define LM_DT_F16 2
+#define LM_DT_F32 3
+#define LM_DT_F64 4
+#define LM_DT_I8 5
+#define LM_DT_I16 6
+#define LM_DT_I32 7
+#define LM_DT_I64 8
+#define LM_DT_U8 9
+#define LM_DT_BOOL 10
+int lm_checkpoint_open(const char* model_dir, lm_checkpoint** out);
+int lm_checkpoint_close(lm_checkpoint* ck);
+/* Distinct tensor names and shards. */
+int lm_checkpoint_count(const lm_checkpoint* ck, int64_t* tensors, int64_t* shards);
+/* WeightStore::find: dtype (LM_DT_*), rank, shape[rank] (rank <= 8), the payload
+ * inside the mapping and its bytes; any output may be null. */
+int lm_checkpoint_find(const lm_checkpoint* ck, const char* name, int32_t* dtype, int32_t* rank, int64_t* shape,
+                       const void** payload, uint64_t* bytes);
+/* WeightStore::require (src/WeightStore.cpp:119-140): the tensor must exist with
+ * exactly this shape and dtype. */
+int lm_checkpoint_require(const lm_checkpoint* ck, const char* name, int32_t rank, const int64_t* shape,
+                          int32_t dtype, const void** payload);
+/* WeightStore::read_float32 (src/WeightStore.cpp:142-185): F32 copied, BF16 and F16
+ * widened exactly; out holds count floats, count the tensor's element count. */
+int lm_checkpoint_read_f32(const lm_checkpoint* ck, const char* name, int32_t rank, const int64_t* shape, float* out,
+                           uint64_t count);
+/* Uploads one layer's FFN from a checkpoint in DeepSeek's tensor names, as
+ * DeepSeekRunner::Impl::resolve_layer resolves them (src/DeepSeekRunner.cpp:157-225),
+ * prefix model.layers.<layer>.:
+ *   post_attention_layernorm.weight [H]                 (any of F32, BF16, F16)
+ *   moe = 1: mlp.gate.weight [E, H] (F32, BF16, F16), mlp.experts.<e>.{gate,up}_proj.weight
+ *            [I, H] and down_proj.weight [H, I] (BF16), and with n_shared_experts > 0
+ *            mlp.shared_experts.* of width I * n_shared_experts;
+ *   moe = 0: mlp.{gate,up}_proj.weight [D, H], mlp.down_proj.weight [H, D] (BF16);
+ *   moe = -1: MoE when the checkpoint holds the layer's mlp.gate.weight.
+ * Every tensor is checked before the first upload; then lm_finalize_layer. */
+int lm_load_layer(lm_context* ctx, const lm_checkpoint* ck, int32_t layer, int32_t moe);
 /* Bytes resident in HBM for weights (all layers). */
 int lm_resident_bytes(lm_context* ctx, uint64_t* out);
 

@@ -91,6 +91,14 @@ PROTOTYPES = {
     "lm_event_elapsed_ms": [_P, _P, _P, _P],
     "lm_stage_timing": [_P, _I32],
     "lm_stage_times": [_P, _P, _P, _I32],
+    "lm_context_config": [_P, _P],
+    "lm_checkpoint_open": [C.c_char_p, _P],
+    "lm_checkpoint_close": [_P],
+    "lm_checkpoint_count": [_P, _P, _P],
+    "lm_checkpoint_find": [_P, C.c_char_p, _P, _P, _P, _P, _P],
+    "lm_checkpoint_require": [_P, C.c_char_p, _I32, _P, _I32, _P],
+    "lm_checkpoint_read_f32": [_P, C.c_char_p, _I32, _P, _P, C.c_uint64],
+    "lm_load_layer": [_P, _P, _I32, _I32],
 }
 _RESTYPE = {"lm_last_error": C.c_char_p}
 
@@ -163,6 +171,77 @@ class DeviceBuffer:
             self.ptr = 0
 
 
+# SafeTensors element types (LM_DT_*) and the numpy type of their raw payload
+# (BF16 as its uint16 bit patterns).
+DT_BF16, DT_F16, DT_F32, DT_F64, DT_I8, DT_I16, DT_I32, DT_I64, DT_U8, DT_BOOL = range(1, 11)
+_DT_NUMPY = {DT_BF16: np.uint16, DT_F16: np.float16, DT_F32: np.float32, DT_F64: np.float64, DT_I8: np.int8,
+             DT_I16: np.int16, DT_I32: np.int32, DT_I64: np.int64, DT_U8: np.uint8, DT_BOOL: np.bool_}
+
+
+def _check_status(lib, status: int) -> None:
+    if status != LM_OK:
+        msg = lib.lm_last_error().decode(errors="replace")
+        raise LmError(f"litemind_amd status {status}: {msg}")
+
+
+class Checkpoint:
+    """A directory of SafeTensors shards mapped read-only (lm_checkpoint_open); the
+    counterpart of LiteMind's WeightStore (src/WeightStore.cpp:52-185).  Needs no GPU."""
+
+    def __init__(self, model_dir):
+        self.lib = load_library()
+        handle = C.c_void_p()
+        _check_status(self.lib, self.lib.lm_checkpoint_open(os.fsencode(str(model_dir)), C.byref(handle)))
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.lm_checkpoint_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def count(self) -> tuple[int, int]:
+        """(distinct tensor names, shards)."""
+        t, sh = C.c_int64(), C.c_int64()
+        _check_status(self.lib, self.lib.lm_checkpoint_count(self.handle, C.byref(t), C.byref(sh)))
+        return t.value, sh.value
+
+    def find(self, name: str):
+        """(dtype code, shape, payload bytes, payload address) of a tensor."""
+        dt, rank, nbytes, payload = C.c_int32(), C.c_int32(), C.c_uint64(), C.c_void_p()
+        shape = (C.c_int64 * 8)()
+        _check_status(self.lib, self.lib.lm_checkpoint_find(self.handle, name.encode(), C.byref(dt), C.byref(rank),
+                                                            shape, C.byref(payload), C.byref(nbytes)))
+        return dt.value, tuple(shape[i] for i in range(rank.value)), nbytes.value, payload.value or 0
+
+    def array(self, name: str) -> np.ndarray:
+        """A copy of the tensor's payload as numpy (BF16 as uint16 bit patterns)."""
+        dt, shape, nbytes, payload = self.find(name)
+        raw = C.string_at(payload, nbytes) if nbytes else b""
+        return np.frombuffer(raw, dtype=_DT_NUMPY[dt]).reshape(shape).copy()
+
+    def require(self, name: str, shape, dtype: int) -> int:
+        """Payload address of a tensor that must have exactly this shape and dtype."""
+        dims = (C.c_int64 * max(len(shape), 1))(*[int(d) for d in shape])
+        payload = C.c_void_p()
+        _check_status(self.lib, self.lib.lm_checkpoint_require(self.handle, name.encode(), len(shape), dims, dtype,
+                                                               C.byref(payload)))
+        return payload.value or 0
+
+    def read_f32(self, name: str, shape) -> np.ndarray:
+        """WeightStore::read_float32: F32, BF16 or F16 as float32."""
+        dims = (C.c_int64 * max(len(shape), 1))(*[int(d) for d in shape])
+        out = np.empty([int(d) for d in shape], np.float32)
+        _check_status(self.lib, self.lib.lm_checkpoint_read_f32(self.handle, name.encode(), len(shape), dims,
+                                                                _ptr(out), out.size))
+        return out
+
+
 class Context:
     """One GPU's resident MoE weights and stream (lm_context)."""
 
@@ -175,9 +254,12 @@ class Context:
         self._buffers: list[DeviceBuffer] = []
 
     def _check(self, status: int) -> None:
-        if status != LM_OK:
-            msg = self.lib.lm_last_error().decode(errors="replace")
-            raise LmError(f"litemind_amd status {status}: {msg}")
+        _check_status(self.lib, status)
+
+    def load_layer(self, checkpoint: "Checkpoint", layer: int, moe: int = -1) -> None:
+        """Uploads a layer's FFN from a checkpoint (lm_load_layer): moe 1, 0, or -1 to
+        decide by whether the checkpoint holds the layer's router."""
+        self._check(self.lib.lm_load_layer(self.handle, checkpoint.handle, layer, moe))
 
     def close(self) -> None:
         if self.handle:

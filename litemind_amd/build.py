@@ -28,6 +28,8 @@ REFERENCE = os.environ.get("LITEMIND_REFERENCE", "/root/reference")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 HIP_SOURCES = ["k_router.hip", "k_permute.hip", "k_gemv.hip", "k_decode.hip", "k_mfma.hip",
                "k_misc.hip", "lm_capi.hip"]
+# Host-only parts of the same library (no device code), compiled by g++.
+HOST_SOURCES = ["lm_checkpoint.cpp"]
 # -ffp-contract=off: every fused multiply-add in the kernels is written out
 # explicitly; the router must not fuse at all to match LiteMind bit for bit.
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 generated from float code.
@@ -57,6 +59,10 @@ def build_hip(jobs: int = 6) -> str:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objects.append(obj)
         cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+        objects.append(obj)
+        cmds.append(["g++", *HOST_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         for fut in [pool.submit(_run, c) for c in cmds]:
             fut.result()

@@ -7,6 +7,7 @@
 // enqueued asynchronously on the context stream.  No exception crosses the ABI;
 // every entry point returns a status and records a thread-local message.
 #include "litemind_moe.h"
+#include "lm_error.h"
 #include "lm_internal.h"
 
 #include <algorithm>
@@ -640,6 +641,8 @@ int ensure_gemm_scratch(lm_context* ctx, size_t floats) {
 
 }  // namespace
 
+int lm::set_error(int code, const std::string& message) { return fail(code, message); }
+
 extern "C" {
 
 const char* lm_last_error(void) { return g_error.c_str(); }
@@ -651,6 +654,14 @@ int lm_version(int32_t* major, int32_t* minor) {
     if (minor != nullptr) {
         *minor = 1;
     }
+    return LM_OK;
+}
+
+int lm_context_config(lm_context* ctx, lm_moe_config* out) {
+    if (ctx == nullptr || out == nullptr) {
+        return fail(LM_EINVAL, "null context or output pointer");
+    }
+    *out = ctx->cfg;
     return LM_OK;
 }
 

@@ -258,3 +258,65 @@ def tiny_model_layers(layer: int = 1):
                         dense_inter=cfg["inter"], layers=cfg["layers"])
             result = (dims, MoeLayer(dims, router_f32, gate, up, down, sg, su, sd))
     return result
+
+
+# ---- SafeTensors checkpoints in DeepSeek's tensor names ----
+
+_ST_DTYPES = {np.dtype(np.float32): "F32", np.dtype(np.float16): "F16", np.dtype(np.float64): "F64",
+              np.dtype(np.int8): "I8", np.dtype(np.int16): "I16", np.dtype(np.int32): "I32",
+              np.dtype(np.int64): "I64", np.dtype(np.uint8): "U8", np.dtype(np.bool_): "BOOL"}
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    """BF16 bit patterns (uint16) of fp32 values, rounded to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def save_safetensors(path, tensors: dict) -> None:
+    """Writes one SafeTensors shard.  Values are numpy arrays; a uint16 array is
+    stored as BF16 bit patterns, other types as their SafeTensors dtype.  Payloads
+    are 8-byte aligned, in the given order."""
+    import json
+
+    header, chunks, offset = {}, [], 0
+    for name, a in tensors.items():
+        a = np.ascontiguousarray(a)
+        dtype = "BF16" if a.dtype == np.uint16 else _ST_DTYPES[a.dtype]
+        raw = a.tobytes()
+        header[name] = {"dtype": dtype, "shape": list(a.shape), "data_offsets": [offset, offset + len(raw)]}
+        pad = (-len(raw)) % 8
+        chunks.append(raw + b"\0" * pad)
+        offset += len(raw) + pad
+    text = json.dumps(header).encode()
+    text += b" " * ((-len(text)) % 8)
+    with open(path, "wb") as f:
+        f.write(len(text).to_bytes(8, "little"))
+        f.write(text)
+        for c in chunks:
+            f.write(c)
+
+
+def moe_layer_tensors(layer: int, L: MoeLayer, norm: np.ndarray, router_dtype=np.float32) -> dict:
+    """A MoE layer's FFN tensors under DeepSeek's names (the names LiteMind's
+    DeepSeekRunner::Impl::resolve_layer requires, src/DeepSeekRunner.cpp:179-225).
+    router_dtype np.uint16 stores the router as BF16 (rounded from L.router)."""
+    p = f"model.layers.{layer}."
+    router = f32_to_bf16(L.router) if router_dtype == np.uint16 else L.router.astype(router_dtype)
+    t = {p + "post_attention_layernorm.weight": norm, p + "mlp.gate.weight": router}
+    for e in range(L.dims.experts):
+        q = f"{p}mlp.experts.{e}."
+        t[q + "gate_proj.weight"], t[q + "up_proj.weight"], t[q + "down_proj.weight"] = L.gate[e], L.up[e], L.down[e]
+    if L.shared_gate is not None:
+        q = p + "mlp.shared_experts."
+        t[q + "gate_proj.weight"], t[q + "up_proj.weight"], t[q + "down_proj.weight"] = (
+            L.shared_gate, L.shared_up, L.shared_down)
+    return t
+
+
+def dense_layer_tensors(layer: int, ffn, norm: np.ndarray) -> dict:
+    """A dense layer's FFN tensors under DeepSeek's names (src/DeepSeekRunner.cpp:192-195)."""
+    p = f"model.layers.{layer}."
+    gate, up, down = ffn
+    return {p + "post_attention_layernorm.weight": norm, p + "mlp.gate_proj.weight": gate,
+            p + "mlp.up_proj.weight": up, p + "mlp.down_proj.weight": down}
