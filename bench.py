@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_t1] [--no-cpu]
     python bench.py --workload stack      # the 27-layer FFN stack at T=1 and T=4096
+    python bench.py --workload load       # SafeTensors shards of 4 layers into HBM
 
 A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
 experts, combine) over one batch of T synthetic tokens whose inputs are already
@@ -239,6 +240,51 @@ def swiglu(res: dict) -> dict:
             "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
 
 
+def run_load(moe_layers: int) -> dict:
+    """Checkpoint to HBM: writes DeepSeek-V2-Lite's dense layer 0 and `moe_layers`
+    MoE layers as SafeTensors shards (one per layer, DeepSeek's tensor names) into a
+    temporary directory, then times lm_checkpoint_open and lm_load_layer per layer
+    (header validation, the gate/up interleave on the host, the copy to HBM and the
+    fp16 shadow).  The shards were just written, so they are read from the page
+    cache, not from disk.  (Parity: tests/test_gpu_checkpoint.py.)"""
+    import tempfile
+
+    from litemind_amd import Checkpoint, Context
+    from litemind_amd import workload as wl
+
+    dims = wl.V2_LITE
+    n = 1 + moe_layers
+    ones = np.ones(dims.hidden, np.float32)
+    with tempfile.TemporaryDirectory(prefix="lm_ckpt_") as d:
+        log(f"load: writing dense + {moe_layers} MoE layer shards")
+        wl.save_safetensors(os.path.join(d, "model-00000.safetensors"),
+                            wl.dense_layer_tensors(0, wl.dense_ffn(wl.MASTER_SEED, 0, dims), ones))
+        for l in range(1, n):
+            wl.save_safetensors(os.path.join(d, f"model-{l:05d}.safetensors"),
+                                wl.moe_layer_tensors(l, wl.moe_layer(wl.MASTER_SEED, l, dims), ones))
+        shard_bytes = sum(os.path.getsize(os.path.join(d, f)) for f in os.listdir(d))
+        ctx = Context(dims.moe_config(num_layers=n))
+        t0 = time.perf_counter()
+        ck = Checkpoint(d)
+        t_open = time.perf_counter() - t0
+        per_layer = []
+        for l in range(n):
+            t1 = time.perf_counter()
+            ctx.load_layer(ck, l)
+            ctx.synchronize()
+            per_layer.append(time.perf_counter() - t1)
+            log(f"load: layer {l} {per_layer[-1] * 1e3:.1f} ms")
+        total = time.perf_counter() - t0
+        tensors, shards = ck.count()
+        ck.close()
+        resident = ctx.resident_bytes()
+        ctx.close()
+    return {"layers": n, "tensors": tensors, "shards": shards, "shard_bytes": shard_bytes,
+            "resident_bytes": resident, "open_ms": round(t_open * 1e3, 2),
+            "layer_ms": [round(t * 1e3, 1) for t in per_layer], "total_s": round(total, 3),
+            "value": round(shard_bytes / total / 1e9, 3), "unit": "GB/s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -261,6 +307,18 @@ def main() -> int:
                 "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-normalised tokens)",
                 "config": {"workload": "stack", "layers": st["layers"], "resident_gb": st["resident_gb"]},
                 "t1": st["t1"], "t4096": st["t4096"]}
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "load":
+        if args.gpus != 1:
+            print("bench.py measures one GPU.", file=sys.stderr)
+            return 2
+        ld = run_load(3)
+        line = {"metric": "SafeTensors checkpoint to HBM (shard bytes per second, page-cache-warm)",
+                "value": ld["value"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+                "data": "synthetic (seeded N(0,0.02) weights written as SafeTensors shards)",
+                "config": {"workload": "load", "layers": ld["layers"], "shards": ld["shards"],
+                           "tensors": ld["tensors"]}, "load": ld}
         print(json.dumps(line), flush=True)
         return 0
     if args.gpus != 1:
