@@ -96,6 +96,15 @@ int lm_upload_dense(lm_context* ctx, int32_t layer, const uint16_t* gate_host, c
                     const uint16_t* down_host);
 /* post_attention_layernorm weight [H] fp32, used by lm_stack_forward (:265-267). */
 int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host);
+/* The final norm weight [H] fp32 and the LM head [vocab, H] BF16 that end
+ * DeepSeekRunner::Impl::forward (src/DeepSeekRunner.cpp:296-300); needs H % 8 == 0. */
+int lm_upload_head(lm_context* ctx, const float* norm_host, const uint16_t* head_host, int64_t vocab);
+/* Per token of hidden_dev [T, H]: logits = head . rms_norm(hidden, norm) with
+ * gemm::rms_norm and gemm::matvec_bf16's roundings, bit for bit; then, into
+ * token_dev [T], Sampler::select_next's greedy choice (src/Sampler.cpp:117-126):
+ * the first maximum (std::max_element), which never picks a NaN after index 0.
+ * logits_dev [T, vocab] or token_dev may be null (not both).  Asynchronous. */
+int lm_head_forward(lm_context* ctx, const float* hidden_dev, int64_t tokens, float* logits_dev, int32_t* token_dev);
 /* Finishes a layer's upload: builds the fp16 shadow copy the MFMA path reads.
  * Must be called after the layer's experts and shared expert are uploaded. */
 int lm_finalize_layer(lm_context* ctx, int32_t layer);
@@ -144,6 +153,10 @@ int lm_checkpoint_read_f32(const lm_checkpoint* ck, const char* name, int32_t ra
  *   moe = -1: MoE when the checkpoint holds the layer's mlp.gate.weight.
  * Every tensor is checked before the first upload; then lm_finalize_layer. */
 int lm_load_layer(lm_context* ctx, const lm_checkpoint* ck, int32_t layer, int32_t moe);
+/* Uploads model.norm.weight [H] (F32, BF16 or F16) and lm_head.weight [vocab, H] BF16,
+ * or model.embed_tokens.weight when the checkpoint has no lm_head.weight (tied
+ * embeddings), as DeepSeekRunner::load resolves them (src/DeepSeekRunner.cpp:364-381). */
+int lm_load_head(lm_context* ctx, const lm_checkpoint* ck, int64_t vocab);
 /* Bytes resident in HBM for weights (all layers). */
 int lm_resident_bytes(lm_context* ctx, uint64_t* out);
 

@@ -99,6 +99,9 @@ PROTOTYPES = {
     "lm_checkpoint_require": [_P, C.c_char_p, _I32, _P, _I32, _P],
     "lm_checkpoint_read_f32": [_P, C.c_char_p, _I32, _P, _P, C.c_uint64],
     "lm_load_layer": [_P, _P, _I32, _I32],
+    "lm_upload_head": [_P, _P, _P, _I64],
+    "lm_head_forward": [_P, _P, _I64, _P, _P],
+    "lm_load_head": [_P, _P, _I64],
 }
 _RESTYPE = {"lm_last_error": C.c_char_p}
 
@@ -255,6 +258,20 @@ class Context:
 
     def _check(self, status: int) -> None:
         _check_status(self.lib, status)
+
+    def upload_head(self, norm: np.ndarray, head: np.ndarray) -> None:
+        """Final norm [H] fp32 and LM head [V, H] BF16 bits (lm_upload_head)."""
+        norm = np.ascontiguousarray(norm, np.float32)
+        head = np.ascontiguousarray(head, np.uint16)
+        self._check(self.lib.lm_upload_head(self.handle, _ptr(norm), _ptr(head), head.shape[0]))
+
+    def head_forward(self, hidden, tokens: int, logits=None, token=None) -> None:
+        """logits = head . rms_norm(hidden) and the greedy next token (lm_head_forward)."""
+        self._check(self.lib.lm_head_forward(self.handle, _ptr(hidden), tokens, _ptr(logits), _ptr(token)))
+
+    def load_head(self, checkpoint: "Checkpoint", vocab: int) -> None:
+        """model.norm.weight and lm_head.weight (or the tied embedding) from a checkpoint."""
+        self._check(self.lib.lm_load_head(self.handle, checkpoint.handle, vocab))
 
     def load_layer(self, checkpoint: "Checkpoint", layer: int, moe: int = -1) -> None:
         """Uploads a layer's FFN from a checkpoint (lm_load_layer): moe 1, 0, or -1 to

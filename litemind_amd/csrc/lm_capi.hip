@@ -130,6 +130,14 @@ struct lm_context {
     float* gemm_b = nullptr;     // second operand
     float* gemm_out = nullptr;   // output
     size_t gemm_cap = 0;         // floats in each scratch buffer
+    // LM head: final norm [H] fp32, head [V, H] BF16, and scratch for one group of
+    // lm::kHeadTokens tokens (normalised hidden states, logits when the caller
+    // passes none)
+    float* head_norm = nullptr;
+    uint16_t* head_w = nullptr;
+    int64_t vocab = 0;
+    float* head_x = nullptr;
+    float* head_logits = nullptr;
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -749,6 +757,10 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->gemm_x);
     (void)hipFree(ctx->gemm_b);
     (void)hipFree(ctx->gemm_out);
+    (void)hipFree(ctx->head_norm);
+    (void)hipFree(ctx->head_w);
+    (void)hipFree(ctx->head_x);
+    (void)hipFree(ctx->head_logits);
     (void)hipFree(ctx->d_overflow);
     (void)hipFree(w.decode_sync);
     if (ctx->staging != nullptr) {
@@ -971,6 +983,71 @@ int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host) {
     LM_HIP(hipMemcpyAsync(L.norm, weight_host, sizeof(float) * static_cast<size_t>(ctx->H), hipMemcpyHostToDevice,
                           ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_upload_head(lm_context* ctx, const float* norm_host, const uint16_t* head_host, int64_t vocab) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || norm_host == nullptr || head_host == nullptr || vocab <= 0 || vocab > INT32_MAX) {
+        return fail(LM_EINVAL, "bad head arguments");
+    }
+    if (ctx->H % 8 != 0) {
+        return fail(LM_EINVAL, "the LM head needs hidden_size % 8 == 0");
+    }
+    int rc = set_device(ctx);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const size_t H = static_cast<size_t>(ctx->H), V = static_cast<size_t>(vocab);
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->head_w != nullptr) {
+        ctx->resident -= sizeof(uint16_t) * static_cast<size_t>(ctx->vocab) * H + sizeof(float) * H;
+    }
+    for (void* q : {static_cast<void*>(ctx->head_norm), static_cast<void*>(ctx->head_w),
+                    static_cast<void*>(ctx->head_x), static_cast<void*>(ctx->head_logits)}) {
+        LM_HIP(hipFree(q));
+    }
+    ctx->head_norm = nullptr;
+    ctx->head_w = nullptr;
+    ctx->head_x = nullptr;
+    ctx->head_logits = nullptr;
+    ctx->vocab = 0;
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_norm), sizeof(float) * H));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_w), sizeof(uint16_t) * V * H));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_x), sizeof(float) * lm::kHeadTokens * H));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_logits), sizeof(float) * lm::kHeadTokens * V));
+    LM_HIP(hipMemcpy(ctx->head_norm, norm_host, sizeof(float) * H, hipMemcpyHostToDevice));
+    LM_HIP(hipMemcpy(ctx->head_w, head_host, sizeof(uint16_t) * V * H, hipMemcpyHostToDevice));
+    ctx->vocab = vocab;
+    ctx->resident += sizeof(uint16_t) * V * H + sizeof(float) * H;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_head_forward(lm_context* ctx, const float* hidden_dev, int64_t tokens, float* logits_dev, int32_t* token_dev) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || hidden_dev == nullptr || tokens < 0 || (logits_dev == nullptr && token_dev == nullptr)) {
+        return fail(LM_EINVAL, "bad head forward arguments");
+    }
+    if (ctx->head_w == nullptr) {
+        return fail(LM_ENOTRES, "no LM head uploaded");
+    }
+    int rc = set_device(ctx);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const int64_t H = ctx->H, V = ctx->vocab;
+    for (int64_t t0 = 0; t0 < tokens; t0 += lm::kHeadTokens) {
+        const int32_t n = static_cast<int32_t>(tokens - t0 < lm::kHeadTokens ? tokens - t0 : lm::kHeadTokens);
+        float* logits = logits_dev != nullptr ? logits_dev + t0 * V : ctx->head_logits;
+        LM_HIP(lm::launch_rms_norm(hidden_dev + t0 * H, ctx->head_norm, ctx->head_x, n, static_cast<int32_t>(H),
+                                   ctx->cfg.rms_norm_eps, ctx->stream));
+        LM_HIP(lm::launch_head_logits(ctx->head_w, ctx->head_x, logits, V, static_cast<int32_t>(H), n, ctx->stream));
+        if (token_dev != nullptr) {
+            LM_HIP(lm::launch_argmax_first(logits, V, n, token_dev + t0, ctx->stream));
+        }
+    }
     return LM_OK;
     LM_GUARD_END
 }

@@ -832,4 +832,30 @@ int lm_load_layer(lm_context* ctx, const lm_checkpoint* ck, int32_t layer, int32
     LM_CK_GUARD_END
 }
 
+int lm_load_head(lm_context* ctx, const lm_checkpoint* ck, int64_t vocab) {
+    LM_CK_GUARD_BEGIN
+    if (ctx == nullptr || ck == nullptr || vocab <= 0) {
+        return lm::set_error(LM_EINVAL, "bad argument");
+    }
+    lm_moe_config cfg{};
+    int rc = lm_context_config(ctx, &cfg);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const int64_t H = cfg.hidden_size;
+    std::vector<float> norm;
+    rc = read_f32(ck, "model.norm.weight", {H}, norm);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const std::string name = ck->find("lm_head.weight") != nullptr ? "lm_head.weight" : "model.embed_tokens.weight";
+    const Tensor* head = nullptr;
+    rc = require(ck, name, {vocab, H}, LM_DT_BF16, &head);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    return lm_upload_head(ctx, norm.data(), static_cast<const uint16_t*>(ck->payload(*head)), vocab);
+    LM_CK_GUARD_END
+}
+
 }  // extern "C"
