@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_t1] [--no-cpu]
     python bench.py --workload stack      # the 27-layer FFN stack at T=1 and T=4096
     python bench.py --workload load       # SafeTensors shards of 4 layers into HBM
+    python bench.py --workload head       # final norm + LM head + greedy token, T=1
 
 A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
 experts, combine) over one batch of T synthetic tokens whose inputs are already
@@ -285,6 +286,38 @@ def run_load(moe_layers: int) -> dict:
             "value": round(shard_bytes / total / 1e9, 3), "unit": "GB/s"}
 
 
+def run_head(steps: int, warmup: int) -> dict:
+    """DeepSeek-V2-Lite's final norm and LM head ([102400, 2048] BF16, resident)
+    for one token, then the greedy next token: lm_head_forward, timed with events
+    on the library's stream.  (Parity: tests/test_gpu_head.py.)"""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = wl.V2_LITE
+    V, H = 102400, dims.hidden
+    ctx = Context(dims.moe_config(num_layers=1))
+    rng = np.random.default_rng(wl.MASTER_SEED)
+    log("head: generating and uploading the [102400, 2048] head")
+    ctx.upload_head(np.ones(H, np.float32), wl.normal_bf16(wl.MASTER_SEED, 7777, 0.02, (V, H)))
+    dh = ctx.to_device(rng.standard_normal((1, H)).astype(np.float32))
+    tok = ctx.empty((1,), np.int32)
+    for _ in range(warmup):
+        ctx.head_forward(dh, 1, token=tok)
+    ctx.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(steps):
+        ctx.head_forward(dh, 1, token=tok)
+    ctx.record(e1)
+    ctx.synchronize()
+    us = ctx.elapsed_ms(e0, e1) * 1e3 / steps
+    ctx.close()
+    head_bytes = V * H * 2 + H * 4 * 2 + V * 4  # head, hidden + norm weight, logits written
+    tbs = head_bytes / (us * 1e-6) / 1e12
+    return {"us": round(us, 2), "bytes": head_bytes, "achieved": round(tbs * 1e3, 1), "unit": "GB/s",
+            "peak": HBM_PEAK_GBS, "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +340,20 @@ def main() -> int:
                 "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-normalised tokens)",
                 "config": {"workload": "stack", "layers": st["layers"], "resident_gb": st["resident_gb"]},
                 "t1": st["t1"], "t4096": st["t4096"]}
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "head":
+        if args.gpus != 1:
+            print("bench.py measures one GPU.", file=sys.stderr)
+            return 2
+        hd = run_head(args.steps, args.warmup)
+        line = {"metric": "LM head + greedy next token, tokens/sec (V=102400, H=2048)",
+                "value": round(1e6 / hd["us"], 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": round(hd["us"] / 1e3, 5), "higher_is_better": True,
+                "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) head)",
+                "config": {"workload": "head", "vocab": 102400, "hidden": 2048},
+                "roofline": {"bound": "hbm", "achieved": hd["achieved"], "peak": hd["peak"], "unit": "GB/s",
+                             "frac": hd["frac"], "traffic": None, "avg_us": hd["us"], "algorithmic_bytes": hd["bytes"]}}
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "load":

@@ -97,7 +97,7 @@ int lm_upload_dense(lm_context* ctx, int32_t layer, const uint16_t* gate_host, c
 /* post_attention_layernorm weight [H] fp32, used by lm_stack_forward (:265-267). */
 int lm_upload_norm(lm_context* ctx, int32_t layer, const float* weight_host);
 /* The final norm weight [H] fp32 and the LM head [vocab, H] BF16 that end
- * DeepSeekRunner::Impl::forward (src/DeepSeekRunner.cpp:296-300); needs H % 8 == 0. */
+ * DeepSeekRunner::Impl::forward (src/DeepSeekRunner.cpp:296-300); needs H % 8 == 0, H <= 16384. */
 int lm_upload_head(lm_context* ctx, const float* norm_host, const uint16_t* head_host, int64_t vocab);
 /* Per token of hidden_dev [T, H]: logits = head . rms_norm(hidden, norm) with
  * gemm::rms_norm and gemm::matvec_bf16's roundings, bit for bit; then, into

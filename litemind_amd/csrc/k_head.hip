@@ -8,118 +8,25 @@
 // The logits follow gemm::dot_bf16's association (src/Gemm.cpp:46-82) bit for
 // bit, like gemv_plain_kernel: 32 sequential fused chains over the elements
 // i = c (mod 32), chains 0..7 continuing over the 8-wide remainder, then
-// (a0+a1)+(a2+a3) per lane, lanes j and j+4 added, (h0+h2)+(h1+h3), and a fused
-// scalar tail.  A chain's elements lie 64 bytes apart, so instead of each lane
-// loading them one by one, a block stages chunks of its 8 rows in LDS with
-// 16-byte coalesced loads and the 32 lanes of a row read their chains from
-// there.  The head streams 420 MB at V = 102400, H = 2048: the kernel is bound
-// by HBM.
+// (a0+a1)+(a2+a3) per lane, lanes j and j+4 added, (h0+h2)+(h1+h3) (no scalar
+// tail: the width is a multiple of 8).  A chain's elements lie 64 bytes apart;
+// a lane that owns 8 consecutive chains reads one 16-byte piece per step, so
+// the loads stay wide and every chain stays in one lane, in order.  The head
+// streams 420 MB at V = 102400, H = 2048: the kernel is bound by HBM.
 #include "lm_internal.h"
 
 namespace lm {
 namespace {
 
-constexpr int kRows = 8;                  // head rows per block, 32 lanes each
-constexpr int kChunk = 1024;              // row elements staged per step
-constexpr int kPitch = kChunk + 32;       // LDS row pitch (elements): the two rows of a wave on different banks
 constexpr int kThreads = 256;
+constexpr int kRowsPerWave = 16;                         // 4 lanes per row
+constexpr int kRows = kRowsPerWave * (kThreads / 64);    // head rows per block
+constexpr int kUnroll = 8;                               // 16-byte loads in flight per lane
 
-__global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* __restrict__ w,
-                                                               const float* __restrict__ x, float* logits,
-                                                               int64_t rows, int32_t in_dim, int32_t tokens) {
-    __shared__ __align__(16) uint16_t ws[kRows * kPitch];
-    __shared__ float part[kRows][33];
-    const int tid = threadIdx.x;
-    const int c = tid & 31;
-    const int slot = tid >> 5;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
-    const int64_t row = r0 + slot;
-    const bool live = row < rows;
-    const int n32 = in_dim / 32 * 32;
-    const int n8 = n32 + (in_dim - n32) / 8 * 8;
-    float acc[kHeadTokens];
-#pragma unroll
-    for (int t = 0; t < kHeadTokens; ++t) {
-        acc[t] = 0.0f;
-    }
-    for (int k0 = 0; k0 < n32; k0 += kChunk) {
-        const int len = n32 - k0 < kChunk ? n32 - k0 : kChunk;  // a multiple of 32
-        const int pieces = len / 8;                                // 16-byte pieces per row
-        for (int f = tid; f < kRows * pieces; f += kThreads) {
-            const int rr = f / pieces;
-            const int p = f - rr * pieces;
-            const int64_t grow = r0 + rr < rows ? r0 + rr : rows - 1;
-            *reinterpret_cast<uint4*>(ws + rr * kPitch + 8 * p) = load_stream16(w + grow * in_dim + k0 + 8 * p);
-        }
-        __syncthreads();
-        if (live) {
-            const uint16_t* wr = ws + slot * kPitch + c;
-            for (int s = 0; s < len / 32; ++s) {
-                const float wv = widen_bf16(wr[32 * s]);
-                const int i = k0 + c + 32 * s;
-#pragma unroll
-                for (int t = 0; t < kHeadTokens; ++t) {
-                    if (t < tokens) {
-                        acc[t] = __builtin_fmaf(wv, x[static_cast<int64_t>(t) * in_dim + i], acc[t]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-    const uint16_t* wrow = w + (live ? row : 0) * in_dim;
-    if (live && c < 8) {
-        for (int i = n32 + c; i < n8; i += 8) {
-            const float wv = widen_bf16(wrow[i]);
-#pragma unroll
-            for (int t = 0; t < kHeadTokens; ++t) {
-                if (t < tokens) {
-                    acc[t] = __builtin_fmaf(wv, x[static_cast<int64_t>(t) * in_dim + i], acc[t]);
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < kHeadTokens; ++t) {
-        if (t >= tokens) {
-            break;
-        }
-        part[slot][c] = acc[t];
-        __syncthreads();
-        if (live && c == 0) {
-            const float* a = part[slot];
-            float lane_sum[8];
-            for (int l = 0; l < 8; ++l) {
-                const float low = a[l] + a[8 + l];
-                const float high = a[16 + l] + a[24 + l];
-                lane_sum[l] = low + high;
-            }
-            const float h0 = lane_sum[0] + lane_sum[4];
-            const float h1 = lane_sum[1] + lane_sum[5];
-            const float h2 = lane_sum[2] + lane_sum[6];
-            const float h3 = lane_sum[3] + lane_sum[7];
-            float total = (h0 + h2) + (h1 + h3);
-            const float* xt = x + static_cast<int64_t>(t) * in_dim;
-            for (int i = n8; i < in_dim; ++i) {
-                total = __builtin_fmaf(widen_bf16(wrow[i]), xt[i], total);
-            }
-            logits[static_cast<int64_t>(t) * rows + row] = total;
-        }
-        __syncthreads();
-    }
-}
-
-// (value, index) of the greedy choice so far; `have` false until a non-NaN value.
-struct Best {
-    float v;
-    int32_t i;
-    int32_t have;
-};
-
-// Combines two candidates: the larger value, the lower index between equal
-// values (IEEE equality: -0 equals +0), NaN never chosen.  Associative, so
-// the order of the tree does not matter.
-__device__ inline Best better(Best a, Best b) {
+// Combines two candidates of the greedy choice: the larger value, the lower
+// index between equal values (IEEE equality: -0 equals +0), NaN never chosen.
+// Associative, so the order of the reduction does not matter.
+__device__ inline HeadBest better(HeadBest a, HeadBest b) {
     if (!b.have) {
         return a;
     }
@@ -129,63 +36,189 @@ __device__ inline Best better(Best a, Best b) {
     return a;
 }
 
-// Sampler::select_next's greedy branch: std::max_element keeps the first of
-// equal values and moves only on a strictly larger one, so a NaN never becomes
-// the choice, except at index 0, which nothing after it can replace.  That is
-// the first maximum of the non-NaN logits, or 0 when logit 0 is NaN.
-__global__ __launch_bounds__(1024) void argmax_first_kernel(const float* __restrict__ logits, int64_t vocab,
-                                                            int32_t* out) {
-    __shared__ Best wave_best[16];
-    const float* l = logits + static_cast<int64_t>(blockIdx.x) * vocab;
-    Best b{0.0f, 0, 0};
-    for (int64_t i = threadIdx.x; i < vocab; i += 1024) {
-        const float v = l[i];
-        if (v == v && (!b.have || v > b.v)) {
-            b = Best{v, static_cast<int32_t>(i), 1};
+__device__ inline HeadBest wave_better(HeadBest b) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const HeadBest other{__shfl_xor(b.v, o), __shfl_xor(b.i, o), __shfl_xor(b.have, o)};
+        b = better(b, other);
+    }
+    return b;
+}
+
+// Four lanes per row: lane q of a row owns chains 8q .. 8q + 7, so one 16-byte
+// load gives it the next element of each of its chains (elements 32 s + 8 q ..
+// + 7), and a wave's load covers 64 contiguous bytes of 16 rows.  The tokens
+// (tokens x in_dim floats, dynamic LDS) are staged once per block.  Lane 0 of a
+// row also owns chains 0..7's continuation over the 8-wide remainder.  Then
+// each block's best row per token goes to `partial`.
+__global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* __restrict__ w,
+                                                               const float* __restrict__ x, float* logits,
+                                                               HeadBest* partial, int64_t rows, int32_t in_dim,
+                                                               int32_t tokens) {
+    extern __shared__ float4 xs4[];  // [tokens][in_dim / 4]
+    __shared__ HeadBest wave_best[kThreads / 64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int q = lane & 3;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + (tid >> 2);
+    const bool live = row < rows;
+    const int n32 = in_dim / 32 * 32;
+    const int n8 = n32 + (in_dim - n32) / 8 * 8;  // == in_dim: the launch requires in_dim % 8 == 0
+    const int q4 = in_dim / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (int i = tid; i < tokens * q4; i += kThreads) {
+        xs4[i] = x4[i];
+    }
+    __syncthreads();
+    const uint16_t* wr = w + (live ? row : rows - 1) * in_dim;
+    float acc[kHeadTokens][8];
+#pragma unroll
+    for (int t = 0; t < kHeadTokens; ++t) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc[t][j] = 0.0f;
+        }
+    }
+    auto step = [&](const uint4 wv, int e) {
+        // elements e .. e + 7 of the row, chains (e % 32) .. + 7
+        float wf[8];
+        wf[0] = widen_bf16(static_cast<uint16_t>(wv.x));
+        wf[1] = widen_bf16(static_cast<uint16_t>(wv.x >> 16));
+        wf[2] = widen_bf16(static_cast<uint16_t>(wv.y));
+        wf[3] = widen_bf16(static_cast<uint16_t>(wv.y >> 16));
+        wf[4] = widen_bf16(static_cast<uint16_t>(wv.z));
+        wf[5] = widen_bf16(static_cast<uint16_t>(wv.z >> 16));
+        wf[6] = widen_bf16(static_cast<uint16_t>(wv.w));
+        wf[7] = widen_bf16(static_cast<uint16_t>(wv.w >> 16));
+#pragma unroll
+        for (int t = 0; t < kHeadTokens; ++t) {
+            if (t < tokens) {
+                const float4 xa = xs4[t * q4 + e / 4];
+                const float4 xb = xs4[t * q4 + e / 4 + 1];
+                acc[t][0] = __builtin_fmaf(wf[0], xa.x, acc[t][0]);
+                acc[t][1] = __builtin_fmaf(wf[1], xa.y, acc[t][1]);
+                acc[t][2] = __builtin_fmaf(wf[2], xa.z, acc[t][2]);
+                acc[t][3] = __builtin_fmaf(wf[3], xa.w, acc[t][3]);
+                acc[t][4] = __builtin_fmaf(wf[4], xb.x, acc[t][4]);
+                acc[t][5] = __builtin_fmaf(wf[5], xb.y, acc[t][5]);
+                acc[t][6] = __builtin_fmaf(wf[6], xb.z, acc[t][6]);
+                acc[t][7] = __builtin_fmaf(wf[7], xb.w, acc[t][7]);
+            }
+        }
+    };
+    const int steps = n32 / 32;
+    int s = 0;
+    for (; s + kUnroll <= steps; s += kUnroll) {
+        uint4 wv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            wv[u] = load_stream16(wr + 32 * (s + u) + 8 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            step(wv[u], 32 * (s + u) + 8 * q);
+        }
+    }
+    for (; s < steps; ++s) {
+        step(load_stream16(wr + 32 * s + 8 * q), 32 * s + 8 * q);
+    }
+    if (q == 0) {
+        // chains 0..7 continue over the remainder, element n32 + 8 k + j on chain j
+        for (int e = n32; e < n8; e += 8) {
+            step(load_stream16(wr + e), e);
         }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const Best other{__shfl_xor(b.v, o), __shfl_xor(b.i, o), __shfl_xor(b.have, o)};
-        b = better(b, other);
+    for (int t = 0; t < kHeadTokens; ++t) {
+        if (t >= tokens) {
+            break;
+        }
+        // lane sums (a[l] + a[8 + l]) + (a[16 + l] + a[24 + l]) over the row's 4 lanes
+        float ls[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float v01 = acc[t][l] + __shfl_xor(acc[t][l], 1);
+            ls[l] = v01 + __shfl_xor(v01, 2);
+        }
+        const float h0 = ls[0] + ls[4];
+        const float h1 = ls[1] + ls[5];
+        const float h2 = ls[2] + ls[6];
+        const float h3 = ls[3] + ls[7];
+        const float total = (h0 + h2) + (h1 + h3);
+        if (live && q == 0) {
+            logits[static_cast<int64_t>(t) * rows + row] = total;
+        }
+        HeadBest b{total, static_cast<int32_t>(row), live && q == 0 && total == total ? 1 : 0};
+        b = wave_better(b);
+        if (lane == 0) {
+            wave_best[tid >> 6] = b;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            HeadBest r = wave_best[0];
+            for (int k = 1; k < kThreads / 64; ++k) {
+                r = better(r, wave_best[k]);
+            }
+            partial[static_cast<int64_t>(t) * gridDim.x + blockIdx.x] = r;
+        }
+        __syncthreads();
     }
+}
+
+// Sampler::select_next's greedy branch over the blocks' candidates:
+// std::max_element keeps the first of equal values and moves only on a strictly
+// larger one, so a NaN never becomes the choice, except at index 0, which
+// nothing after it can replace.  That is the first maximum of the non-NaN
+// logits, or 0 when logit 0 is NaN.
+__global__ __launch_bounds__(1024) void argmax_first_kernel(const HeadBest* __restrict__ partial, int32_t blocks,
+                                                            const float* __restrict__ logits, int64_t vocab,
+                                                            int32_t* out) {
+    __shared__ HeadBest wave_best[16];
+    const HeadBest* p = partial + static_cast<int64_t>(blockIdx.x) * blocks;
+    HeadBest b{0.0f, 0, 0};
+    for (int i = threadIdx.x; i < blocks; i += 1024) {
+        b = better(b, p[i]);
+    }
+    b = wave_better(b);
     if ((threadIdx.x & 63) == 0) {
         wave_best[threadIdx.x >> 6] = b;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        Best r = wave_best[0];
+        HeadBest r = wave_best[0];
         for (int k = 1; k < 16; ++k) {
             r = better(r, wave_best[k]);
         }
-        const float first = l[0];
+        const float first = logits[static_cast<int64_t>(blockIdx.x) * vocab];
         out[blockIdx.x] = (first != first || !r.have) ? 0 : r.i;
     }
 }
 
 }  // namespace
 
-hipError_t launch_head_logits(const uint16_t* w, const float* x, float* logits, int64_t rows, int32_t in_dim,
-                              int32_t tokens, hipStream_t s) {
+int64_t head_blocks(int64_t rows) { return (rows + kRows - 1) / kRows; }
+
+hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBest* partial, int32_t* token,
+                       int64_t rows, int32_t in_dim, int32_t tokens, hipStream_t s) {
     if (rows <= 0 || tokens <= 0) {
         return hipSuccess;
     }
-    if (tokens > kHeadTokens || in_dim <= 0 || in_dim % 8 != 0) {
+    if (tokens > kHeadTokens || in_dim <= 0 || in_dim % 8 != 0 || rows > INT32_MAX) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>((rows + kRows - 1) / kRows)), dim3(kThreads), 0,
-                       s, w, x, logits, rows, in_dim, tokens);
-    return hipGetLastError();
-}
-
-hipError_t launch_argmax_first(const float* logits, int64_t vocab, int64_t tokens, int32_t* out, hipStream_t s) {
-    if (tokens <= 0) {
-        return hipSuccess;
-    }
-    if (vocab <= 0 || vocab > INT32_MAX) {
+    const int64_t blocks = head_blocks(rows);
+    const size_t lds = sizeof(float) * static_cast<size_t>(tokens) * static_cast<size_t>(in_dim);
+    if (lds > 64 * 1024) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(argmax_first_kernel, dim3(static_cast<unsigned>(tokens)), dim3(1024), 0, s, logits, vocab, out);
+    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, s, w, x, logits,
+                       partial, rows, in_dim, tokens);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || token == nullptr) {
+        return err;
+    }
+    hipLaunchKernelGGL(argmax_first_kernel, dim3(static_cast<unsigned>(tokens)), dim3(1024), 0, s, partial,
+                       static_cast<int32_t>(blocks), logits, rows, token);
     return hipGetLastError();
 }
 

@@ -138,6 +138,7 @@ struct lm_context {
     int64_t vocab = 0;
     float* head_x = nullptr;
     float* head_logits = nullptr;
+    lm::HeadBest* head_partial = nullptr;  // per-block candidates of the greedy choice
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -761,6 +762,7 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->head_w);
     (void)hipFree(ctx->head_x);
     (void)hipFree(ctx->head_logits);
+    (void)hipFree(ctx->head_partial);
     (void)hipFree(ctx->d_overflow);
     (void)hipFree(w.decode_sync);
     if (ctx->staging != nullptr) {
@@ -992,8 +994,8 @@ int lm_upload_head(lm_context* ctx, const float* norm_host, const uint16_t* head
     if (ctx == nullptr || norm_host == nullptr || head_host == nullptr || vocab <= 0 || vocab > INT32_MAX) {
         return fail(LM_EINVAL, "bad head arguments");
     }
-    if (ctx->H % 8 != 0) {
-        return fail(LM_EINVAL, "the LM head needs hidden_size % 8 == 0");
+    if (ctx->H % 8 != 0 || ctx->H > 16384) {
+        return fail(LM_EINVAL, "the LM head needs hidden_size % 8 == 0 and hidden_size <= 16384");
     }
     int rc = set_device(ctx);
     if (rc != LM_OK) {
@@ -1005,18 +1007,22 @@ int lm_upload_head(lm_context* ctx, const float* norm_host, const uint16_t* head
         ctx->resident -= sizeof(uint16_t) * static_cast<size_t>(ctx->vocab) * H + sizeof(float) * H;
     }
     for (void* q : {static_cast<void*>(ctx->head_norm), static_cast<void*>(ctx->head_w),
-                    static_cast<void*>(ctx->head_x), static_cast<void*>(ctx->head_logits)}) {
+                    static_cast<void*>(ctx->head_x), static_cast<void*>(ctx->head_logits),
+                    static_cast<void*>(ctx->head_partial)}) {
         LM_HIP(hipFree(q));
     }
     ctx->head_norm = nullptr;
     ctx->head_w = nullptr;
     ctx->head_x = nullptr;
     ctx->head_logits = nullptr;
+    ctx->head_partial = nullptr;
     ctx->vocab = 0;
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_norm), sizeof(float) * H));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_w), sizeof(uint16_t) * V * H));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_x), sizeof(float) * lm::kHeadTokens * H));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_logits), sizeof(float) * lm::kHeadTokens * V));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->head_partial),
+                     sizeof(lm::HeadBest) * lm::kHeadTokens * static_cast<size_t>(lm::head_blocks(vocab))));
     LM_HIP(hipMemcpy(ctx->head_norm, norm_host, sizeof(float) * H, hipMemcpyHostToDevice));
     LM_HIP(hipMemcpy(ctx->head_w, head_host, sizeof(uint16_t) * V * H, hipMemcpyHostToDevice));
     ctx->vocab = vocab;
@@ -1038,15 +1044,16 @@ int lm_head_forward(lm_context* ctx, const float* hidden_dev, int64_t tokens, fl
         return rc;
     }
     const int64_t H = ctx->H, V = ctx->vocab;
-    for (int64_t t0 = 0; t0 < tokens; t0 += lm::kHeadTokens) {
-        const int32_t n = static_cast<int32_t>(tokens - t0 < lm::kHeadTokens ? tokens - t0 : lm::kHeadTokens);
+    // tokens per launch: at most kHeadTokens, and their H floats each within 64 KB of LDS
+    const int64_t group = std::max<int64_t>(1, std::min<int64_t>(lm::kHeadTokens, 16384 / H));
+    for (int64_t t0 = 0; t0 < tokens; t0 += group) {
+        const int32_t n = static_cast<int32_t>(tokens - t0 < group ? tokens - t0 : group);
         float* logits = logits_dev != nullptr ? logits_dev + t0 * V : ctx->head_logits;
         LM_HIP(lm::launch_rms_norm(hidden_dev + t0 * H, ctx->head_norm, ctx->head_x, n, static_cast<int32_t>(H),
                                    ctx->cfg.rms_norm_eps, ctx->stream));
-        LM_HIP(lm::launch_head_logits(ctx->head_w, ctx->head_x, logits, V, static_cast<int32_t>(H), n, ctx->stream));
-        if (token_dev != nullptr) {
-            LM_HIP(lm::launch_argmax_first(logits, V, n, token_dev + t0, ctx->stream));
-        }
+        LM_HIP(lm::launch_head(ctx->head_w, ctx->head_x, logits, ctx->head_partial,
+                               token_dev != nullptr ? token_dev + t0 : nullptr, V, static_cast<int32_t>(H), n,
+                               ctx->stream));
     }
     return LM_OK;
     LM_GUARD_END

@@ -189,10 +189,17 @@ hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 // LM head (k_head.hip): logits [tokens, rows] = w [rows, in_dim] . x [tokens, in_dim]
 // with gemm::dot_bf16's association, tokens <= kHeadTokens, in_dim % 8 == 0; and
 // the greedy choice per token (first maximum of the non-NaN logits).
-constexpr int kHeadTokens = 8;
-hipError_t launch_head_logits(const uint16_t* w, const float* x, float* logits, int64_t rows, int32_t in_dim,
-                              int32_t tokens, hipStream_t s);
-hipError_t launch_argmax_first(const float* logits, int64_t vocab, int64_t tokens, int32_t* out, hipStream_t s);
+constexpr int kHeadTokens = 4;
+struct HeadBest {
+    float v;
+    int32_t i;
+    int32_t have;
+};
+// Blocks of the head launch; partial holds kHeadTokens * head_blocks(rows) candidates.
+int64_t head_blocks(int64_t rows);
+// token may be null (logits only).
+hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBest* partial, int32_t* token,
+                       int64_t rows, int32_t in_dim, int32_t tokens, hipStream_t s);
 // Words of the permutation's scratch for T*K assignments (zeroed once at allocation).
 int64_t permute_scratch_words(int64_t assignments);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);

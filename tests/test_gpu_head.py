@@ -5,7 +5,7 @@ Logits must equal the oracle's gemm::rms_norm + gemm::matvec_bf16
 Sampler::select_next's greedy choice (src/Sampler.cpp:117-126): std::max_element,
 the first of equal maxima.  Hidden widths cover the 32-element chains alone,
 the 8-wide remainder, and more than one staged chunk; token counts cross the
-8-token group of a launch; V = 102400 is DeepSeek-V2-Lite's vocabulary.
+4-token group of a launch; V = 102400 is DeepSeek-V2-Lite's vocabulary.
 """
 import numpy as np
 import pytest
