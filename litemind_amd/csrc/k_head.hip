@@ -50,11 +50,11 @@ __device__ inline HeadBest wave_better(HeadBest b) {
 // + 7), and a wave's load covers 64 contiguous bytes of 16 rows.  The tokens
 // (tokens x in_dim floats, dynamic LDS) are staged once per block.  Lane 0 of a
 // row also owns chains 0..7's continuation over the 8-wide remainder.  Then
-// each block's best row per token goes to `partial`.
+// each block's best row per token goes to `partial` (when given).
 __global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* __restrict__ w,
                                                                const float* __restrict__ x, float* logits,
                                                                HeadBest* partial, int64_t rows, int32_t in_dim,
-                                                               int32_t tokens) {
+                                                               int32_t tokens, float scale, int32_t accumulate) {
     extern __shared__ float4 xs4[];  // [tokens][in_dim / 4]
     __shared__ HeadBest wave_best[kThreads / 64];
     const int tid = threadIdx.x;
@@ -146,7 +146,12 @@ __global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* _
         const float h3 = ls[3] + ls[7];
         const float total = (h0 + h2) + (h1 + h3);
         if (live && q == 0) {
-            logits[static_cast<int64_t>(t) * rows + row] = total;
+            // gemm::matvec_bf16_accumulate folds the row as fma(scale, dot, out) (src/Gemm.cpp:156-175)
+            float* o = logits + static_cast<int64_t>(t) * rows + row;
+            *o = accumulate ? __builtin_fmaf(scale, total, *o) : total;
+        }
+        if (partial == nullptr) {
+            continue;
         }
         HeadBest b{total, static_cast<int32_t>(row), live && q == 0 && total == total ? 1 : 0};
         b = wave_better(b);
@@ -212,13 +217,28 @@ hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBes
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, s, w, x, logits,
-                       partial, rows, in_dim, tokens);
+                       partial, rows, in_dim, tokens, 1.0f, 0);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || token == nullptr) {
         return err;
     }
     hipLaunchKernelGGL(argmax_first_kernel, dim3(static_cast<unsigned>(tokens)), dim3(1024), 0, s, partial,
                        static_cast<int32_t>(blocks), logits, rows, token);
+    return hipGetLastError();
+}
+
+bool matvec_rows_supported(int64_t rows, int64_t in_dim) {
+    return rows > 0 && rows <= INT32_MAX && in_dim > 0 && in_dim % 8 == 0 && in_dim <= 16384;
+}
+
+hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim, float scale,
+                              int32_t accumulate, hipStream_t s) {
+    if (!matvec_rows_supported(rows, in_dim)) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(head_blocks(rows))), dim3(kThreads),
+                       sizeof(float) * static_cast<size_t>(in_dim), s, w, x, out, nullptr, rows,
+                       static_cast<int32_t>(in_dim), 1, scale, accumulate);
     return hipGetLastError();
 }
 

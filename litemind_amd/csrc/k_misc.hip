@@ -350,6 +350,11 @@ hipError_t launch_gemv_plain(const uint16_t* w, const float* x, float* out, int6
     if (out_dim <= 0) {
         return hipSuccess;
     }
+    if (matvec_rows_supported(out_dim, in_dim) && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        // four lanes per row with 16-byte loads (k_head.hip): the same roundings
+        return launch_matvec_rows(w, x, out, out_dim, in_dim, scale, accumulate, s);
+    }
     hipLaunchKernelGGL(gemv_plain_kernel, dim3(static_cast<unsigned>((out_dim + 7) / 8)), dim3(256), 0, s, w, x, out,
                        out_dim, in_dim, scale, accumulate);
     return hipGetLastError();

@@ -200,6 +200,12 @@ int64_t head_blocks(int64_t rows);
 // token may be null (logits only).
 hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBest* partial, int32_t* token,
                        int64_t rows, int32_t in_dim, int32_t tokens, hipStream_t s);
+// The same kernel as one bit-exact gemm::matvec_bf16 (or _accumulate) of a
+// row-major [rows, in_dim] matrix (16-byte aligned), for in_dim % 8 == 0 and
+// in_dim <= 16384.
+bool matvec_rows_supported(int64_t rows, int64_t in_dim);
+hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim, float scale,
+                              int32_t accumulate, hipStream_t s);
 // Words of the permutation's scratch for T*K assignments (zeroed once at allocation).
 int64_t permute_scratch_words(int64_t assignments);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);
