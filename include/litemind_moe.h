@@ -56,10 +56,13 @@ typedef struct lm_moe_config {
 } lm_moe_config;
 
 /* Expert-path selection for lm_moe_forward. */
-#define LM_PATH_AUTO 0  /* GEMV up to LM_MFMA_CROSSOVER tokens, MFMA above */
+#define LM_PATH_AUTO 0  /* up to LM_DECODE_TOKENS tokens one at a time through the single-token kernel
+                            (where the layer's shape has it), else GEMV up to LM_MFMA_CROSSOVER tokens,
+                            MFMA above */
 #define LM_PATH_GEMV 1  /* fp32-activation weight-streaming kernels */
 #define LM_PATH_MFMA 2  /* fp16-operand MFMA grouped GEMM, fp32 accumulate */
 #define LM_MFMA_CROSSOVER 2  /* LM_PATH_AUTO: token counts above this take the MFMA path */
+#define LM_DECODE_TOKENS 3   /* LM_PATH_AUTO: token counts up to this take the single-token kernel per token */
 
 /* ---- errors, context ---- */
 const char* lm_last_error(void);

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "liblitemind_moe.so")
 LM_OK = 0
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 MFMA_CROSSOVER = 2  # LM_MFMA_CROSSOVER: PATH_AUTO takes the MFMA path above this many tokens
+DECODE_TOKENS = 3  # LM_DECODE_TOKENS: LM_PATH_AUTO runs up to this many tokens one at a time on the single-token kernel
 OP_DOT, OP_AXPY, OP_SOFTMAX, OP_SILU_MUL, OP_RMS_NORM, OP_WIDEN = range(6)
 STAGES = ("router", "permute", "gate_up", "down", "combine")
 
