@@ -172,27 +172,64 @@ def run_stack(steps_t1: int, steps_big: int, big_tokens: int, moe_layers: int) -
     return out
 
 
-def cpu_baseline(layer, x, bias, budget_s: float, max_tokens: int):
-    """LiteMind's CPU MoE path (its own Gemm/MoeRouter/ThreadPool, compiled from its
-    sources into oracle/_ref) on the first tokens of the workload, one token at a
-    time as its runner does, with hardware_concurrency() threads."""
+def cpu_layout() -> dict:
+    """The host CPU as /proc/cpuinfo describes it: model, sockets x cores x SMT."""
+    model, sockets, cores, siblings = None, set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                key, value = key.strip(), value.strip()
+                if key == "model name" and model is None:
+                    model = value
+                elif key == "physical id":
+                    sockets.add(value)
+                elif key == "cpu cores" and cores is None:
+                    cores = int(value)
+                elif key == "siblings" and siblings is None:
+                    siblings = int(value)
+    except OSError:
+        pass
+    n_sockets = max(len(sockets), 1)
+    smt = siblings // cores if cores and siblings else None
+    return {"model": model, "sockets": n_sockets, "cores_per_socket": cores, "threads_per_core": smt,
+            "layout": f"{n_sockets} x {cores} x {smt}", "online_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(layers, x, bias, run_seconds: float, runs: int = 5, what: str = "") -> dict | None:
+    """LiteMind's CPU MoE path (its own Gemm/MoeRouter/ThreadPool compiled from
+    its sources into oracle/_ref, -O3 -march=x86-64-v3) on distinct tokens of
+    the workload, one token at a time as its runner does (src/DeepSeekRunner.cpp:
+    472-482), with ThreadPool's hardware_concurrency() workers.  Token j of the
+    sample runs on layers[j % len(layers)], as the GPU leg rotates its layers.
+    One warm-up run, then `runs` timed runs of distinct tokens; the value is
+    tokens / median run time."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as ol
 
     if not ol.have_ref():
         return None
     threads = int(ol.ref().ref_hardware_threads())
-    ol.ref_moe_layer(layer, x[:1], bias, workers=0)  # warm-up (pool start, page-in)
-    done, t0 = 0, time.perf_counter()
-    while done < max_tokens and time.perf_counter() - t0 < budget_s:
-        n = min(4, max_tokens - done)
-        rows = [(done + j) % x.shape[0] for j in range(n)]
-        ol.ref_moe_layer(layer, np.ascontiguousarray(x[rows]), bias, workers=0)
-        done += n
-    dt = time.perf_counter() - t0
-    return dict(value=done / dt, unit="tokens/s", cores=threads, kind="reference",
-                sample=f"first {done} tokens of the workload, sequential per-token MoE block "
-                       f"(LiteMind gemm/MoeRouter/ThreadPool, {threads} threads), {dt:.1f} s")
+
+    def run(rows):
+        t0 = time.perf_counter()
+        for j in rows:
+            ol.ref_moe_layer(layers[j % len(layers)], x[j:j + 1], bias, workers=0)
+        return time.perf_counter() - t0
+
+    probe = run(range(min(4, x.shape[0])))  # warm-up: pool start, page-in, rate estimate
+    per_token = probe / min(4, x.shape[0])
+    n = int(max(4, min(x.shape[0] // (runs + 1), run_seconds / per_token)))
+    run(range(n))  # warm-up run at the timed size
+    times = [run(range((r + 1) * n, (r + 2) * n)) for r in range(runs)]
+    median = float(np.median(times))
+    return dict(value=n / median, unit="tokens/s", cores=threads, kind="reference",
+                sample=f"{what}: {runs} runs of {n} distinct tokens each (after a warm-up run), median "
+                       f"{median:.2f} s per run; sequential per-token MoE block with LiteMind's "
+                       f"gemm/MoeRouter/ThreadPool compiled -O3 -march=x86-64-v3, {threads} threads; "
+                       f"run times {', '.join(f'{t:.2f}' for t in times)} s",
+                cpu=cpu_layout())
 
 
 def roofline(res: dict, mfma: bool) -> dict:
@@ -401,7 +438,15 @@ def main() -> int:
 
     if not args.no_cpu:
         log("cpu baseline (LiteMind's own kernels)")
-        cb = cpu_baseline(res["layers"][0], res["x"], res["bias"], args.cpu_seconds, max_tokens=T if T > 1 else 10**6)
+        if T == 1:
+            # distinct tokens drawn like the workload's, layers rotated as the GPU leg rotates them
+            x_cpu = wl.tokens(wl.MASTER_SEED + 8, 8192, 2048)
+            what = (f"decode: tokens from a seeded N(0,1) RMS-normalised stream, layers rotated over the "
+                    f"{len(res['layers'])} benchmark layers")
+        else:
+            x_cpu = res["x"]
+            what = f"{args.workload}: distinct rows of the workload's {T} tokens"
+        cb = cpu_baseline(res["layers"], x_cpu, res["bias"], args.cpu_seconds / 5, what=what)
         if cb is None:
             cb = {"value": None, "unit": "tokens/s", "cores": os.cpu_count(), "kind": "reference",
                   "sample": "oracle/_ref/libref.so not built"}
@@ -421,6 +466,12 @@ def main() -> int:
         }
         if mfma2:
             line["t2048" if w2.tokens == 2048 else args.second]["grouped_swiglu"] = swiglu(res2)
+        if not args.no_cpu:
+            log(f"cpu baseline on a sample of {args.second}")
+            cb2 = cpu_baseline(res2["layers"], res2["x"], res2["bias"], args.cpu_seconds / 12,
+                               what=f"{args.second}: distinct rows of the workload's {w2.tokens} tokens")
+            if cb2 is not None:
+                line["t2048" if w2.tokens == 2048 else args.second]["cpu_baseline"] = cb2
     print(json.dumps(line), flush=True)
     return 0
 

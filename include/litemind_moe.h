@@ -79,7 +79,8 @@ int lm_context_config(lm_context* ctx, lm_moe_config* out);
 int lm_alloc(lm_context* ctx, size_t bytes, void** out_dev);
 int lm_free(lm_context* ctx, void* dev);
 int lm_copy_h2d(lm_context* ctx, void* dst_dev, const void* src_host, size_t bytes);  /* synchronous */
-int lm_copy_d2h(lm_context* ctx, void* dst_host, const void* src_dev, size_t bytes);  /* synchronous */
+int lm_copy_d2h(lm_context* ctx, void* dst_host, const void* src_dev, size_t bytes);  /* synchronous; reports
+                                                                                    LM_EKERNEL as lm_synchronize */
 int lm_memset(lm_context* ctx, void* dst_dev, int32_t value, size_t bytes);           /* async */
 
 /* ---- HBM residency: replaces ExpertCache + WeightView paging ----
@@ -255,6 +256,13 @@ int lm_weight_resident(lm_context* ctx, const void* host_ptr, int32_t* out_resid
  * makes every speculative rank wrong so that tests exercise the recomputation;
  * outputs must not change.  mode 0 (the default) restores normal operation. */
 int lm_decode_speculation_test(lm_context* ctx, int32_t mode);
+/* Testing hook, no counterpart in LiteMind.  Every hand-off wait inside the
+ * single-token forward is bounded; when one gives up, the kernel still runs to
+ * its end, and the next lm_synchronize or lm_copy_d2h returns LM_EKERNEL.
+ * mode 1 makes every such wait give up after its second poll, so tests can
+ * check that path without a stalled GPU; mode 0 (the default) restores the
+ * normal bound. */
+int lm_decode_wait_test(lm_context* ctx, int32_t mode);
 
 /* ---- timing: hipEvents on the context stream ---- */
 int lm_event_create(lm_context* ctx, void** out_event);

@@ -86,6 +86,7 @@ PROTOTYPES = {
     "lm_weight_release": [_P, _P],
     "lm_weight_resident": [_P, _P, _P],
     "lm_decode_speculation_test": [_P, _I32],
+    "lm_decode_wait_test": [_P, _I32],
     "lm_event_create": [_P, _P],
     "lm_event_destroy": [_P, _P],
     "lm_event_record": [_P, _P],

@@ -380,7 +380,7 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
 // all the same and reports a timeout through the error word.  Counters come in
 // two sets used by alternating launches; each launch clears the set the next one
 // uses (the launch before it, which used that set, has completed).
-constexpr uint32_t kMaxSpins = 1u << 16;  // ~50 ms of polling
+constexpr uint32_t kMaxSpins = 1u << 16;  // ~50 ms of polling (the default limit of every wait)
 // Each logical counter is spread over kLanes slots, one 64-byte line apart, so
 // hundreds of workgroups neither add to nor poll one address.
 constexpr int kLanes = 16;
@@ -401,6 +401,7 @@ struct FusedArgs {
     int32_t parity;
     uint32_t seq;       // this launch's tag of the approx / spec words (nonzero, changes every launch)
     int32_t perturb;    // testing: make the speculation disagree with every rank
+    uint32_t max_spins; // polls before a wait gives up and sets the error word
     int32_t n_router, n_shared_gu, n_routed;
 };
 
@@ -418,6 +419,21 @@ __device__ constexpr bool single_slot(int counter) {
 
 // Counts this workgroup done once every wave's stores are acknowledged; returns
 // the slot's previous value.
+//
+// Ordering of the hand-offs.  Every value one workgroup hands to another is
+// written with an agent-scope atomic store (global_store ... sc1: written
+// through the XCD's L2 to memory) and read with an agent-scope atomic load
+// (global_load ... sc1: read from memory, never from an L2 copy), so no cache
+// can hold a stale copy of it.  The writer's vmcnt(0) waits until memory has
+// acknowledged each of the wave's stores and the barrier waits for every wave,
+// so the counter's add is issued after all of the workgroup's data is in
+// memory; the reader issues its data loads only after its poll has returned
+// the count (the loop exit depends on the loaded value) and behind a barrier
+// the compiler does not move memory operations across.  An agent-scope
+// release / acquire pair states the same order in the memory model but adds
+// an L2 write-back (buffer_wbl2) per signal and an L2 invalidate (buffer_inv)
+// per wait, for data that never sits in L2: measured, it doubles the launch
+// (35 to 70 us per V2-Lite block).
 __device__ inline uint32_t signal_done(uint32_t* set, int counter) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
@@ -433,7 +449,7 @@ __device__ inline uint32_t signal_done(uint32_t* set, int counter) {
 
 // Waits until the counter's slots sum to `target` (wave 0 polls all slots at
 // once, backing off while far from done), then releases the workgroup.
-__device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, uint32_t* error) {
+__device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, uint32_t* error, uint32_t limit) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         uint32_t spins = 0;
@@ -451,7 +467,7 @@ __device__ inline void wait_count(uint32_t* set, int counter, uint32_t target, u
             if (v >= target) {
                 break;
             }
-            if (++spins > kMaxSpins) {
+            if (++spins > limit) {
                 if (lane == 0) {
                     __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
@@ -479,7 +495,7 @@ __device__ inline void publish(uint64_t* p, uint32_t seq, uint32_t bits) {
 
 // One wave polls words [0, n) (n <= 64) until all carry `seq`; lane i < n then
 // holds the low 32 bits of word i.  Bounded like wait_count.
-__device__ inline uint32_t wait_tagged(const uint64_t* p, int n, uint32_t seq, uint32_t* error) {
+__device__ inline uint32_t wait_tagged(const uint64_t* p, int n, uint32_t seq, uint32_t* error, uint32_t limit) {
     const int lane = threadIdx.x & 63;
     uint32_t spins = 0;
     for (;;) {
@@ -489,7 +505,7 @@ __device__ inline uint32_t wait_tagged(const uint64_t* p, int n, uint32_t seq, u
         if (__ballot(static_cast<uint32_t>(v >> 32) != seq) == 0) {
             return static_cast<uint32_t>(v);
         }
-        if (++spins > kMaxSpins) {
+        if (++spins > limit) {
             if (lane == 0) {
                 __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -500,11 +516,13 @@ __device__ inline uint32_t wait_tagged(const uint64_t* p, int n, uint32_t seq, u
 }
 
 // Speculative experts of every rank into LDS (all waves read them afterwards).
+// A wait that gave up returns a word of an earlier launch (or zero); the index
+// is clamped all the same, so no weight address can leave the layer.
 __device__ inline void load_spec(const FusedArgs& f, uint32_t* error, int* spec_lds) {
     if (threadIdx.x < 64) {
-        const uint32_t v = wait_tagged(f.spec, f.a.top_k, f.seq, error);
+        const uint32_t v = wait_tagged(f.spec, f.a.top_k, f.seq, error, f.max_spins);
         if (static_cast<int>(threadIdx.x) < f.a.top_k) {
-            spec_lds[threadIdx.x] = static_cast<int>(v);
+            spec_lds[threadIdx.x] = static_cast<int>(v < static_cast<uint32_t>(f.a.experts) ? v : 0u);
         }
     }
     __syncthreads();
@@ -639,9 +657,9 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             }
         }
     }
-    wait_count(sync, kSharedGuDone, f.n_shared_gu, error);
-    wait_count(sync, kRoutedDone, f.n_routed, error);
-    wait_count(sync, kSelectReady, 1, error);
+    wait_count(sync, kSharedGuDone, f.n_shared_gu, error, f.max_spins);
+    wait_count(sync, kRoutedDone, f.n_routed, error, f.max_spins);
+    wait_count(sync, kSelectReady, 1, error, f.max_spins);
     const uint32_t m = __hip_atomic_load(f.mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float wk[KM];
 #pragma unroll
@@ -726,7 +744,9 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             if (((m >> r) & 1u) == 0) {
                 continue;
             }
-            const int e = load_coherent(a.idx + r);
+            // clamped: after a wait that gave up, idx may hold anything
+            const int e_read = load_coherent(a.idx + r);
+            const int e = e_read >= 0 && e_read < a.experts ? e_read : 0;
             lds_barrier();
             repair_act_row(a, e, acts + r * W);
             lds_barrier();
@@ -826,7 +846,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
                 store_coherent(a.idx + rank, lane);
                 store_coherent(a.wts + rank, weight);
             }
-            const int spec_of_rank = __shfl(static_cast<int>(wait_tagged(f.spec, a.top_k, f.seq, error)),
+            const int spec_of_rank = __shfl(static_cast<int>(wait_tagged(f.spec, a.top_k, f.seq, error, f.max_spins)),
                                             chosen ? rank : 0);
             const uint64_t wrong = __ballot(chosen && spec_of_rank != lane);
             // bit r of the mask: rank r must be recomputed
@@ -860,7 +880,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         // logits and publishes the experts for the routed and down workgroups.
         if (threadIdx.x < 64) {
             const bool valid = lane < a.experts;
-            const float logit = bits_float(wait_tagged(f.approx, a.experts, f.seq, error));
+            const float logit = bits_float(wait_tagged(f.approx, a.experts, f.seq, error, f.max_spins));
             const int rank = speculative_rank(valid ? logit : 0.0f, valid, lane, a.policy, sel);
             if (valid && rank < a.top_k) {
                 publish(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), f.seq, static_cast<uint32_t>(lane));
@@ -952,6 +972,7 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     f.mask = d.sync + kDecodeMaskWord;
     f.parity = d.parity & 1;
     f.perturb = d.perturb;
+    f.max_spins = d.max_spins != 0 ? d.max_spins : kMaxSpins;
     f.n_router = a.experts / kRouterExperts;
     f.n_shared_gu = a.shared_inter_p / kItemRows;
     f.n_routed = top_k * (inter_p / kItemRows);

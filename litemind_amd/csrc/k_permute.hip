@@ -93,7 +93,8 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the counts are out before the ticket
     __syncthreads();
     if (threadIdx.x == 0) {
-        arrived = __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(a.scratch), 1u, __ATOMIC_RELAXED,
+        // release: this segment's counts; acquire: every earlier segment's
+        arrived = __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(a.scratch), 1u, __ATOMIC_ACQ_REL,
                                          __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();

@@ -128,6 +128,7 @@ struct lm_context {
     int32_t decode_parity = 0;   // alternates between single-launch decodes
     uint32_t decode_seq = 0;     // tag of the single-launch decode's hand-off words (never 0 in a launch)
     int32_t decode_perturb = 0;  // testing: force the speculative selection to disagree
+    uint32_t decode_max_spins = 0;  // testing: polls before a wait gives up (0: the kernel's default)
     bool decode_pending = false; // a single-launch decode ran since the last error check
     void* gemm_w = nullptr;      // per-call upload of a matrix that is not resident
     size_t gemm_w_cap = 0;
@@ -475,6 +476,7 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     d.sync = ctx->ws.decode_sync;
     d.parity = ctx->decode_parity;
     d.perturb = ctx->decode_perturb;
+    d.max_spins = ctx->decode_max_spins;
     ctx->decode_parity ^= 1;
     ctx->decode_seq = ctx->decode_seq == 0xffffffffu ? 1u : ctx->decode_seq + 1u;
     d.seq = ctx->decode_seq;
@@ -665,6 +667,23 @@ int ensure_gemm_scratch(lm_context* ctx, size_t floats) {
     return LM_OK;
 }
 
+// After the stream has drained: a bounded wait inside a single-launch decode
+// that ran out has set the error word; report it once and clear it.
+int check_decode_error(lm_context* ctx) {
+    if (!ctx->decode_pending) {
+        return LM_OK;
+    }
+    ctx->decode_pending = false;
+    uint32_t error = 0;
+    uint32_t* word = ctx->ws.decode_sync + lm::kDecodeErrorWord;
+    LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
+    if (error != 0) {
+        LM_HIP(hipMemset(word, 0, sizeof error));
+        return fail(LM_EKERNEL, "a single-token decode wait timed out; its outputs are invalid");
+    }
+    return LM_OK;
+}
+
 }  // namespace
 
 int lm::set_error(int code, const std::string& message) { return fail(code, message); }
@@ -803,18 +822,7 @@ int lm_synchronize(lm_context* ctx) {
         return fail(LM_EINVAL, "null context");
     }
     LM_HIP(hipStreamSynchronize(ctx->stream));
-    if (ctx->decode_pending) {
-        // A bounded wait inside a single-launch decode that ran out reports here.
-        ctx->decode_pending = false;
-        uint32_t error = 0;
-        uint32_t* word = ctx->ws.decode_sync + lm::kDecodeErrorWord;
-        LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
-        if (error != 0) {
-            LM_HIP(hipMemset(word, 0, sizeof error));
-            return fail(LM_EKERNEL, "a single-token decode wait timed out; its outputs are invalid");
-        }
-    }
-    return LM_OK;
+    return check_decode_error(ctx);
 }
 
 int lm_alloc(lm_context* ctx, size_t bytes, void** out_dev) {
@@ -852,7 +860,8 @@ int lm_copy_d2h(lm_context* ctx, void* dst_host, const void* src_dev, size_t byt
     }
     LM_HIP(hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
-    return LM_OK;
+    // the copied data may come from a decode whose wait gave up
+    return check_decode_error(ctx);
 }
 
 int lm_memset(lm_context* ctx, void* dst_dev, int32_t value, size_t bytes) {
@@ -1481,6 +1490,14 @@ int lm_decode_speculation_test(lm_context* ctx, int32_t mode) {
         return fail(LM_EINVAL, "null context");
     }
     ctx->decode_perturb = mode != 0 ? 1 : 0;
+    return LM_OK;
+}
+
+int lm_decode_wait_test(lm_context* ctx, int32_t mode) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    ctx->decode_max_spins = mode != 0 ? 1u : 0u;
     return LM_OK;
 }
 

@@ -169,6 +169,7 @@ struct DecodeLaunch {
     int32_t parity;             // alternates between consecutive launches
     uint32_t seq;               // nonzero, different in consecutive launches: tags the hand-off words
     int32_t perturb;            // testing: the speculative selection disagrees with every rank
+    uint32_t max_spins;         // polls before a wait gives up (0: the kernel's default bound)
 };
 
 // Kernel launchers (implemented in the .hip files).

@@ -10,6 +10,11 @@
 //         y_batch / index_batch / weight_batch: the same tokens through
 //           gpu::MoeBlockGpu (one batched lm_moe_forward);
 //         cache.txt: the ExpertCache counters after the per-token run.
+//   dropin_demo moe-timeout <case_dir>
+//       The same layer through gpu::MoeBlockGpu with the single-token kernel's
+//       hand-off waits made to give up at once (lm_decode_wait_test): forward
+//       must throw with the library's LM_EKERNEL message, and a second forward
+//       with normal waits must succeed.  Exit status 0 when both hold.
 //   dropin_demo cache-trace <budget> <block_bytes> <layer expert>...
 //       Replays touches on an ExpertCache with byte-less views and prints its
 //       counters after each touch and after clear(): resident_bytes,
@@ -26,6 +31,7 @@
 #include "MoeRouter.hpp"
 #include "Threading.hpp"
 #include "litemind_gpu.hpp"
+#include "litemind_moe.h"
 
 #include <cstdint>
 #include <cstdio>
@@ -179,6 +185,58 @@ int run_moe(const std::string& dir) {
                 gemm::kernel_description().c_str());
     return 0;
 }
+int run_moe_timeout(const std::string& dir) {
+    std::ifstream cfg(dir + "/case.txt");
+    std::size_t H = 0, I = 0, E = 0, K = 0, S = 0, T = 0, budget_experts = 0;
+    int norm = 0;
+    float scale = 1.0F;
+    if (!(cfg >> H >> I >> E >> K >> S >> T >> norm >> scale >> budget_experts) || S == 0U) {
+        throw std::runtime_error("bad case.txt (the single-token kernel needs a shared expert)");
+    }
+    Config config;
+    config.hidden_size = H;
+    config.moe_intermediate_size = I;
+    config.n_routed_experts = E;
+    config.num_experts_per_tok = K;
+    config.n_shared_experts = S / I;
+    config.intermediate_size = 0U;
+    config.norm_topk_prob = norm != 0;
+    config.routed_scaling_factor = scale;
+    const auto router = read_array<float>(dir + "/router.f32", E * H);
+    const auto gate = read_array<std::uint16_t>(dir + "/gate.bf16", E * I * H);
+    const auto up = read_array<std::uint16_t>(dir + "/up.bf16", E * I * H);
+    const auto down = read_array<std::uint16_t>(dir + "/down.bf16", E * H * I);
+    const auto sg = read_array<std::uint16_t>(dir + "/shared_gate.bf16", S * H);
+    const auto su = read_array<std::uint16_t>(dir + "/shared_up.bf16", S * H);
+    const auto sd = read_array<std::uint16_t>(dir + "/shared_down.bf16", H * S);
+    const auto x = read_array<float>(dir + "/x.f32", T * H);
+    std::vector<WeightView> gv(E), uv(E), dv(E);
+    for (std::size_t e = 0; e < E; ++e) {
+        gv[e] = view_of(gate, e * I * H, I * H);
+        uv[e] = view_of(up, e * I * H, I * H);
+        dv[e] = view_of(down, e * H * I, H * I);
+    }
+    const WeightView sgv = view_of(sg, 0, S * H), suv = view_of(su, 0, S * H), sdv = view_of(sd, 0, H * S);
+    gpu::MoeBlockGpu block(config, 1);
+    block.upload_layer(0, router, gv, uv, dv, &sgv, &suv, &sdv);
+    std::vector<float> y(H);
+    gpu::check(lm_decode_wait_test(block.context(), 1), "lm_decode_wait_test");
+    bool reported = false;
+    try {
+        block.forward(0, std::span<const float>(x.data(), H), 1, y);
+    } catch (const std::runtime_error& error) {
+        reported = std::string(error.what()).find("timed out") != std::string::npos;
+        std::printf("forward with waits that give up: %s\n", error.what());
+    }
+    gpu::check(lm_decode_wait_test(block.context(), 0), "lm_decode_wait_test");
+    if (!reported) {
+        std::fprintf(stderr, "dropin_demo: a wait that gave up was not reported\n");
+        return 3;
+    }
+    block.forward(0, std::span<const float>(x.data(), H), 1, y);  // normal waits: must succeed
+    std::printf("moe-timeout case %s: LM_EKERNEL reported, next forward ok\n", dir.c_str());
+    return 0;
+}
 
 int run_cache_trace(int argc, char** argv) {
     if (argc < 4 || (argc - 4) % 2 != 0) {
@@ -217,10 +275,13 @@ int main(int argc, char** argv) {
         if (argc >= 3 && std::strcmp(argv[1], "moe") == 0) {
             return run_moe(argv[2]);
         }
+        if (argc >= 3 && std::strcmp(argv[1], "moe-timeout") == 0) {
+            return run_moe_timeout(argv[2]);
+        }
         if (argc >= 2 && std::strcmp(argv[1], "cache-trace") == 0) {
             return run_cache_trace(argc, argv);
         }
-        std::fprintf(stderr, "usage: dropin_demo moe <case_dir> | cache-trace <budget> <block_bytes> <l e>...\n");
+        std::fprintf(stderr, "usage: dropin_demo moe|moe-timeout <case_dir> | cache-trace <budget> <block_bytes> <l e>...\n");
         return 2;
     } catch (const std::exception& error) {
         std::fprintf(stderr, "dropin_demo: %s\n", error.what());

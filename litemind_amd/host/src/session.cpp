@@ -182,6 +182,9 @@ void MoeBlockGpu::forward(int layer, std::span<const float> x, std::size_t token
                          static_cast<float*>(y_dev_), nullptr, static_cast<int32_t*>(idx_dev_),
                          static_cast<float*>(w_dev_), nullptr, LM_PATH_AUTO),
           "lm_moe_forward");
+    // Kernel-side failures (a single-token hand-off wait that gave up) are
+    // reported when the stream drains, not by the enqueueing call.
+    check(lm_synchronize(ctx_), "lm_synchronize");
     check(lm_copy_d2h(ctx_, y.data(), y_dev_, tokens * hidden_ * sizeof(float)), "lm_copy_d2h");
     if (!index.empty()) {
         check(lm_copy_d2h(ctx_, index.data(), idx_dev_, tokens * top_k_ * sizeof(std::int32_t)), "lm_copy_d2h");

@@ -99,3 +99,37 @@ def test_decode_speculation_recovery(v2_ctx):
     finally:
         ctx._check(ctx.lib.lm_decode_speculation_test(ctx.handle, 0))
     _check(out, layers[0], x)
+
+
+def test_decode_wait_timeout_reports_kernel_error(v2_ctx):
+    """Every hand-off wait of the single-token kernel made to give up after its
+    second poll (a bound the host sets, so every wave still runs to its end):
+    the next lm_synchronize returns LM_EKERNEL, the error is reported once, and
+    the context then computes exact results again."""
+    from litemind_amd import LmError
+    from litemind_amd import workload as wl
+
+    ctx, layers = v2_ctx
+    x = wl.tokens(wl.MASTER_SEED + 4343, 1, 2048)
+    dx, y = ctx.to_device(x), ctx.empty((1, 2048))
+    idx, w = ctx.empty((1, 6), np.int32), ctx.empty((1, 6))
+    announce("decode with every hand-off wait giving up at once")
+    reported = 0
+    ctx._check(ctx.lib.lm_decode_wait_test(ctx.handle, 1))
+    try:
+        for _ in range(4):
+            ctx.moe_forward(0, dx, 1, y, idx=idx, w=w)
+            try:
+                ctx.synchronize()
+            except LmError as error:
+                assert "status -5" in str(error) and "timed out" in str(error)
+                reported += 1
+    finally:
+        ctx._check(ctx.lib.lm_decode_wait_test(ctx.handle, 0))
+    assert reported >= 1
+    ctx.synchronize()  # nothing left to report
+    announce("decode after the forced timeouts")
+    out = _one_token_calls(ctx, 0, x)
+    _check(out, layers[0], x)
+    for b in (dx, y, idx, w):
+        b.free()

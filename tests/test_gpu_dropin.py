@@ -91,3 +91,21 @@ def test_dropin_v2lite_layer(tmp_path, v2_layer):
 
     x = wl.tokens(wl.MASTER_SEED + 77, 2, 2048)
     check(run_case(tmp_path, "v2lite", v2_layer, x, 4), v2_layer, x, 4)
+
+
+@pytest.mark.skipif(not os.path.exists(DEMO), reason="dropin_demo not built")
+def test_dropin_reports_kernel_timeout(tmp_path, tiny_layer):
+    """gpu::MoeBlockGpu::forward throws with the library's LM_EKERNEL message
+    when the single-token kernel's waits give up (forced from the host with
+    lm_decode_wait_test), and works again once they no longer do."""
+    from litemind_amd import workload as wl
+
+    dims, layer = tiny_layer
+    x = wl.tokens(37, 1, dims.hidden)
+    write_case(tmp_path, layer, x, 0)
+    announce("dropin_demo moe-timeout tiny T=1")
+    proc = subprocess.run([DEMO, "moe-timeout", str(tmp_path)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                          text=True, timeout=240)
+    print(proc.stdout)
+    assert proc.returncode == 0, proc.stdout
+    assert "LM_EKERNEL reported" in proc.stdout

@@ -4,9 +4,10 @@ RMSNorm with weights 1 and the residual add) against the oracle's chain.
 lm_stack_forward runs h += FFN_l(rms_norm(h)) for every layer, the loop of
 LiteMind's runner with attention omitted (src/DeepSeekRunner.cpp:264-290).
 A short stack (dense + 3 MoE layers) is checked on every token at T = 1 (the
-single-launch decode with the residual fused) and at T = 300 (the grouped MFMA
-paths).  Tokens never mix along this path, so the full-size stack of the
-benchmark is covered by the same per-token check.
+single-launch decode with the residual fused), T = 3 (that kernel once per
+token) and T = 300 (the grouped MFMA paths), and at the benchmark's prefill
+size T = 4096 on a sample of tokens: tokens never mix along this path, so the
+oracle run on a sample of rows checks those rows of the full-size batch.
 """
 import numpy as np
 import pytest
@@ -129,3 +130,61 @@ def test_stack_t1_speculation_recovery(stack_ctx):
     max_abs, mean_rel = layer_error(h, oh)
     print(f"stack T=1 forced repair max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
     assert max_abs <= MAX_ABS and mean_rel < 1e-5
+
+
+def test_stack_t3_matches_oracle(stack_ctx):
+    """T = 3: LM_PATH_AUTO runs each MoE layer as three single-token launches
+    with the norm fused and the residual written in place (the dense layer takes
+    its MFMA path, fp16 operands), checked end to end against the oracle."""
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    h0 = wl.tokens(wl.MASTER_SEED + 333, 3, dims.hidden)
+    announce(f"stack T=3: dense + {MOE_LAYERS} MoE layers")
+    states = ol.oracle_stack(layers, h0, dims.rms_norm_eps, every_layer=True)
+    inputs = [h0] + states[:-1]
+    for l, (h_in, h_out) in enumerate(zip(inputs, states)):
+        got = _run(ctx, h_in, l, l)
+        max_abs, mean_rel = layer_error(got - h_in, h_out - h_in)
+        print(f"T=3 layer {l} ({layers[l][0]}) max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+        assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+        if layers[l][0] == "moe":
+            assert mean_rel < 1e-5  # fp32 activations in the single-token kernel
+    end = _run(ctx, h0)
+    max_abs, mean_rel = layer_error(end, states[-1])
+    print(f"stack T=3 end to end max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+
+
+def test_stack_t4096_sampled(stack_ctx):
+    """The stack at T = 4096 (the benchmark's prefill size: MFMA paths with
+    128-row tiles, 24,576 routed slots per MoE layer).  Per layer, the GPU's
+    own input to the layer is kept and 48 of its rows are run through the
+    oracle's layer: the layer bar holds on those rows.  Then the whole chain in
+    one call, 48 sampled tokens against the oracle's chain (mean-rel 1e-3)."""
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    T = 4096
+    h0 = wl.tokens(wl.MASTER_SEED + 4097, T, dims.hidden)
+    sample = np.unique(np.concatenate([np.arange(0, T, 89), [T - 1]]))
+    announce(f"stack T={T}: dense + {MOE_LAYERS} MoE layers, per layer on {sample.size} sampled rows")
+    dh = ctx.to_device(h0)
+    h_in = h0
+    for l in range(1 + MOE_LAYERS):
+        ctx.stack_forward(l, l, dh, T)
+        ctx.synchronize()
+        h_out = dh.download()
+        assert np.all(np.isfinite(h_out))
+        ref = ol.oracle_stack(layers[l:l + 1], h_in[sample], dims.rms_norm_eps)
+        max_abs, mean_rel = layer_error(h_out[sample] - h_in[sample], ref - h_in[sample])
+        print(f"T=4096 layer {l} ({layers[l][0]}) max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+        assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+        h_in = h_out
+    dh.free()
+    announce(f"stack T={T}: whole chain in one call")
+    end = _run(ctx, h0)
+    oh = ol.oracle_stack(layers, h0[sample], dims.rms_norm_eps)
+    max_abs, mean_rel = layer_error(end[sample], oh)
+    print(f"stack T=4096 end to end (sample) max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert np.all(np.isfinite(end)) and mean_rel <= MEAN_REL
