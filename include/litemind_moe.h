@@ -179,6 +179,23 @@ int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t t
                    const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev,
                    float* logits_dev, int32_t path);
 
+/* No counterpart in LiteMind: lm_moe_forward for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The same MoE block, each token through the
+ * single-token kernel in turn (the LM_PATH_AUTO kernel of one to three
+ * tokens), with every scratch word in one fixed device array of 256 KiB per
+ * GPU instead of the context's workspace: the call makes no hipMalloc, hipFree
+ * or other allocating call.  The array belongs to the GPU, not to the context:
+ * calls on one GPU that overlap (other threads, other contexts' streams) race,
+ * and a wait that gave up is reported by the next lm_synchronize or
+ * lm_copy_d2h of any context on that GPU.  LM_EINVAL for a layer whose shape
+ * has no single-token kernel (lm_moe_forward runs those) or whose scratch
+ * would not fit the array.  topk_index_dev, topk_weight_dev and logits_dev may
+ * be NULL.  Asynchronous. */
+int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
+                           const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev,
+                           float* logits_dev);
+
 /* ---- stage entry points (for tests; each is one step of lm_moe_forward) ---- */
 /* gemm::matvec_f32 + MoeRouter::select for T tokens (src/Gemm.cpp:132-137,
  * src/MoeRouter.cpp:54-107).  Bit-exact with LiteMind for hidden % 8 == 0. */

@@ -73,6 +73,7 @@ PROTOTYPES = {
     "lm_finalize_layer": [_P, _I32],
     "lm_resident_bytes": [_P, _P],
     "lm_moe_forward": [_P, _I32, _P, _I64, _P, _P, _P, _P, _P, _I32],
+    "lm_moe_forward_noalloc": [_P, _I32, _P, _I64, _P, _P, _P, _P, _P],
     "lm_router": [_P, _I32, _P, _I64, _P, _P, _P, _P],
     "lm_router_select": [_P, _P, _I64, _P, _P],
     "lm_permute": [_P, _P, _I64, _P, _P, _P, _P],
@@ -334,6 +335,11 @@ class Context:
     def moe_forward(self, layer, x, tokens, y, bias=None, idx=None, w=None, logits=None, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_moe_forward(self.handle, layer, _ptr(x), tokens, _ptr(y), _ptr(bias), _ptr(idx),
                                             _ptr(w), _ptr(logits), path))
+
+    def moe_forward_noalloc(self, layer, x, tokens, y, bias=None, idx=None, w=None, logits=None) -> None:
+        """lm_moe_forward_noalloc: the single-token kernel per token, scratch in a fixed device array."""
+        self._check(self.lib.lm_moe_forward_noalloc(self.handle, layer, _ptr(x), tokens, _ptr(y), _ptr(bias),
+                                                    _ptr(idx), _ptr(w), _ptr(logits)))
 
     def router(self, layer, x, tokens, idx, w, bias=None, logits=None) -> None:
         self._check(self.lib.lm_router(self.handle, layer, _ptr(x), tokens, _ptr(bias), _ptr(logits), _ptr(idx),

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -104,6 +105,50 @@ struct Workspace {
 struct EventSet {
     hipEvent_t ev[kStages + 1];
 };
+
+// ---- fixed device scratch of lm_moe_forward_noalloc --------------------------
+//
+// For callers that cannot allocate device memory, every scratch word of the
+// single-token launch lives in one file-scope device array, present on each GPU
+// the library runs on from load to process end.  Host code never passes the
+// array's name to a kernel or a copy (in host code it is a stand-in, not a
+// device address): each device's address is taken once with
+// hipGetSymbolAddress, at the first context creation on that device, and only
+// that address is used.  Layout, in 32-bit words:
+//   [0, kStaticSync)                 hand-off words of the single-token kernel
+//   [kStaticLogits, + kMaxExperts)   router logit hand-off
+//   [kStaticIdx, + kMaxTopK)         selection when the caller passes none
+//   [kStaticWts, + kMaxTopK)         weights when the caller passes none
+//   [kStaticAct, kStaticWords)       activations [K Ip + Sp]
+constexpr size_t kStaticScratchBytes = 256 * 1024;
+constexpr int kStaticWords = static_cast<int>(kStaticScratchBytes / 4);
+constexpr int kStaticSync = (lm::kDecodeSyncWords + 63) / 64 * 64;
+constexpr int kStaticLogits = kStaticSync;
+constexpr int kStaticIdx = kStaticLogits + lm::kMaxExperts;
+constexpr int kStaticWts = kStaticIdx + lm::kMaxTopK;
+constexpr int kStaticAct = (kStaticWts + lm::kMaxTopK + 63) / 64 * 64;
+static_assert(kStaticAct < kStaticWords, "static scratch layout");
+
+static __device__ __align__(256) uint32_t scratch[kStaticWords];
+
+constexpr int kMaxDevices = 64;
+// Per device: the array's address and the state the single-token kernel keeps
+// across launches on these words.  Every call on one GPU shares them.
+struct StaticScratch {
+    uint32_t* ptr = nullptr;
+    int32_t parity = 0;
+    uint32_t seq = 0;
+    bool pending = false;
+};
+std::mutex g_static_mutex;
+StaticScratch g_static[kMaxDevices];
+
+__global__ void fill_words_kernel(uint32_t* p, int64_t n, uint32_t v) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        p[i] = v;
+    }
+}
 
 }  // namespace
 
@@ -439,24 +484,48 @@ bool decode_eligible(const lm_context* ctx, const Layer& L) {
     return L.shared_present && lm::decode_supported(ctx->H, ctx->E, ctx->K, ctx->Ip, ctx->Sp);
 }
 
-// One token through the single-launch decode kernel (k_decode.hip).  Routed
-// experts sit back to back in the layer slab, so expert e's FFN is found by
-// offset.  Stage timing sees one launch, attributed to the gate/up stage.
-int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const float* residual, const float* bias,
-                 int32_t* idx, float* wts, float* logits_out, const float* norm) {
+// Scratch of single-token launches: the hand-off words (lm::kDecodeSyncWords,
+// zero before the first launch; each launch clears the counter set the next
+// one uses), the router's logit hand-off [E], the activations [K Ip + Sp], the
+// normalised token [H] when the norm is fused, the parity and tag of the last
+// launch on these words, and the flag that a launch may have left an error.
+struct DecodeScratch {
+    uint32_t* sync;
+    float* logits;
+    float* act;
+    float* xnorm;
+    int32_t* parity;
+    uint32_t* seq;
+    bool* pending;
+};
+
+// The context's own decode scratch (the workspace; the hand-off words are
+// allocated and zeroed on first use).
+int context_decode_scratch(lm_context* ctx, DecodeScratch* out) {
     if (ctx->ws.decode_sync == nullptr) {
         const size_t bytes = sizeof(uint32_t) * lm::kDecodeSyncWords;
         LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_sync), bytes));
         LM_HIP(hipMemsetAsync(ctx->ws.decode_sync, 0, bytes, ctx->stream));
     }
+    *out = DecodeScratch{ctx->ws.decode_sync, ctx->ws.logit_scratch, static_cast<float*>(ctx->ws.act),
+                         ctx->ws.xnorm, &ctx->decode_parity, &ctx->decode_seq, &ctx->decode_pending};
+    return LM_OK;
+}
+
+// One token through the single-launch decode kernel (k_decode.hip).  Routed
+// experts sit back to back in the layer slab, so expert e's FFN is found by
+// offset.  Stage timing sees one launch, attributed to the gate/up stage.
+int decode_layer(lm_context* ctx, Layer& L, const DecodeScratch& sc, const float* x, float* y,
+                 const float* residual, const float* bias, int32_t* idx, float* wts, float* logits_out,
+                 const float* norm) {
     lm::DecodeLaunch d{};
     d.x = x;
     d.norm = norm;
     d.eps = ctx->cfg.rms_norm_eps;
-    d.xnorm = ctx->ws.xnorm;
+    d.xnorm = sc.xnorm;
     d.wq = L.router_t + static_cast<size_t>(ctx->H) * ctx->E;
     d.bias = bias;
-    d.logits = ctx->ws.logit_scratch;
+    d.logits = sc.logits;
     d.logits_out = logits_out;
     d.idx = idx;
     d.wts = wts;
@@ -464,7 +533,7 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     d.routed_stride = static_cast<int64_t>(L.experts[1].gu - L.experts[0].gu);
     d.shared_gu = L.shared.gu;
     d.shared_down = L.shared.down;
-    d.act = static_cast<float*>(ctx->ws.act);
+    d.act = sc.act;
     d.y = y;
     d.residual = residual;
     d.hidden = ctx->H;
@@ -473,14 +542,14 @@ int decode_layer(lm_context* ctx, Layer& L, const float* x, float* y, const floa
     d.shared_inter_p = ctx->Sp;
     d.policy = lm::SelectPolicy{ctx->E, ctx->K, ctx->cfg.norm_topk_prob, ctx->cfg.group_limited, ctx->cfg.n_group,
                                 ctx->cfg.topk_group, ctx->cfg.routed_scaling_factor};
-    d.sync = ctx->ws.decode_sync;
-    d.parity = ctx->decode_parity;
+    d.sync = sc.sync;
+    d.parity = *sc.parity;
     d.perturb = ctx->decode_perturb;
     d.max_spins = ctx->decode_max_spins;
-    ctx->decode_parity ^= 1;
-    ctx->decode_seq = ctx->decode_seq == 0xffffffffu ? 1u : ctx->decode_seq + 1u;
-    d.seq = ctx->decode_seq;
-    ctx->decode_pending = true;
+    *sc.parity ^= 1;
+    *sc.seq = *sc.seq == 0xffffffffu ? 1u : *sc.seq + 1u;
+    d.seq = *sc.seq;
+    *sc.pending = true;
     stage_mark(ctx, 0);
     stage_mark(ctx, 1);
     stage_mark(ctx, 2);
@@ -510,15 +579,18 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     int32_t* idx = idx_out != nullptr ? idx_out : ctx->ws.idx;
     float* wts = w_out != nullptr ? w_out : ctx->ws.wts;
 
-    if (T == 1 && !mfma && decode_eligible(ctx, L)) {
-        return decode_layer(ctx, L, x, y, residual, bias, idx, wts, logits_out, norm);
-    }
-    if (path == LM_PATH_AUTO && T <= kDecodeTokens && decode_eligible(ctx, L)) {
+    if ((T == 1 && !mfma && decode_eligible(ctx, L)) ||
+        (path == LM_PATH_AUTO && T <= kDecodeTokens && decode_eligible(ctx, L))) {
+        DecodeScratch sc{};
+        rc = context_decode_scratch(ctx, &sc);
+        if (rc != LM_OK) {
+            return rc;
+        }
         const int64_t H = ctx->H;
         for (int64_t t = 0; t < T; ++t) {
-            rc = decode_layer(ctx, L, x + t * H, y + t * H, residual != nullptr ? residual + t * H : nullptr, bias,
-                              idx + t * ctx->K, wts + t * ctx->K, logits_out != nullptr ? logits_out + t * ctx->E : nullptr,
-                              norm);
+            rc = decode_layer(ctx, L, sc, x + t * H, y + t * H, residual != nullptr ? residual + t * H : nullptr,
+                              bias, idx + t * ctx->K, wts + t * ctx->K,
+                              logits_out != nullptr ? logits_out + t * ctx->E : nullptr, norm);
             if (rc != LM_OK) {
                 return rc;
             }
@@ -670,17 +742,59 @@ int ensure_gemm_scratch(lm_context* ctx, size_t floats) {
 // After the stream has drained: a bounded wait inside a single-launch decode
 // that ran out has set the error word; report it once and clear it.
 int check_decode_error(lm_context* ctx) {
-    if (!ctx->decode_pending) {
-        return LM_OK;
+    uint32_t* words[2] = {nullptr, nullptr};
+    if (ctx->decode_pending) {
+        ctx->decode_pending = false;
+        words[0] = ctx->ws.decode_sync;
     }
-    ctx->decode_pending = false;
-    uint32_t error = 0;
-    uint32_t* word = ctx->ws.decode_sync + lm::kDecodeErrorWord;
-    LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
-    if (error != 0) {
-        LM_HIP(hipMemset(word, 0, sizeof error));
+    if (ctx->device < kMaxDevices) {
+        // lm_moe_forward_noalloc's launches on this device (any context)
+        std::lock_guard<std::mutex> lock(g_static_mutex);
+        StaticScratch& st = g_static[ctx->device];
+        if (st.pending) {
+            st.pending = false;
+            words[1] = st.ptr;
+        }
+    }
+    bool failed = false;
+    for (uint32_t* sync : words) {
+        if (sync == nullptr) {
+            continue;
+        }
+        uint32_t error = 0;
+        uint32_t* word = sync + lm::kDecodeErrorWord;
+        LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
+        if (error != 0) {
+            hipLaunchKernelGGL(fill_words_kernel, dim3(1), dim3(64), 0, ctx->stream, word, int64_t{1}, 0u);
+            LM_HIP(hipGetLastError());
+            LM_HIP(hipStreamSynchronize(ctx->stream));
+            failed = true;
+        }
+    }
+    if (failed) {
         return fail(LM_EKERNEL, "a single-token decode wait timed out; its outputs are invalid");
     }
+    return LM_OK;
+}
+
+// Once per device, with the device current: the address of `scratch` on it,
+// cleared with a fill kernel on the context's stream.
+int static_scratch_setup(lm_context* ctx) {
+    if (ctx->device >= kMaxDevices) {
+        return LM_OK;  // lm_moe_forward_noalloc reports it
+    }
+    std::lock_guard<std::mutex> lock(g_static_mutex);
+    StaticScratch& st = g_static[ctx->device];
+    if (st.ptr != nullptr) {
+        return LM_OK;
+    }
+    void* ptr = nullptr;
+    LM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    hipLaunchKernelGGL(fill_words_kernel, dim3(64), dim3(256), 0, ctx->stream, static_cast<uint32_t*>(ptr),
+                       static_cast<int64_t>(kStaticWords), 0u);
+    LM_HIP(hipGetLastError());
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    st.ptr = static_cast<uint32_t*>(ptr);
     return LM_OK;
 }
 
@@ -758,6 +872,9 @@ int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** 
     }
     if (rc == LM_OK && hipMalloc(reinterpret_cast<void**>(&ctx->d_overflow), sizeof(int)) != hipSuccess) {
         rc = fail(LM_ENOMEM, "hipMalloc failed");
+    }
+    if (rc == LM_OK) {
+        rc = static_scratch_setup(ctx);
     }
     if (rc != LM_OK) {
         delete ctx;
@@ -1181,6 +1298,57 @@ int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t t
     }
     return moe_layer(ctx, layer, x_dev, tokens, y_dev, nullptr, logit_bias_dev, topk_index_dev, topk_weight_dev,
                      logits_dev, path);
+    LM_GUARD_END
+}
+
+int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
+                           const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev,
+                           float* logits_dev) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (tokens < 0 || (tokens > 0 && (x_dev == nullptr || y_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null x / y");
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.allocated || L.dense || L.router_t == nullptr || !L.finalized) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no finalized MoE weights");
+    }
+    if (!decode_eligible(ctx, L)) {
+        return fail(LM_EINVAL, "lm_moe_forward_noalloc: the layer's shape has no single-token kernel");
+    }
+    const int64_t act_words = static_cast<int64_t>(ctx->K) * ctx->Ip + ctx->Sp;
+    if (act_words > kStaticWords - kStaticAct) {
+        return fail(LM_EINVAL, "lm_moe_forward_noalloc: the layer needs " + std::to_string((kStaticAct + act_words) * 4) +
+                                   " bytes of scratch; the fixed array holds " + std::to_string(kStaticScratchBytes));
+    }
+    if (ctx->device >= kMaxDevices) {
+        return fail(LM_EINVAL, "lm_moe_forward_noalloc: device index beyond the fixed scratch table");
+    }
+    if (tokens == 0) {
+        return LM_OK;
+    }
+    std::lock_guard<std::mutex> lock(g_static_mutex);
+    StaticScratch& st = g_static[ctx->device];
+    if (st.ptr == nullptr) {
+        return fail(LM_EHIP, "lm_moe_forward_noalloc: the fixed scratch was not set up on this device");
+    }
+    float* words = reinterpret_cast<float*>(st.ptr);
+    const DecodeScratch sc{st.ptr, words + kStaticLogits, words + kStaticAct, nullptr, &st.parity, &st.seq,
+                           &st.pending};
+    const int64_t H = ctx->H, K = ctx->K;
+    for (int64_t t = 0; t < tokens; ++t) {
+        int32_t* idx = topk_index_dev != nullptr ? topk_index_dev + t * K : reinterpret_cast<int32_t*>(st.ptr) + kStaticIdx;
+        float* wts = topk_weight_dev != nullptr ? topk_weight_dev + t * K : words + kStaticWts;
+        rc = decode_layer(ctx, L, sc, x_dev + t * H, y_dev + t * H, nullptr, logit_bias_dev, idx, wts,
+                          logits_dev != nullptr ? logits_dev + t * ctx->E : nullptr, nullptr);
+        if (rc != LM_OK) {
+            return rc;
+        }
+    }
+    return LM_OK;
     LM_GUARD_END
 }
 
