@@ -42,7 +42,7 @@ typedef struct lm_context lm_context;
 typedef struct lm_moe_config {
     int32_t hidden_size;            /* 2048 for DeepSeek-V2-Lite */
     int32_t moe_intermediate_size;  /* 1408 */
-    int32_t n_routed_experts;       /* 64 (at most 64) */
+    int32_t n_routed_experts;       /* 64 (at most 512; the single-token kernel takes at most 64) */
     int32_t num_experts_per_tok;    /* 6 (at most 16) */
     int32_t n_shared_experts;       /* 2 -> one fused shared FFN of width 1408*2 */
     int32_t intermediate_size;      /* dense layers: 10944 */

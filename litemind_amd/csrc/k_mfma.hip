@@ -90,20 +90,22 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
                             TileInfo& ti, int* s_info) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
-        const int g = lane;
-        const int n = g < a.experts ? a.rb.counts[g] : 0;
-        const int mts = (n + BM - 1) / BM;
-        const int tiles = mts * nt_routed;
-        int incl = tiles;
+        // Tiles of the routed groups in expert order, 64 experts per pass.
+        int routed_total = 0;
+        for (int g0 = 0; g0 < a.experts; g0 += 64) {
+            const int g = g0 + lane;
+            const int n = g < a.experts ? a.rb.counts[g] : 0;
+            const int tiles = (n + BM - 1) / BM * nt_routed;
+            int incl = tiles;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o);
-            if (lane >= o) {
-                incl += v;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o);
+                if (lane >= o) {
+                    incl += v;
+                }
             }
+            routed_total += __shfl(incl, 63);
         }
-        const int excl = incl - tiles;
-        const int routed_total = __shfl(incl, 63);
         const int mts_s = a.has_shared ? static_cast<int>((a.tokens + BM - 1) / BM) : 0;
         const int64_t total = routed_total + static_cast<int64_t>(mts_s) * nt_shared;
         const int64_t per = total / kXcds, extra = total % kXcds;
@@ -112,11 +114,31 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
         const int64_t tile = idx < count ? xcd * per + (xcd < extra ? xcd : extra) + idx : total;
         int found = -1, local = 0, found_mts = 0;
         if (tile < routed_total) {
-            const uint64_t hit = __ballot(tile >= excl && tile < incl && tiles > 0);
-            const int gl = static_cast<int>(__builtin_ctzll(hit));
-            found = gl;
-            local = static_cast<int>(tile) - __shfl(excl, gl);
-            found_mts = __shfl(mts, gl);
+            int carry = 0;
+            for (int g0 = 0; g0 < a.experts; g0 += 64) {
+                const int g = g0 + lane;
+                const int n = g < a.experts ? a.rb.counts[g] : 0;
+                const int mts = (n + BM - 1) / BM;
+                const int tiles = mts * nt_routed;
+                int incl = tiles;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int v = __shfl_up(incl, o);
+                    if (lane >= o) {
+                        incl += v;
+                    }
+                }
+                const int excl = carry + incl - tiles;
+                const uint64_t hit = __ballot(tile >= excl && tile < carry + incl && tiles > 0);
+                if (hit != 0) {
+                    const int gl = static_cast<int>(__builtin_ctzll(hit));
+                    found = g0 + gl;
+                    local = static_cast<int>(tile) - __shfl(excl, gl);
+                    found_mts = __shfl(mts, gl);
+                    break;
+                }
+                carry += __shfl(incl, 63);
+            }
         } else if (tile < total) {
             found = a.experts;
             local = static_cast<int>(tile - routed_total);

@@ -37,25 +37,38 @@ __device__ inline int32_t load_agent(const int32_t* p) {
     return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Lanes of this step holding the same (valid) expert as this lane.
+// Lanes of this step holding the same (valid) expert as this lane, from one
+// ballot per bit of the expert id (BITS = 6 below 64 experts).
+template <int BITS>
 __device__ inline uint64_t same_expert(int v, int E) {
     const bool valid = v >= 0 && v < E;
     uint64_t m = __ballot(valid);
 #pragma unroll
-    for (int bit = 0; bit < 6; ++bit) {  // experts < 64
+    for (int bit = 0; bit < BITS; ++bit) {
         const uint64_t plane = __ballot(((v >> bit) & 1) != 0);
         m &= ((v >> bit) & 1) != 0 ? plane : ~plane;
     }
     return valid ? m : 0ull;
 }
 
+// Experts per lane (EPL, lane owns experts lane + 64 j) and id bits.
+template <int EPL>
+struct Wide {
+    static constexpr int NE = 64 * EPL;
+    static constexpr int BITS = EPL == 1 ? 6 : (EPL == 2 ? 7 : (EPL == 4 ? 8 : 9));
+};
+
 // This wave's step: its entry (-1 past the end), the lanes sharing its expert,
 // and the step's count per expert into count[] (one LDS row per wave).
+template <int EPL>
 __device__ inline void count_step(const PermuteArgs& a, int64_t i, int lane, int& v, uint64_t& m, int* count) {
     const int64_t total = a.tokens * a.top_k;
     v = i < total ? a.idx[i] : -1;
-    m = same_expert(v, a.experts);
-    count[lane] = 0;
+    m = same_expert<Wide<EPL>::BITS>(v, a.experts);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        count[lane + 64 * j] = 0;
+    }
     __builtin_amdgcn_wave_barrier();
     const uint64_t below = (1ull << lane) - 1ull;
     if (m != 0 && (m & below) == 0) {  // lowest lane of its expert in this step
@@ -63,12 +76,14 @@ __device__ inline void count_step(const PermuteArgs& a, int64_t i, int lane, int
     }
 }
 
-// scratch: [0] the arrival ticket (0 between launches), [16, 16 + 64 G) the
+// scratch: [0] the arrival ticket (0 between launches), [16, 16 + NE G) the
 // segment counts, replaced by the segment bases.
 constexpr int kTicketWords = 16;
 
+template <int EPL>
 __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) {
-    __shared__ int wave_count[kWaves][kMaxExperts];
+    constexpr int NE = Wide<EPL>::NE;
+    __shared__ int wave_count[kWaves][NE];
     __shared__ uint32_t arrived;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -77,17 +92,21 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
     const int G = gridDim.x;
     int v;
     uint64_t m;
-    count_step(a, static_cast<int64_t>(g) * kSegment + wave * 64 + lane, lane, v, m, wave_count[wave]);
+    count_step<EPL>(a, static_cast<int64_t>(g) * kSegment + wave * 64 + lane, lane, v, m, wave_count[wave]);
     __syncthreads();
     int32_t* seg = a.scratch + kTicketWords;
     if (threadIdx.x < 64) {
-        int c = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            c += wave_count[w][lane];
-        }
-        if (lane < E) {
-            store_agent(seg + g * kMaxExperts + lane, c);
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            int c = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                c += wave_count[w][e];
+            }
+            if (e < E) {
+                store_agent(seg + g * NE + e, c);
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the counts are out before the ticket
@@ -102,72 +121,83 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
         return;
     }
     // The last workgroup: lane e scans expert e's counts over the segments (in
-    // batches of 8 loads), then the totals over the experts.
-    const bool valid = lane < E;
-    int tot = 0;
-    for (int g0 = 0; g0 < G; g0 += 8) {
-        int c[8];
+    // batches of 8 loads), then the totals over the experts in expert order.
+    int carry = 0, carry_active = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            c[j] = valid && g0 + j < G ? load_agent(seg + (g0 + j) * kMaxExperts + lane) : 0;
-        }
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        const bool valid = e < E;
+        int tot = 0;
+        for (int g0 = 0; g0 < G; g0 += 8) {
+            int c[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (valid && g0 + j < G) {
-                seg[(g0 + j) * kMaxExperts + lane] = tot;  // relative base, offset added below
-                tot += c[j];
+            for (int q = 0; q < 8; ++q) {
+                c[q] = valid && g0 + q < G ? load_agent(seg + (g0 + q) * NE + e) : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (valid && g0 + q < G) {
+                    seg[(g0 + q) * NE + e] = tot;  // relative base, offset added below
+                    tot += c[q];
+                }
             }
         }
-    }
-    int incl = tot;
+        int incl = tot;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int up = __shfl_up(incl, o);
-        if (lane >= o) {
-            incl += up;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int up = __shfl_up(incl, o);
+            if (lane >= o) {
+                incl += up;
+            }
         }
-    }
-    const int off = incl - tot;
-    if (valid) {
-        for (int s = 0; s < G; ++s) {
-            seg[s * kMaxExperts + lane] += off;
+        const int off = carry + incl - tot;
+        if (valid) {
+            for (int sg = 0; sg < G; ++sg) {
+                seg[sg * NE + e] += off;
+            }
+            a.rb.counts[e] = tot;
+            a.rb.offsets[e] = off;
         }
-        a.rb.counts[lane] = tot;
-        a.rb.offsets[lane] = off;
-    }
-    if (lane == E - 1) {
-        a.rb.offsets[E] = incl;
-    }
-    // Experts with tokens, ascending, and their number.
-    const uint64_t below = (1ull << lane) - 1ull;
-    const uint64_t has = __ballot(valid && tot > 0);
-    if (valid && tot > 0) {
-        a.rb.active[__popcll(has & below)] = lane;
+        carry += __shfl(incl, 63);
+        // Experts with tokens, ascending.
+        const uint64_t has = __ballot(valid && tot > 0);
+        if (valid && tot > 0) {
+            a.rb.active[carry_active + __popcll(has & below)] = e;
+        }
+        carry_active += __popcll(has);
     }
     if (lane == 0) {
-        a.rb.active[E] = __popcll(has);
+        a.rb.offsets[E] = carry;
+        a.rb.active[E] = carry_active;
         a.scratch[0] = 0;  // the ticket, for the next launch
     }
 }
 
+template <int EPL>
 __global__ __launch_bounds__(kThreads) void permute_scatter_kernel(PermuteArgs a) {
-    __shared__ int wave_count[kWaves][kMaxExperts];
-    __shared__ int wave_base[kWaves][kMaxExperts];
+    constexpr int NE = Wide<EPL>::NE;
+    __shared__ int wave_count[kWaves][NE];
+    __shared__ int wave_base[kWaves][NE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = blockIdx.x;
     const int64_t i = static_cast<int64_t>(g) * kSegment + wave * 64 + lane;
     int v;
     uint64_t m;
-    count_step(a, i, lane, v, m, wave_count[wave]);
+    count_step<EPL>(a, i, lane, v, m, wave_count[wave]);
     __syncthreads();
     if (threadIdx.x < 64) {
         // First position of each expert for every wave of the segment.
-        int run = lane < a.experts ? a.scratch[kTicketWords + g * kMaxExperts + lane] : 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            wave_base[w][lane] = run;
-            run += wave_count[w][lane];
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            int run = e < a.experts ? a.scratch[kTicketWords + g * NE + e] : 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                wave_base[w][e] = run;
+                run += wave_count[w][e];
+            }
         }
     }
     __syncthreads();
@@ -179,27 +209,41 @@ __global__ __launch_bounds__(kThreads) void permute_scatter_kernel(PermuteArgs a
     }
 }
 
+template <int EPL>
+hipError_t launch_epl(const PermuteArgs& a, int64_t segments, hipStream_t s) {
+    hipLaunchKernelGGL(permute_count_kernel<EPL>, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL(permute_scatter_kernel<EPL>, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int64_t permute_scratch_words(int64_t assignments) {
-    return kTicketWords + (assignments + kSegment - 1) / kSegment * kMaxExperts;
+    return kTicketWords + (assignments + kSegment - 1) / kSegment * kMaxExpertsWide;
 }
 
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
         return hipSuccess;
     }
-    if (a.experts <= 0 || a.experts > kMaxExperts || a.scratch == nullptr) {
+    if (a.experts <= 0 || a.experts > kMaxExpertsWide || a.scratch == nullptr) {
         return hipErrorInvalidValue;
     }
     const int64_t segments = (a.tokens * a.top_k + kSegment - 1) / kSegment;
-    hipLaunchKernelGGL(permute_count_kernel, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) {
-        return err;
+    if (a.experts <= 64) {
+        return launch_epl<1>(a, segments, s);
     }
-    hipLaunchKernelGGL(permute_scatter_kernel, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
-    return hipGetLastError();
+    if (a.experts <= 128) {
+        return launch_epl<2>(a, segments, s);
+    }
+    if (a.experts <= 256) {
+        return launch_epl<4>(a, segments, s);
+    }
+    return launch_epl<8>(a, segments, s);
 }
 
 }  // namespace lm

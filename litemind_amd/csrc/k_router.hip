@@ -189,6 +189,171 @@ __global__ __launch_bounds__(kWaves * 64) void router_kernel(RouterArgs a, const
     }
 }
 
+// ---------------------------------------------------------------------------
+// More than 64 experts (up to 64 EPL): lane owns experts lane + 64 j.  One
+// workgroup of 4 waves routes 4 TPW tokens; per chunk of R = 64 / EPL gate rows
+// all threads stage the rows of the transposed gate ([H, E]) and the tokens'
+// activations in LDS (16 KB of gate per chunk whatever EPL), and every lane
+// runs EPL x TPW of LiteMind's sequential chains (src/Gemm.cpp:183-189).  With
+// do_matvec = 0, x holds the logits [T, E] (select only).
+// ---------------------------------------------------------------------------
+template <int EPL, int TPW>
+__global__ __launch_bounds__(kWaves * 64) void router_multi_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                   const float* __restrict__ wt) {
+    constexpr int R = 64 / EPL;
+    constexpr int NE = 64 * EPL;
+    constexpr int XT = kWaves * TPW;  // tokens of the workgroup
+    __shared__ float wstage[2][R][NE];
+    __shared__ float xstage[2][XT][R];
+    __shared__ __align__(16) float sel[kWaves][select_multi_words(EPL)];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * XT;
+    const int64_t t0 = tb0 + static_cast<int64_t>(wave) * TPW;
+    const bool active = t0 < a.tokens;
+    const int E = a.experts;
+    const int H = a.hidden;
+
+    float acc[TPW][EPL];
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            acc[k][j] = 0.0f;
+        }
+    }
+    if (a.do_matvec) {
+        constexpr int kPerW = R * NE / (kWaves * 64);  // 16 gate values per thread and chunk
+        float wpre[kPerW];
+        float xpre[(XT * R + kWaves * 64 - 1) / (kWaves * 64)];
+        auto fetch = [&](int i0) {
+#pragma unroll
+            for (int q = 0; q < kPerW; ++q) {
+                const int idx = threadIdx.x + q * kWaves * 64;
+                const int r = idx / NE, e = idx % NE;
+                wpre[q] = (i0 + r < H && e < E) ? wt[static_cast<int64_t>(i0 + r) * E + e] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q * kWaves * 64 < XT * R; ++q) {
+                const int idx = threadIdx.x + q * kWaves * 64;
+                const int tk = idx / R, r = idx % R;
+                const int64_t t = tb0 + tk;
+                xpre[q] = (idx < XT * R && t < a.tokens && i0 + r < H) ? x[t * H + i0 + r] : 0.0f;
+            }
+        };
+        auto store = [&](int buf) {
+#pragma unroll
+            for (int q = 0; q < kPerW; ++q) {
+                const int idx = threadIdx.x + q * kWaves * 64;
+                wstage[buf][idx / NE][idx % NE] = wpre[q];
+            }
+#pragma unroll
+            for (int q = 0; q * kWaves * 64 < XT * R; ++q) {
+                const int idx = threadIdx.x + q * kWaves * 64;
+                if (idx < XT * R) {
+                    xstage[buf][idx / R][idx % R] = xpre[q];
+                }
+            }
+        };
+        const int nchunks = (H + R - 1) / R;
+        fetch(0);
+        store(0);
+        lds_barrier();
+        for (int c = 0; c < nchunks; ++c) {
+            const int i0 = c * R;
+            const int b = c & 1;
+            if (c + 1 < nchunks) {
+                fetch(i0 + R);
+            }
+            if (active) {
+                const int rows = H - i0 < R ? H - i0 : R;
+                for (int r = 0; r < rows; ++r) {
+                    float w[EPL];
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) {
+                        w[j] = wstage[b][r][lane + 64 * j];
+                    }
+#pragma unroll
+                    for (int k = 0; k < TPW; ++k) {
+                        const float xv = xstage[b][wave * TPW + k][r];
+#pragma unroll
+                        for (int j = 0; j < EPL; ++j) {
+                            const float p = w[j] * xv;
+                            acc[k][j] = acc[k][j] + p;
+                        }
+                    }
+                }
+            }
+            if (c + 1 < nchunks) {
+                store((c + 1) & 1);
+            }
+            lds_barrier();
+        }
+    } else if (active) {
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) {
+            const int64_t t = t0 + k;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const int e = lane + 64 * j;
+                acc[k][j] = (e < E && t < a.tokens) ? x[t * E + e] : 0.0f;
+            }
+        }
+    }
+    if (!active) {
+        return;
+    }
+    const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
+    const int K = a.top_k < E ? a.top_k : E;
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+        const int64_t t = t0 + k;
+        if (t >= a.tokens) {
+            break;
+        }
+        float logit[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            logit[j] = acc[k][j];
+            if (a.bias != nullptr && e < E) {
+                logit[j] = logit[j] + a.bias[e];
+            }
+            if (a.logits != nullptr && e < E) {
+                a.logits[t * E + e] = logit[j];
+            }
+        }
+        int rank[EPL];
+        float weight[EPL];
+        select_token_multi<EPL>(logit, lane, p, sel[wave], rank, weight);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            if (rank[j] < K) {
+                a.idx[t * a.top_k + rank[j]] = lane + 64 * j;
+                a.wts[t * a.top_k + rank[j]] = weight[j];
+            }
+        }
+        if (a.x16 != nullptr) {
+            const float* xt = x + t * H;
+            for (int c = lane; c < a.hidden_p; c += 64) {
+                a.x16[panel_index(t, c, a.tokens)] = c < H ? static_cast<_Float16>(xt[c]) : static_cast<_Float16>(0.0f);
+            }
+        }
+    }
+}
+
+template <int EPL>
+void launch_multi(const RouterArgs& a, hipStream_t s) {
+    const int tpw = a.do_matvec && a.tokens >= 1024 ? 2 : 1;
+    const int64_t per_block = static_cast<int64_t>(kWaves) * tpw;
+    const dim3 grid(static_cast<unsigned>((a.tokens + per_block - 1) / per_block));
+    if (tpw == 2) {
+        hipLaunchKernelGGL((router_multi_kernel<EPL, 2>), grid, dim3(kWaves * 64), 0, s, a, a.x, a.wt);
+    } else {
+        hipLaunchKernelGGL((router_multi_kernel<EPL, 1>), grid, dim3(kWaves * 64), 0, s, a, a.x, a.wt);
+    }
+}
+
 // Few-token router (T <= 4) for shapes the wide kernel below does not take
 // (E != 64, or H not a multiple of 256): one workgroup of 16 waves.  The tokens' activations
 // are staged in LDS once; all 1024 threads stream the transposed gate with a
@@ -610,6 +775,19 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
     }
     if (a.tokens <= 0) {
         return hipSuccess;
+    }
+    if (a.experts > kMaxExperts) {
+        if (a.experts > kMaxExpertsWide) {
+            return hipErrorInvalidValue;
+        }
+        if (a.experts <= 128) {
+            launch_multi<2>(a, s);
+        } else if (a.experts <= 256) {
+            launch_multi<4>(a, s);
+        } else {
+            launch_multi<8>(a, s);
+        }
+        return hipGetLastError();
     }
     const size_t split_lds = sizeof(float) * static_cast<size_t>(a.hidden) * kSplitExperts;
     if (a.do_matvec && a.tokens == 1 && a.experts % kSplitExperts == 0 && a.logits_scratch != nullptr &&

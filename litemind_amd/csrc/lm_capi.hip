@@ -834,8 +834,8 @@ int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** 
     if (c.hidden_size <= 0 || c.hidden_size % 8 != 0) {
         return fail(LM_EINVAL, "hidden_size must be a positive multiple of 8");
     }
-    if (c.n_routed_experts <= 0 || c.n_routed_experts > lm::kMaxExperts) {
-        return fail(LM_EINVAL, "n_routed_experts must be in [1, 64]");
+    if (c.n_routed_experts <= 0 || c.n_routed_experts > lm::kMaxExpertsWide) {
+        return fail(LM_EINVAL, "n_routed_experts must be in [1, 512]");
     }
     if (c.num_experts_per_tok <= 0 || c.num_experts_per_tok > lm::kMaxTopK ||
         c.num_experts_per_tok > c.n_routed_experts) {

@@ -16,7 +16,8 @@ constexpr int kGroupRows = 32;
 // Padding granularity of the intermediate (reduction) and hidden dimensions in
 // the resident layout; padded rows and columns are zero.
 constexpr int kPad = 64;
-constexpr int kMaxExperts = 64;   // router kernel: one lane per expert
+constexpr int kMaxExperts = 64;   // one lane per expert: the single-token kernel and the fast router paths
+constexpr int kMaxExpertsWide = 512;  // the general router, selection and permutation (lane owns experts lane + 64 j)
 constexpr int kMaxTopK = 16;
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

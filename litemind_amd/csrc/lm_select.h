@@ -203,4 +203,163 @@ __device__ inline void select_token_lds(float logit, bool valid, int lane, const
     weight = my_w;
 }
 
+// ---- more than 64 experts ----------------------------------------------------
+//
+// MoeRouter takes any expert count (DeepSeek-V2 routes over 160 experts in 8
+// groups, V3 over 256).  Above 64 experts a lane owns experts lane + 64 j,
+// j < EPL, and the all-to-all steps of the selection go through the wave's own
+// LDS scratch: every lane reads the E values in expert order, so the maximum
+// (std::max_element: the first of equal values, a NaN only at index 0) and
+// the softmax total (left to right) are LiteMind's bit for bit.
+// Per-wave scratch of select_token_multi, in 32-bit words: values [64 EPL],
+// keys [64 EPL] (64-bit), group maxima and group flags [64 EPL] each, picked
+// weights [kMaxTopK].
+__host__ __device__ constexpr int select_multi_words(int epl) { return 64 * epl * 5 + kMaxTopK; }
+
+template <int EPL>
+__device__ inline void select_token_multi(const float (&logit)[EPL], int lane, const SelectPolicy& a, float* sh,
+                                          int (&rank)[EPL], float (&weight)[EPL]) {
+    constexpr int NE = 64 * EPL;
+    const int E = a.experts;
+    float* val = sh;
+    uint64_t* keys = reinterpret_cast<uint64_t*>(sh + NE);  // 8-byte aligned: NE is even
+    float* gval = sh + 3 * NE;
+    int* gflag = reinterpret_cast<int*>(sh + 4 * NE);
+    float* picked = sh + 5 * NE;
+    bool valid[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        valid[j] = lane + 64 * j < E;
+        if (valid[j]) {
+            val[lane + 64 * j] = logit[j];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // softmax (src/Gemm.cpp:209-223)
+    float maximum = val[0];
+    for (int e = 1; e < E; ++e) {
+        const float v = val[e];
+        maximum = maximum < v ? v : maximum;
+    }
+    float s[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        s[j] = valid[j] ? expf_ref(logit[j] - maximum) : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        if (valid[j]) {
+            val[lane + 64 * j] = s[j];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float total = 0.0f;
+    for (int e = 0; e < E; ++e) {
+        total = total + val[e];
+    }
+    const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
+    float score[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        score[j] = s[j] * inverse;
+    }
+    // Group-limited mask (src/MoeRouter.cpp:67-84), with the constructor's
+    // fallback to greedy when the groups do not divide the experts (:46-51):
+    // a group's score is its first maximum, and the topk_group groups with the
+    // highest scores (lower index first on equal scores) stay allowed.
+    bool allowed[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        allowed[j] = true;
+    }
+    const int G = a.n_group;
+    if (a.group_limited && G > 1 && E % G == 0) {
+        const int per_group = E / G;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            if (valid[j]) {
+                val[lane + 64 * j] = score[j];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int g = lane; g < G; g += 64) {
+            float best = val[g * per_group];
+            for (int q = 1; q < per_group; ++q) {
+                const float v = val[g * per_group + q];
+                best = best < v ? v : best;
+            }
+            gval[g] = best;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int take = a.topk_group < G ? a.topk_group : G;
+        for (int g = lane; g < G; g += 64) {
+            const float mine = gval[g];
+            int beaten = 0;
+            for (int h = 0; h < G; ++h) {
+                const float other = gval[h];
+                beaten += (other > mine || (other == mine && h < g)) ? 1 : 0;
+            }
+            gflag[g] = beaten < take ? 1 : 0;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            allowed[j] = valid[j] && gflag[(lane + 64 * j) / per_group] != 0;
+        }
+    }
+    // top_k_indices (src/MoeRouter.cpp:14-34): allowed first, then score
+    // descending, then index ascending.  Scores are non-negative, so their bit
+    // patterns order like the values; the index makes every key unique.
+    uint64_t key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        key[j] = valid[j] ? ((allowed[j] ? (1ull << 62) : 0ull) | (static_cast<uint64_t>(float_bits(score[j])) << 16) |
+                             static_cast<uint64_t>(0xffff - e))
+                          : 0ull;
+        if (valid[j]) {
+            keys[e] = key[j];
+        }
+        rank[j] = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int e = 0; e < E; ++e) {
+        const uint64_t k = keys[e];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            rank[j] += k > key[j] ? 1 : 0;
+        }
+    }
+    const int K = a.top_k < E ? a.top_k : E;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        if (valid[j] && rank[j] < K) {
+            picked[rank[j]] = score[j];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // Weights in rank order; the selected sum runs left to right as in :91-94.
+    float selected_sum = 0.0f;
+    for (int r = 0; r < K; ++r) {
+        selected_sum = selected_sum + picked[r];
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        float w = score[j];
+        if (a.top_k > 1 && a.normalize) {
+            const float denominator = selected_sum + 1e-20f;
+            w = w / denominator;
+        } else if (a.scale != 1.0f) {
+            w = w * a.scale;
+        }
+        weight[j] = w;
+        if (!valid[j]) {
+            rank[j] = E;  // never selected
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // the scratch may be reused right after
+}
+
 }  // namespace lm

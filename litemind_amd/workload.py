@@ -44,6 +44,9 @@ class Dims:
     norm_topk_prob: bool = False
     routed_scaling_factor: float = 1.0
     rms_norm_eps: float = 1e-6
+    group_limited: bool = False  # topk_method == "group_limited_greedy"
+    n_group: int = 1
+    topk_group: int = 1
 
     @property
     def shared_inter(self) -> int:
@@ -59,7 +62,8 @@ class Dims:
             hidden_size=self.hidden, moe_intermediate_size=self.inter, n_routed_experts=self.experts,
             num_experts_per_tok=self.top_k, n_shared_experts=self.n_shared, intermediate_size=self.dense_inter,
             norm_topk_prob=1 if self.norm_topk_prob else 0, routed_scaling_factor=self.routed_scaling_factor,
-            group_limited=0, n_group=1, topk_group=1, rms_norm_eps=self.rms_norm_eps,
+            group_limited=1 if self.group_limited else 0, n_group=self.n_group, topk_group=self.topk_group,
+            rms_norm_eps=self.rms_norm_eps,
             num_layers=num_layers if num_layers is not None else self.layers)
 
 

@@ -107,6 +107,36 @@ def router_known():
     np.savez_compressed(os.path.join(HERE, "router_known.npz"), **out)
 
 
+# More than 64 experts, group-limited greedy routing: DeepSeek-V2's 160 experts
+# in 8 groups (3 kept), a 256-expert layer in 8 groups (4 kept, top-8,
+# normalised), and 512 experts in 16 groups (4 kept, scaled).
+WIDE_VARIANTS = {
+    "e160": (160, 6, 0, 1.0, 1, 8, 3),
+    "e256": (256, 8, 1, 1.0, 1, 8, 4),
+    "e512": (512, 8, 0, 2.5, 1, 16, 4),
+    "e160_greedy": (160, 6, 0, 1.0, 0, 1, 1),
+}
+
+
+def router_wide():
+    """The compiled router on 48 logit vectors per configuration: random
+    N(0, 2), rounded (many exact ties between experts and between groups), and
+    one row of equal logits."""
+    out = {}
+    rng = np.random.default_rng(20260160)
+    for name, (E, k, norm, scale, grouped, ng, tg) in WIDE_VARIANTS.items():
+        cfg = ol.router_cfg(E, k, bool(norm), scale, bool(grouped), ng, tg)
+        logits = (rng.standard_normal((48, E)) * 2).astype(np.float32)
+        logits[16:32] = np.round(logits[16:32])
+        logits[40] = 0.5
+        idx = np.zeros((48, k), np.int32)
+        w = np.zeros((48, k), np.float32)
+        for t in range(48):
+            idx[t], w[t] = ol.ref_select(logits[t], cfg)
+        out[f"{name}_logits"], out[f"{name}_index"], out[f"{name}_weight"] = logits, idx, w
+    np.savez_compressed(os.path.join(HERE, "router_wide.npz"), **out)
+
+
 def router_v2lite():
     """Full-width router of DeepSeek-V2-Lite (64 experts, hidden 2048) on 64 seeded tokens."""
     seed, T = wl.MASTER_SEED, 64
@@ -178,6 +208,7 @@ def main():
         sys.exit("oracle/_ref/libref.so is not built (make -C oracle ref)")
     kerneltest()
     router_known()
+    router_wide()
     router_v2lite()
     layer_tiny()
     layer_v2lite()

@@ -141,7 +141,8 @@ def oracle_moe_layer(layer, x: np.ndarray, bias=None, threads: int = 0):
     d = layer.dims
     T = x.shape[0]
     dims = LayerDims(d.hidden, d.inter, d.experts, d.top_k, d.shared_inter if layer.shared_gate is not None else 0)
-    cfg = router_cfg(d.experts, d.top_k, d.norm_topk_prob, d.routed_scaling_factor)
+    cfg = router_cfg(d.experts, d.top_k, d.norm_topk_prob, d.routed_scaling_factor, d.group_limited, d.n_group,
+                     d.topk_group)
     gate, up, down = _ptr_array(layer.gate), _ptr_array(layer.up), _ptr_array(layer.down)
     w = LayerWeights(layer.router.ctypes.data, C.cast(gate, C.c_void_p), C.cast(up, C.c_void_p),
                      C.cast(down, C.c_void_p),
@@ -173,7 +174,8 @@ def ref_moe_layer(layer, x: np.ndarray, bias=None, workers: int = 0):
     b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
     S = d.shared_inter if layer.shared_gate is not None else 0
     rc = ref().ref_moe_layer(d.hidden, d.inter, d.experts, d.top_k, S, 1 if d.norm_topk_prob else 0,
-                             d.routed_scaling_factor, 1, 1, 0, p(layer.router), gate, up, down,
+                             d.routed_scaling_factor, d.n_group, d.topk_group, 1 if d.group_limited else 0,
+                             p(layer.router), gate, up, down,
                              p(layer.shared_gate), p(layer.shared_up), p(layer.shared_down), p(x), T, p(b), p(y),
                              p(idx), p(wt), workers)
     if rc != 0:

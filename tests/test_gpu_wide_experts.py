@@ -1,0 +1,154 @@
+"""Layers of more than 64 routed experts on the GPU (LiteMind's MoeRouter takes
+any expert count; DeepSeek-V2 routes over 160 experts in 8 groups with
+group-limited greedy selection): the general router and selection (a lane owns
+experts lane + 64 j), the permutation and both expert paths, against the
+oracle.  Logits, experts, weights and the permutation bit-exact; layer outputs
+within max-abs 2e-2 and mean-rel 1e-3 (1e-5 on the fp32 GEMV path)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from conftest import MAX_ABS, MEAN_REL, announce, layer_error
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+WIDE_VARIANTS = {"e160": (160, 6, 0, 1.0, 1, 8, 3), "e256": (256, 8, 1, 1.0, 1, 8, 4),
+                 "e512": (512, 8, 0, 2.5, 1, 16, 4), "e160_greedy": (160, 6, 0, 1.0, 0, 1, 1)}
+
+
+def _dims(E=160, k=6, grouped=True, n_group=8, topk_group=3, hidden=1024, inter=256, norm=False, scale=1.0):
+    from litemind_amd import workload as wl
+
+    return wl.Dims(hidden=hidden, inter=inter, experts=E, top_k=k, n_shared=2, dense_inter=0,
+                   norm_topk_prob=norm, routed_scaling_factor=scale, group_limited=grouped, n_group=n_group,
+                   topk_group=topk_group)
+
+
+@pytest.fixture(scope="module")
+def wide_ctx():
+    """DeepSeek-V2's routing (160 experts, 8 groups, 3 kept, top-6) on a reduced
+    hidden / intermediate size (1024 / 256) so the oracle stays fast."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = _dims()
+    announce("create 160-expert context (8 groups, 3 kept)")
+    ctx = Context(dims.moe_config(num_layers=1))
+    layer = wl.moe_layer(wl.MASTER_SEED + 160, 0, dims)
+    wl.upload_moe_layer(ctx, 0, layer)
+    yield ctx, layer
+    ctx.close()
+
+
+def _oracle_route(layer, x):
+    d = layer.dims
+    T = x.shape[0]
+    logits = np.zeros((T, d.experts), np.float32)
+    for t in range(T):
+        ol.oracle().orc_matvec_f32(ol.p(layer.router), ol.p(np.ascontiguousarray(x[t])), ol.p(logits[t]),
+                                   d.experts, d.hidden)
+    cfg = ol.router_cfg(d.experts, d.top_k, d.norm_topk_prob, d.routed_scaling_factor, d.group_limited, d.n_group,
+                        d.topk_group)
+    idx = np.zeros((T, d.top_k), np.int32)
+    w = np.zeros((T, d.top_k), np.float32)
+    for t in range(T):
+        idx[t], w[t] = ol.oracle_select(logits[t], cfg)
+    return logits, idx, w
+
+
+@pytest.mark.parametrize("name", list(WIDE_VARIANTS))
+def test_wide_select_golden(name):
+    """lm_router_select (MoeRouter::select alone) on the compiled router's
+    golden logits, ties included: experts and weights bit for bit."""
+    from litemind_amd import Context
+
+    E, k, norm, scale, grouped, ng, tg = WIDE_VARIANTS[name]
+    g = np.load(os.path.join(GOLDEN, "router_wide.npz"))
+    logits = g[f"{name}_logits"]
+    T = logits.shape[0]
+    dims = _dims(E, k, bool(grouped), ng, tg, hidden=16, inter=16, norm=bool(norm), scale=scale)
+    announce(f"select only, {name}: {T} tokens")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        dl = ctx.to_device(logits)
+        idx, w = ctx.empty((T, k), np.int32), ctx.empty((T, k))
+        ctx.router_select(dl, T, idx, w)
+        ctx.synchronize()
+        gi, gw = idx.download(), w.download()
+    assert np.array_equal(gi, g[f"{name}_index"])
+    assert np.array_equal(gw.view(np.uint32), g[f"{name}_weight"].view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 7, 300, 1500])
+def test_wide_router_bit_exact(wide_ctx, T):
+    """Logits (each LiteMind's sequential fp32 chain), experts and weights at
+    one, a few and many tokens (two tokens per wave from 1024 on)."""
+    from litemind_amd import workload as wl
+
+    ctx, layer = wide_ctx
+    x = wl.tokens(wl.MASTER_SEED + 1600 + T, T, layer.dims.hidden)
+    announce(f"160-expert router T={T}")
+    dx = ctx.to_device(x)
+    lg, idx, w = ctx.empty((T, 160)), ctx.empty((T, 6), np.int32), ctx.empty((T, 6))
+    ctx.router(0, dx, T, idx, w, logits=lg)
+    ctx.synchronize()
+    glg, gidx, gw = lg.download(), idx.download(), w.download()
+    olg, oidx, ow = _oracle_route(layer, x)
+    assert np.array_equal(glg.view(np.uint32), olg.view(np.uint32)), "logits differ"
+    assert np.array_equal(gidx, oidx), "selected experts differ"
+    assert np.array_equal(gw.view(np.uint32), ow.view(np.uint32)), "weights differ"
+    per = 160 // 8
+    assert all(len({e // per for e in row}) <= 3 for row in gidx)  # at most topk_group groups
+    for b in (dx, lg, idx, w):
+        b.free()
+
+
+def test_wide_permute(wide_ctx):
+    """The canonical permutation of 1500 tokens' selections over 160 experts
+    (the counts, offsets, the list of experts with tokens, perm and its inverse)."""
+    from litemind_amd import workload as wl
+
+    ctx, layer = wide_ctx
+    T = 1500
+    _, oidx, _ = _oracle_route(layer, wl.tokens(wl.MASTER_SEED + 1601, T, layer.dims.hidden))
+    announce("160-expert permutation T=1500")
+    di = ctx.to_device(oidx)
+    counts, offsets = ctx.empty((160,), np.int32), ctx.empty((161,), np.int32)
+    perm, slot_of = ctx.empty((T * 6,), np.int32), ctx.empty((T * 6,), np.int32)
+    ctx.permute(di, T, counts, offsets, perm, slot_of)
+    ctx.synchronize()
+    oc, oo, op, os_ = ol.oracle_permute(oidx, 160)
+    assert np.array_equal(counts.download(), oc)
+    assert np.array_equal(offsets.download(), oo)
+    assert np.array_equal(perm.download(), op)
+    assert np.array_equal(slot_of.download(), os_)
+
+
+@pytest.mark.parametrize("T,path", [(1, "auto"), (5, "auto"), (33, "gemv"), (300, "auto")])
+def test_wide_layer(wide_ctx, T, path):
+    """The whole MoE block over 160 experts: at T = 1 and with LM_PATH_GEMV the
+    fp32 weight-streaming kernels, from three tokens on the fp16 MFMA kernels."""
+    from litemind_amd import PATH_AUTO, PATH_GEMV
+    from litemind_amd import workload as wl
+
+    ctx, layer = wide_ctx
+    H = layer.dims.hidden
+    x = wl.tokens(wl.MASTER_SEED + 1700 + T, T, H)
+    announce(f"160-expert layer T={T} path={path}")
+    dx, y = ctx.to_device(x), ctx.empty((T, H))
+    idx, w = ctx.empty((T, 6), np.int32), ctx.empty((T, 6))
+    ctx.moe_forward(0, dx, T, y, idx=idx, w=w, path=PATH_GEMV if path == "gemv" else PATH_AUTO)
+    ctx.synchronize()
+    gy, gidx, gw = y.download(), idx.download(), w.download()
+    oy, oidx, ow, _ = ol.oracle_moe_layer(layer, x)
+    assert np.array_equal(gidx, oidx)
+    assert np.array_equal(gw.view(np.uint32), ow.view(np.uint32))
+    max_abs, mean_rel = layer_error(gy, oy)
+    print(f"E=160 T={T} {path} max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+    if path == "gemv" or T <= 2:
+        assert mean_rel < 1e-5
+    for b in (dx, y, idx, w):
+        b.free()

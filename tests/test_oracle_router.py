@@ -92,7 +92,9 @@ def test_router_matches_compiled_reference_random():
     rng = np.random.default_rng(12)
     configs = [ol.router_cfg(64, 6), ol.router_cfg(64, 6, normalize=True), ol.router_cfg(16, 4, scale=2.5),
                ol.router_cfg(64, 6, group_limited=True, n_group=8, topk_group=3),
-               ol.router_cfg(12, 3, group_limited=True, n_group=5, topk_group=2)]  # 12 % 5 != 0: greedy fallback
+               ol.router_cfg(12, 3, group_limited=True, n_group=5, topk_group=2),  # 12 % 5 != 0: greedy fallback
+               ol.router_cfg(160, 6, group_limited=True, n_group=8, topk_group=3),
+               ol.router_cfg(256, 8, normalize=True, group_limited=True, n_group=8, topk_group=4)]
     for cfg in configs:
         for _ in range(100):
             logits = (rng.standard_normal(cfg.expert_count) * 2).astype(np.float32)
@@ -107,3 +109,49 @@ def test_select_rejects_like_reference():
     assert len(idx) == 0
     idx, _ = ol.oracle_select(np.zeros(8, np.float32), ol.router_cfg(8, 0))
     assert len(idx) == 0
+
+
+WIDE_VARIANTS = {"e160": (160, 6, 0, 1.0, 1, 8, 3), "e256": (256, 8, 1, 1.0, 1, 8, 4),
+                 "e512": (512, 8, 0, 2.5, 1, 16, 4), "e160_greedy": (160, 6, 0, 1.0, 0, 1, 1)}
+
+
+def wide_cfg(name):
+    E, k, norm, scale, grouped, ng, tg = WIDE_VARIANTS[name]
+    return ol.router_cfg(E, k, bool(norm), scale, bool(grouped), ng, tg)
+
+
+@pytest.mark.parametrize("name", list(WIDE_VARIANTS))
+def test_wide_router_golden(name):
+    """More than 64 experts with group-limited greedy routing (DeepSeek-V2's 160
+    experts in 8 groups, 3 kept; 256 and 512 experts): the oracle against the
+    compiled router's outputs (tests/golden/router_wide.npz), ties included."""
+    g = np.load(os.path.join(GOLDEN, "router_wide.npz"))
+    cfg = wide_cfg(name)
+    for t in range(g[f"{name}_logits"].shape[0]):
+        idx, w = ol.oracle_select(g[f"{name}_logits"][t], cfg)
+        assert np.array_equal(idx, g[f"{name}_index"][t]), (name, t)
+        assert np.array_equal(bits(w), bits(g[f"{name}_weight"][t])), (name, t)
+
+
+def test_wide_router_brute_force_groups():
+    """Group-limited selection by its definition (src/MoeRouter.cpp:67-84): each
+    group scored by its maximum softmax score, the topk_group best groups (lower
+    index on ties) kept, then the best experts of the kept groups, ties to the
+    lower index; computed here in float64 order from the oracle's own scores."""
+    rng = np.random.default_rng(13)
+    E, k, ng, tg = 160, 6, 8, 3
+    cfg = ol.router_cfg(E, k, group_limited=True, n_group=ng, topk_group=tg)
+    per = E // ng
+    for t in range(200):
+        logits = (rng.standard_normal(E) * 2).astype(np.float32)
+        if t % 2 == 0:
+            logits = np.round(logits).astype(np.float32)
+        scores = logits.copy()
+        ol.oracle().orc_softmax(ol.p(scores), E)
+        gmax = [float(scores[g * per:(g + 1) * per].max()) for g in range(ng)]
+        kept = sorted(range(ng), key=lambda g: (-gmax[g], g))[:tg]
+        allowed = [e for e in range(E) if e // per in kept]
+        order = sorted(allowed, key=lambda e: (-float(scores[e]), e))[:k]
+        idx, w = ol.oracle_select(logits, cfg)
+        assert list(idx) == order
+        assert np.array_equal(bits(w), bits(scores[order]))
