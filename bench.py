@@ -42,8 +42,11 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over
 # this benchmark, scaled by the counters' readings for a conversion kernel of
-# known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md).
-MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 140_105_165}
+# known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md and
+# profiles/mfma_grouped_kernel_prefill_t2048_skewed.md).
+MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 139_534_937,
+                    ("prefill_t2048_skewed", "gate_up"): 1_156_425_584,
+                    ("prefill_t2048_skewed", "down"): 638_693_503}
 
 
 def log(msg: str) -> None:
@@ -260,8 +263,8 @@ def roofline(res: dict, mfma: bool) -> dict:
         out.update(achieved=round(tfs, 2), peak=MFMA_PEAK_TFLOPS, unit="TFLOP/s", frac=round(tfs / MFMA_PEAK_TFLOPS, 4))
     else:
         out.update(achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4))
-    out.update(traffic=None, avg_us=round(per[dominant] * 1e3, 2), algorithmic_bytes=by, algorithmic_flops=fl,
-               hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    out.update(traffic=MEASURED_TRAFFIC.get((res["workload"], dominant)), avg_us=round(per[dominant] * 1e3, 2),
+               algorithmic_bytes=by, algorithmic_flops=fl, hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     if mfma:
         out["mfma_frac"] = round(tfs / MFMA_PEAK_TFLOPS, 4)
     return out
@@ -274,8 +277,9 @@ def swiglu(res: dict) -> dict:
     alg = algorithmic(res["T"], int(round(res["distinct"])))
     fl = alg["gate_up_flops"] + alg["down_flops"]
     tf = fl / (us * 1e-6) / 1e12 if us else 0.0
+    traffic = [MEASURED_TRAFFIC.get((res["workload"], k)) for k in ("gate_up", "down")]
     return {"us": round(us, 2), "flops": fl, "achieved": round(tf, 2), "unit": "TFLOP/s", "peak": MFMA_PEAK_TFLOPS,
-            "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+            "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": None if None in traffic else sum(traffic)}
 
 
 def run_load(moe_layers: int) -> dict:
