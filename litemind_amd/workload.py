@@ -324,3 +324,66 @@ def dense_layer_tensors(layer: int, ffn, norm: np.ndarray) -> dict:
     gate, up, down = ffn
     return {p + "post_attention_layernorm.weight": norm, p + "mlp.gate_proj.weight": gate,
             p + "mlp.up_proj.weight": up, p + "mlp.down_proj.weight": down}
+
+
+# ---- multi-head latent attention (DeepSeek-V2-Lite: config.json of the model) ----
+
+@dataclasses.dataclass(frozen=True)
+class MlaDims:
+    hidden: int = 2048
+    heads: int = 16
+    q_lora_rank: int = 0
+    kv_lora_rank: int = 512
+    qk_nope: int = 128
+    qk_rope: int = 64
+    v_head: int = 128
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+    yarn: bool = True
+    factor: float = 40.0
+    beta_fast: float = 32.0
+    beta_slow: float = 1.0
+    mscale: float = 0.707
+    mscale_all_dim: float = 0.707
+    original_max: int = 4096
+    max_positions: int = 4096  # rotary table rows = KV cache capacity
+
+    @property
+    def qk_head(self) -> int:
+        return self.qk_nope + self.qk_rope
+
+
+V2_LITE_MLA = MlaDims()
+
+S_Q, S_QA, S_QB, S_KVA, S_KVB, S_O, S_QAN, S_KVAN = range(20, 28)
+
+
+@dataclasses.dataclass
+class MlaLayer:
+    dims: MlaDims
+    q_proj: np.ndarray | None      # [heads * qk_head, hidden] BF16 bits (q_lora_rank == 0)
+    q_a_proj: np.ndarray | None    # [q_lora_rank, hidden]
+    q_a_layernorm: np.ndarray | None
+    q_b_proj: np.ndarray | None    # [heads * qk_head, q_lora_rank]
+    kv_a_proj: np.ndarray          # [kv_lora_rank + qk_rope, hidden]
+    kv_a_layernorm: np.ndarray     # [kv_lora_rank] fp32
+    kv_b_proj: np.ndarray          # [heads * (qk_nope + v_head), kv_lora_rank]
+    o_proj: np.ndarray             # [hidden, heads * v_head]
+
+
+def mla_layer(seed: int, layer: int, d: MlaDims = V2_LITE_MLA, threads: int = 0) -> MlaLayer:
+    """Projections ~N(0, 0.02) BF16 (kv_b and q_b ~N(0, 0.05): their inputs are
+    RMS-normalised latents), layer norms 1 + N(0, 0.1)."""
+    H, nh, qk = d.hidden, d.heads, d.qk_head
+    qp = qa = qan = qb = None
+    if d.q_lora_rank == 0:
+        qp = normal_bf16(seed, stream_id(layer, S_Q), 0.02, (nh * qk, H), threads)
+    else:
+        qa = normal_bf16(seed, stream_id(layer, S_QA), 0.02, (d.q_lora_rank, H), threads)
+        qan = (1.0 + normal_f32(seed, stream_id(layer, S_QAN), 0.1, (d.q_lora_rank,), threads)).astype(np.float32)
+        qb = normal_bf16(seed, stream_id(layer, S_QB), 0.05, (nh * qk, d.q_lora_rank), threads)
+    kva = normal_bf16(seed, stream_id(layer, S_KVA), 0.02, (d.kv_lora_rank + d.qk_rope, H), threads)
+    kvan = (1.0 + normal_f32(seed, stream_id(layer, S_KVAN), 0.1, (d.kv_lora_rank,), threads)).astype(np.float32)
+    kvb = normal_bf16(seed, stream_id(layer, S_KVB), 0.05, (nh * (d.qk_nope + d.v_head), d.kv_lora_rank), threads)
+    o = normal_bf16(seed, stream_id(layer, S_O), 0.02, (H, nh * d.v_head), threads)
+    return MlaLayer(d, qp, qa, qan, qb, kva, kvan, kvb, o)

@@ -15,6 +15,10 @@
  *   orc_router_select           MoeRouterSamplerTest.cpp:30-93 + brute-force sort + compiled reference
  *   orc_permute                 brute-force stable sort + invariants (no reference counterpart)
  *   orc_moe_layer               compiled reference (per-token runner composition) + float64 brute force
+ *   orc_rope_tables / _apply    compiled reference (tables read back through its apply on unit pairs),
+ *                               closed forms (position 0, the rotation's norm), float64 brute force
+ *   orc_mla_forward             compiled reference (Attention::forward over token sequences, cache
+ *                               contents) + float64 brute force of the attention
  */
 #include "oracle.h"
 
@@ -556,4 +560,188 @@ void orc_dense_ffn(const uint16_t* gate, const uint16_t* up, const uint16_t* dow
         orc_matvec_bf16_accumulate(down, act, out, (size_t)hidden, (size_t)inter, 1.0f);
         free(act);
     }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Multi-head latent attention: src/Attention.cpp, src/Rope.cpp, KvCache       */
+/* ------------------------------------------------------------------------- */
+
+static const double kPi = 3.14159265358979323846;
+
+/* src/Rope.cpp:13-18; GCC contracts 0.1 * mscale * log(scale) + 1.0 to a fused
+ * multiply-add of the rounded 0.1 * mscale. */
+static double yarn_mscale(double scale, double mscale) {
+    if (scale <= 1.0) {
+        return 1.0;
+    }
+    return fma(0.1 * mscale, log(scale), 1.0);
+}
+
+/* Config::softmax_scale (src/Config.cpp:114-121): (qk_nope + qk_rope)^-0.5 in
+ * double, times the squared YaRN magnitude when mscale_all_dim is non-zero. */
+float orc_softmax_scale(int32_t qk_nope, int32_t qk_rope, int32_t yarn, double factor, double mscale_all_dim) {
+    double scale = 1.0 / sqrt((double)(qk_nope + qk_rope));
+    if (yarn && mscale_all_dim != 0.0) {
+        const double m = yarn_mscale(factor, mscale_all_dim);
+        scale *= m * m;
+    }
+    return (float)scale;
+}
+
+/* src/Rope.cpp:24-33. */
+static double correction_dimension(double rotations, int32_t dim, double base, int64_t original_max) {
+    const double numerator = (double)dim * log((double)original_max / (rotations * 2.0 * kPi));
+    return numerator / (2.0 * log(base));
+}
+
+/* src/Rope.cpp:36-103: double-precision frequencies (YaRN blend of the
+ * extrapolated and interpolated ones), cos and sin in double times the
+ * magnitude correction, rounded to float. */
+void orc_rope_tables(int32_t dim, int32_t max_positions, double theta, int32_t yarn, double factor,
+                     double beta_fast, double beta_slow, double mscale, double mscale_all_dim,
+                     int64_t original_max_positions, float* cos_out, float* sin_out) {
+    const int32_t half = dim / 2;
+    const double base = theta;
+    double inverse[512];
+    double magnitude = 1.0;
+    if (half > 512) {
+        return;
+    }
+    if (!yarn) {
+        for (int32_t i = 0; i < half; ++i) {
+            const double exponent = 2.0 * (double)i / (double)dim;
+            inverse[i] = 1.0 / pow(base, exponent);
+        }
+    } else {
+        const double f = factor <= 0.0 ? 1.0 : factor;
+        double low = floor(correction_dimension(beta_fast, dim, base, original_max_positions));
+        double high = ceil(correction_dimension(beta_slow, dim, base, original_max_positions));
+        low = low > 0.0 ? low : 0.0;
+        high = high < (double)dim - 1.0 ? high : (double)dim - 1.0;
+        if (high - low < 1e-6) {
+            high = low + 0.001;
+        }
+        for (int32_t i = 0; i < half; ++i) {
+            const double exponent = 2.0 * (double)i / (double)dim;
+            const double extrapolation = 1.0 / pow(base, exponent);
+            const double interpolation = extrapolation / f;
+            double ramp = ((double)i - low) / (high - low);
+            ramp = ramp < 0.0 ? 0.0 : (ramp > 1.0 ? 1.0 : ramp);
+            const double mask = 1.0 - ramp;
+            const double a = interpolation * (1.0 - mask);
+            const double b = extrapolation * mask;
+            inverse[i] = a + b;
+        }
+        magnitude = yarn_mscale(f, mscale) / yarn_mscale(f, mscale_all_dim);
+    }
+    for (int64_t p = 0; p < max_positions; ++p) {
+        for (int32_t i = 0; i < half; ++i) {
+            const double angle = (double)p * inverse[i];
+            cos_out[p * half + i] = (float)(cos(angle) * magnitude);
+            sin_out[p * half + i] = (float)(sin(angle) * magnitude);
+        }
+    }
+}
+
+/* src/Rope.cpp:105-127: channels (2i, 2i + 1) rotated into (i, i + half); GCC
+ * contracts each output to one fused multiply-add whose addend is the other
+ * product, rounded: lo = fma(even, cos, -(odd * sin)), hi = fma(odd, cos,
+ * even * sin) (checked against the compiled RotaryEmbedding::apply). */
+void orc_rope_apply(float* values, int32_t dim, const float* cos_row, const float* sin_row) {
+    float source[1024];
+    const int32_t half = dim / 2;
+    if (dim > 1024) {
+        return;
+    }
+    memcpy(source, values, sizeof(float) * (size_t)dim);
+    for (int32_t i = 0; i < half; ++i) {
+        const float even = source[2 * i];
+        const float odd = source[2 * i + 1];
+        /* even*cos - odd*sin and odd*cos + even*sin as LiteMind's build
+         * contracts them: the first product of each into the fma */
+        const float odd_sin = odd * sin_row[i];
+        const float even_sin = even * sin_row[i];
+        values[i] = fmaf(even, cos_row[i], -odd_sin);
+        values[i + half] = fmaf(odd, cos_row[i], even_sin);
+    }
+}
+
+/* src/Attention.cpp:22-103 with KvCache::append (src/KvCache.cpp) for one token. */
+int orc_mla_forward(const orc_mla_dims* d, const orc_mla_weights* w, const float* cos_table, const float* sin_table,
+                    float* key_nope, float* key_rope, float* value, int64_t capacity, int64_t* token_count,
+                    const float* x, int64_t position, float* out) {
+    const int32_t H = d->hidden, heads = d->heads, nope = d->qk_nope, rope = d->qk_rope, vh = d->v_head;
+    const int32_t qk = nope + rope, rank = d->kv_lora_rank, half = rope / 2;
+    float* query = (float*)malloc(sizeof(float) * (size_t)heads * (size_t)qk);
+    float* q_latent = (float*)malloc(sizeof(float) * (size_t)(d->q_lora_rank > 0 ? d->q_lora_rank : 1));
+    float* latent = (float*)malloc(sizeof(float) * (size_t)(rank + rope));
+    float* expanded = (float*)malloc(sizeof(float) * (size_t)heads * (size_t)(nope + vh));
+    float* context = (float*)malloc(sizeof(float) * (size_t)heads * (size_t)vh);
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(capacity > 0 ? capacity : 1));
+    int rc = 0;
+    /* queries (:34-45) */
+    if (d->q_lora_rank == 0) {
+        orc_matvec_bf16(w->q_proj, x, query, (size_t)heads * (size_t)qk, (size_t)H);
+    } else {
+        orc_matvec_bf16(w->q_a_proj, x, q_latent, (size_t)d->q_lora_rank, (size_t)H);
+        orc_rms_norm(q_latent, w->q_a_layernorm, (size_t)d->q_lora_rank, d->rms_norm_eps);
+        orc_matvec_bf16(w->q_b_proj, q_latent, query, (size_t)heads * (size_t)qk, (size_t)d->q_lora_rank);
+    }
+    /* rotary channels of each head (:48-50); apply is a no-op past the table (src/Rope.cpp:106-108) */
+    const int rotate = position >= 0 && position < d->max_positions;
+    for (int32_t h = 0; h < heads && rotate; ++h) {
+        orc_rope_apply(query + (size_t)h * (size_t)qk + (size_t)nope, rope, cos_table + position * half,
+                       sin_table + position * half);
+    }
+    /* compressed key and value (:53-61) */
+    orc_matvec_bf16(w->kv_a_proj, x, latent, (size_t)(rank + rope), (size_t)H);
+    orc_rms_norm(latent, w->kv_a_layernorm, (size_t)rank, d->rms_norm_eps);
+    if (rotate) {
+        orc_rope_apply(latent + rank, rope, cos_table + position * half, sin_table + position * half);
+    }
+    orc_matvec_bf16(w->kv_b_proj, latent, expanded, (size_t)heads * (size_t)(nope + vh), (size_t)rank);
+    /* append (:63-77, src/KvCache.cpp) */
+    if (*token_count >= capacity) {
+        rc = -1;
+        goto done;
+    }
+    {
+        const int64_t slot = (*token_count)++;
+        for (int32_t h = 0; h < heads; ++h) {
+            memcpy(key_nope + ((size_t)slot * heads + h) * nope, expanded + (size_t)h * (nope + vh),
+                   sizeof(float) * (size_t)nope);
+            memcpy(value + ((size_t)slot * heads + h) * vh, expanded + (size_t)h * (nope + vh) + nope,
+                   sizeof(float) * (size_t)vh);
+        }
+        memcpy(key_rope + (size_t)slot * rope, latent + rank, sizeof(float) * (size_t)rope);
+    }
+    /* attention over every cached position (:79-98) */
+    {
+        const int64_t length = *token_count;
+        memset(context, 0, sizeof(float) * (size_t)heads * (size_t)vh);
+        for (int32_t h = 0; h < heads; ++h) {
+            const float* qn = query + (size_t)h * qk;
+            const float* qr = qn + nope;
+            for (int64_t t = 0; t < length; ++t) {
+                const float a = orc_dot_f32(qn, key_nope + ((size_t)t * heads + h) * nope, (size_t)nope);
+                const float b = orc_dot_f32(qr, key_rope + (size_t)t * rope, (size_t)rope);
+                const float sum = a + b;
+                scores[t] = d->softmax_scale * sum;
+            }
+            orc_softmax(scores, (size_t)length);
+            for (int64_t t = 0; t < length; ++t) {
+                orc_axpy(scores[t], value + ((size_t)t * heads + h) * vh, context + (size_t)h * vh, (size_t)vh);
+            }
+        }
+    }
+    /* output projection (:100-101) */
+    orc_matvec_bf16(w->o_proj, context, out, (size_t)H, (size_t)heads * (size_t)vh);
+done:
+    free(query);
+    free(q_latent);
+    free(latent);
+    free(expanded);
+    free(context);
+    free(scores);
+    return rc;
 }

@@ -93,6 +93,40 @@ int orc_moe_layer(const orc_layer_dims* dims, const orc_router_cfg* rcfg, const 
 void orc_dense_ffn(const uint16_t* gate, const uint16_t* up, const uint16_t* down, int32_t hidden,
                    int32_t inter, const float* x, int64_t tokens, float* y, int32_t threads);
 
+/* ---- multi-head latent attention (src/Attention.cpp, src/Rope.cpp, src/KvCache.cpp) ---- */
+typedef struct orc_mla_dims {
+    int32_t hidden, heads, q_lora_rank, kv_lora_rank, qk_nope, qk_rope, v_head;
+    float softmax_scale, rms_norm_eps;
+    int32_t max_positions;  /* rows of the rotary tables */
+} orc_mla_dims;
+
+typedef struct orc_mla_weights {
+    const uint16_t* q_proj;        /* [heads * (qk_nope + qk_rope), hidden] when q_lora_rank == 0 */
+    const uint16_t* q_a_proj;      /* [q_lora_rank, hidden] */
+    const float* q_a_layernorm;    /* [q_lora_rank] */
+    const uint16_t* q_b_proj;      /* [heads * (qk_nope + qk_rope), q_lora_rank] */
+    const uint16_t* kv_a_proj;     /* [kv_lora_rank + qk_rope, hidden] */
+    const float* kv_a_layernorm;   /* [kv_lora_rank] */
+    const uint16_t* kv_b_proj;     /* [heads * (qk_nope + v_head), kv_lora_rank] */
+    const uint16_t* o_proj;        /* [hidden, heads * v_head] */
+} orc_mla_weights;
+
+/* Config::softmax_scale (src/Config.cpp:114-121). */
+float orc_softmax_scale(int32_t qk_nope, int32_t qk_rope, int32_t yarn, double factor, double mscale_all_dim);
+/* RotaryEmbedding::build (src/Rope.cpp:36-103): cos / sin [max_positions, dim / 2]. */
+void orc_rope_tables(int32_t dim, int32_t max_positions, double theta, int32_t yarn, double factor,
+                     double beta_fast, double beta_slow, double mscale, double mscale_all_dim,
+                     int64_t original_max_positions, float* cos_out, float* sin_out);
+/* RotaryEmbedding::apply (src/Rope.cpp:105-127) on one head's dim rope channels. */
+void orc_rope_apply(float* values, int32_t dim, const float* cos_row, const float* sin_row);
+/* Attention::forward (src/Attention.cpp:22-103) for one token at `position`,
+ * appending to the cache ([capacity, heads, qk_nope], [capacity, qk_rope],
+ * [capacity, heads, v_head], *token_count filled slots); out [hidden].
+ * Returns 0, or -1 when the cache is full (the reference's `false`). */
+int orc_mla_forward(const orc_mla_dims* d, const orc_mla_weights* w, const float* cos_table, const float* sin_table,
+                    float* key_nope, float* key_rope, float* value, int64_t capacity, int64_t* token_count,
+                    const float* x, int64_t position, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,13 +7,21 @@
 // here: this file only calls the reference's public functions so Python tests
 // (ctypes) can cross-check the oracle restatement and time LiteMind's CPU path.
 //
+// ref_mla_sequence() runs the reference's Attention::forward (src/Attention.cpp)
+// with its RotaryEmbedding and KvCache over a sequence of tokens;
+// ref_rope_tables() reads RotaryEmbedding's private tables back through its
+// public apply() on unit channel pairs, which returns (cos, sin) exactly.
+//
 // ref_moe_layer() composes the reference's kernels in the order of
 // DeepSeekRunner::Impl::feed_forward (src/DeepSeekRunner.cpp:228-240) and the
 // MoE block of DeepSeekRunner::Impl::forward (:264-290), because those two are
 // private members of a class that also needs a tokenizer, attention and a
 // checkpoint on disk.
+#include "Attention.hpp"
 #include "ExpertCache.hpp"
 #include "Gemm.hpp"
+#include "KvCache.hpp"
+#include "Rope.hpp"
 #include "MoeRouter.hpp"
 #include "Threading.hpp"
 
@@ -56,9 +64,139 @@ Config routing_config(std::int32_t experts, std::int32_t top_k, std::int32_t n_g
     return config;
 }
 
+Config mla_config(std::int32_t hidden, std::int32_t heads, std::int32_t q_lora_rank, std::int32_t kv_lora_rank,
+                  std::int32_t qk_nope, std::int32_t qk_rope, std::int32_t v_head, float eps, double theta,
+                  std::int32_t yarn, double factor, double beta_fast, double beta_slow, double mscale,
+                  double mscale_all_dim, std::int64_t original_max) {
+    Config c;
+    c.hidden_size = static_cast<std::size_t>(hidden);
+    c.num_attention_heads = static_cast<std::size_t>(heads);
+    c.q_lora_rank = static_cast<std::size_t>(q_lora_rank);
+    c.kv_lora_rank = static_cast<std::size_t>(kv_lora_rank);
+    c.qk_nope_head_dim = static_cast<std::size_t>(qk_nope);
+    c.qk_rope_head_dim = static_cast<std::size_t>(qk_rope);
+    c.v_head_dim = static_cast<std::size_t>(v_head);
+    c.rms_norm_eps = eps;
+    c.rope_theta = static_cast<float>(theta);
+    c.rope_scaling.enabled = yarn != 0;
+    c.rope_scaling.factor = factor;
+    c.rope_scaling.beta_fast = beta_fast;
+    c.rope_scaling.beta_slow = beta_slow;
+    c.rope_scaling.mscale = mscale;
+    c.rope_scaling.mscale_all_dim = mscale_all_dim;
+    c.rope_scaling.original_max_position_embeddings = static_cast<std::size_t>(original_max);
+    return c;
+}
+
+WeightView view_of(const std::uint16_t* p) {
+    WeightView v;
+    v.bytes = reinterpret_cast<const std::byte*>(p);
+    return v;
+}
+
 }  // namespace
 
 extern "C" {
+
+// Config::softmax_scale (src/Config.cpp:114-121) for the given rope scaling.
+float ref_softmax_scale(std::int32_t qk_nope, std::int32_t qk_rope, std::int32_t yarn, double factor,
+                        double mscale_all_dim) {
+    Config c;
+    c.qk_nope_head_dim = static_cast<std::size_t>(qk_nope);
+    c.qk_rope_head_dim = static_cast<std::size_t>(qk_rope);
+    c.rope_scaling.enabled = yarn != 0;
+    c.rope_scaling.factor = factor;
+    c.rope_scaling.mscale_all_dim = mscale_all_dim;
+    return c.softmax_scale();
+}
+
+// RotaryEmbedding::build's tables [positions, dim / 2], read back through apply().
+int ref_rope_tables(std::int32_t dim, std::int32_t positions, double theta, std::int32_t yarn, double factor,
+                    double beta_fast, double beta_slow, double mscale, double mscale_all_dim,
+                    std::int64_t original_max, float* cos_out, float* sin_out) {
+    Config c = mla_config(16, 1, 0, 16, 16, dim, 16, 1e-6F, theta, yarn, factor, beta_fast, beta_slow, mscale,
+                          mscale_all_dim, original_max);
+    RotaryEmbedding rope;
+    rope.build(c, static_cast<std::size_t>(positions));
+    const std::size_t half = static_cast<std::size_t>(dim) / 2U;
+    std::vector<float> v(static_cast<std::size_t>(dim));
+    for (std::size_t p = 0; p < static_cast<std::size_t>(positions); ++p) {
+        for (std::size_t i = 0; i < half; ++i) {
+            v[2 * i] = 1.0F;
+            v[2 * i + 1] = 0.0F;
+        }
+        rope.apply(v.data(), p);
+        for (std::size_t i = 0; i < half; ++i) {
+            cos_out[p * half + i] = v[i];
+            sin_out[p * half + i] = v[i + half];
+        }
+    }
+    return 0;
+}
+
+// RotaryEmbedding::apply on `values` (dim channels) at `position`.
+int ref_rope_apply(std::int32_t dim, std::int32_t positions, double theta, std::int32_t yarn, double factor,
+                   double beta_fast, double beta_slow, double mscale, double mscale_all_dim, std::int64_t original_max,
+                   float* values, std::int64_t position) {
+    Config c = mla_config(16, 1, 0, 16, 16, dim, 16, 1e-6F, theta, yarn, factor, beta_fast, beta_slow, mscale,
+                          mscale_all_dim, original_max);
+    RotaryEmbedding rope;
+    rope.build(c, static_cast<std::size_t>(positions));
+    rope.apply(values, static_cast<std::size_t>(position));
+    return 0;
+}
+
+// Attention::forward for tokens [0, T) at positions position0 + t, one cache of
+// `capacity` positions, then the cache contents.  Returns the number of tokens
+// processed before the cache was full.
+std::int64_t ref_mla_sequence(std::int32_t hidden, std::int32_t heads, std::int32_t q_lora_rank,
+                              std::int32_t kv_lora_rank, std::int32_t qk_nope, std::int32_t qk_rope,
+                              std::int32_t v_head, float eps, double theta, std::int32_t yarn, double factor,
+                              double beta_fast, double beta_slow, double mscale, double mscale_all_dim,
+                              std::int64_t original_max, std::int64_t capacity, const std::uint16_t* q_proj,
+                              const std::uint16_t* q_a_proj, const float* q_a_layernorm, const std::uint16_t* q_b_proj,
+                              const std::uint16_t* kv_a_proj, const float* kv_a_layernorm,
+                              const std::uint16_t* kv_b_proj, const std::uint16_t* o_proj, const float* x,
+                              std::int64_t tokens, std::int64_t position0, float* out, float* key_nope,
+                              float* key_rope, float* value) {
+    const Config c = mla_config(hidden, heads, q_lora_rank, kv_lora_rank, qk_nope, qk_rope, v_head, eps, theta, yarn,
+                                factor, beta_fast, beta_slow, mscale, mscale_all_dim, original_max);
+    RotaryEmbedding rope;
+    rope.build(c, static_cast<std::size_t>(capacity));
+    ThreadPool& pool = pool_for(0);
+    Attention attention;
+    attention.configure(c, pool, rope);
+    AttentionWeights w;
+    if (q_lora_rank == 0) {
+        w.q_proj = view_of(q_proj);
+    } else {
+        w.q_a_proj = view_of(q_a_proj);
+        w.q_a_layernorm.assign(q_a_layernorm, q_a_layernorm + q_lora_rank);
+        w.q_b_proj = view_of(q_b_proj);
+    }
+    w.kv_a_proj = view_of(kv_a_proj);
+    w.kv_a_layernorm.assign(kv_a_layernorm, kv_a_layernorm + kv_lora_rank);
+    w.kv_b_proj = view_of(kv_b_proj);
+    w.o_proj = view_of(o_proj);
+    KvCache cache;
+    cache.configure(static_cast<std::size_t>(heads), static_cast<std::size_t>(qk_nope),
+                    static_cast<std::size_t>(qk_rope), static_cast<std::size_t>(v_head),
+                    static_cast<std::size_t>(capacity));
+    std::int64_t done = 0;
+    for (std::int64_t t = 0; t < tokens; ++t) {
+        if (!attention.forward(x + t * hidden, w, cache, static_cast<std::size_t>(position0 + t), out + t * hidden)) {
+            break;
+        }
+        ++done;
+    }
+    const std::size_t n = cache.token_count();
+    for (std::size_t slot = 0; slot < n; ++slot) {
+        std::memcpy(key_nope + slot * heads * qk_nope, cache.key_nope(slot), sizeof(float) * heads * qk_nope);
+        std::memcpy(key_rope + slot * qk_rope, cache.key_rope(slot), sizeof(float) * qk_rope);
+        std::memcpy(value + slot * heads * v_head, cache.value(slot), sizeof(float) * heads * v_head);
+    }
+    return done;
+}
 
 int ref_kernel_description(char* buffer, std::size_t size) {
     const std::string text = gemm::kernel_description();

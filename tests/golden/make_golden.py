@@ -203,6 +203,62 @@ def expert_cache_trace():
         json.dump(out, f)
 
 
+MLA_SMALL = dict(hidden=256, heads=4, kv_lora_rank=64, qk_nope=32, qk_rope=16, v_head=32, original_max=16,
+                 factor=4.0, max_positions=16)
+MLA_CASES = {
+    # name: (dims overrides, seed, tokens, first position)
+    "small_yarn": (dict(MLA_SMALL), 11, 10, 0),
+    "small_qlora_plain": (dict(MLA_SMALL, q_lora_rank=96, yarn=False), 12, 10, 3),
+    "small_full": (dict(MLA_SMALL, max_positions=4), 13, 6, 0),
+    "v2lite": (dict(max_positions=8), 14, 8, 0),
+}
+
+
+def mla_dims(overrides):
+    import dataclasses
+    return dataclasses.replace(wl.V2_LITE_MLA, **overrides)
+
+
+def mla_layer_digest(L) -> str:
+    return sha(*[a for a in (L.q_proj, L.q_a_proj, L.q_a_layernorm, L.q_b_proj, L.kv_a_proj, L.kv_a_layernorm,
+                             L.kv_b_proj, L.o_proj) if a is not None])
+
+
+def mla():
+    """Attention::forward (src/Attention.cpp:22-103) through the compiled
+    reference over short token sequences with a fresh KvCache of capacity
+    max_positions (as DeepSeekRunner sizes both from the context length), and
+    the rotary tables of DeepSeek-V2-Lite read back through RotaryEmbedding::apply."""
+    out = {}
+    for name, (over, seed, T, pos0) in MLA_CASES.items():
+        d = mla_dims(over)
+        L = wl.mla_layer(seed, 0, d)
+        x = wl.tokens(seed + 1, T, d.hidden)
+        y, done, kn, kr, v = ol.ref_mla(L, x, pos0, d.max_positions)
+        out[name + "/dims"] = np.array(json.dumps(over))
+        out[name + "/meta"] = np.array([seed, T, pos0, done], np.int64)
+        out[name + "/weights_sha"] = np.array(mla_layer_digest(L))
+        out[name + "/out"] = y
+        if name == "v2lite":
+            out[name + "/x_sha"] = np.array(sha(x))
+            out[name + "/cache_sha"] = np.array(sha(kn[:done], kr[:done], v[:done]))
+        else:
+            out[name + "/x"] = x
+            out[name + "/key_nope"] = kn[:done]
+            out[name + "/key_rope"] = kr[:done]
+            out[name + "/value"] = v[:done]
+    d = wl.V2_LITE_MLA
+    cos, sin = ol.ref_rope_tables(d)
+    rows = np.array([0, 1, 2, 100, 1000, d.max_positions - 1], np.int64)
+    out["rope/rows"] = rows
+    out["rope/cos"] = cos[rows]
+    out["rope/sin"] = sin[rows]
+    out["rope/sha"] = np.array(sha(cos, sin))
+    out["rope/softmax_scale"] = np.float32(ol.ref().ref_softmax_scale(d.qk_nope, d.qk_rope, 1, d.factor,
+                                                                      d.mscale_all_dim))
+    np.savez_compressed(os.path.join(HERE, "mla.npz"), **out)
+
+
 def main():
     if not ol.have_ref():
         sys.exit("oracle/_ref/libref.so is not built (make -C oracle ref)")
@@ -213,6 +269,7 @@ def main():
     layer_tiny()
     layer_v2lite()
     expert_cache_trace()
+    mla()
     print("golden fixtures written to", HERE)
 
 

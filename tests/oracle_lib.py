@@ -31,6 +31,17 @@ class LayerWeights(C.Structure):
                 ("shared_gate", C.c_void_p), ("shared_up", C.c_void_p), ("shared_down", C.c_void_p)]
 
 
+class MlaDims(C.Structure):
+    _fields_ = [("hidden", C.c_int32), ("heads", C.c_int32), ("q_lora_rank", C.c_int32), ("kv_lora_rank", C.c_int32),
+                ("qk_nope", C.c_int32), ("qk_rope", C.c_int32), ("v_head", C.c_int32), ("softmax_scale", C.c_float),
+                ("rms_norm_eps", C.c_float), ("max_positions", C.c_int32)]
+
+
+class MlaWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("q_proj", "q_a_proj", "q_a_layernorm", "q_b_proj", "kv_a_proj",
+                                          "kv_a_layernorm", "kv_b_proj", "o_proj")]
+
+
 def p(a):
     if a is None:
         return None
@@ -68,6 +79,15 @@ def oracle() -> C.CDLL:
         lib.orc_permute.argtypes = [_P, _I64, _I32, _I32, _P, _P, _P, _P]
         lib.orc_moe_layer.argtypes = [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I32]
         lib.orc_dense_ffn.argtypes = [_P, _P, _P, _I32, _I32, _P, _I64, _P, _I32]
+        lib.orc_softmax_scale.argtypes = [_I32, _I32, _I32, C.c_double, C.c_double]
+        lib.orc_softmax_scale.restype = C.c_float
+        lib.orc_rope_tables.argtypes = [_I32, _I32, C.c_double, _I32, C.c_double, C.c_double, C.c_double,
+                                        C.c_double, C.c_double, _I64, _P, _P]
+        lib.orc_rope_apply.argtypes = [_P, _I32, _P, _P]
+        lib.orc_mla_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _I64, _P]
+        lib.orc_mla_forward.restype = C.c_int
+        for name in ("orc_rope_tables", "orc_rope_apply"):
+            getattr(lib, name).restype = None
         for name in ("orc_matvec_bf16", "orc_matvec_bf16_accumulate", "orc_matvec_f32", "orc_softmax",
                      "orc_silu_multiply", "orc_rms_norm", "orc_axpy", "orc_permute", "orc_dense_ffn"):
             getattr(lib, name).restype = None
@@ -110,6 +130,16 @@ def ref() -> C.CDLL:
         lib.ref_moe_layer.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32, _F, _I32, _I32, _I32, _P, _P, _P, _P,
                                       _P, _P, _P, _P, _I64, _P, _P, _P, _P, _SZ]
         lib.ref_hardware_threads.restype = _SZ
+        lib.ref_softmax_scale.argtypes = [_I32, _I32, _I32, C.c_double, C.c_double]
+        lib.ref_softmax_scale.restype = C.c_float
+        lib.ref_rope_tables.argtypes = [_I32, _I32, C.c_double, _I32, C.c_double, C.c_double, C.c_double,
+                                        C.c_double, C.c_double, _I64, _P, _P]
+        lib.ref_rope_apply.argtypes = [_I32, _I32, C.c_double, _I32, C.c_double, C.c_double, C.c_double, C.c_double,
+                                       C.c_double, _I64, _P, _I64]
+        lib.ref_mla_sequence.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32, _I32, C.c_float, C.c_double, _I32,
+                                         C.c_double, C.c_double, C.c_double, C.c_double, C.c_double, _I64, _I64,
+                                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P]
+        lib.ref_mla_sequence.restype = _I64
         lib.ref_kernel_description.argtypes = [_P, _SZ]
         _ref = lib
     return _ref
@@ -224,3 +254,92 @@ def oracle_stack(layers, h: np.ndarray, eps: float, every_layer: bool = False):
             o.orc_axpy(1.0, p(y[t]), p(h[t]), H)
         states.append(h.copy())
     return states if every_layer else h
+
+
+# ---- multi-head latent attention ----
+
+def _rope_args(d):
+    return (d.qk_rope, d.max_positions, float(d.rope_theta), 1 if d.yarn else 0, float(d.factor), float(d.beta_fast),
+            float(d.beta_slow), float(d.mscale), float(d.mscale_all_dim), int(d.original_max))
+
+
+def softmax_scale(d) -> float:
+    return float(oracle().orc_softmax_scale(d.qk_nope, d.qk_rope, 1 if d.yarn else 0, float(d.factor),
+                                            float(d.mscale_all_dim)))
+
+
+def oracle_rope_tables(d):
+    half = d.qk_rope // 2
+    cos = np.zeros((d.max_positions, half), np.float32)
+    sin = np.zeros((d.max_positions, half), np.float32)
+    oracle().orc_rope_tables(*_rope_args(d), p(cos), p(sin))
+    return cos, sin
+
+
+def ref_rope_tables(d):
+    half = d.qk_rope // 2
+    cos = np.zeros((d.max_positions, half), np.float32)
+    sin = np.zeros((d.max_positions, half), np.float32)
+    ref().ref_rope_tables(*_rope_args(d), p(cos), p(sin))
+    return cos, sin
+
+
+def _mla_structs(layer, scale=None):
+    d = layer.dims
+    dims = MlaDims(d.hidden, d.heads, d.q_lora_rank, d.kv_lora_rank, d.qk_nope, d.qk_rope, d.v_head,
+                   softmax_scale(d) if scale is None else scale, d.rms_norm_eps, d.max_positions)
+    keep = [a for a in (layer.q_proj, layer.q_a_proj, layer.q_a_layernorm, layer.q_b_proj, layer.kv_a_proj,
+                        layer.kv_a_layernorm, layer.kv_b_proj, layer.o_proj)]
+    w = MlaWeights(*[None if a is None else a.ctypes.data for a in keep])
+    return dims, w, keep
+
+
+class OracleKvCache:
+    """KvCache (include/KvCache.hpp) for the oracle: [capacity, heads, qk_nope],
+    [capacity, qk_rope], [capacity, heads, v_head] and the filled count."""
+
+    def __init__(self, d, capacity):
+        self.key_nope = np.zeros((capacity, d.heads, d.qk_nope), np.float32)
+        self.key_rope = np.zeros((capacity, d.qk_rope), np.float32)
+        self.value = np.zeros((capacity, d.heads, d.v_head), np.float32)
+        self.capacity = capacity
+        self.count = C.c_int64(0)
+
+
+def oracle_mla(layer, x: np.ndarray, position0: int, cache: OracleKvCache, tables=None):
+    """Attention::forward for every row of x [T, hidden] in turn (positions
+    position0 + t), appending to cache; returns out [T, hidden] and how many
+    tokens fit in the cache."""
+    d = layer.dims
+    dims, w, keep = _mla_structs(layer)
+    cos, sin = tables if tables is not None else oracle_rope_tables(d)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    done = 0
+    for t in range(x.shape[0]):
+        rc = oracle().orc_mla_forward(C.byref(dims), C.byref(w), p(cos), p(sin), p(cache.key_nope), p(cache.key_rope),
+                                      p(cache.value), cache.capacity, C.byref(cache.count), p(x[t]), position0 + t,
+                                      p(out[t]))
+        if rc != 0:
+            break
+        done += 1
+    return out, done
+
+
+def ref_mla(layer, x: np.ndarray, position0: int, capacity: int):
+    """LiteMind's Attention::forward (compiled) over the rows of x; returns
+    (out, tokens done, key_nope, key_rope, value) with a fresh cache."""
+    d = layer.dims
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    kn = np.zeros((capacity, d.heads, d.qk_nope), np.float32)
+    kr = np.zeros((capacity, d.qk_rope), np.float32)
+    v = np.zeros((capacity, d.heads, d.v_head), np.float32)
+    done = ref().ref_mla_sequence(d.hidden, d.heads, d.q_lora_rank, d.kv_lora_rank, d.qk_nope, d.qk_rope, d.v_head,
+                                  d.rms_norm_eps, float(d.rope_theta), 1 if d.yarn else 0, float(d.factor),
+                                  float(d.beta_fast), float(d.beta_slow), float(d.mscale), float(d.mscale_all_dim),
+                                  int(d.original_max), capacity, p(layer.q_proj), p(layer.q_a_proj),
+                                  p(layer.q_a_layernorm), p(layer.q_b_proj), p(layer.kv_a_proj),
+                                  p(layer.kv_a_layernorm), p(layer.kv_b_proj), p(layer.o_proj), p(x), x.shape[0],
+                                  position0, p(out), p(kn), p(kr), p(v))
+    return out, int(done), kn, kr, v
