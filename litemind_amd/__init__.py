@@ -23,8 +23,15 @@ OP_DOT, OP_AXPY, OP_SOFTMAX, OP_SILU_MUL, OP_RMS_NORM, OP_WIDEN = range(6)
 STAGES = ("router", "permute", "gate_up", "down", "combine")
 
 
+LM_EFULL = -6  # the KV cache had no free slot (include/litemind_attention.h)
+
+
 class LmError(RuntimeError):
-    """A litemind_amd C ABI call returned a non-zero status."""
+    """A litemind_amd C ABI call returned a non-zero status (``status``)."""
+
+    def __init__(self, message: str, status: int = 0):
+        super().__init__(message)
+        self.status = status
 
 
 class MoeConfig(C.Structure):
@@ -44,6 +51,31 @@ class MoeConfig(C.Structure):
         ("topk_group", C.c_int32),
         ("rms_norm_eps", C.c_float),
         ("num_layers", C.c_int32),
+    ]
+
+
+class MlaConfig(C.Structure):
+    """lm_mla_config: the attention subset of LiteMind's Config (include/Config.hpp) and
+    the context length sizing RotaryEmbedding::build and KvCache::configure."""
+
+    _fields_ = [
+        ("hidden_size", C.c_int32),
+        ("num_heads", C.c_int32),
+        ("q_lora_rank", C.c_int32),
+        ("kv_lora_rank", C.c_int32),
+        ("qk_nope_head_dim", C.c_int32),
+        ("qk_rope_head_dim", C.c_int32),
+        ("v_head_dim", C.c_int32),
+        ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_double),
+        ("yarn", C.c_int32),
+        ("factor", C.c_double),
+        ("beta_fast", C.c_double),
+        ("beta_slow", C.c_double),
+        ("mscale", C.c_double),
+        ("mscale_all_dim", C.c_double),
+        ("original_max_positions", C.c_int64),
+        ("context_length", C.c_int64),
     ]
 
 
@@ -105,6 +137,16 @@ PROTOTYPES = {
     "lm_upload_head": [_P, _P, _P, _I64],
     "lm_head_forward": [_P, _P, _I64, _P, _P],
     "lm_load_head": [_P, _P, _I64],
+    "lm_mla_softmax_scale": [_P, _P],
+    "lm_rope_tables": [_P, _I64, _P, _P],
+    "lm_attention_configure": [_P, _P],
+    "lm_upload_attention": [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P],
+    "lm_upload_input_norm": [_P, _I32, _P],
+    "lm_attention_forward": [_P, _I32, _P, _I64, _I64, _P, _I32],
+    "lm_kv_cache_clear": [_P],
+    "lm_kv_cache_tokens": [_P, _I32, _P],
+    "lm_kv_cache_read": [_P, _I32, _I64, _P, _P, _P],
+    "lm_decoder_forward": [_P, _I32, _I32, _P, _I64, _I64, _I32],
 }
 _RESTYPE = {"lm_last_error": C.c_char_p}
 
@@ -187,7 +229,25 @@ _DT_NUMPY = {DT_BF16: np.uint16, DT_F16: np.float16, DT_F32: np.float32, DT_F64:
 def _check_status(lib, status: int) -> None:
     if status != LM_OK:
         msg = lib.lm_last_error().decode(errors="replace")
-        raise LmError(f"litemind_amd status {status}: {msg}")
+        raise LmError(f"litemind_amd status {status}: {msg}", status)
+
+
+def rope_tables(config: MlaConfig, positions: int):
+    """RotaryEmbedding::build's cos / sin tables [positions, qk_rope / 2] (lm_rope_tables, host only)."""
+    lib = load_library()
+    half = config.qk_rope_head_dim // 2
+    cos = np.zeros((positions, half), np.float32)
+    sin = np.zeros((positions, half), np.float32)
+    _check_status(lib, lib.lm_rope_tables(C.byref(config), positions, _ptr(cos), _ptr(sin)))
+    return cos, sin
+
+
+def mla_softmax_scale(config: MlaConfig) -> float:
+    """Config::softmax_scale (lm_mla_softmax_scale, host only)."""
+    lib = load_library()
+    out = C.c_float()
+    _check_status(lib, lib.lm_mla_softmax_scale(C.byref(config), C.byref(out)))
+    return out.value
 
 
 class Checkpoint:
@@ -335,6 +395,46 @@ class Context:
     def moe_forward(self, layer, x, tokens, y, bias=None, idx=None, w=None, logits=None, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_moe_forward(self.handle, layer, _ptr(x), tokens, _ptr(y), _ptr(bias), _ptr(idx),
                                             _ptr(w), _ptr(logits), path))
+
+    # ---- multi-head latent attention (include/litemind_attention.h) ----
+    def attention_configure(self, config: MlaConfig) -> None:
+        self.mla_config = config
+        self._check(self.lib.lm_attention_configure(self.handle, C.byref(config)))
+
+    def upload_attention(self, layer: int, q_proj=None, q_a_proj=None, q_a_layernorm=None, q_b_proj=None,
+                         kv_a_proj=None, kv_a_layernorm=None, kv_b_proj=None, o_proj=None) -> None:
+        keep = [None if a is None else np.ascontiguousarray(a) for a in
+                (q_proj, q_a_proj, q_a_layernorm, q_b_proj, kv_a_proj, kv_a_layernorm, kv_b_proj, o_proj)]
+        self._check(self.lib.lm_upload_attention(self.handle, layer, *[_ptr(a) for a in keep]))
+
+    def upload_input_norm(self, layer: int, weight: np.ndarray) -> None:
+        weight = np.ascontiguousarray(weight, dtype=np.float32)
+        self._check(self.lib.lm_upload_input_norm(self.handle, layer, _ptr(weight)))
+
+    def attention_forward(self, layer, x, tokens, position0, out, accumulate=False) -> None:
+        self._check(self.lib.lm_attention_forward(self.handle, layer, _ptr(x), tokens, position0, _ptr(out),
+                                                  1 if accumulate else 0))
+
+    def kv_cache_clear(self) -> None:
+        self._check(self.lib.lm_kv_cache_clear(self.handle))
+
+    def kv_cache_tokens(self, layer: int) -> int:
+        out = C.c_int64()
+        self._check(self.lib.lm_kv_cache_tokens(self.handle, layer, C.byref(out)))
+        return out.value
+
+    def kv_cache_read(self, layer: int, tokens: int):
+        """The cache's first `tokens` entries in KvCache's layout: key_nope [T, heads, nope],
+        key_rope [T, rope], value [T, heads, v_head]."""
+        c = self.mla_config
+        kn = np.zeros((tokens, c.num_heads, c.qk_nope_head_dim), np.float32)
+        kr = np.zeros((tokens, c.qk_rope_head_dim), np.float32)
+        v = np.zeros((tokens, c.num_heads, c.v_head_dim), np.float32)
+        self._check(self.lib.lm_kv_cache_read(self.handle, layer, tokens, _ptr(kn), _ptr(kr), _ptr(v)))
+        return kn, kr, v
+
+    def decoder_forward(self, first, last, hidden, tokens, position0, path=PATH_AUTO) -> None:
+        self._check(self.lib.lm_decoder_forward(self.handle, first, last, _ptr(hidden), tokens, position0, path))
 
     def moe_forward_noalloc(self, layer, x, tokens, y, bias=None, idx=None, w=None, logits=None) -> None:
         """lm_moe_forward_noalloc: the single-token kernel per token, scratch in a fixed device array."""

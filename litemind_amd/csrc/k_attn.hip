@@ -1,0 +1,430 @@
+// k_attn.hip -- multi-head latent attention over a resident KV cache.
+//
+// Reference: Attention::forward (src/Attention.cpp:22-103), RotaryEmbedding::
+// apply (src/Rope.cpp:96-118), KvCache (include/KvCache.hpp, src/KvCache.cpp)
+// and gemm::{dot, softmax, axpy, rms_norm} (src/Gemm.cpp:183-231).  The
+// projections run through the LM head's bit-exact matvec (k_head.hip); this
+// file holds everything between them, for T tokens at once:
+//
+//   rope_query     each head's rotary channels of q, in place
+//   kv_prep        RMSNorm of the latent's first kv_lora_rank channels, the
+//                  rotary key tail rotated and stored in the cache
+//   kv_append      kv_b_proj's [key_nope | value] per head into the cache
+//   scores         scale * (dot(q_nope, k_nope) + dot(q_rope, k_rope)) for every
+//                  (token, head, cached key) the token may see
+//   softmax_rows   gemm::softmax per (token, head) row
+//   context        gemm::axpy over the cached values, in token order
+//
+// Cache layout in HBM, per layer, fp32 (capacity C tokens):
+//   key_nope  [heads][qk_nope][C]   keys of one (head, channel) contiguous, so
+//                                   the score lanes (one key each) read coalesced
+//   key_rope  [qk_rope][C]          the rotary key, shared by the heads
+//   value     [heads][C][v_head]    one token's values of a head contiguous, so
+//                                   the context lanes (one channel each) read
+//                                   coalesced while walking the tokens in order
+//
+// Every sum keeps LiteMind's order: the score dots add rounded products left to
+// right (a fused tail past the last multiple of four, as GCC's vector loop
+// leaves it), the softmax total is one left-to-right chain per row, and each
+// context channel is one fused chain over the cached tokens.  Those chains are
+// sequential by definition; the kernels parallelise across them (heads,
+// channels, tokens, keys), never within one.
+#include "lm_internal.h"
+
+#include <algorithm>
+
+namespace lm {
+namespace {
+
+constexpr int kKeyTile = 256;   // keys per score block (one per lane)
+constexpr int kQueries = 8;     // tokens per score / context block when T > 1
+constexpr int kChunk = 256;     // probabilities staged in LDS per context step
+
+// RotaryEmbedding::apply on one channel pair: the first output is
+// even*cos - odd*sin and the second odd*cos + even*sin, each contracted to one
+// fused multiply-add whose addend is the other product rounded (GCC's
+// contraction of the reference's expressions).
+__device__ inline void rotate_pair(float e, float o, float c, float s, float& lo, float& hi) {
+    const float os = o * s;
+    const float es = e * s;
+    lo = __builtin_fmaf(e, c, -os);
+    hi = __builtin_fmaf(o, c, es);
+}
+
+// q [T, heads, qk_nope + qk_rope]: each head's rotary channels at position
+// pos0 + t (src/Attention.cpp:45-48).  One wave per (token, head); the pair
+// values are read before any is written (the rotation permutes channels).
+__global__ __launch_bounds__(64) void rope_query_kernel(float* q, int32_t heads, int32_t nope, int32_t rope,
+                                                        const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, int64_t pos0,
+                                                        int64_t max_positions) {
+    const int64_t t = blockIdx.x / heads;
+    const int h = static_cast<int>(blockIdx.x - t * heads);
+    const int64_t pos = pos0 + t;
+    if (pos >= max_positions) {
+        return;  // RotaryEmbedding::apply leaves positions past its table alone
+    }
+    const int half = rope / 2;
+    float* v = q + (t * heads + h) * static_cast<int64_t>(nope + rope) + nope;
+    const float* c = cos_t + pos * half;
+    const float* s = sin_t + pos * half;
+    float lo[2], hi[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = threadIdx.x + 64 * k;
+        if (i < half) {
+            rotate_pair(v[2 * i], v[2 * i + 1], c[i], s[i], lo[k], hi[k]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = threadIdx.x + 64 * k;
+        if (i < half) {
+            v[i] = lo[k];
+            v[i + half] = hi[k];
+        }
+    }
+}
+
+// One token per block (src/Attention.cpp:54-56, :75): kvn[t] = rms_norm of the
+// latent's first `rank` channels (gemm::rms_norm: squares summed in double,
+// inverse = float(1 / sqrt(mean + eps)), x * inverse * weight), and the rotary
+// tail rotated at pos0 + t into the cache's key_rope column slot0 + t.
+__global__ __launch_bounds__(256) void kv_prep_kernel(const float* __restrict__ lat, const float* __restrict__ norm_w,
+                                                      float* __restrict__ kvn, float* __restrict__ key_rope,
+                                                      int32_t rank, int32_t rope, int64_t cap, int64_t slot0,
+                                                      const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                      int64_t pos0, int64_t max_positions, float eps) {
+    __shared__ double part[4];
+    const int64_t t = blockIdx.x;
+    const float* row = lat + t * static_cast<int64_t>(rank + rope);
+    double sq = 0.0;
+    for (int c = threadIdx.x; c < rank; c += 256) {
+        const double v = static_cast<double>(row[c]);
+        sq = sq + v * v;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        sq += __shfl_xor(sq, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = sq;
+    }
+    __syncthreads();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inverse =
+        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(rank) + static_cast<double>(eps)));
+    for (int c = threadIdx.x; c < rank; c += 256) {
+        const float scaled = row[c] * inverse;
+        kvn[t * rank + c] = scaled * norm_w[c];
+    }
+    const int half = rope / 2;
+    const int64_t pos = pos0 + t;
+    const int64_t slot = slot0 + t;
+    const float* tail = row + rank;
+    for (int i = threadIdx.x; i < half; i += 256) {
+        const float e = tail[2 * i];
+        const float o = tail[2 * i + 1];
+        if (pos < max_positions) {
+            float lo, hi;
+            rotate_pair(e, o, cos_t[pos * half + i], sin_t[pos * half + i], lo, hi);
+            key_rope[static_cast<int64_t>(i) * cap + slot] = lo;
+            key_rope[static_cast<int64_t>(i + half) * cap + slot] = hi;
+        } else {
+            key_rope[static_cast<int64_t>(2 * i) * cap + slot] = e;
+            key_rope[static_cast<int64_t>(2 * i + 1) * cap + slot] = o;
+        }
+    }
+}
+
+// kvx [T, heads, qk_nope + v_head] (kv_b_proj's output) into the cache at
+// slots slot0 .. slot0 + T - 1 (src/Attention.cpp:66-74).  One thread per
+// element, channel fastest.
+__global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict__ kvx, float* __restrict__ key_nope,
+                                                        float* __restrict__ value, int32_t heads, int32_t nope,
+                                                        int32_t vh, int64_t cap, int64_t slot0, int64_t total) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= total) {
+        return;
+    }
+    const int width = nope + vh;
+    const int64_t th = i / width;  // token * heads + head
+    const int j = static_cast<int>(i - th * width);
+    const int64_t t = th / heads;
+    const int h = static_cast<int>(th - t * heads);
+    const int64_t slot = slot0 + t;
+    const float v = kvx[i];
+    if (j < nope) {
+        key_nope[(static_cast<int64_t>(h) * nope + j) * cap + slot] = v;
+    } else {
+        value[(static_cast<int64_t>(h) * cap + slot) * vh + (j - nope)] = v;
+    }
+}
+
+// gemm::dot's association for one term of a chain: the first count - count % 4
+// products are rounded and added in order, the rest fused.
+__device__ inline float dot_step(float acc, float a, float b, bool fused) {
+    return fused ? __builtin_fmaf(a, b, acc) : acc + a * b;
+}
+
+// Scores S[(t * heads + h) * n_stride + key] for token t (cache slot n0 + t,
+// seeing keys 0 .. n0 + t) and head h (src/Attention.cpp:83-91): one key per
+// lane, KQ tokens per block sharing each key load; q rows staged in LDS.
+// grid: x = key tiles, y = heads, z = token blocks of KQ.
+template <int KQ>
+__global__ __launch_bounds__(kKeyTile) void scores_kernel(const float* __restrict__ q,
+                                                          const float* __restrict__ key_nope,
+                                                          const float* __restrict__ key_rope, float* __restrict__ S,
+                                                          int32_t heads, int32_t nope, int32_t rope, int64_t cap,
+                                                          int64_t n0, int64_t T, int64_t n_stride, float scale) {
+    extern __shared__ float qs[];  // [KQ][nope + rope]
+    const int qk = nope + rope;
+    const int h = blockIdx.y;
+    const int64_t i0 = static_cast<int64_t>(blockIdx.z) * KQ;
+    const int nq = static_cast<int>(std::min<int64_t>(KQ, T - i0));
+    const int64_t n_hi = n0 + i0 + nq;  // keys the block's last token sees
+    const int64_t key0 = static_cast<int64_t>(blockIdx.x) * kKeyTile;
+    if (key0 >= n_hi) {
+        return;  // uniform over the block
+    }
+    for (int j = threadIdx.x; j < KQ * qk; j += kKeyTile) {
+        const int iq = j / qk;
+        const int d = j - iq * qk;
+        qs[j] = iq < nq ? q[((i0 + iq) * heads + h) * qk + d] : 0.0f;
+    }
+    __syncthreads();
+    const int64_t key = key0 + threadIdx.x;
+    const int64_t kc = key < n_hi ? key : n_hi - 1;  // lanes past the last key read a valid one
+    const float* kn = key_nope + static_cast<int64_t>(h) * nope * cap + kc;
+    const float* kr = key_rope + kc;
+    float a[KQ], b[KQ];
+#pragma unroll
+    for (int iq = 0; iq < KQ; ++iq) {
+        a[iq] = 0.0f;
+        b[iq] = 0.0f;
+    }
+    const int nope_body = nope - nope % 4;
+    for (int d = 0; d < nope; ++d) {
+        const float k = kn[static_cast<int64_t>(d) * cap];
+        const bool fused = d >= nope_body;
+#pragma unroll
+        for (int iq = 0; iq < KQ; ++iq) {
+            a[iq] = dot_step(a[iq], qs[iq * qk + d], k, fused);
+        }
+    }
+    const int rope_body = rope - rope % 4;
+    for (int d = 0; d < rope; ++d) {
+        const float k = kr[static_cast<int64_t>(d) * cap];
+        const bool fused = d >= rope_body;
+#pragma unroll
+        for (int iq = 0; iq < KQ; ++iq) {
+            b[iq] = dot_step(b[iq], qs[iq * qk + nope + d], k, fused);
+        }
+    }
+#pragma unroll
+    for (int iq = 0; iq < KQ; ++iq) {
+        if (iq < nq && key <= n0 + i0 + iq) {
+            S[((i0 + iq) * heads + h) * n_stride + key] = scale * (a[iq] + b[iq]);
+        }
+    }
+}
+
+// gemm::softmax (src/Gemm.cpp:209-223) on each row (token t, head h) of S,
+// n0 + t + 1 entries: the maximum, expf(s - max) in place with the total
+// accumulated left to right in one chain (each chunk of 64 is added in lane
+// order from the lanes' registers), then one reciprocal and a product.  One
+// wave per row, four rows per block.
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t rows, int32_t heads, int64_t n0,
+                                                           int64_t n_stride) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) {
+        return;
+    }
+    const int64_t n = n0 + row / heads + 1;
+    float* s = S + row * n_stride;
+    float m = -__builtin_inff();
+    for (int64_t c = lane; c < n; c += 64) {
+        m = fmaxf(m, s[c]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o));
+    }
+    float total = 0.0f;
+    int64_t c0 = 0;
+    for (; c0 + 64 <= n; c0 += 64) {
+        const float e = expf_ref(s[c0 + lane] - m);
+        s[c0 + lane] = e;
+        const int eb = static_cast<int>(float_bits(e));
+#pragma unroll
+        for (int k = 0; k < 64; ++k) {
+            total = total + bits_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(eb, k)));
+        }
+    }
+    if (c0 < n) {
+        const int cnt = static_cast<int>(n - c0);
+        float e = 0.0f;
+        if (lane < cnt) {
+            e = expf_ref(s[c0 + lane] - m);
+            s[c0 + lane] = e;
+        }
+        const int eb = static_cast<int>(float_bits(e));
+        for (int k = 0; k < cnt; ++k) {
+            total = total + bits_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(eb, k)));
+        }
+    }
+    const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
+    for (int64_t c = lane; c < n; c += 64) {
+        s[c] = s[c] * inverse;
+    }
+}
+
+// ctx[t, h, v] = sum over cached tokens j <= n0 + t, in order, of
+// fma(P[t, h, j], value[h, j, v], .) from 0 (gemm::axpy per token,
+// src/Attention.cpp:94-97).  One lane per value channel, KQ tokens per block
+// sharing each value load; probabilities staged in LDS in chunks.
+// grid: x = heads, y = token blocks of KQ; block = v_head rounded up to 64.
+template <int KQ>
+__global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ P, const float* __restrict__ value,
+                                                      float* __restrict__ ctx, int32_t heads, int32_t vh, int64_t cap,
+                                                      int64_t n0, int64_t T, int64_t n_stride) {
+    __shared__ float ps[KQ][kChunk];
+    const int h = blockIdx.x;
+    const int64_t i0 = static_cast<int64_t>(blockIdx.y) * KQ;
+    const int nq = static_cast<int>(std::min<int64_t>(KQ, T - i0));
+    const int64_t n_hi = n0 + i0 + nq;
+    const int v = threadIdx.x;
+    const bool live = v < vh;
+    const float* vp = value + static_cast<int64_t>(h) * cap * vh + (live ? v : 0);
+    float acc[KQ];
+#pragma unroll
+    for (int iq = 0; iq < KQ; ++iq) {
+        acc[iq] = 0.0f;
+    }
+    for (int64_t c0 = 0; c0 < n_hi; c0 += kChunk) {
+        __syncthreads();
+        for (int j = threadIdx.x; j < KQ * kChunk; j += blockDim.x) {
+            const int iq = j / kChunk;
+            const int64_t key = c0 + (j - iq * kChunk);
+            ps[iq][j - iq * kChunk] =
+                iq < nq && key <= n0 + i0 + iq ? P[((i0 + iq) * heads + h) * n_stride + key] : 0.0f;
+        }
+        __syncthreads();
+        const int cend = static_cast<int>(std::min<int64_t>(kChunk, n_hi - c0));
+        int j = 0;
+        for (; j + 8 <= cend; j += 8) {
+            float val[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                val[u] = vp[(c0 + j + u) * vh];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t rel = c0 + j + u - n0 - i0;  // token iq sees this key when rel <= iq
+#pragma unroll
+                for (int iq = 0; iq < KQ; ++iq) {
+                    if (rel <= iq) {
+                        acc[iq] = __builtin_fmaf(ps[iq][j + u], val[u], acc[iq]);
+                    }
+                }
+            }
+        }
+        for (; j < cend; ++j) {
+            const float val = vp[(c0 + j) * vh];
+            const int64_t rel = c0 + j - n0 - i0;
+#pragma unroll
+            for (int iq = 0; iq < KQ; ++iq) {
+                if (rel <= iq) {
+                    acc[iq] = __builtin_fmaf(ps[iq][j], val, acc[iq]);
+                }
+            }
+        }
+    }
+    if (live) {
+#pragma unroll
+        for (int iq = 0; iq < KQ; ++iq) {
+            if (iq < nq) {
+                ctx[((i0 + iq) * heads + h) * vh + v] = acc[iq];
+            }
+        }
+    }
+}
+
+unsigned blocks_of(int64_t n, int64_t per) { return static_cast<unsigned>((n + per - 1) / per); }
+
+}  // namespace
+
+bool attention_shape_supported(const AttnShape& a) {
+    return a.heads > 0 && a.nope >= 0 && a.rope >= 0 && a.rope % 2 == 0 && a.rope <= 256 && a.vh > 0 &&
+           a.vh <= 256 && a.rank > 0 && a.cap > 0;
+}
+
+hipError_t launch_rope_query(const AttnShape& a, float* q, int64_t T, int64_t pos0, hipStream_t s) {
+    if (T <= 0 || a.rope == 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(rope_query_kernel, dim3(static_cast<unsigned>(T * a.heads)), dim3(64), 0, s, q, a.heads, a.nope,
+                       a.rope, a.cos_t, a.sin_t, pos0, a.max_positions);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_prep(const AttnShape& a, const KvCacheDev& c, const float* lat, const float* norm_w, float* kvn,
+                          int64_t T, int64_t slot0, int64_t pos0, float eps, hipStream_t s) {
+    if (T <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(kv_prep_kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, s, lat, norm_w, kvn, c.key_rope,
+                       a.rank, a.rope, a.cap, slot0, a.cos_t, a.sin_t, pos0, a.max_positions, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float* kvx, int64_t T, int64_t slot0,
+                            hipStream_t s) {
+    const int64_t total = T * a.heads * static_cast<int64_t>(a.nope + a.vh);
+    if (total <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_of(total, 256)), dim3(256), 0, s, kvx, c.key_nope, c.value,
+                       a.heads, a.nope, a.vh, a.cap, slot0, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const float* q, float* S, float* ctx,
+                                 int64_t T, int64_t n0, float scale, hipStream_t s) {
+    if (T <= 0) {
+        return hipSuccess;
+    }
+    const int64_t n_stride = n0 + T;
+    const int qk = a.nope + a.rope;
+    const unsigned tiles = blocks_of(n_stride, kKeyTile);
+    if (T == 1) {
+        hipLaunchKernelGGL(scores_kernel<1>, dim3(tiles, a.heads, 1), dim3(kKeyTile), sizeof(float) * qk, s, q,
+                           c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope, a.cap, n0, T, n_stride, scale);
+    } else {
+        hipLaunchKernelGGL(scores_kernel<kQueries>, dim3(tiles, a.heads, blocks_of(T, kQueries)), dim3(kKeyTile),
+                           sizeof(float) * kQueries * qk, s, q, c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope,
+                           a.cap, n0, T, n_stride, scale);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    const int64_t rows = T * a.heads;
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, S, rows, a.heads, n0, n_stride);
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    const unsigned threads = static_cast<unsigned>((a.vh + 63) / 64 * 64);
+    if (T == 1) {
+        hipLaunchKernelGGL(context_kernel<1>, dim3(a.heads, 1), dim3(threads), 0, s, S, c.value, ctx, a.heads, a.vh,
+                           a.cap, n0, T, n_stride);
+    } else {
+        hipLaunchKernelGGL(context_kernel<kQueries>, dim3(a.heads, blocks_of(T, kQueries)), dim3(threads), 0, s, S,
+                           c.value, ctx, a.heads, a.vh, a.cap, n0, T, n_stride);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lm

@@ -15,13 +15,18 @@
 // streams 420 MB at V = 102400, H = 2048: the kernel is bound by HBM.
 #include "lm_internal.h"
 
+#include <algorithm>
+
 namespace lm {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                            // the head: 4 waves per block
 constexpr int kRowsPerWave = 16;                         // 4 lanes per row
 constexpr int kRows = kRowsPerWave * (kThreads / 64);    // head rows per block
 constexpr int kUnroll = 8;                               // 16-byte loads in flight per lane
+// Projections with few rows (attention: 576 to 4096) take one wave per block,
+// so that a launch still spreads over the CUs.
+constexpr int kSmallThreads = 64;
 
 // Combines two candidates of the greedy choice: the larger value, the lower
 // index between equal values (IEEE equality: -0 equals +0), NaN never chosen.
@@ -51,22 +56,24 @@ __device__ inline HeadBest wave_better(HeadBest b) {
 // (tokens x in_dim floats, dynamic LDS) are staged once per block.  Lane 0 of a
 // row also owns chains 0..7's continuation over the 8-wide remainder.  Then
 // each block's best row per token goes to `partial` (when given).
-__global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* __restrict__ w,
-                                                               const float* __restrict__ x, float* logits,
-                                                               HeadBest* partial, int64_t rows, int32_t in_dim,
-                                                               int32_t tokens, float scale, int32_t accumulate) {
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void head_logits_kernel(const uint16_t* __restrict__ w,
+                                                              const float* __restrict__ x, float* logits,
+                                                              HeadBest* partial, int64_t rows, int32_t in_dim,
+                                                              int32_t tokens, float scale, int32_t accumulate) {
+    constexpr int ROWS = kRowsPerWave * (THREADS / 64);
     extern __shared__ float4 xs4[];  // [tokens][in_dim / 4]
-    __shared__ HeadBest wave_best[kThreads / 64];
+    __shared__ HeadBest wave_best[THREADS / 64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int q = lane & 3;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + (tid >> 2);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS + (tid >> 2);
     const bool live = row < rows;
     const int n32 = in_dim / 32 * 32;
     const int n8 = n32 + (in_dim - n32) / 8 * 8;  // == in_dim: the launch requires in_dim % 8 == 0
     const int q4 = in_dim / 4;
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    for (int i = tid; i < tokens * q4; i += kThreads) {
+    for (int i = tid; i < tokens * q4; i += THREADS) {
         xs4[i] = x4[i];
     }
     __syncthreads();
@@ -161,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void head_logits_kernel(const uint16_t* _
         __syncthreads();
         if (tid == 0) {
             HeadBest r = wave_best[0];
-            for (int k = 1; k < kThreads / 64; ++k) {
+            for (int k = 1; k < THREADS / 64; ++k) {
                 r = better(r, wave_best[k]);
             }
             partial[static_cast<int64_t>(t) * gridDim.x + blockIdx.x] = r;
@@ -216,8 +223,8 @@ hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBes
     if (lds > 64 * 1024) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, s, w, x, logits,
-                       partial, rows, in_dim, tokens, 1.0f, 0);
+    hipLaunchKernelGGL(head_logits_kernel<kThreads>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, s, w,
+                       x, logits, partial, rows, in_dim, tokens, 1.0f, 0);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || token == nullptr) {
         return err;
@@ -236,10 +243,36 @@ hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int
     if (!matvec_rows_supported(rows, in_dim)) {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(head_blocks(rows))), dim3(kThreads),
+    hipLaunchKernelGGL(head_logits_kernel<kThreads>, dim3(static_cast<unsigned>(head_blocks(rows))), dim3(kThreads),
                        sizeof(float) * static_cast<size_t>(in_dim), s, w, x, out, nullptr, rows,
                        static_cast<int32_t>(in_dim), 1, scale, accumulate);
     return hipGetLastError();
+}
+
+hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim,
+                                int64_t tokens, float scale, int32_t accumulate, hipStream_t s) {
+    if (tokens <= 0) {
+        return hipSuccess;
+    }
+    if (!matvec_rows_supported(rows, in_dim)) {
+        return hipErrorInvalidValue;
+    }
+    // tokens per launch: at most kHeadTokens, and their rows must fit 64 KiB of LDS
+    const int64_t per = std::min<int64_t>(kHeadTokens, std::max<int64_t>(1, 16384 / in_dim));
+    const int64_t rows_per_block = kRowsPerWave * (kSmallThreads / 64);
+    const unsigned blocks = static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block);
+    for (int64_t t0 = 0; t0 < tokens; t0 += per) {
+        const int32_t n = static_cast<int32_t>(std::min<int64_t>(per, tokens - t0));
+        hipLaunchKernelGGL(head_logits_kernel<kSmallThreads>, dim3(blocks), dim3(kSmallThreads),
+                           sizeof(float) * static_cast<size_t>(n) * static_cast<size_t>(in_dim), s, w,
+                           x + t0 * in_dim, out + t0 * rows, nullptr, rows, static_cast<int32_t>(in_dim), n, scale,
+                           accumulate);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) {
+            return err;
+        }
+    }
+    return hipSuccess;
 }
 
 }  // namespace lm

@@ -1,0 +1,721 @@
+// lm_attn.hip -- the C ABI of include/litemind_attention.h: multi-head latent
+// attention with its rotary tables and KV caches resident in HBM.
+//
+// Per layer and call (T tokens, cache slots n0 .. n0 + T - 1), on the context
+// stream:
+//   q      = q_proj x                 or  q_b_proj rms_norm(q_a_proj x)    (matvec, k_head.hip)
+//   q      = rope(q) per head                                             (k_attn.hip)
+//   lat    = kv_a_proj x                                                  (matvec)
+//   kvn    = rms_norm(lat[:rank]);  cache.key_rope <- rope(lat[rank:])    (k_attn.hip)
+//   kvx    = kv_b_proj kvn;         cache.key_nope, cache.value <- kvx    (matvec, k_attn.hip)
+//   ctx    = softmax(scale * q . keys) . values, causal                   (k_attn.hip)
+//   out    = o_proj ctx   (or out += o_proj ctx)                          (matvec)
+// which is Attention::forward (src/Attention.cpp:22-103) for each token in turn.
+#include "litemind_attention.h"
+#include "lm_error.h"
+#include "lm_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <new>
+#include <string>
+#include <vector>
+
+#define LM_ATT_HIP(call)                                                                                     \
+    do {                                                                                                     \
+        const hipError_t lm_status_ = (call);                                                                \
+        if (lm_status_ != hipSuccess) {                                                                      \
+            return lm::set_error(LM_EHIP, std::string(#call) + ": " + hipGetErrorString(lm_status_));        \
+        }                                                                                                    \
+    } while (0)
+
+namespace lm {
+
+struct AttnLayer {
+    void* slab = nullptr;  // the layer's projections (BF16) and norm weights (fp32)
+    const uint16_t* q_proj = nullptr;
+    const uint16_t* q_a = nullptr;
+    const float* q_a_norm = nullptr;
+    const uint16_t* q_b = nullptr;
+    const uint16_t* kv_a = nullptr;
+    const float* kv_a_norm = nullptr;
+    const uint16_t* kv_b = nullptr;
+    const uint16_t* o = nullptr;
+    float* input_norm = nullptr;  // [H], lm_decoder_forward
+    KvCacheDev cache;
+    int64_t count = 0;  // KvCache::token_count
+};
+
+struct AttnState {
+    lm_mla_config cfg{};
+    AttnShape shape;
+    float scale = 0.0f;
+    float* tables = nullptr;  // cos [max_positions, rope / 2] then sin
+    float* caches = nullptr;  // every layer's cache
+    std::vector<AttnLayer> layers;
+    float* ws = nullptr;      // per-call scratch (floats)
+    size_t ws_floats = 0;
+    float* xn = nullptr;      // lm_decoder_forward: normalised rows [T, H]
+    size_t xn_floats = 0;
+};
+
+void attention_release(AttnState* st) {
+    if (st == nullptr) {
+        return;
+    }
+    for (AttnLayer& L : st->layers) {
+        (void)hipFree(L.slab);
+        (void)hipFree(L.input_norm);
+    }
+    (void)hipFree(st->tables);
+    (void)hipFree(st->caches);
+    (void)hipFree(st->ws);
+    (void)hipFree(st->xn);
+    delete st;
+}
+
+}  // namespace lm
+
+namespace {
+
+using lm::AttnLayer;
+using lm::AttnState;
+
+// Query tokens per launch of the attention core: bounds the score scratch to
+// kCoreTokens * heads * (n0 + T) floats.
+constexpr int64_t kCoreTokens = 512;
+
+int fail(int code, const std::string& message) { return lm::set_error(code, message); }
+
+// yarn_get_mscale (src/Rope.cpp:13-18, src/Config.cpp:12-17):
+// 0.1 * mscale * log(scale) + 1, which LiteMind's GCC build fuses into one
+// multiply-add of the rounded 0.1 * mscale.
+double yarn_mscale(double scale, double mscale) {
+    if (scale <= 1.0) {
+        return 1.0;
+    }
+    return std::fma(0.1 * mscale, std::log(scale), 1.0);
+}
+
+float softmax_scale(const lm_mla_config& c) {
+    // Config::softmax_scale (src/Config.cpp:114-121)
+    double scale = 1.0 / std::sqrt(static_cast<double>(c.qk_nope_head_dim + c.qk_rope_head_dim));
+    if (c.yarn != 0 && c.mscale_all_dim != 0.0) {
+        const double m = yarn_mscale(c.factor, c.mscale_all_dim);
+        scale *= m * m;
+    }
+    return static_cast<float>(scale);
+}
+
+// RotaryEmbedding::build (src/Rope.cpp:35-94) into cos / sin [positions, dim / 2]:
+// inverse frequencies in double (YaRN: the interpolated and extrapolated
+// frequency blended over the correction band, src/Rope.cpp:20-31, 50-81), then
+// float(cos(p * f) * magnitude) and float(sin(p * f) * magnitude).
+void rope_tables(const lm_mla_config& c, int64_t positions, float* cos_out, float* sin_out) {
+    const int32_t dim = c.qk_rope_head_dim;
+    const int32_t half = dim / 2;
+    const double base = static_cast<double>(static_cast<float>(c.rope_theta));  // Config::rope_theta is a float
+    std::vector<double> inv(static_cast<size_t>(half));
+    double magnitude = 1.0;
+    if (c.yarn == 0) {
+        for (int32_t i = 0; i < half; ++i) {
+            inv[i] = 1.0 / std::pow(base, 2.0 * static_cast<double>(i) / static_cast<double>(dim));
+        }
+    } else {
+        const double factor = c.factor <= 0.0 ? 1.0 : c.factor;
+        const double pi = 3.14159265358979323846;
+        auto correction = [&](double rotations) {
+            const double num = static_cast<double>(dim) *
+                               std::log(static_cast<double>(c.original_max_positions) / (rotations * 2.0 * pi));
+            return num / (2.0 * std::log(base));
+        };
+        double low = std::max(std::floor(correction(c.beta_fast)), 0.0);
+        double high = std::min(std::ceil(correction(c.beta_slow)), static_cast<double>(dim) - 1.0);
+        if (high - low < 1e-6) {
+            high = low + 0.001;
+        }
+        for (int32_t i = 0; i < half; ++i) {
+            const double extrapolated = 1.0 / std::pow(base, 2.0 * static_cast<double>(i) / static_cast<double>(dim));
+            const double interpolated = extrapolated / factor;
+            const double ramp = std::clamp((static_cast<double>(i) - low) / (high - low), 0.0, 1.0);
+            const double keep = 1.0 - ramp;
+            const double from_interpolated = interpolated * (1.0 - keep);
+            const double from_extrapolated = extrapolated * keep;
+            inv[i] = from_interpolated + from_extrapolated;
+        }
+        magnitude = yarn_mscale(factor, c.mscale) / yarn_mscale(factor, c.mscale_all_dim);
+    }
+    for (int64_t p = 0; p < positions; ++p) {
+        for (int32_t i = 0; i < half; ++i) {
+            const double angle = static_cast<double>(p) * inv[i];
+            cos_out[p * half + i] = static_cast<float>(std::cos(angle) * magnitude);
+            sin_out[p * half + i] = static_cast<float>(std::sin(angle) * magnitude);
+        }
+    }
+}
+
+int check_config(const lm_mla_config* c) {
+    if (c == nullptr) {
+        return fail(LM_EINVAL, "null attention config");
+    }
+    if (c->hidden_size <= 0 || c->num_heads <= 0 || c->q_lora_rank < 0 || c->kv_lora_rank <= 0 ||
+        c->qk_nope_head_dim < 0 || c->qk_rope_head_dim < 0 || c->v_head_dim <= 0 || c->context_length <= 0) {
+        return fail(LM_EINVAL, "attention config: sizes must be positive");
+    }
+    if (c->qk_rope_head_dim % 2 != 0 || c->qk_rope_head_dim > 256 || c->v_head_dim > 256) {
+        return fail(LM_EINVAL, "attention config: qk_rope_head_dim must be even and <= 256, v_head_dim <= 256");
+    }
+    const int64_t widths[] = {c->hidden_size, c->q_lora_rank, c->kv_lora_rank,
+                              static_cast<int64_t>(c->num_heads) * c->v_head_dim};
+    for (int64_t w : widths) {
+        if (w % 8 != 0 || w > 16384) {
+            return fail(LM_EINVAL, "attention config: hidden_size, q_lora_rank, kv_lora_rank and heads * v_head_dim "
+                                   "must be multiples of 8 and at most 16384");
+        }
+    }
+    return LM_OK;
+}
+
+int get_state(lm_context* ctx, AttnState** out) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    AttnState* st = lm::context_attention(ctx);
+    if (st == nullptr) {
+        return fail(LM_EINVAL, "attention is not configured (lm_attention_configure)");
+    }
+    *out = st;
+    return LM_OK;
+}
+
+int check_attn_layer(AttnState* st, int32_t layer) {
+    if (layer < 0 || layer >= static_cast<int32_t>(st->layers.size())) {
+        return fail(LM_EINVAL, "layer " + std::to_string(layer) + " out of range");
+    }
+    return LM_OK;
+}
+
+// Grows a scratch buffer (after the stream drains, since queued work may use it).
+int ensure_buffer(float** buf, size_t* have, hipStream_t stream, size_t floats) {
+    if (*have >= floats) {
+        return LM_OK;
+    }
+    LM_ATT_HIP(hipStreamSynchronize(stream));
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+    const hipError_t err = hipMalloc(reinterpret_cast<void**>(buf), floats * sizeof(float));
+    if (err != hipSuccess) {
+        *buf = nullptr;
+        return fail(LM_ENOMEM, "attention scratch of " + std::to_string(floats) + " floats: " + hipGetErrorString(err));
+    }
+    *have = floats;
+    return LM_OK;
+}
+
+// Attention::forward for F tokens that all fit the cache; out = o_proj ctx or
+// out += o_proj ctx.  x [F, H] must not overlap out.
+int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const float* x, int64_t F, int64_t pos0,
+                     float* out, int32_t accumulate) {
+    const lm_mla_config& c = st->cfg;
+    AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+    if (L.kv_a == nullptr) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no attention weights (lm_upload_attention)");
+    }
+    const lm::AttnShape& a = st->shape;
+    const int64_t H = c.hidden_size, heads = c.num_heads, qk = c.qk_nope_head_dim + c.qk_rope_head_dim;
+    const int64_t rank = c.kv_lora_rank, rope = c.qk_rope_head_dim, vh = c.v_head_dim, ql = c.q_lora_rank;
+    const int64_t n0 = L.count;
+    const int64_t n_total = n0 + F;
+    const int64_t core = std::min(F, kCoreTokens);
+    // scratch: q | q latent | kv latent | kv normalised | kv expanded | scores | context
+    const size_t q_f = static_cast<size_t>(F * heads * qk);
+    const size_t ql_f = static_cast<size_t>(F * ql);
+    const size_t lat_f = static_cast<size_t>(F * (rank + rope));
+    const size_t kvn_f = static_cast<size_t>(F * rank);
+    const size_t kvx_f = static_cast<size_t>(F * heads * (c.qk_nope_head_dim + vh));
+    const size_t s_f = static_cast<size_t>(core * heads * n_total);
+    const size_t ctx_f = static_cast<size_t>(F * heads * vh);
+    int rc = ensure_buffer(&st->ws, &st->ws_floats, stream, q_f + ql_f + lat_f + kvn_f + kvx_f + s_f + ctx_f);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    float* q = st->ws;
+    float* qlat = q + q_f;
+    float* lat = qlat + ql_f;
+    float* kvn = lat + lat_f;
+    float* kvx = kvn + kvn_f;
+    float* S = kvx + kvx_f;
+    float* ctxv = S + s_f;
+
+    // queries (src/Attention.cpp:33-48)
+    if (ql == 0) {
+        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_proj, x, q, heads * qk, H, F, 1.0f, 0, stream));
+    } else {
+        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_a, x, qlat, ql, H, F, 1.0f, 0, stream));
+        LM_ATT_HIP(lm::launch_rms_norm(qlat, L.q_a_norm, qlat, F, static_cast<int32_t>(ql), c.rms_norm_eps, stream));
+        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_b, qlat, q, heads * qk, ql, F, 1.0f, 0, stream));
+    }
+    LM_ATT_HIP(lm::launch_rope_query(a, q, F, pos0, stream));
+    // compressed keys and values, appended at slots n0 .. n0 + F - 1 (:50-75)
+    LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_a, x, lat, rank + rope, H, F, 1.0f, 0, stream));
+    LM_ATT_HIP(lm::launch_kv_prep(a, L.cache, lat, L.kv_a_norm, kvn, F, n0, pos0, c.rms_norm_eps, stream));
+    LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_b, kvn, kvx, heads * (c.qk_nope_head_dim + vh), rank, F, 1.0f, 0,
+                                        stream));
+    LM_ATT_HIP(lm::launch_kv_append(a, L.cache, kvx, F, n0, stream));
+    // causal attention over the cache (:77-98), in groups of query tokens
+    for (int64_t t0 = 0; t0 < F; t0 += core) {
+        const int64_t n = std::min(core, F - t0);
+        LM_ATT_HIP(lm::launch_attention_core(a, L.cache, q + t0 * heads * qk, S, ctxv + t0 * heads * vh, n, n0 + t0,
+                                             st->scale, stream));
+    }
+    // output projection (:100-101)
+    LM_ATT_HIP(lm::launch_matvec_tokens(L.o, ctxv, out, H, heads * vh, F, 1.0f, accumulate, stream));
+    L.count = n_total;
+    return LM_OK;
+}
+
+int upload(hipStream_t stream, void* dst, const void* src, size_t bytes) {
+    LM_ATT_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
+    return LM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lm_mla_softmax_scale(const lm_mla_config* config, float* out) {
+    int rc = check_config(config);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (out == nullptr) {
+        return fail(LM_EINVAL, "null output");
+    }
+    *out = softmax_scale(*config);
+    return LM_OK;
+}
+
+int lm_rope_tables(const lm_mla_config* config, int64_t positions, float* cos_host, float* sin_host) {
+    try {
+        int rc = check_config(config);
+        if (rc != LM_OK) {
+            return rc;
+        }
+        if (positions < 0 || (positions > 0 && (cos_host == nullptr || sin_host == nullptr))) {
+            return fail(LM_EINVAL, "bad position count or null table");
+        }
+        rope_tables(*config, positions, cos_host, sin_host);
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
+int lm_attention_configure(lm_context* ctx, const lm_mla_config* config) {
+    try {
+        if (ctx == nullptr) {
+            return fail(LM_EINVAL, "null context");
+        }
+        int rc = check_config(config);
+        if (rc != LM_OK) {
+            return rc;
+        }
+        const lm::ContextInfo info = lm::context_info(ctx);
+        if (config->hidden_size != info.hidden) {
+            return fail(LM_EINVAL, "attention hidden_size " + std::to_string(config->hidden_size) +
+                                       " differs from the context's " + std::to_string(info.hidden));
+        }
+        if (lm::context_attention(ctx) != nullptr) {
+            return fail(LM_EINVAL, "attention is already configured for this context");
+        }
+        LM_ATT_HIP(hipSetDevice(info.device));
+        auto* st = new AttnState();
+        st->cfg = *config;
+        st->scale = softmax_scale(*config);
+        const int64_t cap = config->context_length;
+        const int64_t half = config->qk_rope_head_dim / 2;
+        const int64_t heads = config->num_heads, nope = config->qk_nope_head_dim, rope = config->qk_rope_head_dim,
+                      vh = config->v_head_dim;
+        lm::AttnShape& a = st->shape;
+        a.heads = config->num_heads;
+        a.nope = config->qk_nope_head_dim;
+        a.rope = config->qk_rope_head_dim;
+        a.vh = config->v_head_dim;
+        a.rank = config->kv_lora_rank;
+        a.cap = cap;
+        a.max_positions = cap;
+        auto cleanup = [&](int code) {
+            lm::attention_release(st);
+            return code;
+        };
+        // rotary tables, built on the host in double as RotaryEmbedding::build does
+        std::vector<float> tables(static_cast<size_t>(2 * cap * half) + 1);
+        rope_tables(*config, cap, tables.data(), tables.data() + cap * half);
+        hipError_t err = hipMalloc(reinterpret_cast<void**>(&st->tables), tables.size() * sizeof(float));
+        if (err == hipSuccess) {
+            err = hipMemcpy(st->tables, tables.data(), tables.size() * sizeof(float), hipMemcpyHostToDevice);
+        }
+        if (err != hipSuccess) {
+            return cleanup(fail(err == hipErrorOutOfMemory ? LM_ENOMEM : LM_EHIP,
+                                std::string("rotary tables: ") + hipGetErrorString(err)));
+        }
+        a.cos_t = st->tables;
+        a.sin_t = st->tables + cap * half;
+        // every layer's cache: key_nope [heads][nope][cap], key_rope [rope][cap], value [heads][cap][vh]
+        const int64_t per_layer = cap * (heads * nope + rope + heads * vh);
+        const size_t cache_bytes = static_cast<size_t>(per_layer) * static_cast<size_t>(info.layers) * sizeof(float);
+        err = hipMalloc(reinterpret_cast<void**>(&st->caches), cache_bytes);
+        if (err != hipSuccess) {
+            return cleanup(fail(LM_ENOMEM, "KV caches (" + std::to_string(cache_bytes) + " bytes): " +
+                                               hipGetErrorString(err)));
+        }
+        st->layers.resize(static_cast<size_t>(info.layers));
+        for (int32_t l = 0; l < info.layers; ++l) {
+            float* base = st->caches + static_cast<int64_t>(l) * per_layer;
+            st->layers[l].cache.key_nope = base;
+            st->layers[l].cache.key_rope = base + cap * heads * nope;
+            st->layers[l].cache.value = base + cap * (heads * nope + rope);
+        }
+        if (!lm::attention_shape_supported(a)) {
+            return cleanup(fail(LM_EINVAL, "attention shape not supported"));
+        }
+        lm::context_attention(ctx) = st;
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
+int lm_upload_attention(lm_context* ctx, int32_t layer, const uint16_t* q_proj_host, const uint16_t* q_a_proj_host,
+                        const float* q_a_layernorm_host, const uint16_t* q_b_proj_host,
+                        const uint16_t* kv_a_proj_host, const float* kv_a_layernorm_host,
+                        const uint16_t* kv_b_proj_host, const uint16_t* o_proj_host) {
+    AttnState* st = nullptr;
+    int rc = get_state(ctx, &st);
+    if (rc == LM_OK) {
+        rc = check_attn_layer(st, layer);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    const lm_mla_config& c = st->cfg;
+    const bool lora = c.q_lora_rank > 0;
+    if (lora ? (q_proj_host != nullptr || q_a_proj_host == nullptr || q_a_layernorm_host == nullptr ||
+                q_b_proj_host == nullptr)
+             : (q_proj_host == nullptr || q_a_proj_host != nullptr || q_a_layernorm_host != nullptr ||
+                q_b_proj_host != nullptr)) {
+        return fail(LM_EINVAL, lora ? "q_lora_rank > 0: pass q_a_proj, q_a_layernorm and q_b_proj, not q_proj"
+                                    : "q_lora_rank == 0: pass q_proj, not q_a_proj / q_a_layernorm / q_b_proj");
+    }
+    if (kv_a_proj_host == nullptr || kv_a_layernorm_host == nullptr || kv_b_proj_host == nullptr ||
+        o_proj_host == nullptr) {
+        return fail(LM_EINVAL, "null kv_a_proj, kv_a_layernorm, kv_b_proj or o_proj");
+    }
+    const lm::ContextInfo info = lm::context_info(ctx);
+    LM_ATT_HIP(hipSetDevice(info.device));
+    const int64_t H = c.hidden_size, heads = c.num_heads, qk = c.qk_nope_head_dim + c.qk_rope_head_dim;
+    const int64_t rank = c.kv_lora_rank, rope = c.qk_rope_head_dim, vh = c.v_head_dim, ql = c.q_lora_rank;
+    // element counts, each piece 256-byte aligned in the slab
+    const int64_t n_q = lora ? 0 : heads * qk * H;
+    const int64_t n_qa = lora ? ql * H : 0;
+    const int64_t n_qan = lora ? ql : 0;
+    const int64_t n_qb = lora ? heads * qk * ql : 0;
+    const int64_t n_kva = (rank + rope) * H;
+    const int64_t n_kvb = heads * (c.qk_nope_head_dim + vh) * rank;
+    const int64_t n_o = H * heads * vh;
+    auto align = [](int64_t bytes) { return (bytes + 255) / 256 * 256; };
+    const int64_t off_q = 0;
+    const int64_t off_qa = off_q + align(2 * n_q);
+    const int64_t off_qan = off_qa + align(2 * n_qa);
+    const int64_t off_qb = off_qan + align(4 * n_qan);
+    const int64_t off_kva = off_qb + align(2 * n_qb);
+    const int64_t off_kvan = off_kva + align(2 * n_kva);
+    const int64_t off_kvb = off_kvan + align(4 * rank);
+    const int64_t off_o = off_kvb + align(2 * n_kvb);
+    const int64_t total = off_o + align(2 * n_o);
+    AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+    LM_ATT_HIP(hipStreamSynchronize(info.stream));
+    (void)hipFree(L.slab);
+    L.slab = nullptr;
+    L.kv_a = nullptr;
+    hipError_t err = hipMalloc(&L.slab, static_cast<size_t>(total));
+    if (err != hipSuccess) {
+        return fail(LM_ENOMEM, "attention weights of layer " + std::to_string(layer) + ": " + hipGetErrorString(err));
+    }
+    char* base = static_cast<char*>(L.slab);
+    if (lora) {
+        rc = upload(info.stream, base + off_qa, q_a_proj_host, static_cast<size_t>(2 * n_qa));
+        if (rc == LM_OK) {
+            rc = upload(info.stream, base + off_qan, q_a_layernorm_host, static_cast<size_t>(4 * n_qan));
+        }
+        if (rc == LM_OK) {
+            rc = upload(info.stream, base + off_qb, q_b_proj_host, static_cast<size_t>(2 * n_qb));
+        }
+    } else {
+        rc = upload(info.stream, base + off_q, q_proj_host, static_cast<size_t>(2 * n_q));
+    }
+    if (rc == LM_OK) {
+        rc = upload(info.stream, base + off_kva, kv_a_proj_host, static_cast<size_t>(2 * n_kva));
+    }
+    if (rc == LM_OK) {
+        rc = upload(info.stream, base + off_kvan, kv_a_layernorm_host, static_cast<size_t>(4 * rank));
+    }
+    if (rc == LM_OK) {
+        rc = upload(info.stream, base + off_kvb, kv_b_proj_host, static_cast<size_t>(2 * n_kvb));
+    }
+    if (rc == LM_OK) {
+        rc = upload(info.stream, base + off_o, o_proj_host, static_cast<size_t>(2 * n_o));
+    }
+    if (rc == LM_OK) {
+        const hipError_t e = hipStreamSynchronize(info.stream);
+        if (e != hipSuccess) {
+            rc = fail(LM_EHIP, std::string("upload: ") + hipGetErrorString(e));
+        }
+    }
+    if (rc != LM_OK) {
+        (void)hipFree(L.slab);
+        L.slab = nullptr;
+        return rc;
+    }
+    L.q_proj = lora ? nullptr : reinterpret_cast<const uint16_t*>(base + off_q);
+    L.q_a = lora ? reinterpret_cast<const uint16_t*>(base + off_qa) : nullptr;
+    L.q_a_norm = lora ? reinterpret_cast<const float*>(base + off_qan) : nullptr;
+    L.q_b = lora ? reinterpret_cast<const uint16_t*>(base + off_qb) : nullptr;
+    L.kv_a_norm = reinterpret_cast<const float*>(base + off_kvan);
+    L.kv_b = reinterpret_cast<const uint16_t*>(base + off_kvb);
+    L.o = reinterpret_cast<const uint16_t*>(base + off_o);
+    L.kv_a = reinterpret_cast<const uint16_t*>(base + off_kva);
+    return LM_OK;
+}
+
+int lm_upload_input_norm(lm_context* ctx, int32_t layer, const float* weight_host) {
+    AttnState* st = nullptr;
+    int rc = get_state(ctx, &st);
+    if (rc == LM_OK) {
+        rc = check_attn_layer(st, layer);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (weight_host == nullptr) {
+        return fail(LM_EINVAL, "null input_layernorm weight");
+    }
+    const lm::ContextInfo info = lm::context_info(ctx);
+    LM_ATT_HIP(hipSetDevice(info.device));
+    AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+    if (L.input_norm == nullptr) {
+        LM_ATT_HIP(hipMalloc(reinterpret_cast<void**>(&L.input_norm), sizeof(float) * info.hidden));
+    }
+    LM_ATT_HIP(hipMemcpyAsync(L.input_norm, weight_host, sizeof(float) * info.hidden, hipMemcpyHostToDevice,
+                              info.stream));
+    LM_ATT_HIP(hipStreamSynchronize(info.stream));
+    return LM_OK;
+}
+
+int lm_attention_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, int64_t position0,
+                         float* out_dev, int32_t accumulate) {
+    try {
+        AttnState* st = nullptr;
+        int rc = get_state(ctx, &st);
+        if (rc == LM_OK) {
+            rc = check_attn_layer(st, layer);
+        }
+        if (rc != LM_OK) {
+            return rc;
+        }
+        if (tokens < 0 || position0 < 0) {
+            return fail(LM_EINVAL, "negative token count or position");
+        }
+        if (tokens == 0) {
+            return LM_OK;
+        }
+        if (x_dev == nullptr || out_dev == nullptr) {
+            return fail(LM_EINVAL, "null input or output");
+        }
+        const lm::ContextInfo info = lm::context_info(ctx);
+        const size_t row_bytes = sizeof(float) * static_cast<size_t>(info.hidden) * static_cast<size_t>(tokens);
+        const char* xb = reinterpret_cast<const char*>(x_dev);
+        const char* ob = reinterpret_cast<const char*>(out_dev);
+        if (xb < ob + row_bytes && ob < xb + row_bytes) {
+            return fail(LM_EINVAL, "out_dev overlaps x_dev");
+        }
+        AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+        const int64_t room = st->cfg.context_length - L.count;
+        const int64_t F = std::min(tokens, room);
+        if (F > 0) {
+            rc = attention_tokens(st, info.stream, layer, x_dev, F, position0, out_dev, accumulate);
+            if (rc != LM_OK) {
+                return rc;
+            }
+        }
+        if (F < tokens) {
+            return fail(LM_EFULL, "the KV cache of layer " + std::to_string(layer) + " is full (" +
+                                      std::to_string(st->cfg.context_length) + " tokens)");
+        }
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
+int lm_kv_cache_clear(lm_context* ctx) {
+    AttnState* st = nullptr;
+    const int rc = get_state(ctx, &st);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    // KvCache::clear only resets the count: slots are overwritten before any
+    // score reads them.
+    for (AttnLayer& L : st->layers) {
+        L.count = 0;
+    }
+    return LM_OK;
+}
+
+int lm_kv_cache_tokens(lm_context* ctx, int32_t layer, int64_t* out_tokens) {
+    AttnState* st = nullptr;
+    int rc = get_state(ctx, &st);
+    if (rc == LM_OK) {
+        rc = check_attn_layer(st, layer);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (out_tokens == nullptr) {
+        return fail(LM_EINVAL, "null output");
+    }
+    *out_tokens = st->layers[static_cast<size_t>(layer)].count;
+    return LM_OK;
+}
+
+int lm_kv_cache_read(lm_context* ctx, int32_t layer, int64_t tokens, float* key_nope_host, float* key_rope_host,
+                     float* value_host) {
+    try {
+        AttnState* st = nullptr;
+        int rc = get_state(ctx, &st);
+        if (rc == LM_OK) {
+            rc = check_attn_layer(st, layer);
+        }
+        if (rc != LM_OK) {
+            return rc;
+        }
+        const AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+        if (tokens < 0 || tokens > L.count) {
+            return fail(LM_EINVAL, "tokens must be within the cache's " + std::to_string(L.count));
+        }
+        if (tokens == 0) {
+            return LM_OK;
+        }
+        const lm::ContextInfo info = lm::context_info(ctx);
+        LM_ATT_HIP(hipSetDevice(info.device));
+        LM_ATT_HIP(hipStreamSynchronize(info.stream));
+        const int64_t cap = st->cfg.context_length, heads = st->cfg.num_heads, nope = st->cfg.qk_nope_head_dim,
+                      rope = st->cfg.qk_rope_head_dim, vh = st->cfg.v_head_dim;
+        const size_t tb = sizeof(float) * static_cast<size_t>(tokens);
+        std::vector<float> tmp;
+        if (key_nope_host != nullptr && nope > 0) {
+            tmp.resize(static_cast<size_t>(heads * nope * tokens));
+            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb, L.cache.key_nope, sizeof(float) * cap, tb,
+                                   static_cast<size_t>(heads * nope), hipMemcpyDeviceToHost));
+            for (int64_t h = 0; h < heads; ++h) {
+                for (int64_t d = 0; d < nope; ++d) {
+                    const float* src = tmp.data() + (h * nope + d) * tokens;
+                    for (int64_t t = 0; t < tokens; ++t) {
+                        key_nope_host[(t * heads + h) * nope + d] = src[t];
+                    }
+                }
+            }
+        }
+        if (key_rope_host != nullptr && rope > 0) {
+            tmp.resize(static_cast<size_t>(rope * tokens));
+            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb, L.cache.key_rope, sizeof(float) * cap, tb,
+                                   static_cast<size_t>(rope), hipMemcpyDeviceToHost));
+            for (int64_t d = 0; d < rope; ++d) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    key_rope_host[t * rope + d] = tmp[static_cast<size_t>(d * tokens + t)];
+                }
+            }
+        }
+        if (value_host != nullptr) {
+            tmp.resize(static_cast<size_t>(heads * tokens * vh));
+            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb * vh, L.cache.value, sizeof(float) * cap * vh, tb * vh,
+                                   static_cast<size_t>(heads), hipMemcpyDeviceToHost));
+            for (int64_t h = 0; h < heads; ++h) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    std::copy_n(tmp.data() + (h * tokens + t) * vh, vh, value_host + (t * heads + h) * vh);
+                }
+            }
+        }
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
+int lm_decoder_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
+                       int64_t position0, int32_t path) {
+    try {
+        AttnState* st = nullptr;
+        int rc = get_state(ctx, &st);
+        if (rc == LM_OK) {
+            rc = check_attn_layer(st, first_layer);
+        }
+        if (rc == LM_OK) {
+            rc = check_attn_layer(st, last_layer);
+        }
+        if (rc != LM_OK) {
+            return rc;
+        }
+        if (tokens < 0 || position0 < 0 || first_layer > last_layer) {
+            return fail(LM_EINVAL, "negative token count or position, or first_layer > last_layer");
+        }
+        if (tokens == 0) {
+            return LM_OK;
+        }
+        if (hidden_dev == nullptr) {
+            return fail(LM_EINVAL, "null hidden state");
+        }
+        const lm::ContextInfo info = lm::context_info(ctx);
+        int64_t F = tokens;
+        for (int32_t l = first_layer; l <= last_layer; ++l) {
+            const AttnLayer& L = st->layers[static_cast<size_t>(l)];
+            if (L.input_norm == nullptr || L.kv_a == nullptr) {
+                return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no attention weights or input norm");
+            }
+            F = std::min(F, st->cfg.context_length - L.count);
+        }
+        if (F > 0) {
+            // normalised input rows live in a buffer of their own (the attention
+            // scratch is resized inside each layer's call)
+            rc = ensure_buffer(&st->xn, &st->xn_floats, info.stream, static_cast<size_t>(info.hidden * F));
+            if (rc != LM_OK) {
+                return rc;
+            }
+            float* xn = st->xn;
+            for (int32_t l = first_layer; l <= last_layer && rc == LM_OK; ++l) {
+                const hipError_t e = lm::launch_rms_norm(hidden_dev, st->layers[l].input_norm, xn, F, info.hidden,
+                                                         st->cfg.rms_norm_eps, info.stream);
+                if (e != hipSuccess) {
+                    rc = fail(LM_EHIP, std::string("rms_norm: ") + hipGetErrorString(e));
+                    break;
+                }
+                rc = attention_tokens(st, info.stream, l, xn, F, position0, hidden_dev, 1);
+                if (rc == LM_OK) {
+                    rc = lm::ffn_sublayer(ctx, l, hidden_dev, F, path);
+                }
+            }
+            if (rc != LM_OK) {
+                return rc;
+            }
+        }
+        if (F < tokens) {
+            return fail(LM_EFULL, "the KV cache is full (" + std::to_string(st->cfg.context_length) + " tokens)");
+        }
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
+}  // extern "C"

@@ -190,6 +190,7 @@ struct lm_context {
     float* head_x = nullptr;
     float* head_logits = nullptr;
     lm::HeadBest* head_partial = nullptr;  // per-block candidates of the greedy choice
+    lm::AttnState* attention = nullptr;  // lm_attention_configure: MLA weights, rotary tables, KV caches
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -802,6 +803,36 @@ int static_scratch_setup(lm_context* ctx) {
 
 int lm::set_error(int code, const std::string& message) { return fail(code, message); }
 
+lm::ContextInfo lm::context_info(const lm_context* ctx) {
+    ContextInfo info;
+    info.device = ctx->device;
+    info.stream = ctx->stream;
+    info.hidden = ctx->H;
+    info.layers = static_cast<int32_t>(ctx->layers.size());
+    return info;
+}
+
+lm::AttnState*& lm::context_attention(lm_context* ctx) { return ctx->attention; }
+
+int lm::ffn_sublayer(lm_context* ctx, int32_t l, float* hidden, int64_t T, int32_t path) {
+    int rc = ensure_workspace(ctx, T);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(l)];
+    if (L.norm == nullptr) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no norm weight");
+    }
+    // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290).  The MoE block
+    // normalises the hidden state itself (inside the single-token launch, or
+    // with rms_norm_kernel before the batched path).
+    if (L.dense) {
+        LM_HIP(lm::launch_rms_norm(hidden, L.norm, ctx->ws.xnorm, T, ctx->H, ctx->cfg.rms_norm_eps, ctx->stream));
+        return dense_layer(ctx, l, ctx->ws.xnorm, T, hidden, hidden, path);
+    }
+    return moe_layer(ctx, l, hidden, T, hidden, hidden, nullptr, nullptr, nullptr, nullptr, path, L.norm);
+}
+
 extern "C" {
 
 const char* lm_last_error(void) { return g_error.c_str(); }
@@ -918,6 +949,8 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->head_partial);
     (void)hipFree(ctx->d_overflow);
     (void)hipFree(w.decode_sync);
+    lm::attention_release(ctx->attention);
+    ctx->attention = nullptr;
     if (ctx->staging != nullptr) {
         (void)hipHostFree(ctx->staging);
     }
@@ -1496,21 +1529,7 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
         return rc;
     }
     for (int32_t l = first_layer; l <= last_layer; ++l) {
-        Layer& L = ctx->layers[static_cast<size_t>(l)];
-        if (L.norm == nullptr) {
-            return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no norm weight");
-        }
-        // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290, attention omitted).  The
-        // MoE block normalises the hidden state itself (inside the single-token
-        // launch, or with rms_norm_kernel before the batched path).
-        if (L.dense) {
-            LM_HIP(lm::launch_rms_norm(hidden_dev, L.norm, ctx->ws.xnorm, tokens, ctx->H, ctx->cfg.rms_norm_eps,
-                                       ctx->stream));
-            rc = dense_layer(ctx, l, ctx->ws.xnorm, tokens, hidden_dev, hidden_dev, path);
-        } else {
-            rc = moe_layer(ctx, l, hidden_dev, tokens, hidden_dev, hidden_dev, nullptr, nullptr, nullptr, nullptr,
-                           path, L.norm);
-        }
+        rc = lm::ffn_sublayer(ctx, l, hidden_dev, tokens, path);
         if (rc != LM_OK) {
             return rc;
         }

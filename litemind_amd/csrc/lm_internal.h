@@ -6,6 +6,8 @@
 
 #include "lm_math.h"
 
+struct lm_context;
+
 namespace lm {
 
 // Weight rows are stored with gate and up interleaved in groups of kGroupRows:
@@ -208,6 +210,55 @@ hipError_t launch_head(const uint16_t* w, const float* x, float* logits, HeadBes
 bool matvec_rows_supported(int64_t rows, int64_t in_dim);
 hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim, float scale,
                               int32_t accumulate, hipStream_t s);
+// The same kernel over T tokens x [T, in_dim] -> out [T, rows] (or out +=
+// fma(scale, ., out)), one wave per 16 rows, in launches of up to kHeadTokens
+// tokens; conditions as matvec_rows_supported.
+hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim,
+                                int64_t tokens, float scale, int32_t accumulate, hipStream_t s);
+// ---- multi-head latent attention (k_attn.hip) ----
+// Shapes of one attention launch; cos_t / sin_t are the rotary tables
+// [max_positions, rope / 2] in HBM.
+struct AttnShape {
+    int32_t heads = 0, nope = 0, rope = 0, vh = 0, rank = 0;
+    int64_t cap = 0;            // KV cache capacity (token stride of key_nope and key_rope)
+    int64_t max_positions = 0;  // rotary table rows
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+};
+// One layer's KV cache: key_nope [heads][nope][cap], key_rope [rope][cap],
+// value [heads][cap][vh], fp32.
+struct KvCacheDev {
+    float* key_nope = nullptr;
+    float* key_rope = nullptr;
+    float* value = nullptr;
+};
+bool attention_shape_supported(const AttnShape& a);
+hipError_t launch_rope_query(const AttnShape& a, float* q, int64_t T, int64_t pos0, hipStream_t s);
+hipError_t launch_kv_prep(const AttnShape& a, const KvCacheDev& c, const float* lat, const float* norm_w, float* kvn,
+                          int64_t T, int64_t slot0, int64_t pos0, float eps, hipStream_t s);
+hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float* kvx, int64_t T, int64_t slot0,
+                            hipStream_t s);
+// scores -> softmax -> context for T tokens in slots n0 .. n0 + T - 1 (already
+// appended); S holds T * heads * (n0 + T) floats, ctx [T, heads * vh].
+hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const float* q, float* S, float* ctx,
+                                 int64_t T, int64_t n0, float scale, hipStream_t s);
+
+// ---- services of the context (lm_capi.hip) to the attention translation unit ----
+struct AttnState;
+struct ContextInfo {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int32_t hidden = 0;
+    int32_t layers = 0;
+};
+ContextInfo context_info(const lm_context* ctx);
+AttnState*& context_attention(lm_context* ctx);
+// h += FFN_l(rms_norm(h, post_attention_layernorm_l)) for T rows of hidden
+// (src/DeepSeekRunner.cpp:264-290), as one layer of lm_stack_forward.
+int ffn_sublayer(lm_context* ctx, int32_t layer, float* hidden, int64_t T, int32_t path);
+// Frees what lm_attention_configure allocated (lm_attn.hip); null is a no-op.
+void attention_release(AttnState* st);
+
 // Words of the permutation's scratch for T*K assignments (zeroed once at allocation).
 int64_t permute_scratch_words(int64_t assignments);
 hipError_t launch_gemv_gateup(const ExpertArgs& a, int64_t max_groups, hipStream_t s);

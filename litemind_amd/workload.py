@@ -387,3 +387,17 @@ def mla_layer(seed: int, layer: int, d: MlaDims = V2_LITE_MLA, threads: int = 0)
     kvb = normal_bf16(seed, stream_id(layer, S_KVB), 0.05, (nh * (d.qk_nope + d.v_head), d.kv_lora_rank), threads)
     o = normal_bf16(seed, stream_id(layer, S_O), 0.02, (H, nh * d.v_head), threads)
     return MlaLayer(d, qp, qa, qan, qb, kva, kvan, kvb, o)
+
+
+def mla_config(d: MlaDims = V2_LITE_MLA, context_length: int | None = None):
+    """lm_mla_config for these dimensions (context_length defaults to max_positions)."""
+    from litemind_amd import MlaConfig
+    return MlaConfig(d.hidden, d.heads, d.q_lora_rank, d.kv_lora_rank, d.qk_nope, d.qk_rope, d.v_head,
+                     d.rms_norm_eps, d.rope_theta, 1 if d.yarn else 0, d.factor, d.beta_fast, d.beta_slow, d.mscale,
+                     d.mscale_all_dim, d.original_max, d.max_positions if context_length is None else context_length)
+
+
+def upload_mla_layer(ctx, layer_id: int, L: MlaLayer) -> None:
+    ctx.upload_attention(layer_id, q_proj=L.q_proj, q_a_proj=L.q_a_proj, q_a_layernorm=L.q_a_layernorm,
+                         q_b_proj=L.q_b_proj, kv_a_proj=L.kv_a_proj, kv_a_layernorm=L.kv_a_layernorm,
+                         kv_b_proj=L.kv_b_proj, o_proj=L.o_proj)

@@ -1,5 +1,6 @@
-"""The C ABI library loads and exports every entry point include/litemind_moe.h
-declares (no GPU calls)."""
+"""The C ABI library loads and exports every entry point include/*.h declares
+(no GPU calls)."""
+import glob
 import os
 import re
 import subprocess
@@ -7,17 +8,20 @@ import subprocess
 import litemind_amd
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "litemind_moe.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(lm_[a-z0-9_]+)\(", text, re.M)))
+    names = set()
+    for h in HEADERS:
+        names.update(re.findall(r"^(?:int|const char\*)\s+(lm_[a-z0-9_]+)\(", open(h).read(), re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_abi():
     names = declared()
     assert "lm_moe_forward" in names and "lm_last_error" in names and len(names) >= 30
+    assert "lm_attention_forward" in names and "lm_kv_cache_read" in names
 
 
 def test_library_exports_every_declared_symbol():

@@ -233,3 +233,19 @@ def test_mla_cache_full_returns_and_keeps_cache():
     y2, n2 = ol.oracle_mla(L, x[3:], 3, cache)
     assert n2 == 0 and cache.count.value == 3
     np.testing.assert_array_equal(cache.value, before)
+
+
+# ---- the library's host-side table builder (no GPU) ----
+
+@pytest.mark.parametrize("over", [dict(), dict(yarn=False), dict(mscale=0.5, mscale_all_dim=1.0),
+                                  dict(factor=8.0, mscale_all_dim=0.0, original_max=2048)])
+def test_library_rope_tables_match_oracle(over):
+    """lm_rope_tables / lm_mla_softmax_scale (the product's RotaryEmbedding::build
+    and Config::softmax_scale, run on the host) against the oracle, bit for bit."""
+    import litemind_amd
+    d = dataclasses.replace(wl.V2_LITE_MLA, max_positions=2048, **over)
+    cos, sin = litemind_amd.rope_tables(wl.mla_config(d), d.max_positions)
+    oc, osn = ol.oracle_rope_tables(d)
+    np.testing.assert_array_equal(bits(cos), bits(oc))
+    np.testing.assert_array_equal(bits(sin), bits(osn))
+    assert litemind_amd.mla_softmax_scale(wl.mla_config(d)) == ol.softmax_scale(d)
