@@ -16,6 +16,26 @@
 #include "gemv_items.h"
 #include "lm_select.h"
 
+
+// Timeline hooks: a build with LM_DECODE_TRACE defined records, per workgroup,
+// four s_memrealtime stamps (100 MHz) into lm_decode_trace, read back with
+// lm_decode_trace_read: 0 the start, 1 the speculation known (routed, down),
+// 2 the weights consumed (gate/up) or every wait passed (down), 3 the end.  The
+// library's own build compiles them out.
+#ifdef LM_DECODE_TRACE
+__device__ unsigned long long lm_decode_trace[4 * 4096];
+#define LM_TRACE(k)                                                                   \
+    do {                                                                              \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) {                                  \
+            lm_decode_trace[4 * blockIdx.x + (k)] = __builtin_amdgcn_s_memrealtime(); \
+        }                                                                             \
+    } while (0)
+#else
+#define LM_TRACE(k) \
+    do {            \
+    } while (0)
+#endif
+
 namespace lm {
 namespace {
 
@@ -360,6 +380,7 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    LM_TRACE(2);
     const float sum = transpose_reduce<R>(acc, lane);
     constexpr int L = log2c<R>();
     const int vi = lane >> (6 - L);
@@ -635,6 +656,7 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     }
     __shared__ int spec_lds[kMaxTopK];
     load_spec(f, error, spec_lds);
+    LM_TRACE(1);
     const int64_t down_base = static_cast<int64_t>(2) * W * a.hidden_p;
     uint4 w[RW][KM][DI];
     {
@@ -660,6 +682,7 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     wait_count(sync, kSharedGuDone, f.n_shared_gu, error, f.max_spins);
     wait_count(sync, kRoutedDone, f.n_routed, error, f.max_spins);
     wait_count(sync, kSelectReady, 1, error, f.max_spins);
+    LM_TRACE(2);
     const uint32_t m = __hip_atomic_load(f.mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float wk[KM];
 #pragma unroll
@@ -814,6 +837,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     int b = blockIdx.x;
+    LM_TRACE(0);
     if (b == static_cast<int>(gridDim.x) - 1) {
         // the last workgroup, off the critical path, clears the next launch's counters
         uint32_t* next = f.sync + (1 - f.parity) * kSetWords;
@@ -863,6 +887,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
             }
         }
         signal_done(sync, kSelectReady);
+        LM_TRACE(3);
         return;
     }
     b -= f.n_router;
@@ -871,6 +896,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         // until the router's loads were in, the launch measured 0.2 us longer).
         gateup_item<GI>(a.shared_gu, a, b, a.act + a.top_k * a.inter_p, reinterpret_cast<float*>(lds));
         signal_done(sync, kSharedGuDone);
+        LM_TRACE(3);
         return;
     }
     b -= f.n_shared_gu;
@@ -893,14 +919,17 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         const int item = b + f.n_routed;
         const int r = item / chunks;
         load_spec(f, error, expert_of_rank);
+        LM_TRACE(1);
         gateup_item<GI>(a.routed + static_cast<int64_t>(expert_of_rank[r]) * a.routed_stride, a,
                         item - r * chunks, a.act + static_cast<int64_t>(r) * a.inter_p,
                         reinterpret_cast<float*>(lds));
         signal_done(sync, kRoutedDone);
+        LM_TRACE(3);
         return;
     }
     down_fused<KM, DI, SI, kDownRows>(f, sync, error, b * kFusedRows + wave * kDownRows,
                                       reinterpret_cast<float*>(lds));
+    LM_TRACE(3);
 }
 
 int iters_of(int width) { return (width + 511) / 512; }
@@ -990,3 +1019,9 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
 }
 
 }  // namespace lm
+
+#ifdef LM_DECODE_TRACE
+extern "C" int lm_decode_trace_read(unsigned long long* host, int n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(lm_decode_trace), sizeof(unsigned long long) * n) == hipSuccess ? 0 : -1;
+}
+#endif
