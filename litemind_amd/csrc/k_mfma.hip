@@ -80,13 +80,21 @@ struct TileInfo {
 
 // Maps workgroup `blk` to a tile and finds the tile's group from per-group tile
 // counts (routed experts in expert order, then the shared expert); M tiles of
-// one column block are consecutive.  Workgroup b runs on XCD b % 8: XCD x gets
-// the x-th of eight contiguous, equal (within one) ranges of the tiles that
-// exist, so the M tiles of a column block share one L2 and no XCD is left with
-// only the empty tail of the grid.  s_info: 3 ints of LDS for the hand-off
-// from wave 0 (the caller lends a pipeline buffer that no load writes before
-// every wave has passed a later barrier).
-__device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_routed, int nt_shared,
+// one column block are consecutive.  Workgroup b runs on XCD b % 8.  With
+// `split` (the down projection, whose shared tiles have a longer K than the
+// routed ones: 2816 against 1408 on V2-Lite) every XCD gets an equal share
+// (within one) of the shared expert's tiles and of the routed tiles, each a
+// contiguous range, its shared tiles first; one contiguous split of all tiles
+// left the XCD that holds the shared tiles with twice the work of the others
+// (measured: down at T = 2048 222 -> 179 us, T = 4096 351 -> 261 us).  Without
+// it (gate/up: every tile has the same K) XCD x takes the x-th of eight
+// contiguous, equal ranges of all tiles; dealing column blocks round robin over
+// the XCDs instead (every XCD a share of every expert) measured 8% slower at
+// T = 2048 and 5% at T = 4096.  M tiles of a column block share one L2.
+// s_info: 3 ints of LDS for the hand-off from wave 0 (the caller lends a
+// pipeline buffer that no load writes before every wave has passed a later
+// barrier).
+__device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_routed, int nt_shared, bool split,
                             TileInfo& ti, int* s_info) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
@@ -107,13 +115,33 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
             routed_total += __shfl(incl, 63);
         }
         const int mts_s = a.has_shared ? static_cast<int>((a.tokens + BM - 1) / BM) : 0;
-        const int64_t total = routed_total + static_cast<int64_t>(mts_s) * nt_shared;
-        const int64_t per = total / kXcds, extra = total % kXcds;
+        const int64_t shared_total = static_cast<int64_t>(mts_s) * nt_shared;
         const int64_t xcd = blk % kXcds, idx = blk / kXcds;
-        const int64_t count = per + (xcd < extra ? 1 : 0);
-        const int64_t tile = idx < count ? xcd * per + (xcd < extra ? xcd : extra) + idx : total;
+        // this XCD's contiguous share of n tiles: [first, first + count)
+        auto share = [&](int64_t n, int64_t& first, int64_t& count) {
+            const int64_t per = n / kXcds, extra = n % kXcds;
+            count = per + (xcd < extra ? 1 : 0);
+            first = xcd * per + (xcd < extra ? xcd : extra);
+        };
+        int64_t tile = -1;  // routed tile index, or shared tile routed_total + i
+        if (split) {
+            int64_t s_first, s_count, r_first, r_count;
+            share(shared_total, s_first, s_count);
+            share(routed_total, r_first, r_count);
+            if (idx < s_count) {
+                tile = routed_total + s_first + idx;
+            } else if (idx - s_count < r_count) {
+                tile = r_first + (idx - s_count);
+            }
+        } else {
+            int64_t first, count;
+            share(routed_total + shared_total, first, count);
+            if (idx < count) {
+                tile = first + idx;
+            }
+        }
         int found = -1, local = 0, found_mts = 0;
-        if (tile < routed_total) {
+        if (tile >= 0 && tile < routed_total) {
             int carry = 0;
             for (int g0 = 0; g0 < a.experts; g0 += 64) {
                 const int g = g0 + lane;
@@ -139,7 +167,7 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
                 }
                 carry += __shfl(incl, 63);
             }
-        } else if (tile < total) {
+        } else if (tile >= routed_total) {
             found = a.experts;
             local = static_cast<int>(tile - routed_total);
             found_mts = mts_s;
@@ -208,7 +236,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     // The last stage buffer holds the tile hand-off: the prologue never loads
     // into it, and the first load that does follows the main loop's first
     // barrier, after every wave has read its tile.
-    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, ti,
+    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, MODE == kDown, ti,
                      reinterpret_cast<int*>(As[STAGES - 1]))) {
         return;
     }
@@ -385,16 +413,15 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     }
 }
 
-// Upper bound of the tile count (the kernel maps workgroups onto the tiles that
-// exist and the rest return at once), rounded to whole XCD rounds.
+// Upper bound of the workgroups the tile walk needs (the kernel maps
+// workgroups onto the tiles that exist and the rest return at once): per XCD
+// at most ceil(routed / 8) + ceil(shared / 8) tiles.
 int64_t tile_bound(const ExpertArgs& a, int BM, int nt_routed, int nt_shared) {
     const int64_t TK = a.tokens * a.top_k;
     const int64_t groups = a.experts < TK ? a.experts : TK;
-    int64_t tiles = ((TK + BM - 1) / BM + groups) * nt_routed;
-    if (a.has_shared) {
-        tiles += (a.tokens + BM - 1) / BM * nt_shared;
-    }
-    return (tiles + kXcds - 1) / kXcds * kXcds;
+    const int64_t routed = ((TK + BM - 1) / BM + groups) * nt_routed;
+    const int64_t shared = a.has_shared ? (a.tokens + BM - 1) / BM * nt_shared : 0;
+    return ((routed + kXcds - 1) / kXcds + (shared + kXcds - 1) / kXcds) * kXcds;
 }
 
 template <int MODE, int WM, int WN, int MI, int NJ, int STAGES>
