@@ -44,6 +44,62 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     *reinterpret_cast<float4*>(a.y + t * a.hidden + c) = acc;
 }
 
+// combine_kernel's sum for one token row, then the next layer's RMSNorm of the
+// row just written (rms_norm_kernel's arithmetic: thread-strided double sums of
+// exact squares, wave butterfly, (w0 + w1) + (w2 + w3)) and its fp16 panel copy
+// (to_f16_rows_kernel's conversion): the next layer's input is the same bits as
+// the separate kernels', without reading the hidden state again.  One
+// workgroup of 256 threads per token; thread t owns elements t + 256 k.
+__global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
+    __shared__ double part[4];
+    const int64_t t = blockIdx.x;
+    const int H = a.hidden;
+    float* yrow = a.y + t * H;
+    const float* rrow = a.residual != nullptr ? a.residual + t * H : nullptr;
+    double s = 0.0;
+    for (int c = threadIdx.x; c < H; c += blockDim.x) {
+        float acc = 0.0f;
+        for (int r = 0; r < a.top_k; ++r) {
+            const int64_t slot = a.slot_of[t * a.top_k + r];
+            acc = __builtin_fmaf(a.wts[t * a.top_k + r], a.down_out[slot * H + c], acc);
+        }
+        if (a.has_shared) {
+            acc = acc + a.down_out[(a.tokens * a.top_k + t) * H + c];
+        }
+        if (rrow != nullptr) {
+            acc = rrow[c] + acc;
+        }
+        yrow[c] = acc;
+        const double v = static_cast<double>(acc);
+        s = s + v * v;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        s += __shfl_xor(s, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();  // also orders this workgroup's y stores before the reads below
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inverse =
+        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(H) + static_cast<double>(a.eps)));
+    for (int c = threadIdx.x; c < a.hidden_p; c += blockDim.x) {
+        float v = 0.0f;
+        if (c < H) {
+            const float scaled = yrow[c] * inverse;
+            v = scaled * a.next_norm[c];
+            a.xnorm[t * H + c] = v;
+        }
+        if (a.x16 != nullptr) {
+            // from the rounded fp32 value, as to_f16_rows_kernel converts it:
+            // the compiler would otherwise fold the product and the conversion
+            // into one mixed-precision instruction that rounds once, to fp16
+            asm volatile("" : "+v"(v));
+            a.x16[panel_index(t, c, a.tokens)] = static_cast<_Float16>(v);
+        }
+    }
+}
+
 // BF16 -> fp16 re-encoding of resident weights for the MFMA path, written in
 // panel layout.  Exact for every BF16 value of magnitude in [2^-17, 65504];
 // smaller ones round to fp16 subnormals (absolute error <= 2^-25), larger ones
@@ -312,6 +368,13 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
         return hipSuccess;
+    }
+    if (a.next_norm != nullptr) {
+        if (a.xnorm == nullptr || a.hidden_p < a.hidden) {
+            return hipErrorInvalidValue;
+        }
+        hipLaunchKernelGGL(combine_norm_kernel, dim3(static_cast<unsigned>(a.tokens)), dim3(256), 0, s, a);
+        return hipGetLastError();
     }
     const int64_t n = a.tokens * (a.hidden / 4);
     hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);

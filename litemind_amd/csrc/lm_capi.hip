@@ -420,8 +420,10 @@ lm::RouteBufs route_bufs(lm_context* ctx, int32_t* idx, float* wts) {
 }
 
 // Expert kernels + combine for a layer whose routing is in rb (or a dense FFN).
+// next_norm: the next stack layer's RMSNorm weight; the combine then also
+// writes that layer's input (ws.xnorm, and ws.x16 when the MFMA path follows).
 int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, int64_t T, const lm::RouteBufs& rb,
-                float* y, const float* residual, bool mfma) {
+                float* y, const float* residual, bool mfma, const float* next_norm = nullptr) {
     lm::ExpertArgs ea{};
     ea.groups.gu = reinterpret_cast<const uint16_t* const*>(L.table);
     const int ng = L.dense ? 1 : ctx->E + 1;
@@ -472,6 +474,11 @@ int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, 
     ca.hidden = ctx->H;
     ca.top_k = ea.top_k;
     ca.has_shared = ea.has_shared;
+    ca.next_norm = next_norm;
+    ca.xnorm = ctx->ws.xnorm;
+    ca.x16 = mfma ? ctx->ws.x16 : nullptr;
+    ca.hidden_p = ctx->Hp;
+    ca.eps = ctx->cfg.rms_norm_eps;
     LM_HIP(lm::launch_combine(ca, ctx->stream));
     stage_mark(ctx, 5);
     return LM_OK;
@@ -483,6 +490,13 @@ bool want_mfma(int32_t path, int64_t tokens) {
 
 bool decode_eligible(const lm_context* ctx, const Layer& L) {
     return L.shared_present && lm::decode_supported(ctx->H, ctx->E, ctx->K, ctx->Ip, ctx->Sp);
+}
+
+// True when lm_moe_forward runs T tokens of this MoE layer through the
+// single-token kernel (one launch per token) rather than the batched path.
+bool takes_decode_path(const lm_context* ctx, const Layer& L, int64_t T, int32_t path) {
+    return (T == 1 && !want_mfma(path, T) && decode_eligible(ctx, L)) ||
+           (path == LM_PATH_AUTO && T <= kDecodeTokens && decode_eligible(ctx, L));
 }
 
 // Scratch of single-token launches: the hand-off words (lm::kDecodeSyncWords,
@@ -562,9 +576,11 @@ int decode_layer(lm_context* ctx, Layer& L, const DecodeScratch& sc, const float
 }
 
 // norm: when set, x is the hidden state and the block's input is rms_norm(x, norm).
+// prenormed (batched path only): the previous layer's combine already wrote
+// this layer's normalised input to ws.xnorm (and ws.x16 for the MFMA path).
 int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
               const float* bias, int32_t* idx_out, float* w_out, float* logits_out, int32_t path,
-              const float* norm = nullptr) {
+              const float* norm = nullptr, const float* next_norm = nullptr, bool prenormed = false) {
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
     if (!L.allocated || L.dense || L.router_t == nullptr) {
         return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no resident MoE weights");
@@ -580,8 +596,10 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     int32_t* idx = idx_out != nullptr ? idx_out : ctx->ws.idx;
     float* wts = w_out != nullptr ? w_out : ctx->ws.wts;
 
-    if ((T == 1 && !mfma && decode_eligible(ctx, L)) ||
-        (path == LM_PATH_AUTO && T <= kDecodeTokens && decode_eligible(ctx, L))) {
+    if (takes_decode_path(ctx, L, T, path)) {
+        if (prenormed || next_norm != nullptr) {
+            return fail(LM_EINVAL, "internal: a fused norm was planned for the single-token path");
+        }
         DecodeScratch sc{};
         rc = context_decode_scratch(ctx, &sc);
         if (rc != LM_OK) {
@@ -598,7 +616,9 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
         }
         return LM_OK;
     }
-    if (norm != nullptr) {
+    if (prenormed) {
+        x = ctx->ws.xnorm;
+    } else if (norm != nullptr) {
         LM_HIP(lm::launch_rms_norm(x, norm, ctx->ws.xnorm, T, ctx->H, ctx->cfg.rms_norm_eps, ctx->stream));
         x = ctx->ws.xnorm;
     }
@@ -611,7 +631,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     ra.logits = logits_out;
     ra.idx = idx;
     ra.wts = wts;
-    ra.x16 = mfma ? ctx->ws.x16 : nullptr;
+    ra.x16 = mfma && !prenormed ? ctx->ws.x16 : nullptr;
     ra.tokens = T;
     ra.hidden = ctx->H;
     ra.hidden_p = ctx->Hp;
@@ -642,7 +662,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
         LM_HIP(lm::launch_permute(pa, ctx->stream));
     }
 
-    rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma);
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma, next_norm);
     if (rc != LM_OK) {
         return rc;
     }
@@ -650,7 +670,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
 }
 
 int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* y, const float* residual,
-                int32_t path) {
+                int32_t path, const float* next_norm = nullptr, bool prenormed = false) {
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
     if (!L.allocated || !L.dense || !L.finalized) {
         return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no finalized dense FFN");
@@ -660,7 +680,7 @@ int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float
     if (rc != LM_OK) {
         return rc;
     }
-    if (mfma) {
+    if (mfma && !prenormed) {
         LM_HIP(lm::launch_to_f16_rows(x, ctx->ws.x16, T, ctx->H, ctx->Hp, ctx->stream));
     }
     lm::RouteBufs rb{};
@@ -673,7 +693,7 @@ int dense_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float
     rb.wt = ctx->ws.wts;
     stage_mark(ctx, 0);
     stage_mark(ctx, 1);
-    rc = run_experts(ctx, L, x, ctx->ws.x16, T, rb, y, residual, mfma);
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, rb, y, residual, mfma, next_norm);
     if (rc != LM_OK) {
         return rc;
     }
@@ -814,7 +834,15 @@ lm::ContextInfo lm::context_info(const lm_context* ctx) {
 
 lm::AttnState*& lm::context_attention(lm_context* ctx) { return ctx->attention; }
 
-int lm::ffn_sublayer(lm_context* ctx, int32_t l, float* hidden, int64_t T, int32_t path) {
+namespace {
+
+// h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290) for one layer.  The
+// MoE block normalises the hidden state itself (inside the single-token
+// launch, or with rms_norm_kernel before the batched path), unless
+// `prenormed`: the previous layer's combine already wrote the normalised input.
+// With next_norm this layer's combine does the same for the next layer.
+int ffn_sublayer_fused(lm_context* ctx, int32_t l, float* hidden, int64_t T, int32_t path, const float* next_norm,
+                       bool prenormed) {
     int rc = ensure_workspace(ctx, T);
     if (rc != LM_OK) {
         return rc;
@@ -823,14 +851,30 @@ int lm::ffn_sublayer(lm_context* ctx, int32_t l, float* hidden, int64_t T, int32
     if (L.norm == nullptr) {
         return fail(LM_ENOTRES, "layer " + std::to_string(l) + " has no norm weight");
     }
-    // h += FFN(rms_norm(h)) (src/DeepSeekRunner.cpp:265-290).  The MoE block
-    // normalises the hidden state itself (inside the single-token launch, or
-    // with rms_norm_kernel before the batched path).
     if (L.dense) {
-        LM_HIP(lm::launch_rms_norm(hidden, L.norm, ctx->ws.xnorm, T, ctx->H, ctx->cfg.rms_norm_eps, ctx->stream));
-        return dense_layer(ctx, l, ctx->ws.xnorm, T, hidden, hidden, path);
+        if (!prenormed) {
+            LM_HIP(lm::launch_rms_norm(hidden, L.norm, ctx->ws.xnorm, T, ctx->H, ctx->cfg.rms_norm_eps, ctx->stream));
+        }
+        return dense_layer(ctx, l, ctx->ws.xnorm, T, hidden, hidden, path, next_norm, prenormed);
     }
-    return moe_layer(ctx, l, hidden, T, hidden, hidden, nullptr, nullptr, nullptr, nullptr, path, L.norm);
+    return moe_layer(ctx, l, hidden, T, hidden, hidden, nullptr, nullptr, nullptr, nullptr, path, L.norm, next_norm,
+                     prenormed);
+}
+
+// Whether layer l of a stack pass at T tokens takes the batched path (whose
+// combine can hand the next layer its normalised input).
+bool batched_layer(const lm_context* ctx, int32_t l, int64_t T, int32_t path) {
+    const Layer& L = ctx->layers[static_cast<size_t>(l)];
+    if (!L.allocated || !L.finalized || L.norm == nullptr) {
+        return false;  // the layer reports its own error
+    }
+    return L.dense || (L.router_t != nullptr && !takes_decode_path(ctx, L, T, path));
+}
+
+}  // namespace
+
+int lm::ffn_sublayer(lm_context* ctx, int32_t l, float* hidden, int64_t T, int32_t path) {
+    return ffn_sublayer_fused(ctx, l, hidden, T, path, nullptr, false);
 }
 
 extern "C" {
@@ -1528,11 +1572,19 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
     if (rc != LM_OK) {
         return rc;
     }
+    // Between two batched layers the first one's combine also applies the
+    // second one's RMSNorm (and its fp16 copy): bit for bit the separate
+    // kernels' results, one pass over the hidden state instead of three.
+    bool prenormed = false;
     for (int32_t l = first_layer; l <= last_layer; ++l) {
-        rc = lm::ffn_sublayer(ctx, l, hidden_dev, tokens, path);
+        const bool fuse_next = l < last_layer && batched_layer(ctx, l, tokens, path) &&
+                               batched_layer(ctx, l + 1, tokens, path);
+        const float* next_norm = fuse_next ? ctx->layers[static_cast<size_t>(l + 1)].norm : nullptr;
+        rc = ffn_sublayer_fused(ctx, l, hidden_dev, tokens, path, next_norm, prenormed);
         if (rc != LM_OK) {
             return rc;
         }
+        prenormed = fuse_next;
     }
     return LM_OK;
     LM_GUARD_END

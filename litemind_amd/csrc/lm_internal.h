@@ -138,6 +138,14 @@ struct CombineArgs {
     const float* residual;   // [T, H] or null: y = residual + ffn
     int64_t tokens;
     int32_t hidden, top_k, has_shared;
+    // The next stack layer's RMSNorm applied to y in the same pass (null: none):
+    // xnorm [T, H] = rms_norm(y, next_norm), and x16 (or null) its fp16 copy in
+    // panel layout [T, hidden_p].
+    const float* next_norm;
+    float* xnorm;
+    _Float16* x16;
+    int32_t hidden_p;
+    float eps;
 };
 
 // The routing policy of MoeRouter (src/MoeRouter.cpp:38-52).

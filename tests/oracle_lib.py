@@ -232,22 +232,24 @@ def oracle_dense(gate, up, down, x: np.ndarray, threads: int = 0):
     return y
 
 
-def oracle_stack(layers, h: np.ndarray, eps: float, every_layer: bool = False):
+def oracle_stack(layers, h: np.ndarray, eps: float, every_layer: bool = False, norms=None):
     """The FFN chain of LiteMind's runner with attention omitted
-    (src/DeepSeekRunner.cpp:264-290): for each layer, xn = rms_norm(h, 1)
-    (src/Gemm.cpp:197-207), then h += 1 * FFN(xn) with gemm::axpy
-    (src/Gemm.cpp:191-195).  ``layers`` is a list of ("dense", (gate, up, down))
-    or ("moe", MoeLayer); h [T, H] is not modified.  Returns the final h, or
-    with every_layer the hidden state after each layer."""
+    (src/DeepSeekRunner.cpp:264-290): for each layer, xn = rms_norm(h, w_l)
+    (src/Gemm.cpp:197-207; w_l = 1 unless ``norms`` gives the weights), then
+    h += 1 * FFN(xn) with gemm::axpy (src/Gemm.cpp:191-195).  ``layers`` is a
+    list of ("dense", (gate, up, down)) or ("moe", MoeLayer); h [T, H] is not
+    modified.  Returns the final h, or with every_layer the hidden state after
+    each layer."""
     h = np.array(h, dtype=np.float32, copy=True)
     T, H = h.shape
     ones = np.ones(H, np.float32)
     o = oracle()
     states = []
-    for kind, data in layers:
+    for l, (kind, data) in enumerate(layers):
         xn = h.copy()
+        w = ones if norms is None else np.ascontiguousarray(norms[l], dtype=np.float32)
         for t in range(T):
-            o.orc_rms_norm(p(xn[t]), p(ones), H, eps)
+            o.orc_rms_norm(p(xn[t]), p(w), H, eps)
         y = oracle_dense(*data, xn) if kind == "dense" else oracle_moe_layer(data, xn)[0]
         y = np.ascontiguousarray(y, dtype=np.float32)
         for t in range(T):

@@ -188,3 +188,45 @@ def test_stack_t4096_sampled(stack_ctx):
     max_abs, mean_rel = layer_error(end[sample], oh)
     print(f"stack T=4096 end to end (sample) max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
     assert np.all(np.isfinite(end)) and mean_rel <= MEAN_REL
+
+
+@pytest.mark.parametrize("T,path_name", [(8, "gemv"), (64, "auto")])
+def test_stack_fused_norm_is_bit_exact(stack_ctx, T, path_name):
+    """Between two batched layers lm_stack_forward folds the next layer's
+    RMSNorm (and its fp16 copy) into the current layer's combine.  A pass over
+    the whole stack must give the same bits as the same layers called one at a
+    time (a single-layer call never fuses), with norm weights that are not all
+    ones so that a wrong weight vector would show."""
+    import litemind_amd as lm
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    path = lm.PATH_GEMV if path_name == "gemv" else lm.PATH_AUTO
+    rng = np.random.default_rng(31 + T)
+    norms = [rng.uniform(0.5, 1.5, dims.hidden).astype(np.float32) for _ in range(1 + MOE_LAYERS)]
+    try:
+        for l, w in enumerate(norms):
+            ctx.upload_norm(l, w)
+        h0 = wl.tokens(wl.MASTER_SEED + 77 + T, T, dims.hidden)
+        announce(f"stack T={T} ({path_name}): one pass against layer-by-layer calls")
+        dh = ctx.to_device(h0)
+        ctx.stack_forward(0, MOE_LAYERS, dh, T, path=path)
+        ctx.synchronize()
+        fused = dh.download()
+        dh.free()
+        dh = ctx.to_device(h0)
+        for l in range(1 + MOE_LAYERS):
+            ctx.stack_forward(l, l, dh, T, path=path)
+        ctx.synchronize()
+        separate = dh.download()
+        dh.free()
+        assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
+        # and the chain still follows the oracle with these norm weights
+        ref = ol.oracle_stack(layers, h0[:4], dims.rms_norm_eps, norms=norms)
+        max_abs, mean_rel = layer_error(fused[:4], ref)
+        print(f"max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+        assert max_abs <= MAX_ABS and mean_rel <= MEAN_REL
+    finally:
+        ones = np.ones(dims.hidden, np.float32)
+        for l in range(1 + MOE_LAYERS):
+            ctx.upload_norm(l, ones)
