@@ -49,53 +49,117 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 // exact squares, wave butterfly, (w0 + w1) + (w2 + w3)) and its fp16 panel copy
 // (to_f16_rows_kernel's conversion): the next layer's input is the same bits as
 // the separate kernels', without reading the hidden state again.  One
-// workgroup of 256 threads per token; thread t owns elements t + 256 k.
+// workgroup of 256 threads per token.  The row is formed as combine_kernel
+// forms it (16-byte loads, thread t owning columns 4 t .. 4 t + 3 of every
+// 1024-column step) and staged in LDS, where thread t then adds the squares of
+// columns t, t + 256, ... in rms_norm_kernel's order.  hidden % 4 == 0 and
+// hidden <= kCombineNormMax.
+constexpr int kCombineNormMax = 8192;
+constexpr int kCombineNormSteps = kCombineNormMax / 1024;
+
 __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
+    __shared__ float row[kCombineNormMax];
     __shared__ double part[4];
     const int64_t t = blockIdx.x;
     const int H = a.hidden;
-    float* yrow = a.y + t * H;
-    const float* rrow = a.residual != nullptr ? a.residual + t * H : nullptr;
+    const int tid = threadIdx.x;
+    const float* __restrict__ dout = a.down_out;
+    float4 y[kCombineNormSteps];
+#pragma unroll
+    for (int k = 0; k < kCombineNormSteps; ++k) {
+        y[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // every load is issued before any store (y may be the residual)
+    for (int r = 0; r < a.top_k; ++r) {
+        const int64_t slot = a.slot_of[t * a.top_k + r];
+        const float w = a.wts[t * a.top_k + r];
+#pragma unroll
+        for (int k = 0; k < kCombineNormSteps; ++k) {
+            const int c = 1024 * k + 4 * tid;
+            if (c < H) {
+                const float4 d = *reinterpret_cast<const float4*>(dout + slot * H + c);
+                y[k].x = __builtin_fmaf(w, d.x, y[k].x);
+                y[k].y = __builtin_fmaf(w, d.y, y[k].y);
+                y[k].z = __builtin_fmaf(w, d.z, y[k].z);
+                y[k].w = __builtin_fmaf(w, d.w, y[k].w);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kCombineNormSteps; ++k) {
+        const int c = 1024 * k + 4 * tid;
+        if (c < H) {
+            if (a.has_shared) {
+                const float4 d = *reinterpret_cast<const float4*>(dout + (a.tokens * a.top_k + t) * H + c);
+                y[k].x = y[k].x + d.x;
+                y[k].y = y[k].y + d.y;
+                y[k].z = y[k].z + d.z;
+                y[k].w = y[k].w + d.w;
+            }
+            if (a.residual != nullptr) {
+                const float4 h = *reinterpret_cast<const float4*>(a.residual + t * H + c);
+                y[k].x = h.x + y[k].x;
+                y[k].y = h.y + y[k].y;
+                y[k].z = h.z + y[k].z;
+                y[k].w = h.w + y[k].w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kCombineNormSteps; ++k) {
+        const int c = 1024 * k + 4 * tid;
+        if (c < H) {
+            *reinterpret_cast<float4*>(a.y + t * H + c) = y[k];
+            *reinterpret_cast<float4*>(row + c) = y[k];
+        }
+    }
+    __syncthreads();
     double s = 0.0;
-    for (int c = threadIdx.x; c < H; c += blockDim.x) {
-        float acc = 0.0f;
-        for (int r = 0; r < a.top_k; ++r) {
-            const int64_t slot = a.slot_of[t * a.top_k + r];
-            acc = __builtin_fmaf(a.wts[t * a.top_k + r], a.down_out[slot * H + c], acc);
-        }
-        if (a.has_shared) {
-            acc = acc + a.down_out[(a.tokens * a.top_k + t) * H + c];
-        }
-        if (rrow != nullptr) {
-            acc = rrow[c] + acc;
-        }
-        yrow[c] = acc;
-        const double v = static_cast<double>(acc);
+    for (int c = tid; c < H; c += 256) {
+        const double v = static_cast<double>(row[c]);
         s = s + v * v;
     }
     for (int o = 32; o >= 1; o >>= 1) {
         s += __shfl_xor(s, o);
     }
-    if ((threadIdx.x & 63) == 0) {
-        part[threadIdx.x >> 6] = s;
+    if ((tid & 63) == 0) {
+        part[tid >> 6] = s;
     }
-    __syncthreads();  // also orders this workgroup's y stores before the reads below
+    __syncthreads();
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
     const float inverse =
         static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(H) + static_cast<double>(a.eps)));
-    for (int c = threadIdx.x; c < a.hidden_p; c += blockDim.x) {
-        float v = 0.0f;
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    const int Hp = a.hidden_p;
+    for (int k = 0; 1024 * k < Hp; ++k) {
+        const int c = 1024 * k + 4 * tid;
+        if (c >= Hp) {
+            continue;
+        }
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < H) {
-            const float scaled = yrow[c] * inverse;
-            v = scaled * a.next_norm[c];
-            a.xnorm[t * H + c] = v;
+            float4 yy = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int kk = 0; kk < kCombineNormSteps; ++kk) {
+                if (kk == k) {
+                    yy = y[kk];
+                }
+            }
+            const float4 nw = *reinterpret_cast<const float4*>(a.next_norm + c);
+            v.x = (yy.x * inverse) * nw.x;
+            v.y = (yy.y * inverse) * nw.y;
+            v.z = (yy.z * inverse) * nw.z;
+            v.w = (yy.w * inverse) * nw.w;
+            *reinterpret_cast<float4*>(a.xnorm + t * H + c) = v;
         }
         if (a.x16 != nullptr) {
-            // from the rounded fp32 value, as to_f16_rows_kernel converts it:
-            // the compiler would otherwise fold the product and the conversion
-            // into one mixed-precision instruction that rounds once, to fp16
-            asm volatile("" : "+v"(v));
-            a.x16[panel_index(t, c, a.tokens)] = static_cast<_Float16>(v);
+            // from the rounded fp32 values, as to_f16_rows_kernel converts them:
+            // the compiler would otherwise fold the products and the conversions
+            // into mixed-precision instructions that round once, to fp16
+            asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+            const half4 h = half4{static_cast<_Float16>(v.x), static_cast<_Float16>(v.y), static_cast<_Float16>(v.z),
+                                  static_cast<_Float16>(v.w)};
+            *reinterpret_cast<half4*>(a.x16 + panel_index(t, c, a.tokens)) = h;
         }
     }
 }
@@ -370,7 +434,7 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
         return hipSuccess;
     }
     if (a.next_norm != nullptr) {
-        if (a.xnorm == nullptr || a.hidden_p < a.hidden) {
+        if (a.xnorm == nullptr || a.hidden_p < a.hidden || a.hidden % 4 != 0 || a.hidden_p > kCombineNormMax) {
             return hipErrorInvalidValue;
         }
         hipLaunchKernelGGL(combine_norm_kernel, dim3(static_cast<unsigned>(a.tokens)), dim3(256), 0, s, a);
