@@ -46,7 +46,7 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 # profiles/mfma_grouped_kernel_prefill_t2048_skewed.md).
 MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 139_534_937,
                     ("prefill_t2048_skewed", "gate_up"): 1_156_425_584,
-                    ("prefill_t2048_skewed", "down"): 638_693_503}
+                    ("prefill_t2048_skewed", "down"): 701_822_246}
 
 
 def log(msg: str) -> None:
