@@ -429,12 +429,16 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
     return hipGetLastError();
 }
 
+bool combine_norm_supported(int32_t hidden, int32_t hidden_p) {
+    return hidden > 0 && hidden % 4 == 0 && hidden_p >= hidden && hidden_p % 4 == 0 && hidden_p <= kCombineNormMax;
+}
+
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
         return hipSuccess;
     }
     if (a.next_norm != nullptr) {
-        if (a.xnorm == nullptr || a.hidden_p < a.hidden || a.hidden % 4 != 0 || a.hidden_p > kCombineNormMax) {
+        if (a.xnorm == nullptr || !combine_norm_supported(a.hidden, a.hidden_p)) {
             return hipErrorInvalidValue;
         }
         hipLaunchKernelGGL(combine_norm_kernel, dim3(static_cast<unsigned>(a.tokens)), dim3(256), 0, s, a);

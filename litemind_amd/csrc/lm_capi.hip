@@ -1577,8 +1577,8 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
     // kernels' results, one pass over the hidden state instead of three.
     bool prenormed = false;
     for (int32_t l = first_layer; l <= last_layer; ++l) {
-        const bool fuse_next = l < last_layer && batched_layer(ctx, l, tokens, path) &&
-                               batched_layer(ctx, l + 1, tokens, path);
+        const bool fuse_next = l < last_layer && lm::combine_norm_supported(ctx->H, ctx->Hp) &&
+                               batched_layer(ctx, l, tokens, path) && batched_layer(ctx, l + 1, tokens, path);
         const float* next_norm = fuse_next ? ctx->layers[static_cast<size_t>(l + 1)].norm : nullptr;
         rc = ffn_sublayer_fused(ctx, l, hidden_dev, tokens, path, next_norm, prenormed);
         if (rc != LM_OK) {

@@ -275,6 +275,8 @@ hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t
 hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
+// True when launch_combine can apply the next layer's norm (CombineArgs::next_norm).
+bool combine_norm_supported(int32_t hidden, int32_t hidden_p);
 // dst = fp16 panels of the BF16 matrix src [rows, cols] (cols % kPanel == 0);
 // counts values outside the fp16 range into *overflow.
 hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t rows, int64_t cols, int* overflow,
