@@ -13,6 +13,8 @@
 // waits only on workgroups with lower indices (see decode_fused_kernel), and
 // the routed experts start from a speculative selection while the exact
 // logits are still being summed.
+#include <algorithm>
+
 #include "gemv_items.h"
 #include "lm_select.h"
 
@@ -66,7 +68,9 @@ struct DecodeArgs {
     int64_t routed_stride;     // elements between consecutive experts
     const uint16_t* shared_gu;
     const uint16_t* shared_down;
-    float* act;                // [K, Ip] routed activations in rank order, then [Sp] shared
+    const uint16_t* shared_t;  // [Sp, Hp] the shared expert's down matrix transposed
+    float* shared_part;        // [Sp / 16, H] the shared items' partial down projections
+    float* act;                // [K, Ip] routed activations in rank order
     float* y;                  // [H]
     const float* residual;     // [H] or null
     int32_t hidden, hidden_p, experts, top_k, inter_p, shared_inter_p, has_shared;
@@ -390,6 +394,148 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
     }
 }
 
+// A shared-expert item: gate/up rows [16 chunk, 16 chunk + 16) as gateup_item
+// forms them (LiteMind's roundings), and then the item's share of the shared
+// expert's down projection of every output row, p[h] = sum_j act_j down[h][j]
+// over its 16 rows j, from the transposed down matrix (row j of it is column j
+// of down, contiguous).  Gate, up and down rows (192 KB) are requested
+// together.  The four waves' sums go through LDS to part[chunk][h] with
+// device-scope stores, two floats per lane, consecutive lanes at consecutive
+// addresses.  The shared items run from the launch's start, while the router
+// still decides, so this moves the shared expert's down stream (11.5 MB on
+// V2-Lite) out of the down workgroups' late phase.  LDS: xs (hidden floats),
+// red (4 hidden floats).
+template <int GI>
+__device__ __forceinline__ void shared_item(const DecodeArgs& a, int chunk, float* xs, float* red) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    constexpr int R = 2 * kRpw;
+    const uint16_t* rows[R];
+    const uint16_t* drows[kRpw];
+    const int j0 = chunk * kItemRows + wave * kRpw;
+#pragma unroll
+    for (int r = 0; r < kRpw; ++r) {
+        const int j = j0 + r;
+        const int64_t gate_row = static_cast<int64_t>(j / kGroupRows) * (2 * kGroupRows) + (j % kGroupRows);
+        rows[r] = a.shared_gu + gate_row * a.hidden_p;
+        rows[kRpw + r] = a.shared_gu + (gate_row + kGroupRows) * a.hidden_p;
+        drows[r] = a.shared_t + static_cast<int64_t>(j) * a.hidden_p;
+    }
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        acc[i] = 0.0f;
+    }
+    uint4 w[R][GI];
+    uint4 dw[kRpw][GI];
+    constexpr int XS = (GI * 128 + kThreads - 1) / kThreads;  // float4 per thread
+    const int n4 = a.hidden / 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    float4 xv[XS];
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+        xv[i] = x4[f < n4 ? f : n4 - 1];
+    }
+    // the norm's inputs are requested before the weight rows (results return
+    // in issue order)
+    float nv[norm_elems<GI>()];
+    float4 nw[XS];
+    if (a.norm != nullptr) {
+        norm_load(a, nv);
+        const float4* n4w = reinterpret_cast<const float4*>(a.norm);
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+            nw[i] = n4w[f < n4 ? f : n4 - 1];
+        }
+    }
+    load_rows<R, GI>(rows, a.hidden, lane, w);
+    load_rows<kRpw, GI>(drows, a.hidden, lane, dw);
+    const float inverse = a.norm != nullptr ? norm_reduce(a, nv) : 1.0f;
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+#pragma unroll
+    for (int i = 0; i < XS; ++i) {
+        const int f = static_cast<int>(threadIdx.x) + i * kThreads;
+        if (f < n4) {
+            float4 t = xv[i];
+            if (a.norm != nullptr) {  // rms_norm's (x * inverse) * w
+                t.x = (t.x * inverse) * nw[i].x;
+                t.y = (t.y * inverse) * nw[i].y;
+                t.z = (t.z * inverse) * nw[i].z;
+                t.w = (t.w * inverse) * nw[i].w;
+            }
+            xs4[f] = t;
+        }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int it = 0; it < GI; ++it) {
+        const int c = it * 512 + lane * 8;
+        const bool in = c < a.hidden;
+        const int cc = in ? c : 0;
+        float4 x0 = xs4[cc / 4];
+        float4 x1 = xs4[cc / 4 + 1];
+        if (!in) {
+            x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+            x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            fma8(acc[r], w[r][it], x0, x1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    LM_TRACE(2);
+    const float sum = transpose_reduce<R>(acc, lane);
+    constexpr int L = log2c<R>();
+    // lanes r << (6 - L), r < kRpw, hold gate row j0 + r; its up row is 32 lanes up
+    const float up = __shfl_xor(sum, kRpw << (6 - L));
+    const float act = silu_mul_ref(sum, up);
+    float av[kRpw];
+#pragma unroll
+    for (int r = 0; r < kRpw; ++r) {
+        av[r] = __shfl(act, r << (6 - L));
+    }
+    // This wave's four rows of the down projection for the lane's columns.
+    float4* red4 = reinterpret_cast<float4*>(red);
+    const int H = a.hidden;
+#pragma unroll
+    for (int it = 0; it < GI; ++it) {
+        const int c = it * 512 + lane * 8;
+        float p[8];
+#pragma unroll
+        for (int r = 0; r < kRpw; ++r) {
+            const uint4 d = dw[r][it];
+            const float dv[8] = {bits_float(d.x << 16), bits_float(d.x & 0xffff0000u), bits_float(d.y << 16),
+                                 bits_float(d.y & 0xffff0000u), bits_float(d.z << 16), bits_float(d.z & 0xffff0000u),
+                                 bits_float(d.w << 16), bits_float(d.w & 0xffff0000u)};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                p[e] = r == 0 ? av[0] * dv[e] : __builtin_fmaf(av[r], dv[e], p[e]);
+            }
+        }
+        if (c < H) {
+            red4[(wave * H + c) / 4] = make_float4(p[0], p[1], p[2], p[3]);
+            red4[(wave * H + c) / 4 + 1] = make_float4(p[4], p[5], p[6], p[7]);
+        }
+    }
+    lds_barrier();
+    const float2* red2 = reinterpret_cast<const float2*>(red);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(a.shared_part + static_cast<int64_t>(chunk) * H);
+    for (int h2 = threadIdx.x; h2 < H / 2; h2 += kThreads) {
+        float2 v[kWaves];
+#pragma unroll
+        for (int u = 0; u < kWaves; ++u) {
+            v[u] = red2[u * (H / 2) + h2];
+        }
+        const float o0 = (v[0].x + v[1].x) + (v[2].x + v[3].x);
+        const float o1 = (v[0].y + v[1].y) + (v[2].y + v[3].y);
+        __hip_atomic_store(dst + h2, static_cast<uint64_t>(float_bits(o0)) | (static_cast<uint64_t>(float_bits(o1)) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ---- the single launch --------------------------------------------------------
 //
 // One grid, roles by workgroup index, in dependency order:
@@ -639,21 +785,11 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     const DecodeArgs& a = f.a;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    static_assert(RW == 2, "a wave's two rows are one 8-byte pair of the shared partial sums");
     const int K = a.top_k;
     const int W = a.inter_p;
-    const int WS = a.shared_inter_p;
-    // Rows h0 .. h0 + RW - 1 of the output.  The shared expert's down rows do
-    // not depend on the selection.
-    uint4 ws[RW][SI];
-#pragma unroll
-    for (int j = 0; j < RW; ++j) {
-        const uint16_t* srow = a.shared_down + static_cast<int64_t>(h0 + j) * WS;
-#pragma unroll
-        for (int it = 0; it < SI; ++it) {
-            const int c = it * 512 + lane * 8;
-            ws[j][it] = load_stream16(srow + (c < WS ? c : WS - 8));
-        }
-    }
+    const int n_sitems = a.shared_inter_p / kItemRows;
+    // Rows h0 .. h0 + RW - 1 of the output (h0 even).
     __shared__ int spec_lds[kMaxTopK];
     load_spec(f, error, spec_lds);
     LM_TRACE(1);
@@ -679,7 +815,34 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             }
         }
     }
+    // The shared expert's projection of the two rows: its items' partial sums,
+    // each lane adding items lane, lane + 64, ... in order, then the wave's
+    // butterfly (device-scope loads: the items ran on other XCDs).
     wait_count(sync, kSharedGuDone, f.n_shared_gu, error, f.max_spins);
+    float shared_h[RW] = {0.0f, 0.0f};
+    {
+        constexpr int kPer = (SI * 512 / kItemRows + 63) / 64;  // items per lane at most
+        uint64_t pv[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = lane + 64 * u;
+            pv[u] = i < n_sitems ? __hip_atomic_load(reinterpret_cast<uint64_t*>(a.shared_part + static_cast<int64_t>(i) * a.hidden + h0),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            shared_h[0] = shared_h[0] + bits_float(static_cast<uint32_t>(pv[u]));
+            shared_h[1] = shared_h[1] + bits_float(static_cast<uint32_t>(pv[u] >> 32));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+#pragma unroll
+            for (int j = 0; j < RW; ++j) {
+                shared_h[j] += __shfl_xor(shared_h[j], o);
+            }
+        }
+    }
     wait_count(sync, kRoutedDone, f.n_routed, error, f.max_spins);
     wait_count(sync, kSelectReady, 1, error, f.max_spins);
     LM_TRACE(2);
@@ -689,10 +852,9 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     for (int r = 0; r < KM; ++r) {
         wk[r] = load_coherent(a.wts + (r < K ? r : 0));
     }
-    // The activations of the confirmed ranks and of the shared expert (stored
-    // right after the routed ones), once per workgroup, into LDS.
+    // The activations of the confirmed ranks, once per workgroup, into LDS.
     const int routed4 = K * W / 4;
-    const int n4 = routed4 + WS / 4;
+    const int n4 = routed4;
     for (int f0 = threadIdx.x; f0 < n4; f0 += 4 * kThreads) {
         float4 v[4];
 #pragma unroll
@@ -703,7 +865,7 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int g = f0 + u * kThreads;
-            if (g < n4 && (g >= routed4 || ((m >> (4 * g / W)) & 1u) == 0)) {
+            if (g < n4 && ((m >> (4 * g / W)) & 1u) == 0) {
                 *reinterpret_cast<float4*>(acts + 4 * g) = v[u];
             }
         }
@@ -715,32 +877,11 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     }
     lds_barrier();
     // acc[j KP + r]: row j, rank r (ranks past K read valid data and are never
-    // combined); the shared expert's projection of row j is summed separately.
+    // combined).
     float acc[RW * KP];
-    float shared_h[RW];
 #pragma unroll
     for (int i = 0; i < RW * KP; ++i) {
         acc[i] = 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < RW; ++j) {
-        shared_h[j] = 0.0f;
-#pragma unroll
-        for (int it = 0; it < SI; ++it) {
-            const int c = it * 512 + lane * 8;
-            if (c < WS) {
-                const float4 x0 = *reinterpret_cast<const float4*>(acts + K * W + c);
-                const float4 x1 = *reinterpret_cast<const float4*>(acts + K * W + c + 4);
-                fma8(shared_h[j], ws[j][it], x0, x1);
-            }
-        }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-#pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            shared_h[j] += __shfl_xor(shared_h[j], o);
-        }
     }
 #pragma unroll
     for (int it = 0; it < DI; ++it) {
@@ -894,7 +1035,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     if (b < f.n_shared_gu) {
         // Streams from the start: nothing here depends on the router (held
         // until the router's loads were in, the launch measured 0.2 us longer).
-        gateup_item<GI>(a.shared_gu, a, b, a.act + a.top_k * a.inter_p, reinterpret_cast<float*>(lds));
+        shared_item<GI>(a, b, reinterpret_cast<float*>(lds), reinterpret_cast<float*>(lds) + a.hidden);
         signal_done(sync, kSharedGuDone);
         LM_TRACE(3);
         return;
@@ -960,9 +1101,14 @@ bool decode_supported(int hidden, int experts, int top_k, int inter_p, int share
            fused_shape(hidden, top_k, inter_p, shared_inter_p) >= 0;
 }
 
+int64_t decode_shared_part_floats(int hidden, int shared_inter_p) {
+    return static_cast<int64_t>(hidden) * (shared_inter_p / kItemRows);
+}
+
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     const int hidden = d.hidden, top_k = d.policy.top_k, inter_p = d.inter_p;
-    if (d.sync == nullptr || d.shared_gu == nullptr || (d.norm != nullptr && d.xnorm == nullptr) ||
+    if (d.sync == nullptr || d.shared_gu == nullptr || d.shared_t == nullptr || d.shared_part == nullptr ||
+        (d.norm != nullptr && d.xnorm == nullptr) ||
         !decode_supported(hidden, d.policy.experts, top_k, inter_p, d.shared_inter_p)) {
         return hipErrorInvalidValue;
     }
@@ -982,6 +1128,8 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     a.routed_stride = d.routed_stride;
     a.shared_gu = d.shared_gu;
     a.shared_down = d.shared_down;
+    a.shared_t = d.shared_t;
+    a.shared_part = d.shared_part;
     a.act = d.act;
     a.y = d.y;
     a.residual = d.residual;
@@ -1008,8 +1156,9 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     const int n_down = hidden / kFusedRows;
     const dim3 grid(static_cast<unsigned>(f.n_router + f.n_shared_gu + f.n_routed + n_down));
     const size_t router_lds = sizeof(float) * static_cast<size_t>(hidden) * kRouterExperts;
-    const size_t down_lds = sizeof(float) * (static_cast<size_t>(top_k) * inter_p + d.shared_inter_p);
-    const size_t lds = router_lds > down_lds ? router_lds : down_lds;
+    const size_t down_lds = sizeof(float) * static_cast<size_t>(top_k) * inter_p;
+    const size_t shared_lds = sizeof(float) * static_cast<size_t>(hidden) * (1 + kWaves);
+    const size_t lds = std::max(router_lds, std::max(down_lds, shared_lds));
     if (fused_shape(hidden, top_k, inter_p, d.shared_inter_p) == 0) {
         hipLaunchKernelGGL((decode_fused_kernel<4, 6, 6, 3>), grid, dim3(kThreads), lds, s, f);
     } else {

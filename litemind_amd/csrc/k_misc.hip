@@ -396,6 +396,28 @@ __global__ __launch_bounds__(256) void vector_op_kernel(int op, const void* a_ra
     }
 }
 
+// dst [cols, dst_stride] = transpose of src [rows, src_stride] (16-bit
+// elements), through a 64 x 64 LDS tile: reads and writes are row-contiguous.
+// dst columns >= rows are left as they are.
+__global__ __launch_bounds__(256) void transpose_u16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                            int64_t rows, int64_t cols, int64_t src_stride,
+                                                            int64_t dst_stride) {
+    __shared__ uint16_t tile[64][65];
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        tile[i][tx] = r < rows && c < cols ? src[r * src_stride + c] : static_cast<uint16_t>(0);
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) {
+            dst[c * dst_stride + r] = tile[tx][i];
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
@@ -464,6 +486,19 @@ hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t
     }
     hipLaunchKernelGGL(bf16_to_f16_panels_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, rows,
                        cols, overflow);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_u16(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t cols, int64_t src_stride,
+                               int64_t dst_stride, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) {
+        return hipSuccess;
+    }
+    if ((rows + 63) / 64 > 65535 || (cols + 63) / 64 > 0x7fffffff) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(transpose_u16_kernel, dim3(static_cast<unsigned>((cols + 63) / 64), static_cast<unsigned>((rows + 63) / 64)),
+                       dim3(256), 0, s, src, dst, rows, cols, src_stride, dst_stride);
     return hipGetLastError();
 }
 

@@ -98,6 +98,7 @@ struct Workspace {
     int32_t* zero = nullptr;      // a device int holding 0 (dense layers have no routed experts)
     float* logit_scratch = nullptr;  // [E] single-token router hand-off
     uint32_t* decode_sync = nullptr;  // single-launch decode counters (zeroed once) + error word
+    float* decode_part = nullptr;     // single-launch decode: the shared items' partial down projections
     uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
     int32_t* permute_scratch = nullptr;  // segment counts and arrival ticket of the permutation
 };
@@ -119,15 +120,18 @@ struct EventSet {
 //   [kStaticLogits, + kMaxExperts)   router logit hand-off
 //   [kStaticIdx, + kMaxTopK)         selection when the caller passes none
 //   [kStaticWts, + kMaxTopK)         weights when the caller passes none
-//   [kStaticAct, kStaticWords)       activations [K Ip + Sp]
-constexpr size_t kStaticScratchBytes = 256 * 1024;
+//   [kStaticAct, kStaticPart)        activations [K Ip + Sp]
+//   [kStaticPart, kStaticWords)      the shared items' partial down projections
+// 2 MiB: V2-Lite's shape needs 1.4 MiB of partial sums.
+constexpr size_t kStaticScratchBytes = 2u << 20;
 constexpr int kStaticWords = static_cast<int>(kStaticScratchBytes / 4);
 constexpr int kStaticSync = (lm::kDecodeSyncWords + 63) / 64 * 64;
 constexpr int kStaticLogits = kStaticSync;
 constexpr int kStaticIdx = kStaticLogits + lm::kMaxExperts;
 constexpr int kStaticWts = kStaticIdx + lm::kMaxTopK;
 constexpr int kStaticAct = (kStaticWts + lm::kMaxTopK + 63) / 64 * 64;
-static_assert(kStaticAct < kStaticWords, "static scratch layout");
+constexpr int kStaticPart = 64 * 1024;
+static_assert(kStaticAct < kStaticPart && kStaticPart < kStaticWords, "static scratch layout");
 
 static __device__ __align__(256) uint32_t scratch[kStaticWords];
 
@@ -264,9 +268,13 @@ int allocate_layer(lm_context* ctx, int32_t layer, bool dense) {
     for (auto& f : ffns) {
         total += ffn_bytes(lm::round_up(f.second, lm::kPad), H, Hp);
     }
+    // The single-token kernel's shared items read the shared expert's down
+    // matrix transposed ([Sp, Hp] BF16, 11.5 MB on V2-Lite).
+    const bool shared_t = !dense && ctx->S > 0 && lm::decode_supported(ctx->H, ctx->E, ctx->K, ctx->Ip, ctx->Sp);
+    const size_t t_bytes = shared_t ? static_cast<size_t>(ctx->Sp) * static_cast<size_t>(Hp) * 2 : 0;
     void* slab = nullptr;
-    LM_HIP(hipMalloc(&slab, 2 * total));
-    LM_HIP(hipMemsetAsync(slab, 0, 2 * total, ctx->stream));
+    LM_HIP(hipMalloc(&slab, 2 * total + t_bytes));
+    LM_HIP(hipMemsetAsync(slab, 0, 2 * total + t_bytes, ctx->stream));
     char* bf = static_cast<char*>(slab);
     char* fh = bf + total;
     for (auto& f : ffns) {
@@ -283,11 +291,14 @@ int allocate_layer(lm_context* ctx, int32_t layer, bool dense) {
         bf += n;
         fh += n;
     }
+    if (shared_t) {
+        L.shared.down_t = reinterpret_cast<uint16_t*>(static_cast<char*>(slab) + 2 * total);
+    }
     L.slab = slab;
-    L.slab_bytes = 2 * total;
+    L.slab_bytes = 2 * total + t_bytes;
     L.allocated = true;
     L.dense = dense;
-    ctx->resident += 2 * total;
+    ctx->resident += 2 * total + t_bytes;
     return LM_OK;
 }
 
@@ -508,6 +519,7 @@ struct DecodeScratch {
     uint32_t* sync;
     float* logits;
     float* act;
+    float* shared_part;  // lm::decode_shared_part_floats
     float* xnorm;
     int32_t* parity;
     uint32_t* seq;
@@ -522,8 +534,13 @@ int context_decode_scratch(lm_context* ctx, DecodeScratch* out) {
         LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_sync), bytes));
         LM_HIP(hipMemsetAsync(ctx->ws.decode_sync, 0, bytes, ctx->stream));
     }
-    *out = DecodeScratch{ctx->ws.decode_sync, ctx->ws.logit_scratch, static_cast<float*>(ctx->ws.act),
-                         ctx->ws.xnorm, &ctx->decode_parity, &ctx->decode_seq, &ctx->decode_pending};
+    if (ctx->ws.decode_part == nullptr) {
+        const size_t floats = static_cast<size_t>(lm::decode_shared_part_floats(ctx->H, ctx->Sp));
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_part), sizeof(float) * floats));
+    }
+    *out = DecodeScratch{ctx->ws.decode_sync, ctx->ws.logit_scratch,  static_cast<float*>(ctx->ws.act),
+                         ctx->ws.decode_part, ctx->ws.xnorm,          &ctx->decode_parity,
+                         &ctx->decode_seq,    &ctx->decode_pending};
     return LM_OK;
 }
 
@@ -548,6 +565,8 @@ int decode_layer(lm_context* ctx, Layer& L, const DecodeScratch& sc, const float
     d.routed_stride = static_cast<int64_t>(L.experts[1].gu - L.experts[0].gu);
     d.shared_gu = L.shared.gu;
     d.shared_down = L.shared.down;
+    d.shared_t = L.shared.down_t;
+    d.shared_part = sc.shared_part;
     d.act = sc.act;
     d.y = y;
     d.residual = residual;
@@ -993,6 +1012,7 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->head_partial);
     (void)hipFree(ctx->d_overflow);
     (void)hipFree(w.decode_sync);
+    (void)hipFree(w.decode_part);
     lm::attention_release(ctx->attention);
     ctx->attention = nullptr;
     if (ctx->staging != nullptr) {
@@ -1317,6 +1337,9 @@ int lm_finalize_layer(lm_context* ctx, int32_t layer) {
         LM_HIP(lm::launch_bf16_to_f16_panels(f->gu, f->gu_h, 2 * static_cast<int64_t>(f->inter_p), ctx->Hp,
                                              ctx->d_overflow, ctx->stream));
         LM_HIP(lm::launch_bf16_to_f16_panels(f->down, f->down_h, ctx->H, f->inter_p, ctx->d_overflow, ctx->stream));
+        if (f->down_t != nullptr) {
+            LM_HIP(lm::launch_transpose_u16(f->down, f->down_t, ctx->H, f->inter_p, f->inter_p, ctx->Hp, ctx->stream));
+        }
     }
     int overflow = 0;
     LM_HIP(hipMemcpyAsync(&overflow, ctx->d_overflow, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
@@ -1397,9 +1420,12 @@ int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, i
         return fail(LM_EINVAL, "lm_moe_forward_noalloc: the layer's shape has no single-token kernel");
     }
     const int64_t act_words = static_cast<int64_t>(ctx->K) * ctx->Ip + ctx->Sp;
-    if (act_words > kStaticWords - kStaticAct) {
-        return fail(LM_EINVAL, "lm_moe_forward_noalloc: the layer needs " + std::to_string((kStaticAct + act_words) * 4) +
-                                   " bytes of scratch; the fixed array holds " + std::to_string(kStaticScratchBytes));
+    const int64_t part_words = lm::decode_shared_part_floats(ctx->H, ctx->Sp);
+    if (act_words > kStaticPart - kStaticAct || part_words > kStaticWords - kStaticPart) {
+        return fail(LM_EINVAL, "lm_moe_forward_noalloc: the layer needs " +
+                                   std::to_string((kStaticPart + part_words) * 4) +
+                                   " bytes of scratch (activations up to " + std::to_string((kStaticAct + act_words) * 4) +
+                                   "); the fixed array holds " + std::to_string(kStaticScratchBytes));
     }
     if (ctx->device >= kMaxDevices) {
         return fail(LM_EINVAL, "lm_moe_forward_noalloc: device index beyond the fixed scratch table");
@@ -1413,7 +1439,7 @@ int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, i
         return fail(LM_EHIP, "lm_moe_forward_noalloc: the fixed scratch was not set up on this device");
     }
     float* words = reinterpret_cast<float*>(st.ptr);
-    const DecodeScratch sc{st.ptr, words + kStaticLogits, words + kStaticAct, nullptr, &st.parity, &st.seq,
+    const DecodeScratch sc{st.ptr, words + kStaticLogits, words + kStaticAct, words + kStaticPart, nullptr, &st.parity, &st.seq,
                            &st.pending};
     const int64_t H = ctx->H, K = ctx->K;
     for (int64_t t = 0; t < tokens; ++t) {

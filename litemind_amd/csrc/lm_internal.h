@@ -57,9 +57,12 @@ __device__ inline uint4 load_stream16(const void* p) {
 //   gu:   [2 * inter_p, hidden_p] BF16, gate/up interleaved as above
 //   down: [hidden, inter_p] BF16 (columns >= inter are zero)
 //   *_h:  the same matrices re-encoded as fp16 in panel layout for the MFMA path
+//   down_t: [inter_p, hidden_p] BF16, the down matrix transposed (the shared
+//         expert of a layer the single-token kernel runs; null otherwise)
 struct FfnDev {
     uint16_t* gu = nullptr;
     uint16_t* down = nullptr;
+    uint16_t* down_t = nullptr;
     _Float16* gu_h = nullptr;
     _Float16* down_h = nullptr;
     int32_t inter = 0;    // logical intermediate width
@@ -171,6 +174,8 @@ struct DecodeLaunch {
     int64_t routed_stride;      // elements from one expert's FFN to the next
     const uint16_t* shared_gu;  // shared expert (null: none)
     const uint16_t* shared_down;
+    const uint16_t* shared_t;   // the shared expert's down matrix transposed [Sp, Hp]
+    float* shared_part;         // [Sp / 16, H] the shared items' partial down projections
     float* act;                 // [K * Ip + Sp]
     float* y;                   // [H]
     const float* residual;      // [H] or null
@@ -188,6 +193,8 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted);
 // True when the single-token forward has a one-launch kernel for this shape.
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p);
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s);
+// Floats of the shared items' partial down projections of the single-token kernel.
+int64_t decode_shared_part_floats(int hidden, int shared_inter_p);
 // Single-launch decode scratch, in 32-bit words: two sets of 4 counters x 16
 // slots x 64 B, the error word, approximate logits [64] and speculative experts
 // [16] as tagged 64-bit words, and the mask of ranks the speculation got wrong.
@@ -284,6 +291,9 @@ hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t
 // x16 = fp16 panels of x [rows, cols], zero-padded to cols_p columns.
 hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
                               hipStream_t s);
+// dst [cols, dst_stride] = src [rows, src_stride] transposed (16-bit elements).
+hipError_t launch_transpose_u16(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t cols, int64_t src_stride,
+                               int64_t dst_stride, hipStream_t s);
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
                            hipStream_t s);
 hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
