@@ -183,7 +183,7 @@ int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t t
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  The same MoE block, each token through the
  * single-token kernel in turn (the LM_PATH_AUTO kernel of one to three
- * tokens), with every scratch word in one fixed device array of 256 KiB per
+ * tokens), with every scratch word in one fixed device array of 2 MiB per
  * GPU instead of the context's workspace: the call makes no hipMalloc, hipFree
  * or other allocating call.  The array belongs to the GPU, not to the context:
  * calls on one GPU that overlap (other threads, other contexts' streams) race,
