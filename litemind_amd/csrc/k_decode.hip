@@ -41,6 +41,9 @@ __device__ unsigned long long lm_decode_trace[4 * 4096];
 namespace lm {
 namespace {
 
+typedef __attribute__((address_space(1))) const void decode_global_void;
+typedef __attribute__((address_space(3))) void decode_lds_void;
+
 using gemv::dot_rows;
 using gemv::fma8;
 using gemv::load_rows;
@@ -852,22 +855,22 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     for (int r = 0; r < KM; ++r) {
         wk[r] = load_coherent(a.wts + (r < K ? r : 0));
     }
-    // The activations of the confirmed ranks, once per workgroup, into LDS.
-    const int routed4 = K * W / 4;
-    const int n4 = routed4;
-    for (int f0 = threadIdx.x; f0 < n4; f0 += 4 * kThreads) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int g = f0 + u * kThreads;
-            v[u] = load_coherent4(a.act + 4 * (g < n4 ? g : n4 - 1));
+    // The routed ranks' activations, once per workgroup, into LDS in one round
+    // trip: direct-to-LDS loads that read memory past the XCD's L2 (sc1, like
+    // load_coherent), 1 KB per wave instruction, then 256 B ones for the rest
+    // (W is a multiple of 64).  A rank the speculation got wrong is staged too
+    // and overwritten by the repair below.
+    {
+        const int n = K * W;
+        const int full = n / 256;
+        for (int c = wave; c < full; c += kWaves) {
+            __builtin_amdgcn_global_load_lds((decode_global_void*)(a.act + c * 256 + 4 * lane),
+                                             (decode_lds_void*)(acts + c * 256), 16, 0, 16);
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int g = f0 + u * kThreads;
-            if (g < n4 && ((m >> (4 * g / W)) & 1u) == 0) {
-                *reinterpret_cast<float4*>(acts + 4 * g) = v[u];
-            }
+        for (int g = wave; g < (n - full * 256) / 64; g += kWaves) {
+            const int o = full * 256 + g * 64;
+            __builtin_amdgcn_global_load_lds((decode_global_void*)(a.act + o + lane), (decode_lds_void*)(acts + o), 4, 0,
+                                             16);
         }
     }
     float residual[RW];
@@ -875,6 +878,7 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     for (int j = 0; j < RW; ++j) {
         residual[j] = a.residual != nullptr ? a.residual[h0 + j] : 0.0f;
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged activations are in
     lds_barrier();
     // acc[j KP + r]: row j, rank r (ranks past K read valid data and are never
     // combined).
