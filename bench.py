@@ -44,7 +44,7 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 # this benchmark, scaled by the counters' readings for a conversion kernel of
 # known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md and
 # profiles/mfma_grouped_kernel_prefill_t2048_skewed.md).
-MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 139_534_937,
+MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 146_700_013,
                     ("prefill_t2048_skewed", "gate_up"): 1_156_425_584,
                     ("prefill_t2048_skewed", "down"): 701_822_246}
 
