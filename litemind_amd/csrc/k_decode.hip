@@ -402,9 +402,10 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
 // expert's down projection of every output row, p[h] = sum_j act_j down[h][j]
 // over its 16 rows j, from the transposed down matrix (row j of it is column j
 // of down, contiguous).  Gate, up and down rows (192 KB) are requested
-// together.  The four waves' sums go through LDS to part[chunk][h] with
-// device-scope stores, two floats per lane, consecutive lanes at consecutive
-// addresses.  The shared items run from the launch's start, while the router
+// together.  The four waves' sums go through LDS to part with device-scope
+// stores, two floats per lane.  Layout [H / 8][items][8]: output rows 8b ..
+// 8b + 7 of every item form one contiguous run, which is what one down
+// workgroup reads (four lanes fill one 32-byte piece).  The shared items run from the launch's start, while the router
 // still decides, so this moves the shared expert's down stream (11.5 MB on
 // V2-Lite) out of the down workgroups' late phase.  LDS: xs (hidden floats),
 // red (4 hidden floats).
@@ -525,7 +526,7 @@ __device__ __forceinline__ void shared_item(const DecodeArgs& a, int chunk, floa
     }
     lds_barrier();
     const float2* red2 = reinterpret_cast<const float2*>(red);
-    uint64_t* dst = reinterpret_cast<uint64_t*>(a.shared_part + static_cast<int64_t>(chunk) * H);
+    const int64_t n_items = a.shared_inter_p / kItemRows;
     for (int h2 = threadIdx.x; h2 < H / 2; h2 += kThreads) {
         float2 v[kWaves];
 #pragma unroll
@@ -534,7 +535,9 @@ __device__ __forceinline__ void shared_item(const DecodeArgs& a, int chunk, floa
         }
         const float o0 = (v[0].x + v[1].x) + (v[2].x + v[3].x);
         const float o1 = (v[0].y + v[1].y) + (v[2].y + v[3].y);
-        __hip_atomic_store(dst + h2, static_cast<uint64_t>(float_bits(o0)) | (static_cast<uint64_t>(float_bits(o1)) << 32),
+        const int h = 2 * h2;
+        uint64_t* dst = reinterpret_cast<uint64_t*>(a.shared_part + ((h >> 3) * n_items + chunk) * 8 + (h & 7));
+        __hip_atomic_store(dst, static_cast<uint64_t>(float_bits(o0)) | (static_cast<uint64_t>(float_bits(o1)) << 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -789,6 +792,7 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     static_assert(RW == 2, "a wave's two rows are one 8-byte pair of the shared partial sums");
+    static_assert(kFusedRows == 8, "a down workgroup's rows are one 8-row block of the shared partial sums");
     const int K = a.top_k;
     const int W = a.inter_p;
     const int n_sitems = a.shared_inter_p / kItemRows;
@@ -818,25 +822,38 @@ __device__ __forceinline__ void down_fused(const FusedArgs& f, uint32_t* sync, u
             }
         }
     }
-    // The shared expert's projection of the two rows: its items' partial sums,
-    // each lane adding items lane, lane + 64, ... in order, then the wave's
-    // butterfly (device-scope loads: the items ran on other XCDs).
+    // The shared expert's projection of the two rows: its items' partial sums.
+    // The workgroup's eight rows of every item are one contiguous run
+    // (n_sitems x 32 B), staged once into LDS behind the activations' region
+    // with direct-to-LDS loads past the XCD's L2 (the items ran on other
+    // XCDs), whole 256-byte pieces (the buffer has the slack); then each lane
+    // adds items lane, lane + 64, ... in order, and the wave's butterfly.
     wait_count(sync, kSharedGuDone, f.n_shared_gu, error, f.max_spins);
     float shared_h[RW] = {0.0f, 0.0f};
     {
+        float* staged = acts + K * W;
+        const float* src = a.shared_part + static_cast<int64_t>(h0 >> 3) * n_sitems * 8;
+        const int nf = (n_sitems * 8 + 63) / 64 * 64;
+        for (int c = wave; c < nf / 256; c += kWaves) {
+            __builtin_amdgcn_global_load_lds((decode_global_void*)(src + c * 256 + 4 * lane),
+                                             (decode_lds_void*)(staged + c * 256), 16, 0, 16);
+        }
+        for (int g = wave; g < (nf % 256) / 64; g += kWaves) {
+            const int o = nf / 256 * 256 + g * 64;
+            __builtin_amdgcn_global_load_lds((decode_global_void*)(src + o + lane), (decode_lds_void*)(staged + o), 4, 0,
+                                             16);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        lds_barrier();
         constexpr int kPer = (SI * 512 / kItemRows + 63) / 64;  // items per lane at most
-        uint64_t pv[kPer];
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
             const int i = lane + 64 * u;
-            pv[u] = i < n_sitems ? __hip_atomic_load(reinterpret_cast<uint64_t*>(a.shared_part + static_cast<int64_t>(i) * a.hidden + h0),
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                 : 0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            shared_h[0] = shared_h[0] + bits_float(static_cast<uint32_t>(pv[u]));
-            shared_h[1] = shared_h[1] + bits_float(static_cast<uint32_t>(pv[u] >> 32));
+            if (i < n_sitems) {
+                const float2 v = *reinterpret_cast<const float2*>(staged + i * 8 + (h0 & 7));
+                shared_h[0] = shared_h[0] + v.x;
+                shared_h[1] = shared_h[1] + v.y;
+            }
         }
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) {
@@ -1100,13 +1117,15 @@ int fused_shape(int hidden, int top_k, int inter_p, int shared_inter_p) {
 bool decode_supported(int hidden, int experts, int top_k, int inter_p, int shared_inter_p) {
     return experts % kRouterExperts == 0 && experts >= 2 && experts <= kMaxExperts && top_k >= 1 &&
            top_k <= 8 && top_k <= experts && shared_inter_p > 0 && shared_inter_p % 4 == 0 &&
-           hidden % kFusedRows == 0 && hidden * 16 <= 65536 && (top_k * inter_p + shared_inter_p) * 4 <= 65536 &&
-           inter_p % kItemRows == 0 && shared_inter_p % kItemRows == 0 &&
+           hidden % kFusedRows == 0 && hidden * 16 <= 65536 &&
+           (top_k * inter_p + (shared_inter_p / kItemRows * 8 + 63) / 64 * 64) * 4 <= 65536 &&
+           inter_p % 64 == 0 && shared_inter_p % kItemRows == 0 &&  // activations staged in 256-byte pieces
            fused_shape(hidden, top_k, inter_p, shared_inter_p) >= 0;
 }
 
 int64_t decode_shared_part_floats(int hidden, int shared_inter_p) {
-    return static_cast<int64_t>(hidden) * (shared_inter_p / kItemRows);
+    // + 64: the down workgroups stage whole 256-byte pieces of their run
+    return static_cast<int64_t>(hidden) * (shared_inter_p / kItemRows) + 64;
 }
 
 hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
@@ -1160,7 +1179,8 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     const int n_down = hidden / kFusedRows;
     const dim3 grid(static_cast<unsigned>(f.n_router + f.n_shared_gu + f.n_routed + n_down));
     const size_t router_lds = sizeof(float) * static_cast<size_t>(hidden) * kRouterExperts;
-    const size_t down_lds = sizeof(float) * static_cast<size_t>(top_k) * inter_p;
+    const size_t down_lds =
+        sizeof(float) * (static_cast<size_t>(top_k) * inter_p + (d.shared_inter_p / kItemRows * 8 + 63) / 64 * 64);
     const size_t shared_lds = sizeof(float) * static_cast<size_t>(hidden) * (1 + kWaves);
     const size_t lds = std::max(router_lds, std::max(down_lds, shared_lds));
     if (fused_shape(hidden, top_k, inter_p, d.shared_inter_p) == 0) {
