@@ -590,8 +590,9 @@ __device__ constexpr bool single_slot(int counter) {
     return counter == kRouterDone || counter == kSelectReady;
 }
 
-// Counts this workgroup done once every wave's stores are acknowledged; returns
-// the slot's previous value.
+// Counts this workgroup done once every wave's stores are acknowledged.  The
+// add returns nothing, so the workgroup ends (and frees its slot for a later
+// workgroup) without waiting for it.
 //
 // Ordering of the hand-offs.  Every value one workgroup hands to another is
 // written with an agent-scope atomic store (global_store ... sc1: written
@@ -607,17 +608,14 @@ __device__ constexpr bool single_slot(int counter) {
 // an L2 write-back (buffer_wbl2) per signal and an L2 invalidate (buffer_inv)
 // per wait, for data that never sits in L2: measured, it doubles the launch
 // (35 to 70 us per V2-Lite block).
-__device__ inline uint32_t signal_done(uint32_t* set, int counter) {
+__device__ inline void signal_done(uint32_t* set, int counter) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    __shared__ uint32_t previous;
     if (threadIdx.x == 0) {
         const int slot = single_slot(counter) ? 0 : static_cast<int>(blockIdx.x % kLanes);
-        previous = __hip_atomic_fetch_add(counter_slot(set, counter, slot), 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
+        (void)__hip_atomic_fetch_add(counter_slot(set, counter, slot), 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
     }
-    __syncthreads();
-    return previous;
 }
 
 // Waits until the counter's slots sum to `target` (wave 0 polls all slots at
