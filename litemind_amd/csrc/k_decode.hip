@@ -173,8 +173,15 @@ constexpr int norm_elems() { return 2 * GI; }
 // [H][4] weights; then lane e adds its expert's products strictly left to
 // right, at raised wave priority (the chain shares its SIMD with streaming
 // waves).  after_load runs on every thread once the products are in LDS.
-template <int GI, typename AfterLoad>
-__device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4* prod, AfterLoad after_load) {
+// With the norm fused and no logit bias, the approximate logits come earlier,
+// from the unnormalised products w (x nw): the norm's inverse is one positive
+// factor of every expert's logit, so it does not change their order, and the
+// speculation then waits for neither the norm's reduction nor the products'
+// LDS round; `early(e, t)` runs on threads e < 4 with expert e0 + e's sum, and
+// after_load is not called.
+template <int GI, typename AfterLoad, typename Early>
+__device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4* prod, AfterLoad after_load,
+                                             Early early) {
     const int tid = threadIdx.x;
     const int H = a.hidden;
     const float4* slice = reinterpret_cast<const float4*>(a.wq) + static_cast<int64_t>(e0 / 4) * H;
@@ -205,6 +212,38 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
         }
     }
     load_block(0, w);
+    const bool early_spec = kBlocks == 1 && a.norm != nullptr && a.bias == nullptr;
+    if (early_spec) {
+        float p[kRouterExperts] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j * kThreads + tid < H) {
+                const float u = v[j] * nw[j];
+                p[0] = __builtin_fmaf(w[j].x, u, p[0]);
+                p[1] = __builtin_fmaf(w[j].y, u, p[1]);
+                p[2] = __builtin_fmaf(w[j].z, u, p[2]);
+                p[3] = __builtin_fmaf(w[j].w, u, p[3]);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+#pragma unroll
+            for (int e = 0; e < kRouterExperts; ++e) {
+                p[e] += __shfl_xor(p[e], o);
+            }
+        }
+        __shared__ float early_red[kWaves][kRouterExperts];
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int e = 0; e < kRouterExperts; ++e) {
+                early_red[tid >> 6][e] = p[e];
+            }
+        }
+        lds_barrier();
+        if (tid < kRouterExperts) {
+            early(tid, (early_red[0][tid] + early_red[1][tid]) + (early_red[2][tid] + early_red[3][tid]));
+        }
+    }
     if (a.norm != nullptr) {
         inverse = norm_reduce(a, v);
     }
@@ -244,7 +283,9 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
         }
     }
     lds_barrier();
-    after_load();
+    if (!early_spec) {
+        after_load();
+    }
     if (tid >= kRouterExperts) {
         return;
     }
@@ -1007,7 +1048,8 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     }
     if (b < f.n_router) {
         const int e0 = b * kRouterExperts;
-        router_slice<GI>(a, e0, lds, [&] { speculate(f, e0, lds); });
+        router_slice<GI>(a, e0, lds, [&] { speculate(f, e0, lds); },
+                         [&](int e, float t) { publish(f.approx + e0 + e, f.seq, float_bits(t)); });
         // The last router workgroup to finish its exact logits selects for the output.
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
