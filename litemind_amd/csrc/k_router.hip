@@ -615,6 +615,26 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs
     __builtin_amdgcn_s_waitcnt(0x0070);  // drain the clamped reloads
     __builtin_amdgcn_s_barrier();
 
+    // With a.x16, the fp16 panel copy of the wave's tokens for the MFMA path
+    // (to_f16_rows_kernel's conversion), from rows the loop above has just
+    // brought into L2.  After the loop: a global store inside it makes the
+    // compiler keep far more registers live (256 VGPRs + 256 AGPRs against 100).
+    if (a.x16 != nullptr) {
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) {
+            const int64_t t = tb0 + wave * TPW + k;
+            if (t < a.tokens) {
+                for (int c = 4 * lane; c < H; c += 256) {
+                    const float4 v = *reinterpret_cast<const float4*>(x + t * H + c);
+                    *reinterpret_cast<half4_t*>(a.x16 + panel_index(t, c, a.tokens)) =
+                        half4_t{static_cast<_Float16>(v.x), static_cast<_Float16>(v.y), static_cast<_Float16>(v.z),
+                                static_cast<_Float16>(v.w)};
+                }
+            }
+        }
+    }
+
     float* sh = reinterpret_cast<float*>(r0) + wave * kSelectScratch;
 #pragma unroll
     for (int k = 0; k < TPW; ++k) {
@@ -807,13 +827,19 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         const int tpw = a.tokens > kWideTpw4Tokens ? 4 : (a.tokens > kWideTpw2Tokens ? 2 : 1);
         const int64_t per_block = static_cast<int64_t>(kWideWaves) * tpw;
         const dim3 grid(static_cast<unsigned>((a.tokens + per_block - 1) / per_block));
+        // the kernel writes the fp16 copy itself when it covers every column
+        RouterArgs k = a;
+        const bool separate_x16 = a.x16 != nullptr && a.hidden_p != a.hidden;
+        if (separate_x16) {
+            k.x16 = nullptr;
+        }
         switch (tpw) {
-            case 4: hipLaunchKernelGGL(router_wide_kernel<4>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
-            case 2: hipLaunchKernelGGL(router_wide_kernel<2>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
-            default: hipLaunchKernelGGL(router_wide_kernel<1>, grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4); break;
+            case 4: hipLaunchKernelGGL(router_wide_kernel<4>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+            case 2: hipLaunchKernelGGL(router_wide_kernel<2>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+            default: hipLaunchKernelGGL(router_wide_kernel<1>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
         }
         hipError_t err = hipGetLastError();
-        if (err == hipSuccess && a.x16 != nullptr) {
+        if (err == hipSuccess && separate_x16) {
             err = launch_to_f16_rows(a.x, a.x16, a.tokens, a.hidden, a.hidden_p, s);
         }
         return err;
