@@ -4,6 +4,7 @@
     python bench.py --workload stack      # the 27-layer FFN stack at T=1 and T=4096
     python bench.py --workload load       # SafeTensors shards of 4 layers into HBM
     python bench.py --workload head       # final norm + LM head + greedy token, T=1
+    python bench.py --workload attention  # one MLA attention layer: decode near 512 / 4K cache tokens, prefill T=512
 
 A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
 experts, combine) over one batch of T synthetic tokens whose inputs are already
@@ -327,6 +328,88 @@ def run_load(moe_layers: int) -> dict:
             "value": round(shard_bytes / total / 1e9, 3), "unit": "GB/s"}
 
 
+MLA_CACHE_BYTES_PER_TOKEN = 4 * (16 * (128 + 128) + 64)  # 16,640: fp32 key_nope, value, key_rope
+
+
+def mla_projection_bytes(d) -> int:
+    """BF16 bytes of one attention layer's projections (q without LoRA)."""
+    q = d.heads * d.qk_head * d.hidden
+    kv_a = (d.kv_lora_rank + d.qk_rope) * d.hidden
+    kv_b = d.heads * (d.qk_nope + d.v_head) * d.kv_lora_rank
+    o = d.hidden * d.heads * d.v_head
+    return 2 * (q + kv_a + kv_b + o)
+
+
+def run_attention(steps: int, warmup: int) -> dict:
+    """One DeepSeek-V2-Lite attention layer (multi-head latent attention, q
+    without LoRA, YaRN rotary, 4096-token KV cache) resident in HBM.  Decode:
+    `steps` single-token calls after `warmup` untimed ones, the cache filled
+    before them by a batched prefill to `start` tokens, so the timed steps see
+    contexts start .. start + steps - 1.  Prefill: 512 tokens from position 0
+    (causal) into an emptied cache, each call timed with events.  A decode step
+    reads the projections and the whole cache once (LiteMind's KvCache holds
+    fp32 per-head keys and values)."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    d = wl.V2_LITE_MLA
+    H = d.hidden
+    log("attention: uploading one V2-Lite attention layer")
+    ctx = Context(wl.V2_LITE.moe_config(num_layers=1))
+    ctx.attention_configure(wl.mla_config(d))
+    wl.upload_mla_layer(ctx, 0, wl.mla_layer(wl.MASTER_SEED, 0, d))
+    cap = d.max_positions
+    if steps + warmup > cap - 600:
+        raise ValueError(f"attention: at most {cap - 600 - warmup} decode steps fit the {cap}-token cache")
+    xs = ctx.to_device(wl.tokens(wl.MASTER_SEED + 21, cap, H))
+    dout = ctx.empty((cap, H))
+    row = H * 4
+    proj = mla_projection_bytes(d)
+    out = {"projection_bytes": proj, "cache_bytes_per_token": MLA_CACHE_BYTES_PER_TOKEN}
+    for start in (512, cap - steps - 56):
+        ctx.kv_cache_clear()
+        pos = start - warmup
+        for p0 in range(0, pos, 512):
+            n = min(512, pos - p0)
+            ctx.attention_forward(0, xs.ptr + p0 * row, n, p0, dout.ptr + p0 * row)
+        for i in range(warmup):
+            ctx.attention_forward(0, xs.ptr + pos * row, 1, pos, dout.ptr + pos * row)
+            pos += 1
+        ctx.synchronize()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for i in range(steps):
+            ctx.attention_forward(0, xs.ptr + pos * row, 1, pos, dout.ptr + pos * row)
+            pos += 1
+        ctx.record(e1)
+        ctx.synchronize()
+        us = ctx.elapsed_ms(e0, e1) * 1e3 / steps
+        by = proj + (start + (steps - 1) / 2 + 1) * MLA_CACHE_BYTES_PER_TOKEN + 2 * row
+        out[f"decode_ctx{start}"] = {"context": [start, start + steps - 1], "us_per_step": round(us, 2),
+                                     "tokens_per_s": round(1e6 / us, 1), "bytes_per_step": int(by),
+                                     "achieved_gbs": round(by / us / 1e3, 1),
+                                     "hbm_frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"attention decode from context {start}: {us:.2f} us per step")
+    T = 512
+    times = []
+    for i in range(warmup + 10):
+        ctx.kv_cache_clear()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        ctx.attention_forward(0, xs, T, 0, dout)
+        ctx.record(e1)
+        ctx.synchronize()
+        if i >= warmup:
+            times.append(ctx.elapsed_ms(e0, e1) * 1e3)
+    us = float(np.median(times))
+    out["prefill_t512"] = {"tokens": T, "us": round(us, 2), "tokens_per_s": round(T / us * 1e6, 1)}
+    log(f"attention prefill T={T}: {us:.2f} us")
+    xs.free()
+    dout.free()
+    ctx.close()
+    return out
+
+
 def run_head(steps: int, warmup: int) -> dict:
     """DeepSeek-V2-Lite's final norm and LM head ([102400, 2048] BF16, resident)
     for one token, then the greedy next token: lm_head_forward, timed with events
@@ -381,6 +464,24 @@ def main() -> int:
                 "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-normalised tokens)",
                 "config": {"workload": "stack", "layers": st["layers"], "resident_gb": st["resident_gb"]},
                 "t1": st["t1"], "t4096": st["t4096"]}
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "attention":
+        if args.gpus != 1:
+            print("bench.py measures one GPU.", file=sys.stderr)
+            return 2
+        at = run_attention(args.steps, args.warmup)
+        main = at[max((k for k in at if k.startswith("decode_ctx")), key=lambda k: int(k[len("decode_ctx"):]))]
+        line = {"metric": "MLA attention decode tokens/sec (one V2-Lite layer, KV cache near 4K tokens)",
+                "value": main["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": round(main["us_per_step"] / 1e3, 5), "higher_is_better": True,
+                "dtype": "fp32", "data": "synthetic (seeded N(0,0.02) BF16 projections, N(0,1) RMS-normalised tokens)",
+                "config": {"workload": "attention", "hidden": 2048, "heads": 16, "kv_lora_rank": 512,
+                           "qk_nope": 128, "qk_rope": 64, "v_head": 128, "cache_tokens": 4096},
+                "roofline": {"bound": "hbm", "achieved": main["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": main["hbm_frac"], "traffic": None, "avg_us": main["us_per_step"],
+                             "algorithmic_bytes": main["bytes_per_step"]},
+                "attention": at}
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "head":

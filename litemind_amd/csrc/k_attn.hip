@@ -253,8 +253,15 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
     }
     float total = 0.0f;
     int64_t c0 = 0;
+    // the next chunk's score is requested before this chunk's chain, so the
+    // chain never waits for a load
+    float next = lane < n ? s[lane] : 0.0f;
     for (; c0 + 64 <= n; c0 += 64) {
-        const float e = expf_ref(s[c0 + lane] - m);
+        const float cur = next;
+        if (c0 + 64 + lane < n) {
+            next = s[c0 + 64 + lane];
+        }
+        const float e = expf_ref(cur - m);
         s[c0 + lane] = e;
         const int eb = static_cast<int>(float_bits(e));
 #pragma unroll
@@ -277,6 +284,106 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
     const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
     for (int64_t c = lane; c < n; c += 64) {
         s[c] = s[c] * inverse;
+    }
+}
+
+// softmax_rows_kernel's arithmetic for one query token (decode, T = 1): one
+// workgroup per head.  All threads find the maximum and form expf(s - max)
+// into LDS; wave 0 adds them left to right in one chain, reading LDS with
+// broadcast loads a batch of 64 ahead (a VGPR operand: no lane-to-SGPR hand-off
+// per step); then every thread writes e * (1 / total).  n <= kSoftmaxLds.
+constexpr int kSoftmaxLds = 8192;  // a multiple of 128
+
+__global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n, int64_t n_stride) {
+    constexpr int kPer = kSoftmaxLds / 256;  // scores per thread
+    __shared__ __align__(16) float e[kSoftmaxLds];
+    __shared__ float red[4];
+    __shared__ float inverse_lds;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    float* s = S + static_cast<int64_t>(blockIdx.x) * n_stride;
+    const int nn = static_cast<int>(n);
+    // every score of the thread requested at once
+    float v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = tid + 256 * k;
+        v[k] = c < nn ? s[c] : -__builtin_inff();
+    }
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        m = fmaxf(m, v[k]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o));
+    }
+    if (lane == 0) {
+        red[wave] = m;
+    }
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // e past n is 0 up to the next multiple of 128: adding those exact zeros to
+    // the (non-negative) total changes nothing, and the chain below runs in
+    // whole pairs of batches without a bounds test
+    const int n64 = (nn + 127) / 128 * 128;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = tid + 256 * k;
+        if (c < nn) {
+            e[c] = expf_ref(v[k] - m);
+        } else if (c < n64) {
+            e[c] = 0.0f;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // one batch of 64 values (16 broadcast reads) requested ahead of the
+        // batch being added, so the chain does not wait for LDS
+        const float4* e4 = reinterpret_cast<const float4*>(e);
+        const int nb = n64 / 64;  // even
+        float4 a[16], b[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            a[u] = e4[u];
+        }
+        float total = 0.0f;
+        auto add16 = [&](const float4 (&q)[16]) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                total = total + q[u].x;
+                total = total + q[u].y;
+                total = total + q[u].z;
+                total = total + q[u].w;
+            }
+        };
+        for (int bb = 0; bb < nb; bb += 2) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                b[u] = e4[(bb + 1) * 16 + u];
+            }
+            add16(a);
+            const int na = (bb + 2 < nb ? bb + 2 : bb) * 16;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                a[u] = e4[na + u];
+            }
+            add16(b);
+        }
+        if (lane == 0) {
+            inverse_lds = total > 0.0f ? 1.0f / total : 0.0f;
+        }
+    }
+    __syncthreads();
+    const float inverse = inverse_lds;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int c = tid + 256 * k;
+        if (c < nn) {
+            s[c] = e[c] * inverse;
+        }
     }
 }
 
@@ -351,6 +458,135 @@ __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ 
     }
 }
 
+// The same sum for one query token (decode), T = 1: ctx[h, v] over cached
+// tokens j < n in order.  One workgroup per (head, 64 value channels); wave 0
+// runs the 64 chains (one per lane) from LDS.  The channels' values (256 B per
+// cached token) and the head's probabilities stream through a ring of
+// kCtxDepth LDS slots of kCtxChunk tokens (16 KB) by direct-to-LDS loads that
+// all four waves issue (a wave can have 63 loads of 1 KB in flight, which alone
+// would bound the stream at ~48 KB in flight), so the chain never waits for
+// memory.  One slot per LDS array and the step loop unrolled over the slots,
+// so the compiler knows which slot each load writes and waits only through the
+// explicit vmcnt.  vh % 64 == 0.
+typedef __attribute__((address_space(1))) const void attn_global_void;
+typedef __attribute__((address_space(3))) void attn_lds_void;
+constexpr int kCtxChunk = 64;
+constexpr int kCtxDepth = 8;
+constexpr int kCtxWaves = 4;
+constexpr int kCtxValueLoads = kCtxChunk / 4 / kCtxWaves;  // 1 KB value loads per wave per chunk
+static_assert((kCtxDepth - 1) * (kCtxValueLoads + 1) < 64, "vmcnt immediate");
+
+__global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const float* __restrict__ P,
+                                                                        const float* __restrict__ value,
+                                                                        float* __restrict__ ctx, int32_t vh,
+                                                                        int64_t cap, int64_t n, int64_t n_stride) {
+    // slot = [token][64 channels] values, then the chunk's probabilities: one
+    // array per slot (eight LDS objects are what the compiler's wait insertion
+    // tells apart; sixteen made it wait for every load before each read)
+    constexpr int kSlot = kCtxChunk * 64 + kCtxChunk;
+    __shared__ __align__(16) float s0[kSlot], s1[kSlot], s2[kSlot], s3[kSlot], s4[kSlot], s5[kSlot], s6[kSlot],
+        s7[kSlot];
+    float* const vring[kCtxDepth] = {s0, s1, s2, s3, s4, s5, s6, s7};
+    float* const pring[kCtxDepth] = {s0 + kCtxChunk * 64, s1 + kCtxChunk * 64, s2 + kCtxChunk * 64,
+                                     s3 + kCtxChunk * 64, s4 + kCtxChunk * 64, s5 + kCtxChunk * 64,
+                                     s6 + kCtxChunk * 64, s7 + kCtxChunk * 64};
+    const int lane = threadIdx.x & 63;
+    // wave-uniform as far as the compiler knows, so the branches on it stay
+    // scalar and its wait insertion keeps track of each slot's loads
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int groups = vh / 64;
+    const int h = blockIdx.x / groups;
+    const int c0 = (blockIdx.x - h * groups) * 64;
+    const float* vbase = value + static_cast<int64_t>(h) * cap * vh + c0;
+    const float* prow = P + static_cast<int64_t>(h) * n_stride;
+    const int64_t nchunks = (n + kCtxChunk - 1) / kCtxChunk;
+    // this wave's share of chunk c (clamped to the last chunk, so every step
+    // issues the same count): value load i (i = wave, wave + 4, ...) brings
+    // tokens 4 i .. 4 i + 3, lane l token 4 i + l / 16 and channels
+    // 4 (l % 16) .. + 3, to [token][64 channels]; every wave also brings the
+    // chunk's probabilities (the same 256 B to the same place), so all waves
+    // issue alike; tokens past n read token n - 1 and are never used
+    auto issue = [&](int64_t c, float* vs, float* ps) {
+        c = c < nchunks ? c : nchunks - 1;
+#pragma unroll
+        for (int k = 0; k < kCtxValueLoads; ++k) {
+            const int i = k * kCtxWaves + wave;
+            int64_t tok = c * kCtxChunk + 4 * i + (lane >> 4);
+            tok = tok < n ? tok : n - 1;
+            __builtin_amdgcn_global_load_lds((attn_global_void*)(vbase + tok * vh + 4 * (lane & 15)),
+                                             (attn_lds_void*)(vs + i * 256), 16, 0, 0);
+        }
+        int64_t tok = c * kCtxChunk + lane;
+        tok = tok < n ? tok : n - 1;
+        __builtin_amdgcn_global_load_lds((attn_global_void*)(prow + tok), (attn_lds_void*)ps, 4, 0, 0);
+    };
+#pragma unroll
+    for (int d = 0; d < kCtxDepth - 1; ++d) {
+        issue(d, vring[d], pring[d]);
+    }
+    // chunk c is in once at most the kCtxDepth - 2 chunks issued after it are
+    // in flight
+    constexpr int kVm = (kCtxDepth - 2) * (kCtxValueLoads + 1);
+    constexpr int kWait = 0x0070 | 0x0F00 | (kVm & 15) | ((kVm >> 4) << 14);
+    float acc = 0.0f;
+    for (int64_t cb = 0; cb < nchunks; cb += kCtxDepth) {
+        // no early exit: the loop unrolls over the slots (steps past the last
+        // chunk wait and reload as the others and add nothing)
+#pragma unroll
+        for (int j = 0; j < kCtxDepth; ++j) {
+            const int64_t c = cb + j;
+            __builtin_amdgcn_s_waitcnt(kWait);
+            // every wave's share of chunk c is in; wave 0 has read the slot
+            // refilled next (chunk c - 1) and used all of it
+            __builtin_amdgcn_s_barrier();
+            issue(c + kCtxDepth - 1, vring[(j + kCtxDepth - 1) % kCtxDepth], pring[(j + kCtxDepth - 1) % kCtxDepth]);
+            if (wave != 0) {
+                continue;
+            }
+            const float* vs = vring[j];
+            const float* ps = pring[j];
+            const int64_t rem = n - c * kCtxChunk;
+            const int cnt = static_cast<int>(rem < kCtxChunk ? (rem > 0 ? rem : 0) : kCtxChunk);
+            if (cnt == kCtxChunk) {
+                // two halves of 32 tokens, the second half's LDS reads issued
+                // before the first half's chain, so the chain never waits
+                constexpr int kHalf = kCtxChunk / 2;
+                float x[2][kHalf];
+                float4 pv[2][kHalf / 4];
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+                    for (int t = 0; t < kHalf; ++t) {
+                        x[hf][t] = vs[(hf * kHalf + t) * 64 + lane];
+                    }
+#pragma unroll
+                    for (int t = 0; t < kHalf / 4; ++t) {
+                        pv[hf][t] = *reinterpret_cast<const float4*>(ps + hf * kHalf + 4 * t);
+                    }
+                }
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+                    for (int t = 0; t < kHalf / 4; ++t) {
+                        acc = __builtin_fmaf(pv[hf][t].x, x[hf][4 * t + 0], acc);
+                        acc = __builtin_fmaf(pv[hf][t].y, x[hf][4 * t + 1], acc);
+                        acc = __builtin_fmaf(pv[hf][t].z, x[hf][4 * t + 2], acc);
+                        acc = __builtin_fmaf(pv[hf][t].w, x[hf][4 * t + 3], acc);
+                    }
+                }
+            } else {
+                for (int t = 0; t < cnt; ++t) {
+                    acc = __builtin_fmaf(ps[t], vs[t * 64 + lane], acc);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);  // vmcnt(0): the clamped reloads have landed
+    if (wave == 0) {
+        ctx[static_cast<int64_t>(h) * vh + c0 + lane] = acc;
+    }
+}
+
 unsigned blocks_of(int64_t n, int64_t per) { return static_cast<unsigned>((n + per - 1) / per); }
 
 }  // namespace
@@ -411,13 +647,23 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
         return err;
     }
     const int64_t rows = T * a.heads;
-    hipLaunchKernelGGL(softmax_rows_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, S, rows, a.heads, n0, n_stride);
+    if (T == 1 && n0 + 1 <= kSoftmaxLds) {
+        hipLaunchKernelGGL(softmax_decode_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, S, n0 + 1,
+                           n_stride);
+    } else {
+        hipLaunchKernelGGL(softmax_rows_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, S, rows, a.heads, n0,
+                           n_stride);
+    }
     err = hipGetLastError();
     if (err != hipSuccess) {
         return err;
     }
     const unsigned threads = static_cast<unsigned>((a.vh + 63) / 64 * 64);
-    if (T == 1) {
+    if (T == 1 && a.vh % 64 == 0) {
+        hipLaunchKernelGGL(context_decode_kernel, dim3(static_cast<unsigned>(a.heads * (a.vh / 64))),
+                           dim3(kCtxWaves * 64), 0, s,
+                           S, c.value, ctx, a.vh, a.cap, n0 + 1, n_stride);
+    } else if (T == 1) {
         hipLaunchKernelGGL(context_kernel<1>, dim3(a.heads, 1), dim3(threads), 0, s, S, c.value, ctx, a.heads, a.vh,
                            a.cap, n0, T, n_stride);
     } else {
