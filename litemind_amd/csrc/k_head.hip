@@ -177,6 +177,108 @@ __global__ __launch_bounds__(THREADS) void head_logits_kernel(const uint16_t* __
     }
 }
 
+// The same dot products for many tokens (the projections of a batched
+// attention call): one lane per token, 64 tokens per wave, RW weight rows per
+// wave.  A lane keeps all 32 chains of each (token, row) pair and reduces them
+// as above, so the results are bit for bit head_logits_kernel's.  The rows are
+// the same for every lane, so they come through the scalar cache (one 64-byte
+// load per row and 32-element block, widened on the scalar unit, used as the
+// FMAs' scalar operand), and each lane reads its own token's values with
+// 16-byte loads; the next block of both is requested before the current one's
+// FMAs (blocks in pairs, no register copies).  in_dim % 64 == 0.
+constexpr int kManyRows = 2;  // rows per wave
+typedef const __attribute__((address_space(4))) uint32_t const_u32;
+
+template <int RW>
+__global__ __launch_bounds__(256) void matvec_many_kernel(const uint16_t* __restrict__ w, const float* __restrict__ x,
+                                                          float* out, int64_t rows, int32_t in_dim, int64_t tokens,
+                                                          float scale, int32_t accumulate) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const bool live_t = t < tokens;
+    const float4* xr = reinterpret_cast<const float4*>(x + (live_t ? t : tokens - 1) * in_dim);
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * RW;
+    const_u32* wr[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;  // rows past the end load the last, store nothing
+        wr[r] = (const_u32*)(w + row * in_dim);
+    }
+    float acc[RW][32];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+#pragma unroll
+        for (int c = 0; c < 32; ++c) {
+            acc[r][c] = 0.0f;
+        }
+    }
+    float4 xa[8], xb[8];
+    uint32_t wa[RW][16], wb[RW][16];
+    auto load = [&](int e0, float4 (&xv)[8], uint32_t (&wv)[RW][16]) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            xv[k] = xr[e0 / 4 + k];
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                wv[r][k] = wr[r][e0 / 2 + k];
+            }
+        }
+    };
+    // elements e0 .. e0 + 31: element e0 + c on chain c
+    auto fma_block = [&](const float4 (&xv)[8], const uint32_t (&wv)[RW][16]) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float xs[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint32_t pair = wv[r][2 * k + j];
+                    acc[r][4 * k + 2 * j] = __builtin_fmaf(bits_float(pair << 16), xs[2 * j], acc[r][4 * k + 2 * j]);
+                    acc[r][4 * k + 2 * j + 1] =
+                        __builtin_fmaf(bits_float(pair & 0xffff0000u), xs[2 * j + 1], acc[r][4 * k + 2 * j + 1]);
+                }
+            }
+        }
+    };
+    // the scheduling barriers keep each group of loads ahead of the FMAs that
+    // precede their use (the compiler would otherwise move every load next to
+    // its first use and wait for it there)
+    load(0, xa, wa);
+    for (int e0 = 0; e0 < in_dim; e0 += 64) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(e0 + 32, xb, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        fma_block(xa, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        load(e0 + 64 < in_dim ? e0 + 64 : e0, xa, wa);  // the last pair reloads a block it does not use
+        __builtin_amdgcn_sched_barrier(0);
+        fma_block(xb, wb);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        // (a[l] + a[8 + l]) + (a[16 + l] + a[24 + l]), lanes j and j + 4, (h0 + h2) + (h1 + h3)
+        float ls[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            ls[l] = (acc[r][l] + acc[r][8 + l]) + (acc[r][16 + l] + acc[r][24 + l]);
+        }
+        const float h0 = ls[0] + ls[4];
+        const float h1 = ls[1] + ls[5];
+        const float h2 = ls[2] + ls[6];
+        const float h3 = ls[3] + ls[7];
+        const float total = (h0 + h2) + (h1 + h3);
+        if (live_t && row0 + r < rows) {
+            float* o = out + t * rows + row0 + r;
+            *o = accumulate ? __builtin_fmaf(scale, total, *o) : total;
+        }
+    }
+}
+
 // Sampler::select_next's greedy branch over the blocks' candidates:
 // std::max_element keeps the first of equal values and moves only on a strictly
 // larger one, so a NaN never becomes the choice, except at index 0, which
@@ -256,6 +358,13 @@ hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, i
     }
     if (!matvec_rows_supported(rows, in_dim)) {
         return hipErrorInvalidValue;
+    }
+    if (tokens > kHeadTokens && in_dim % 64 == 0) {
+        const dim3 grid(static_cast<unsigned>((tokens + 63) / 64),
+                        static_cast<unsigned>((rows + 4 * kManyRows - 1) / (4 * kManyRows)));
+        hipLaunchKernelGGL(matvec_many_kernel<kManyRows>, grid, dim3(256), 0, s, w, x, out, rows,
+                           static_cast<int32_t>(in_dim), tokens, scale, accumulate);
+        return hipGetLastError();
     }
     // tokens per launch: at most kHeadTokens, and their rows must fit 64 KiB of LDS
     const int64_t per = std::min<int64_t>(kHeadTokens, std::max<int64_t>(1, 16384 / in_dim));
