@@ -459,75 +459,98 @@ __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ 
 }
 
 // The same sum for one query token (decode), T = 1: ctx[h, v] over cached
-// tokens j < n in order.  One workgroup per (head, 64 value channels); wave 0
-// runs the 64 chains (one per lane) from LDS.  The channels' values (256 B per
+// tokens j < n in order.  One workgroup per (head, 16 value channels); lanes
+// 0..15 of wave 0 run the 16 chains from LDS.  The channels' values (64 B per
 // cached token) and the head's probabilities stream through a ring of
-// kCtxDepth LDS slots of kCtxChunk tokens (16 KB) by direct-to-LDS loads that
-// all four waves issue (a wave can have 63 loads of 1 KB in flight, which alone
-// would bound the stream at ~48 KB in flight), so the chain never waits for
-// memory.  One slot per LDS array and the step loop unrolled over the slots,
+// kCtxDepth LDS slots of kCtxChunk tokens (16 KB of values) by direct-to-LDS
+// buffer loads that all four waves issue: ~119 KB in flight per workgroup, and
+// the narrow groups put 128 workgroups (so 128 CUs' worth of loads) on a
+// V2-Lite layer, so the stream (~7 us near 4K cached tokens) outruns the
+// chains.  The chains cost ~9 cycles per token: a dependent fused multiply-add
+// (~4.4 cycles) plus the wave's share of issuing three LDS reads per four
+// tokens.  One slot per LDS array and the step loop unrolled over the slots,
 // so the compiler knows which slot each load writes and waits only through the
-// explicit vmcnt.  vh % 64 == 0.
-typedef __attribute__((address_space(1))) const void attn_global_void;
+// explicit vmcnt.  vh % 16 == 0.
 typedef __attribute__((address_space(3))) void attn_lds_void;
-constexpr int kCtxChunk = 64;
+// buffer descriptor word 3 for raw 32-bit buffer access on gfx950
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kCtxCh = 16;        // value channels per workgroup
+constexpr int kCtxChunk = 256;    // cached tokens per slot
 constexpr int kCtxDepth = 8;
 constexpr int kCtxWaves = 4;
-constexpr int kCtxValueLoads = kCtxChunk / 4 / kCtxWaves;  // 1 KB value loads per wave per chunk
-static_assert((kCtxDepth - 1) * (kCtxValueLoads + 1) < 64, "vmcnt immediate");
+constexpr int kCtxTokPerLoad = 64 * 4 / kCtxCh;                          // tokens per 1 KB value load
+constexpr int kCtxLoads = kCtxChunk / kCtxTokPerLoad / kCtxWaves + kCtxChunk / 64 / kCtxWaves;  // per wave per chunk
+static_assert(kCtxChunk % (kCtxTokPerLoad * kCtxWaves) == 0 && kCtxChunk % (64 * kCtxWaves) == 0, "even shares");
+static_assert((kCtxDepth - 1) * kCtxLoads < 64, "vmcnt immediate");
 
 __global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const float* __restrict__ P,
                                                                         const float* __restrict__ value,
                                                                         float* __restrict__ ctx, int32_t vh,
                                                                         int64_t cap, int64_t n, int64_t n_stride) {
-    // slot = [token][64 channels] values, then the chunk's probabilities: one
+    // slot = [token][16 channels] values, then the chunk's probabilities: one
     // array per slot (eight LDS objects are what the compiler's wait insertion
-    // tells apart; sixteen made it wait for every load before each read)
-    constexpr int kSlot = kCtxChunk * 64 + kCtxChunk;
+    // tells apart)
+    constexpr int kSlot = kCtxChunk * kCtxCh + kCtxChunk;
     __shared__ __align__(16) float s0[kSlot], s1[kSlot], s2[kSlot], s3[kSlot], s4[kSlot], s5[kSlot], s6[kSlot],
         s7[kSlot];
-    float* const vring[kCtxDepth] = {s0, s1, s2, s3, s4, s5, s6, s7};
-    float* const pring[kCtxDepth] = {s0 + kCtxChunk * 64, s1 + kCtxChunk * 64, s2 + kCtxChunk * 64,
-                                     s3 + kCtxChunk * 64, s4 + kCtxChunk * 64, s5 + kCtxChunk * 64,
-                                     s6 + kCtxChunk * 64, s7 + kCtxChunk * 64};
+    float* const ring[kCtxDepth] = {s0, s1, s2, s3, s4, s5, s6, s7};
     const int lane = threadIdx.x & 63;
     // wave-uniform as far as the compiler knows, so the branches on it stay
     // scalar and its wait insertion keeps track of each slot's loads
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int groups = vh / 64;
-    const int h = blockIdx.x / groups;
-    const int c0 = (blockIdx.x - h * groups) * 64;
+    // workgroup b serves head b % heads, channels 16 (b / heads) ..: with the
+    // heads a multiple of eight, the groups of one head (which split each
+    // token's 128-byte lines between them) share an XCD and so its L2, and
+    // every line is fetched from memory once
+    const int heads = static_cast<int>(gridDim.x) / (vh / kCtxCh);
+    const int h = static_cast<int>(blockIdx.x) % heads;
+    const int c0 = (static_cast<int>(blockIdx.x) / heads) * kCtxCh;
     const float* vbase = value + static_cast<int64_t>(h) * cap * vh + c0;
     const float* prow = P + static_cast<int64_t>(h) * n_stride;
     const int64_t nchunks = (n + kCtxChunk - 1) / kCtxChunk;
     // this wave's share of chunk c (clamped to the last chunk, so every step
     // issues the same count): value load i (i = wave, wave + 4, ...) brings
-    // tokens 4 i .. 4 i + 3, lane l token 4 i + l / 16 and channels
-    // 4 (l % 16) .. + 3, to [token][64 channels]; every wave also brings the
-    // chunk's probabilities (the same 256 B to the same place), so all waves
-    // issue alike; tokens past n read token n - 1 and are never used
-    auto issue = [&](int64_t c, float* vs, float* ps) {
+    // tokens kCtxTokPerLoad i .. + kCtxTokPerLoad - 1, lane l token
+    // kCtxTokPerLoad i + l / 4 and channels 4 (l % 4) .. + 3, to [token][16];
+    // probability load k (k = wave, wave + 4, ...) tokens 64 k .. 64 k + 63;
+    // tokens past n read token n - 1 and are never used
+    // buffer loads rather than global ones: a global load to LDS counts as a
+    // pending flat access, for which the compiler waits for every LDS read at
+    // each use (lgkmcnt(0)) and so cannot keep the next block's reads in
+    // flight.  Offsets are 32-bit: the host sends here only caches with
+    // cap * vh * 4 < 2^31 bytes per head
+    const __amdgpu_buffer_rsrc_t vres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, static_cast<int>((cap * vh - c0) * 4), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t pres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)prow, 0, static_cast<int>(n * 4), kBufferWord3);
+    auto issue = [&](int64_t c, float* slot) {
         c = c < nchunks ? c : nchunks - 1;
 #pragma unroll
-        for (int k = 0; k < kCtxValueLoads; ++k) {
+        for (int k = 0; k < kCtxChunk / kCtxTokPerLoad / kCtxWaves; ++k) {
             const int i = k * kCtxWaves + wave;
-            int64_t tok = c * kCtxChunk + 4 * i + (lane >> 4);
+            int64_t tok = c * kCtxChunk + kCtxTokPerLoad * i + (lane >> 2);
             tok = tok < n ? tok : n - 1;
-            __builtin_amdgcn_global_load_lds((attn_global_void*)(vbase + tok * vh + 4 * (lane & 15)),
-                                             (attn_lds_void*)(vs + i * 256), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (attn_lds_void*)(slot + i * 256), 16,
+                                                     static_cast<unsigned>((tok * vh + 4 * (lane & 3)) * 4), 0, 0, 0);
         }
-        int64_t tok = c * kCtxChunk + lane;
-        tok = tok < n ? tok : n - 1;
-        __builtin_amdgcn_global_load_lds((attn_global_void*)(prow + tok), (attn_lds_void*)ps, 4, 0, 0);
+#pragma unroll
+        for (int k = 0; k < kCtxChunk / 64 / kCtxWaves; ++k) {
+            const int i = k * kCtxWaves + wave;
+            int64_t tok = c * kCtxChunk + 64 * i + lane;
+            tok = tok < n ? tok : n - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(pres, (attn_lds_void*)(slot + kCtxChunk * kCtxCh + 64 * i), 4,
+                                                     static_cast<unsigned>(tok * 4), 0, 0, 0);
+        }
     };
 #pragma unroll
     for (int d = 0; d < kCtxDepth - 1; ++d) {
-        issue(d, vring[d], pring[d]);
+        issue(d, ring[d]);
     }
     // chunk c is in once at most the kCtxDepth - 2 chunks issued after it are
     // in flight
-    constexpr int kVm = (kCtxDepth - 2) * (kCtxValueLoads + 1);
+    constexpr int kVm = (kCtxDepth - 2) * kCtxLoads;
     constexpr int kWait = 0x0070 | 0x0F00 | (kVm & 15) | ((kVm >> 4) << 14);
+    const int ch = lane < kCtxCh ? lane : kCtxCh - 1;  // lanes past the group repeat its last channel
     float acc = 0.0f;
     for (int64_t cb = 0; cb < nchunks; cb += kCtxDepth) {
         // no early exit: the loop unrolls over the slots (steps past the last
@@ -539,50 +562,67 @@ __global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const fl
             // every wave's share of chunk c is in; wave 0 has read the slot
             // refilled next (chunk c - 1) and used all of it
             __builtin_amdgcn_s_barrier();
-            issue(c + kCtxDepth - 1, vring[(j + kCtxDepth - 1) % kCtxDepth], pring[(j + kCtxDepth - 1) % kCtxDepth]);
+            issue(c + kCtxDepth - 1, ring[(j + kCtxDepth - 1) % kCtxDepth]);
             if (wave != 0) {
                 continue;
             }
-            const float* vs = vring[j];
-            const float* ps = pring[j];
+            const float* vs = ring[j];
+            const float* ps = ring[j] + kCtxChunk * kCtxCh;
             const int64_t rem = n - c * kCtxChunk;
             const int cnt = static_cast<int>(rem < kCtxChunk ? (rem > 0 ? rem : 0) : kCtxChunk);
             if (cnt == kCtxChunk) {
-                // two halves of 32 tokens, the second half's LDS reads issued
-                // before the first half's chain, so the chain never waits
-                constexpr int kHalf = kCtxChunk / 2;
-                float x[2][kHalf];
-                float4 pv[2][kHalf / 4];
+                // blocks of 16 tokens (8 paired value reads + 4 probability
+                // reads: few enough that the wait for one block while the
+                // next one's reads are in flight fits lgkmcnt's 4 bits), the
+                // next block's reads issued before this block's chain
+                constexpr int kBlk = 16;
+                float xa[kBlk], xb[kBlk];
+                float4 pa[kBlk / 4], pb[kBlk / 4];
+                auto read = [&](int t0, float (&x)[kBlk], float4 (&p)[kBlk / 4]) {
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-                    for (int t = 0; t < kHalf; ++t) {
-                        x[hf][t] = vs[(hf * kHalf + t) * 64 + lane];
+                    for (int t = 0; t < kBlk; ++t) {
+                        x[t] = vs[(t0 + t) * kCtxCh + ch];
                     }
 #pragma unroll
-                    for (int t = 0; t < kHalf / 4; ++t) {
-                        pv[hf][t] = *reinterpret_cast<const float4*>(ps + hf * kHalf + 4 * t);
+                    for (int t = 0; t < kBlk / 4; ++t) {
+                        p[t] = *reinterpret_cast<const float4*>(ps + t0 + 4 * t);
                     }
-                }
+                };
+                auto chain = [&](const float (&x)[kBlk], const float4 (&p)[kBlk / 4]) {
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-                    for (int t = 0; t < kHalf / 4; ++t) {
-                        acc = __builtin_fmaf(pv[hf][t].x, x[hf][4 * t + 0], acc);
-                        acc = __builtin_fmaf(pv[hf][t].y, x[hf][4 * t + 1], acc);
-                        acc = __builtin_fmaf(pv[hf][t].z, x[hf][4 * t + 2], acc);
-                        acc = __builtin_fmaf(pv[hf][t].w, x[hf][4 * t + 3], acc);
+                    for (int t = 0; t < kBlk / 4; ++t) {
+                        acc = __builtin_fmaf(p[t].x, x[4 * t + 0], acc);
+                        acc = __builtin_fmaf(p[t].y, x[4 * t + 1], acc);
+                        acc = __builtin_fmaf(p[t].z, x[4 * t + 2], acc);
+                        acc = __builtin_fmaf(p[t].w, x[4 * t + 3], acc);
                     }
+                };
+                // the scheduling fences keep each block's reads ahead of the
+                // previous block's chain (left to itself the scheduler sinks
+                // them into it and waits for all of them at once)
+                read(0, xa, pa);
+#pragma unroll
+                for (int t0 = 0; t0 < kCtxChunk; t0 += 2 * kBlk) {
+                    read(t0 + kBlk, xb, pb);
+                    __builtin_amdgcn_sched_barrier(0);
+                    chain(xa, pa);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (t0 + 2 * kBlk < kCtxChunk) {
+                        read(t0 + 2 * kBlk, xa, pa);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    chain(xb, pb);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
                 for (int t = 0; t < cnt; ++t) {
-                    acc = __builtin_fmaf(ps[t], vs[t * 64 + lane], acc);
+                    acc = __builtin_fmaf(ps[t], vs[t * kCtxCh + ch], acc);
                 }
             }
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);  // vmcnt(0): the clamped reloads have landed
-    if (wave == 0) {
+    if (wave == 0 && lane < kCtxCh) {
         ctx[static_cast<int64_t>(h) * vh + c0 + lane] = acc;
     }
 }
@@ -659,8 +699,8 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
         return err;
     }
     const unsigned threads = static_cast<unsigned>((a.vh + 63) / 64 * 64);
-    if (T == 1 && a.vh % 64 == 0) {
-        hipLaunchKernelGGL(context_decode_kernel, dim3(static_cast<unsigned>(a.heads * (a.vh / 64))),
+    if (T == 1 && a.vh % kCtxCh == 0 && a.cap * a.vh < (int64_t{1} << 29)) {  // 32-bit buffer offsets
+        hipLaunchKernelGGL(context_decode_kernel, dim3(static_cast<unsigned>(a.heads * (a.vh / kCtxCh))),
                            dim3(kCtxWaves * 64), 0, s,
                            S, c.value, ctx, a.vh, a.cap, n0 + 1, n_stride);
     } else if (T == 1) {

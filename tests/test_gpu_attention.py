@@ -240,6 +240,29 @@ def test_v2_lite_shapes_prefill_and_decode(q_lora):
         m.close()
 
 
+@pytest.mark.parametrize("prefill", [255, 2303])
+def test_decode_across_value_chunks(prefill):
+    """Decode steps whose cached lengths cross the single-token context
+    kernel's 256-token chunks: n = 256, 257, 258 (one full chunk, then a
+    partial one) and n = 2304, 2305, 2306 (nine chunks, more than its LDS
+    ring holds, so slots are refilled), after a batched prefill."""
+    d = small_dims(max_positions=prefill + 8)
+    announce(f"attention prefill T={prefill} + decode x3 small")
+    m = Mla(d, 181)
+    try:
+        x = tokens(182, prefill + 3, d.hidden)
+        y = m.forward(x[:prefill], 0)
+        want, _ = m.oracle(x[:prefill], 0)
+        np.testing.assert_array_equal(bits(y), bits(want))
+        for t in range(prefill, prefill + 3):
+            y = m.forward(x[t:t + 1], t)
+            want, _ = m.oracle(x[t:t + 1], t)
+            np.testing.assert_array_equal(bits(y), bits(want))
+        m.check_cache()
+    finally:
+        m.close()
+
+
 def test_v2_lite_long_prefill_sampled():
     """A 600-token prefill in one call (two groups of query tokens in the
     attention core, three key tiles) at V2-Lite shapes: tokens 0..599 are
