@@ -229,6 +229,83 @@ __global__ __launch_bounds__(kKeyTile) void scores_kernel(const float* __restric
     }
 }
 
+// scores_kernel's sums for one query token (decode, T = 1) when qk_nope and
+// qk_rope are multiples of 16 (no fused tail, and whole groups): one key per
+// lane, the key's channels taken in groups of 16 (the nope groups, then the
+// rope groups) with the loads of the next two groups in flight while a group is
+// added, so a lane waits for memory once per group of 16 rather than once per
+// loop step.  The head's query row is staged in LDS and read four channels at a
+// time.  Each chain keeps scores_kernel's order: products rounded, added from
+// channel 0 up.
+constexpr int kScoreGroup = 16;
+
+__global__ __launch_bounds__(kKeyTile) void scores_decode_kernel(const float* __restrict__ q,
+                                                                 const float* __restrict__ key_nope,
+                                                                 const float* __restrict__ key_rope,
+                                                                 float* __restrict__ S, int32_t nope, int32_t rope,
+                                                                 int64_t cap, int64_t n, float scale) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) float qs[];  // [nope + rope]
+    const int qk = nope + rope;
+    const int h = blockIdx.y;
+    for (int j = threadIdx.x; j < qk; j += kKeyTile) {
+        qs[j] = q[static_cast<int64_t>(h) * qk + j];
+    }
+    __syncthreads();
+    const int64_t key = static_cast<int64_t>(blockIdx.x) * kKeyTile + threadIdx.x;
+    const int64_t kc = key < n ? key : n - 1;  // lanes past the last key read a valid one
+    const float* kn = key_nope + static_cast<int64_t>(h) * nope * cap + kc;
+    const float* kr = key_rope + kc;
+    const int gn = nope / kScoreGroup;
+    const int groups = gn + rope / kScoreGroup;
+    // group g's 16 keys; groups past the last reload it (every step issues the
+    // same loads, so the compiler's waits count exactly)
+    auto load = [&](int g, float (&x)[kScoreGroup]) {
+        g = g < groups ? g : groups - 1;
+        const float* base = g < gn ? kn + static_cast<int64_t>(g) * kScoreGroup * cap
+                                   : kr + static_cast<int64_t>(g - gn) * kScoreGroup * cap;
+#pragma unroll
+        for (int i = 0; i < kScoreGroup; ++i) {
+            x[i] = base[static_cast<int64_t>(i) * cap];
+        }
+    };
+    float a = 0.0f, b = 0.0f;
+    auto add = [&](int g, const float (&x)[kScoreGroup]) {
+        if (g >= groups) {
+            return;
+        }
+        const f4v* q4 = reinterpret_cast<const f4v*>(qs + g * kScoreGroup);
+        float acc = g < gn ? a : b;
+#pragma unroll
+        for (int i = 0; i < kScoreGroup / 4; ++i) {
+            const f4v w = q4[i];
+            acc = acc + w.x * x[4 * i + 0];
+            acc = acc + w.y * x[4 * i + 1];
+            acc = acc + w.z * x[4 * i + 2];
+            acc = acc + w.w * x[4 * i + 3];
+        }
+        if (g < gn) {
+            a = acc;
+        } else {
+            b = acc;
+        }
+    };
+    float x0[kScoreGroup], x1[kScoreGroup], x2[kScoreGroup];
+    load(0, x0);
+    load(1, x1);
+    for (int g = 0; g < groups; g += 3) {
+        load(g + 2, x2);
+        add(g, x0);
+        load(g + 3, x0);
+        add(g + 1, x1);
+        load(g + 4, x1);
+        add(g + 2, x2);
+    }
+    if (key < n) {
+        S[static_cast<int64_t>(h) * n + key] = scale * (a + b);
+    }
+}
+
 // gemm::softmax (src/Gemm.cpp:209-223) on each row (token t, head h) of S,
 // n0 + t + 1 entries: the maximum, expf(s - max) in place with the total
 // accumulated left to right in one chain (each chunk of 64 is added in lane
@@ -236,6 +313,13 @@ __global__ __launch_bounds__(kKeyTile) void scores_kernel(const float* __restric
 // wave per row, four rows per block.
 __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t rows, int32_t heads, int64_t n0,
                                                            int64_t n_stride) {
+    // expf's 2^(i/32) table in LDS: one read in place of a select tree
+    __shared__ uint64_t exp_tab[32];
+    if (threadIdx.x < 32) {
+        exp_tab[threadIdx.x] = exp2_table(threadIdx.x);
+    }
+    __syncthreads();
+    const auto tab = [&](uint32_t i) { return exp_tab[i]; };
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= rows) {
@@ -261,7 +345,7 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
         if (c0 + 64 + lane < n) {
             next = s[c0 + 64 + lane];
         }
-        const float e = expf_ref(cur - m);
+        const float e = expf_with(cur - m, tab);
         s[c0 + lane] = e;
         const int eb = static_cast<int>(float_bits(e));
 #pragma unroll
@@ -273,7 +357,7 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
         const int cnt = static_cast<int>(n - c0);
         float e = 0.0f;
         if (lane < cnt) {
-            e = expf_ref(s[c0 + lane] - m);
+            e = expf_with(s[c0 + lane] - m, tab);
             s[c0 + lane] = e;
         }
         const int eb = static_cast<int>(float_bits(e));
@@ -298,6 +382,10 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
     constexpr int kPer = kSoftmaxLds / 256;  // scores per thread
     __shared__ __align__(16) float e[kSoftmaxLds];
     __shared__ float red[4];
+    __shared__ uint64_t exp_tab[32];  // expf's 2^(i/32) table: one LDS read in place of a select tree
+    if (threadIdx.x < 32) {
+        exp_tab[threadIdx.x] = exp2_table(threadIdx.x);
+    }
     __shared__ float inverse_lds;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -333,7 +421,7 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
     for (int k = 0; k < kPer; ++k) {
         const int c = tid + 256 * k;
         if (c < nn) {
-            e[c] = expf_ref(v[k] - m);
+            e[c] = expf_with(v[k] - m, [&](uint32_t i) { return exp_tab[i]; });
         } else if (c < n64) {
             e[c] = 0.0f;
         }
@@ -342,15 +430,18 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
     if (wave == 0) {
         // one batch of 64 values (16 broadcast reads) requested ahead of the
         // batch being added, so the chain does not wait for LDS
-        const float4* e4 = reinterpret_cast<const float4*>(e);
+        // a native 4-float vector, so each read stays one 16-byte LDS read
+        // (HIP's float4 struct is split into four)
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v* e4 = reinterpret_cast<const f4v*>(e);
         const int nb = n64 / 64;  // even
-        float4 a[16], b[16];
+        f4v a[16], b[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             a[u] = e4[u];
         }
         float total = 0.0f;
-        auto add16 = [&](const float4 (&q)[16]) {
+        auto add16 = [&](const f4v (&q)[16]) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 total = total + q[u].x;
@@ -674,7 +765,10 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
     const int64_t n_stride = n0 + T;
     const int qk = a.nope + a.rope;
     const unsigned tiles = blocks_of(n_stride, kKeyTile);
-    if (T == 1) {
+    if (T == 1 && a.nope % kScoreGroup == 0 && a.rope % kScoreGroup == 0 && qk > 0) {
+        hipLaunchKernelGGL(scores_decode_kernel, dim3(tiles, a.heads), dim3(kKeyTile), sizeof(float) * qk, s, q,
+                           c.key_nope, c.key_rope, S, a.nope, a.rope, a.cap, n_stride, scale);
+    } else if (T == 1) {
         hipLaunchKernelGGL(scores_kernel<1>, dim3(tiles, a.heads, 1), dim3(kKeyTile), sizeof(float) * qk, s, q,
                            c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope, a.cap, n0, T, n_stride, scale);
     } else {

@@ -74,8 +74,11 @@ LM_HD inline uint64_t exp2_table(uint32_t i) {
     return b4 ? y1 : y0;
 }
 
-// expf as glibc 2.35 computes it on an FMA-capable x86-64 host (see the header).
-LM_HD inline float expf_ref(float x) {
+// expf as glibc 2.35 computes it on an FMA-capable x86-64 host (see the header),
+// with the 2^(i/32) entry (exp2_table's value for i = ki % 32) supplied by
+// `table`: the select tree above, or a copy of it that a kernel keeps in LDS.
+template <class Table>
+LM_HD inline float expf_with(float x, Table table) {
     const uint32_t abstop = (float_bits(x) >> 20) & 0x7ffu;
     if (abstop >= (float_bits(88.0f) >> 20)) {
         if (float_bits(x) == float_bits(-__builtin_inff())) {
@@ -101,7 +104,7 @@ LM_HD inline float expf_ref(float x) {
     const uint64_t ki = double_bits(kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = exp2_table(static_cast<uint32_t>(ki % 32u));
+    uint64_t t = table(static_cast<uint32_t>(ki % 32u));
     t += ki << 47;
     const double s = bits_double(t);
     const double z = __builtin_fma(c0, r, c1);
@@ -111,6 +114,8 @@ LM_HD inline float expf_ref(float x) {
     y = y * s;
     return static_cast<float>(y);
 }
+
+LM_HD inline float expf_ref(float x) { return expf_with(x, exp2_table); }
 
 // silu(g) * u with LiteMind's rounding steps: g / (1 + exp(-g)), then * u (src/Gemm.cpp:225-231).
 LM_HD inline float silu_mul_ref(float g, float u) {
