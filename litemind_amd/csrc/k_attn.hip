@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ 
 // 0..15 of wave 0 run the 16 chains from LDS.  The channels' values (64 B per
 // cached token) and the head's probabilities stream through a ring of
 // kCtxDepth LDS slots of kCtxChunk tokens (16 KB of values) by direct-to-LDS
-// buffer loads that all four waves issue: ~119 KB in flight per workgroup, and
+// buffer loads that four loader waves issue: ~119 KB in flight per workgroup, and
 // the narrow groups put 128 workgroups (so 128 CUs' worth of loads) on a
 // V2-Lite layer, so the stream (~7 us near 4K cached tokens) outruns the
 // chains.  The chains cost ~9 cycles per token: a dependent fused multiply-add
@@ -568,13 +568,15 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr int kCtxCh = 16;        // value channels per workgroup
 constexpr int kCtxChunk = 256;    // cached tokens per slot
 constexpr int kCtxDepth = 8;
-constexpr int kCtxWaves = 4;
-constexpr int kCtxTokPerLoad = 64 * 4 / kCtxCh;                          // tokens per 1 KB value load
-constexpr int kCtxLoads = kCtxChunk / kCtxTokPerLoad / kCtxWaves + kCtxChunk / 64 / kCtxWaves;  // per wave per chunk
-static_assert(kCtxChunk % (kCtxTokPerLoad * kCtxWaves) == 0 && kCtxChunk % (64 * kCtxWaves) == 0, "even shares");
+constexpr int kCtxLoaders = 4;  // waves 1 .. 4 issue the loads, wave 0 only adds
+constexpr int kCtxThreads = (kCtxLoaders + 1) * 64;
+constexpr int kCtxTokPerLoad = 64 * 4 / kCtxCh;  // tokens per 1 KB value load
+constexpr int kCtxLoads = kCtxChunk / kCtxTokPerLoad / kCtxLoaders + kCtxChunk / 64 / kCtxLoaders;  // per loader
+static_assert(kCtxChunk % (kCtxTokPerLoad * kCtxLoaders) == 0 && kCtxChunk % (64 * kCtxLoaders) == 0,
+              "even shares");
 static_assert((kCtxDepth - 1) * kCtxLoads < 64, "vmcnt immediate");
 
-__global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const float* __restrict__ P,
+__global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float* __restrict__ P,
                                                                         const float* __restrict__ value,
                                                                         float* __restrict__ ctx, int32_t vh,
                                                                         int64_t cap, int64_t n, int64_t n_stride) {
@@ -599,12 +601,13 @@ __global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const fl
     const float* vbase = value + static_cast<int64_t>(h) * cap * vh + c0;
     const float* prow = P + static_cast<int64_t>(h) * n_stride;
     const int64_t nchunks = (n + kCtxChunk - 1) / kCtxChunk;
-    // this wave's share of chunk c (clamped to the last chunk, so every step
-    // issues the same count): value load i (i = wave, wave + 4, ...) brings
-    // tokens kCtxTokPerLoad i .. + kCtxTokPerLoad - 1, lane l token
+    // loader wave w = wave - 1's share of chunk c (clamped to the last chunk,
+    // so every step issues the same count): value load i (i = w, w + 4, ...)
+    // brings tokens kCtxTokPerLoad i .. + kCtxTokPerLoad - 1, lane l token
     // kCtxTokPerLoad i + l / 4 and channels 4 (l % 4) .. + 3, to [token][16];
-    // probability load k (k = wave, wave + 4, ...) tokens 64 k .. 64 k + 63;
-    // tokens past n read token n - 1 and are never used
+    // probability load k (k = w, w + 4, ...) tokens 64 k .. 64 k + 63; tokens
+    // past n read token n - 1 and are never used.  Wave 0 issues nothing: the
+    // address arithmetic and the issue of the loads stay off the chains' wave
     // buffer loads rather than global ones: a global load to LDS counts as a
     // pending flat access, for which the compiler waits for every LDS read at
     // each use (lgkmcnt(0)) and so cannot keep the next block's reads in
@@ -614,28 +617,31 @@ __global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const fl
         __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, static_cast<int>((cap * vh - c0) * 4), kBufferWord3);
     const __amdgpu_buffer_rsrc_t pres =
         __builtin_amdgcn_make_buffer_rsrc((void*)prow, 0, static_cast<int>(n * 4), kBufferWord3);
+    const int lw = wave - 1;
     auto issue = [&](int64_t c, float* slot) {
         c = c < nchunks ? c : nchunks - 1;
 #pragma unroll
-        for (int k = 0; k < kCtxChunk / kCtxTokPerLoad / kCtxWaves; ++k) {
-            const int i = k * kCtxWaves + wave;
+        for (int k = 0; k < kCtxChunk / kCtxTokPerLoad / kCtxLoaders; ++k) {
+            const int i = k * kCtxLoaders + lw;
             int64_t tok = c * kCtxChunk + kCtxTokPerLoad * i + (lane >> 2);
             tok = tok < n ? tok : n - 1;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (attn_lds_void*)(slot + i * 256), 16,
                                                      static_cast<unsigned>((tok * vh + 4 * (lane & 3)) * 4), 0, 0, 0);
         }
 #pragma unroll
-        for (int k = 0; k < kCtxChunk / 64 / kCtxWaves; ++k) {
-            const int i = k * kCtxWaves + wave;
+        for (int k = 0; k < kCtxChunk / 64 / kCtxLoaders; ++k) {
+            const int i = k * kCtxLoaders + lw;
             int64_t tok = c * kCtxChunk + 64 * i + lane;
             tok = tok < n ? tok : n - 1;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(pres, (attn_lds_void*)(slot + kCtxChunk * kCtxCh + 64 * i), 4,
                                                      static_cast<unsigned>(tok * 4), 0, 0, 0);
         }
     };
+    if (wave != 0) {
 #pragma unroll
-    for (int d = 0; d < kCtxDepth - 1; ++d) {
-        issue(d, ring[d]);
+        for (int d = 0; d < kCtxDepth - 1; ++d) {
+            issue(d, ring[d]);
+        }
     }
     // chunk c is in once at most the kCtxDepth - 2 chunks issued after it are
     // in flight
@@ -650,11 +656,11 @@ __global__ __launch_bounds__(kCtxWaves * 64) void context_decode_kernel(const fl
         for (int j = 0; j < kCtxDepth; ++j) {
             const int64_t c = cb + j;
             __builtin_amdgcn_s_waitcnt(kWait);
-            // every wave's share of chunk c is in; wave 0 has read the slot
+            // every loader's share of chunk c is in; wave 0 has read the slot
             // refilled next (chunk c - 1) and used all of it
             __builtin_amdgcn_s_barrier();
-            issue(c + kCtxDepth - 1, ring[(j + kCtxDepth - 1) % kCtxDepth]);
             if (wave != 0) {
+                issue(c + kCtxDepth - 1, ring[(j + kCtxDepth - 1) % kCtxDepth]);
                 continue;
             }
             const float* vs = ring[j];
@@ -795,7 +801,7 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
     const unsigned threads = static_cast<unsigned>((a.vh + 63) / 64 * 64);
     if (T == 1 && a.vh % kCtxCh == 0 && a.cap * a.vh < (int64_t{1} << 29)) {  // 32-bit buffer offsets
         hipLaunchKernelGGL(context_decode_kernel, dim3(static_cast<unsigned>(a.heads * (a.vh / kCtxCh))),
-                           dim3(kCtxWaves * 64), 0, s,
+                           dim3(kCtxThreads), 0, s,
                            S, c.value, ctx, a.vh, a.cap, n0 + 1, n_stride);
     } else if (T == 1) {
         hipLaunchKernelGGL(context_kernel<1>, dim3(a.heads, 1), dim3(threads), 0, s, S, c.value, ctx, a.heads, a.vh,
