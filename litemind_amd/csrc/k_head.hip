@@ -177,90 +177,173 @@ __global__ __launch_bounds__(THREADS) void head_logits_kernel(const uint16_t* __
     }
 }
 
-// The same dot products for many tokens (the projections of a batched
-// attention call): one lane per token, 64 tokens per wave, RW weight rows per
-// wave.  A lane keeps all 32 chains of each (token, row) pair and reduces them
-// as above, so the results are bit for bit head_logits_kernel's.  The rows are
-// the same for every lane, so they come through the scalar cache (one 64-byte
-// load per row and 32-element block, widened on the scalar unit, used as the
-// FMAs' scalar operand), and each lane reads its own token's values with
-// 16-byte loads; the next block of both is requested before the current one's
-// FMAs (blocks in pairs, no register copies).  in_dim % 64 == 0.
-constexpr int kManyRows = 2;  // rows per wave
+// Weight rows read through the scalar cache (uniform across the lanes).
 typedef const __attribute__((address_space(4))) uint32_t const_u32;
 
-template <int RW>
-__global__ __launch_bounds__(256) void matvec_many_kernel(const uint16_t* __restrict__ w, const float* __restrict__ x,
-                                                          float* out, int64_t rows, int32_t in_dim, int64_t tokens,
-                                                          float scale, int32_t accumulate) {
+// The same dot products for many tokens, with each token's inputs read from
+// memory once per workgroup rather than once per wave: 64 tokens (one per
+// lane) and four waves of kTokRows rows.  The tokens' inputs pass through LDS in
+// tiles of 64 elements, a kTokStages-slot ring filled by direct-to-LDS buffer
+// loads (each wave a quarter of each tile) and read by all four waves; the rows
+// come through the scalar cache, 16 elements per step.  The steps are
+// pipelined on one wait: at the start of a step everything requested so far is
+// in (lgkmcnt(0)), then the next step's LDS reads and scalar loads are issued,
+// then this step's FMAs run while they land (a scalar load can complete out of
+// order, so no finer wait on the shared counter would be exact).  Every
+// (token, row) pair keeps its 32 chains in one lane and reduces them as
+// head_logits_kernel does, bit for bit.  in_dim % 64 == 0.
+constexpr int kTokRows = 3;    // rows per wave
+constexpr int kTokTile = 64;   // input elements per LDS slot
+constexpr int kTokStages = 4;
+constexpr int kTokStep = 16;   // elements per weight step
+typedef __attribute__((address_space(3))) void head_lds_void;
+constexpr int kHeadBufferWord3 = 0x00020000;  // buffer descriptor word 3, raw 32-bit access
+// s_waitcnt immediates (vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kWaitLgkm0 = 0xC07F;             // lgkmcnt(0), the others unconstrained
+constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0F00; }
+
+__global__ __launch_bounds__(256) void matvec_tokens_kernel(const uint16_t* __restrict__ w,
+                                                            const float* __restrict__ x, float* out, int64_t rows,
+                                                            int32_t in_dim, int64_t tokens, float scale,
+                                                            int32_t accumulate) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    // slot: 64 tokens x 16 units of 4 elements; unit q of token t at position
+    // t * 16 + (q ^ (t % 16)), so the 16 lanes of each quarter-wave read 16
+    // distinct bank groups.  One array per slot, so the compiler's waits
+    // tell the slots apart.
+    __shared__ __align__(16) float s0[64 * kTokTile], s1[64 * kTokTile], s2[64 * kTokTile], s3[64 * kTokTile];
+    float* const ring[kTokStages] = {s0, s1, s2, s3};
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + lane;
-    const bool live_t = t < tokens;
-    const float4* xr = reinterpret_cast<const float4*>(x + (live_t ? t : tokens - 1) * in_dim);
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * RW;
-    const_u32* wr[RW];
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int64_t ntok = std::min<int64_t>(64, tokens - t0);
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * kTokRows;
+    const_u32* wr[kTokRows];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int r = 0; r < kTokRows; ++r) {
         const int64_t row = row0 + r < rows ? row0 + r : rows - 1;  // rows past the end load the last, store nothing
         wr[r] = (const_u32*)(w + row * in_dim);
     }
-    float acc[RW][32];
+    const int ntiles = in_dim / kTokTile;
+    // this wave's four loads of a tile: load j covers positions (4 wave + j) 64
+    // + lane, i.e. token u / 16 and unit (u % 16) ^ (token % 16); tokens past
+    // the last read the last
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(x + t0 * in_dim), 0, static_cast<int>(ntok * in_dim * 4), kHeadBufferWord3);
+    unsigned src[4];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int j = 0; j < 4; ++j) {
+        const int u = (4 * wave + j) * 64 + lane;
+        const int tt = u >> 4;
+        const int q = (u & 15) ^ (tt & 15);
+        const int ttc = tt < ntok ? tt : static_cast<int>(ntok) - 1;
+        src[j] = static_cast<unsigned>((ttc * in_dim + 4 * q) * 4);
+    }
+    auto issue = [&](int tile, float* slot) {
+        tile = tile < ntiles ? tile : ntiles - 1;  // past the end: reload the last tile (every step issues alike)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (head_lds_void*)(slot + (4 * wave + j) * 256), 16,
+                                                     src[j] + static_cast<unsigned>(tile * kTokTile * 4), 0, 0, 0);
+        }
+    };
+    float acc[kTokRows][32];
+#pragma unroll
+    for (int r = 0; r < kTokRows; ++r) {
 #pragma unroll
         for (int c = 0; c < 32; ++c) {
             acc[r][c] = 0.0f;
         }
     }
-    float4 xa[8], xb[8];
-    uint32_t wa[RW][16], wb[RW][16];
-    auto load = [&](int e0, float4 (&xv)[8], uint32_t (&wv)[RW][16]) {
+    f4v xa[4], xb[4];
+    uint32_t wa[kTokRows][8], wb[kTokRows][8];
+    const int sw = lane & 15;
+    // step `st` (0..3) of `tile` from `slot`: the lane's token's 16 inputs and
+    // each row's 16 weights (8 bf16 pairs)
+    auto read = [&](const float* slot, int tile, int st, f4v (&xv)[4], uint32_t (&wv)[kTokRows][8]) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            xv[k] = xr[e0 / 4 + k];
+        for (int i = 0; i < 4; ++i) {
+            xv[i] = *reinterpret_cast<const f4v*>(slot + (lane * 16 + ((4 * st + i) ^ sw)) * 4);
         }
+        const int e = (tile < ntiles ? tile : ntiles - 1) * kTokTile + st * kTokStep;
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
+        for (int r = 0; r < kTokRows; ++r) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                wv[r][k] = wr[r][e0 / 2 + k];
+            for (int k = 0; k < 8; ++k) {
+                wv[r][k] = wr[r][e / 2 + k];
             }
         }
     };
-    // elements e0 .. e0 + 31: element e0 + c on chain c
-    auto fma_block = [&](const float4 (&xv)[8], const uint32_t (&wv)[RW][16]) {
+    // elements e .. e + 15 of a step with parity `half` (e % 32 == 16 half):
+    // element e + m on chain 16 half + m
+    auto fma_step = [&](int half, const f4v (&xv)[4], const uint32_t (&wv)[kTokRows][8]) {
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
+        for (int r = 0; r < kTokRows; ++r) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float xs[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const uint32_t pair = wv[r][2 * k + j];
-                    acc[r][4 * k + 2 * j] = __builtin_fmaf(bits_float(pair << 16), xs[2 * j], acc[r][4 * k + 2 * j]);
-                    acc[r][4 * k + 2 * j + 1] =
-                        __builtin_fmaf(bits_float(pair & 0xffff0000u), xs[2 * j + 1], acc[r][4 * k + 2 * j + 1]);
+                    const uint32_t pair = wv[r][2 * i + j];
+                    const int c = 16 * half + 4 * i + 2 * j;
+                    acc[r][c] = __builtin_fmaf(bits_float(pair << 16), xv[i][2 * j], acc[r][c]);
+                    acc[r][c + 1] = __builtin_fmaf(bits_float(pair & 0xffff0000u), xv[i][2 * j + 1], acc[r][c + 1]);
                 }
             }
         }
     };
-    // the scheduling barriers keep each group of loads ahead of the FMAs that
-    // precede their use (the compiler would otherwise move every load next to
-    // its first use and wait for it there)
-    load(0, xa, wa);
-    for (int e0 = 0; e0 < in_dim; e0 += 64) {
+    auto wait_all_lgkm = [] {
         __builtin_amdgcn_sched_barrier(0);
-        load(e0 + 32, xb, wb);
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         __builtin_amdgcn_sched_barrier(0);
-        fma_block(xa, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        load(e0 + 64 < in_dim ? e0 + 64 : e0, xa, wa);  // the last pair reloads a block it does not use
-        __builtin_amdgcn_sched_barrier(0);
-        fma_block(xb, wb);
-    }
+    };
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int d = 0; d < kTokStages - 1; ++d) {
+        issue(d, ring[d]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm(4 * (kTokStages - 2)));  // tile 0 is in
+    __builtin_amdgcn_s_barrier();
+    read(ring[0], 0, 0, xa, wa);
+    for (int tb = 0; tb < ntiles; tb += kTokStages) {
+#pragma unroll
+        for (int j = 0; j < kTokStages; ++j) {
+            const int tile = tb + j;  // tiles past the end load alike and add nothing
+            const float* slot = ring[j];
+            const bool live = tile < ntiles;
+            wait_all_lgkm();
+            read(slot, tile, 1, xb, wb);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) {
+                fma_step(0, xa, wa);
+            }
+            wait_all_lgkm();
+            read(slot, tile, 2, xa, wa);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) {
+                fma_step(1, xb, wb);
+            }
+            wait_all_lgkm();
+            read(slot, tile, 3, xb, wb);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) {
+                fma_step(0, xa, wa);
+            }
+            wait_all_lgkm();
+            // tile + 1 is in (the one issued after it may still be in flight),
+            // and every wave has read all of tile - 1: its slot takes tile + 3
+            __builtin_amdgcn_s_waitcnt(kWaitVm(4 * (kTokStages - 3)));
+            __builtin_amdgcn_s_barrier();
+            issue(tile + kTokStages - 1, ring[(j + kTokStages - 1) % kTokStages]);
+            read(ring[(j + 1) % kTokStages], tile + 1, 0, xa, wa);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) {
+                fma_step(1, xb, wb);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every load to LDS has landed before the workgroup ends
+    const int64_t t = t0 + lane;
+#pragma unroll
+    for (int r = 0; r < kTokRows; ++r) {
         // (a[l] + a[8 + l]) + (a[16 + l] + a[24 + l]), lanes j and j + 4, (h0 + h2) + (h1 + h3)
         float ls[8];
 #pragma unroll
@@ -272,7 +355,7 @@ __global__ __launch_bounds__(256) void matvec_many_kernel(const uint16_t* __rest
         const float h2 = ls[2] + ls[6];
         const float h3 = ls[3] + ls[7];
         const float total = (h0 + h2) + (h1 + h3);
-        if (live_t && row0 + r < rows) {
+        if (t < tokens && row0 + r < rows) {
             float* o = out + t * rows + row0 + r;
             *o = accumulate ? __builtin_fmaf(scale, total, *o) : total;
         }
@@ -417,8 +500,8 @@ hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, i
     }
     if (tokens > kHeadTokens && in_dim % 64 == 0) {
         const dim3 grid(static_cast<unsigned>((tokens + 63) / 64),
-                        static_cast<unsigned>((rows + 4 * kManyRows - 1) / (4 * kManyRows)));
-        hipLaunchKernelGGL(matvec_many_kernel<kManyRows>, grid, dim3(256), 0, s, w, x, out, rows,
+                        static_cast<unsigned>((rows + 4 * kTokRows - 1) / (4 * kTokRows)));
+        hipLaunchKernelGGL(matvec_tokens_kernel, grid, dim3(256), 0, s, w, x, out, rows,
                            static_cast<int32_t>(in_dim), tokens, scale, accumulate);
         return hipGetLastError();
     }
