@@ -38,7 +38,7 @@ namespace {
 
 constexpr int kKeyTile = 256;   // keys per score block (one per lane)
 constexpr int kQueries = 8;     // tokens per score / context block when T > 1
-constexpr int kChunk = 256;     // probabilities staged in LDS per context step
+constexpr int kChunk = 1024;    // probabilities staged in LDS per context step (T > 1)
 
 // RotaryEmbedding::apply on one channel pair: the first output is
 // even*cos - odd*sin and the second odd*cos + even*sin, each contracted to one
@@ -229,31 +229,42 @@ __global__ __launch_bounds__(kKeyTile) void scores_kernel(const float* __restric
     }
 }
 
-// scores_kernel's sums for one query token (decode, T = 1) when qk_nope and
-// qk_rope are multiples of 16 (no fused tail, and whole groups): one key per
-// lane, the key's channels taken in groups of 16 (the nope groups, then the
-// rope groups) with the loads of the next two groups in flight while a group is
-// added, so a lane waits for memory once per group of 16 rather than once per
-// loop step.  The head's query row is staged in LDS and read four channels at a
-// time.  Each chain keeps scores_kernel's order: products rounded, added from
-// channel 0 up.
+// scores_kernel's sums when qk_nope and qk_rope are multiples of 16 (no fused
+// tail, and whole groups): one key per lane and KQ query tokens per block, the
+// key's channels taken in groups of 16 (the nope groups, then the rope groups)
+// with the loads of the next two groups in flight while a group is added, so a
+// lane waits for memory once per group of 16 rather than once per loop step.
+// The query rows are staged in LDS and read four channels at a time.  Each
+// chain keeps scores_kernel's order: products rounded, added from channel 0
+// up.  grid: x = key tiles, y = heads, z = token blocks of KQ.
 constexpr int kScoreGroup = 16;
 
-__global__ __launch_bounds__(kKeyTile) void scores_decode_kernel(const float* __restrict__ q,
-                                                                 const float* __restrict__ key_nope,
-                                                                 const float* __restrict__ key_rope,
-                                                                 float* __restrict__ S, int32_t nope, int32_t rope,
-                                                                 int64_t cap, int64_t n, float scale) {
+template <int KQ>
+__global__ __launch_bounds__(kKeyTile) void scores_grouped_kernel(const float* __restrict__ q,
+                                                                  const float* __restrict__ key_nope,
+                                                                  const float* __restrict__ key_rope,
+                                                                  float* __restrict__ S, int32_t heads, int32_t nope,
+                                                                  int32_t rope, int64_t cap, int64_t n0, int64_t T,
+                                                                  int64_t n_stride, float scale) {
     typedef float f4v __attribute__((ext_vector_type(4)));
-    extern __shared__ __align__(16) float qs[];  // [nope + rope]
+    extern __shared__ __align__(16) float qs[];  // [KQ][nope + rope]
     const int qk = nope + rope;
     const int h = blockIdx.y;
-    for (int j = threadIdx.x; j < qk; j += kKeyTile) {
-        qs[j] = q[static_cast<int64_t>(h) * qk + j];
+    const int64_t i0 = static_cast<int64_t>(blockIdx.z) * KQ;
+    const int nq = static_cast<int>(std::min<int64_t>(KQ, T - i0));
+    const int64_t n_hi = n0 + i0 + nq;  // keys the block's last token sees
+    const int64_t key0 = static_cast<int64_t>(blockIdx.x) * kKeyTile;
+    if (key0 >= n_hi) {
+        return;  // uniform over the block
+    }
+    for (int j = threadIdx.x; j < KQ * qk; j += kKeyTile) {
+        const int iq = j / qk;
+        const int d = j - iq * qk;
+        qs[j] = iq < nq ? q[((i0 + iq) * heads + h) * qk + d] : 0.0f;
     }
     __syncthreads();
-    const int64_t key = static_cast<int64_t>(blockIdx.x) * kKeyTile + threadIdx.x;
-    const int64_t kc = key < n ? key : n - 1;  // lanes past the last key read a valid one
+    const int64_t key = key0 + threadIdx.x;
+    const int64_t kc = key < n_hi ? key : n_hi - 1;  // lanes past the last key read a valid one
     const float* kn = key_nope + static_cast<int64_t>(h) * nope * cap + kc;
     const float* kr = key_rope + kc;
     const int gn = nope / kScoreGroup;
@@ -269,25 +280,34 @@ __global__ __launch_bounds__(kKeyTile) void scores_decode_kernel(const float* __
             x[i] = base[static_cast<int64_t>(i) * cap];
         }
     };
-    float a = 0.0f, b = 0.0f;
+    float a[KQ], b[KQ];
+#pragma unroll
+    for (int iq = 0; iq < KQ; ++iq) {
+        a[iq] = 0.0f;
+        b[iq] = 0.0f;
+    }
     auto add = [&](int g, const float (&x)[kScoreGroup]) {
         if (g >= groups) {
             return;
         }
-        const f4v* q4 = reinterpret_cast<const f4v*>(qs + g * kScoreGroup);
-        float acc = g < gn ? a : b;
+        const bool nope_part = g < gn;
 #pragma unroll
-        for (int i = 0; i < kScoreGroup / 4; ++i) {
-            const f4v w = q4[i];
-            acc = acc + w.x * x[4 * i + 0];
-            acc = acc + w.y * x[4 * i + 1];
-            acc = acc + w.z * x[4 * i + 2];
-            acc = acc + w.w * x[4 * i + 3];
-        }
-        if (g < gn) {
-            a = acc;
-        } else {
-            b = acc;
+        for (int iq = 0; iq < KQ; ++iq) {
+            const f4v* q4 = reinterpret_cast<const f4v*>(qs + iq * qk + g * kScoreGroup);
+            float acc = nope_part ? a[iq] : b[iq];
+#pragma unroll
+            for (int i = 0; i < kScoreGroup / 4; ++i) {
+                const f4v w = q4[i];
+                acc = acc + w.x * x[4 * i + 0];
+                acc = acc + w.y * x[4 * i + 1];
+                acc = acc + w.z * x[4 * i + 2];
+                acc = acc + w.w * x[4 * i + 3];
+            }
+            if (nope_part) {
+                a[iq] = acc;
+            } else {
+                b[iq] = acc;
+            }
         }
     };
     float x0[kScoreGroup], x1[kScoreGroup], x2[kScoreGroup];
@@ -301,8 +321,11 @@ __global__ __launch_bounds__(kKeyTile) void scores_decode_kernel(const float* __
         load(g + 4, x1);
         add(g + 2, x2);
     }
-    if (key < n) {
-        S[static_cast<int64_t>(h) * n + key] = scale * (a + b);
+#pragma unroll
+    for (int iq = 0; iq < KQ; ++iq) {
+        if (iq < nq && key <= n0 + i0 + iq) {
+            S[((i0 + iq) * heads + h) * n_stride + key] = scale * (a[iq] + b[iq]);
+        }
     }
 }
 
@@ -481,17 +504,23 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
 // ctx[t, h, v] = sum over cached tokens j <= n0 + t, in order, of
 // fma(P[t, h, j], value[h, j, v], .) from 0 (gemm::axpy per token,
 // src/Attention.cpp:94-97).  One lane per value channel, KQ tokens per block
-// sharing each value load; probabilities staged in LDS in chunks.
+// sharing each value load; probabilities staged in LDS in chunks of kChunk
+// keys and read four at a time.  The keys go in groups of 16 with the loads of
+// the next two groups in flight while a group is added; only groups that reach
+// the block's first token's own position test which tokens see each key.
 // grid: x = heads, y = token blocks of KQ; block = v_head rounded up to 64.
 template <int KQ>
 __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ P, const float* __restrict__ value,
                                                       float* __restrict__ ctx, int32_t heads, int32_t vh, int64_t cap,
                                                       int64_t n0, int64_t T, int64_t n_stride) {
-    __shared__ float ps[KQ][kChunk];
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    constexpr int kG = 16;  // keys per group
+    __shared__ __align__(16) float ps[KQ][kChunk];
     const int h = blockIdx.x;
     const int64_t i0 = static_cast<int64_t>(blockIdx.y) * KQ;
     const int nq = static_cast<int>(std::min<int64_t>(KQ, T - i0));
-    const int64_t n_hi = n0 + i0 + nq;
+    const int64_t n_hi = n0 + i0 + nq;  // keys the block's last token sees
+    const int64_t n_all = n0 + i0;      // keys every token of the block sees
     const int v = threadIdx.x;
     const bool live = v < vh;
     const float* vp = value + static_cast<int64_t>(h) * cap * vh + (live ? v : 0);
@@ -510,33 +539,59 @@ __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ 
         }
         __syncthreads();
         const int cend = static_cast<int>(std::min<int64_t>(kChunk, n_hi - c0));
-        int j = 0;
-        for (; j + 8 <= cend; j += 8) {
-            float val[8];
+        const int ng = (cend + kG - 1) / kG;
+        // group g's 16 values; groups past the last reload it and keys past
+        // the last read the last (every step issues the same loads)
+        auto load = [&](int g, float (&x)[kG]) {
+            g = g < ng ? g : ng - 1;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                val[u] = vp[(c0 + j + u) * vh];
+            for (int i = 0; i < kG; ++i) {
+                int64_t key = c0 + kG * g + i;
+                key = key < n_hi ? key : n_hi - 1;
+                x[i] = vp[key * vh];
             }
+        };
+        auto add = [&](int g, const float (&x)[kG]) {
+            if (g >= ng) {
+                return;
+            }
+            const int64_t kfirst = c0 + kG * g;
+            if (kfirst + kG <= n_all) {
+                // every token of the block sees all 16 keys
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int64_t rel = c0 + j + u - n0 - i0;  // token iq sees this key when rel <= iq
+                for (int u = 0; u < kG / 4; ++u) {
 #pragma unroll
-                for (int iq = 0; iq < KQ; ++iq) {
-                    if (rel <= iq) {
-                        acc[iq] = __builtin_fmaf(ps[iq][j + u], val[u], acc[iq]);
+                    for (int iq = 0; iq < KQ; ++iq) {
+                        const f4v p = *reinterpret_cast<const f4v*>(&ps[iq][kG * g + 4 * u]);
+                        acc[iq] = __builtin_fmaf(p.x, x[4 * u + 0], acc[iq]);
+                        acc[iq] = __builtin_fmaf(p.y, x[4 * u + 1], acc[iq]);
+                        acc[iq] = __builtin_fmaf(p.z, x[4 * u + 2], acc[iq]);
+                        acc[iq] = __builtin_fmaf(p.w, x[4 * u + 3], acc[iq]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kG; ++i) {
+                    const int64_t rel = kfirst + i - n_all;  // token iq sees this key when rel <= iq
+#pragma unroll
+                    for (int iq = 0; iq < KQ; ++iq) {
+                        if (rel <= iq) {
+                            acc[iq] = __builtin_fmaf(ps[iq][kG * g + i], x[i], acc[iq]);
+                        }
                     }
                 }
             }
-        }
-        for (; j < cend; ++j) {
-            const float val = vp[(c0 + j) * vh];
-            const int64_t rel = c0 + j - n0 - i0;
-#pragma unroll
-            for (int iq = 0; iq < KQ; ++iq) {
-                if (rel <= iq) {
-                    acc[iq] = __builtin_fmaf(ps[iq][j], val, acc[iq]);
-                }
-            }
+        };
+        float x0[kG], x1[kG], x2[kG];
+        load(0, x0);
+        load(1, x1);
+        for (int g = 0; g < ng; g += 3) {
+            load(g + 2, x2);
+            add(g, x0);
+            load(g + 3, x0);
+            add(g + 1, x1);
+            load(g + 4, x1);
+            add(g + 2, x2);
         }
     }
     if (live) {
@@ -771,9 +826,14 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
     const int64_t n_stride = n0 + T;
     const int qk = a.nope + a.rope;
     const unsigned tiles = blocks_of(n_stride, kKeyTile);
-    if (T == 1 && a.nope % kScoreGroup == 0 && a.rope % kScoreGroup == 0 && qk > 0) {
-        hipLaunchKernelGGL(scores_decode_kernel, dim3(tiles, a.heads), dim3(kKeyTile), sizeof(float) * qk, s, q,
-                           c.key_nope, c.key_rope, S, a.nope, a.rope, a.cap, n_stride, scale);
+    const bool grouped = a.nope % kScoreGroup == 0 && a.rope % kScoreGroup == 0 && qk > 0;
+    if (T == 1 && grouped) {
+        hipLaunchKernelGGL(scores_grouped_kernel<1>, dim3(tiles, a.heads, 1), dim3(kKeyTile), sizeof(float) * qk, s,
+                           q, c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope, a.cap, n0, T, n_stride, scale);
+    } else if (grouped) {
+        hipLaunchKernelGGL(scores_grouped_kernel<kQueries>, dim3(tiles, a.heads, blocks_of(T, kQueries)),
+                           dim3(kKeyTile), sizeof(float) * kQueries * qk, s, q, c.key_nope, c.key_rope, S, a.heads,
+                           a.nope, a.rope, a.cap, n0, T, n_stride, scale);
     } else if (T == 1) {
         hipLaunchKernelGGL(scores_kernel<1>, dim3(tiles, a.heads, 1), dim3(kKeyTile), sizeof(float) * qk, s, q,
                            c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope, a.cap, n0, T, n_stride, scale);
