@@ -161,6 +161,125 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
     }
 }
 
+// One token (decode): the query projection's rows as matvec_one_kernel forms
+// them (two rows per wave, 32 lanes each), then rope_query_kernel's step on
+// them before they are stored: rows 2k and 2k + 1 of a wave are a rotary pair
+// when nope is even, so each half takes the other's total by one shuffle and
+// stores its own output (the even one at nope + i, the odd one at nope + half
+// + i).  Positions at or past the table store the rows as they are.
+__global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ x, float* __restrict__ q,
+                                                             int64_t rows, int32_t in_dim, int32_t nope,
+                                                             int32_t rope, const float* __restrict__ cos_t,
+                                                             const float* __restrict__ sin_t, int64_t pos,
+                                                             int64_t max_positions) {
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 31;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+    const bool live = row < rows;
+    const uint16_t* wr = w + (live ? row : rows - 1) * in_dim;
+    const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
+    const float other = __shfl_xor(total, 32);  // the pair partner's total
+    if (!live || c != 0) {
+        return;
+    }
+    const int qk = nope + rope;
+    const int64_t head = row / qk;
+    const int d = static_cast<int>(row - head * qk);
+    if (d < nope || pos >= max_positions) {
+        q[row] = total;
+        return;
+    }
+    const int half = rope / 2;
+    const int i = (d - nope) >> 1;
+    const bool even = ((d - nope) & 1) == 0;
+    float lo, hi;
+    rotate_pair(even ? total : other, even ? other : total, cos_t[pos * half + i], sin_t[pos * half + i], lo, hi);
+    float* v = q + head * qk + nope;
+    if (even) {
+        v[i] = lo;
+    } else {
+        v[i + half] = hi;
+    }
+}
+
+// One token: kv_prep_kernel, kv_b's projection of the normalised latent and
+// kv_append_kernel in one launch.  Every workgroup forms the latent's inverse
+// RMS with kv_prep_kernel's thread-strided double sum (the same value in each),
+// reads the normalised inputs as (latent * inverse) * weight on the fly, and
+// stores its rows straight into the cache; workgroup 0 also stores the rotary
+// key.
+__global__ __launch_bounds__(256) void kv_one_kernel(const uint16_t* __restrict__ w, const float* __restrict__ lat,
+                                                     const float* __restrict__ norm_w, float* __restrict__ key_nope,
+                                                     float* __restrict__ value, float* __restrict__ key_rope,
+                                                     int32_t heads, int32_t nope, int32_t vh, int32_t rank,
+                                                     int32_t rope, int64_t cap, int64_t slot,
+                                                     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                     int64_t pos, int64_t max_positions, float eps) {
+    __shared__ double part[4];
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 31;
+    const int width = nope + vh;
+    const int64_t rows = static_cast<int64_t>(heads) * width;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+    const bool live = row < rows;
+    const uint16_t* wr = w + (live ? row : rows - 1) * rank;
+    // the lane's first weights, requested before the norm's reduction so they
+    // arrive while it runs
+    uint16_t pre[kOneAhead];
+    const bool use_pre = rank / 32 >= kOneAhead;
+    if (use_pre) {
+#pragma unroll
+        for (int u = 0; u < kOneAhead; ++u) {
+            pre[u] = wr[32 * u + c];
+        }
+    }
+    double sq = 0.0;
+    for (int e = threadIdx.x; e < rank; e += 256) {
+        const double v = static_cast<double>(lat[e]);
+        sq = sq + v * v;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        sq += __shfl_xor(sq, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = sq;
+    }
+    __syncthreads();
+    const double total_sq = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inverse =
+        static_cast<float>(1.0 / __builtin_sqrt(total_sq / static_cast<double>(rank) + static_cast<double>(eps)));
+    if (blockIdx.x == 0) {
+        const int half = rope / 2;
+        const float* tail = lat + rank;
+        for (int i = threadIdx.x; i < half; i += 256) {
+            const float e = tail[2 * i];
+            const float o = tail[2 * i + 1];
+            if (pos < max_positions) {
+                float lo, hi;
+                rotate_pair(e, o, cos_t[pos * half + i], sin_t[pos * half + i], lo, hi);
+                key_rope[static_cast<int64_t>(i) * cap + slot] = lo;
+                key_rope[static_cast<int64_t>(i + half) * cap + slot] = hi;
+            } else {
+                key_rope[static_cast<int64_t>(2 * i) * cap + slot] = e;
+                key_rope[static_cast<int64_t>(2 * i + 1) * cap + slot] = o;
+            }
+        }
+    }
+    const float total = dot_bf16_lanes32(wr, [&](int e) { return (lat[e] * inverse) * norm_w[e]; }, rank, c,
+                                         use_pre ? pre : nullptr);
+    if (!live || c != 0) {
+        return;
+    }
+    const int h = static_cast<int>(row / width);
+    const int j = static_cast<int>(row - static_cast<int64_t>(h) * width);
+    if (j < nope) {
+        key_nope[(static_cast<int64_t>(h) * nope + j) * cap + slot] = total;
+    } else {
+        value[(static_cast<int64_t>(h) * cap + slot) * vh + (j - nope)] = total;
+    }
+}
+
 // gemm::dot's association for one term of a chain: the first count - count % 4
 // products are rounded and added in order, the rest fused.
 __device__ inline float dot_step(float acc, float a, float b, bool fused) {
@@ -815,6 +934,37 @@ hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float
     }
     hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_of(total, 256)), dim3(256), 0, s, kvx, c.key_nope, c.value,
                        a.heads, a.nope, a.vh, a.cap, slot0, total);
+    return hipGetLastError();
+}
+
+bool query_rope_one_supported(const AttnShape& a, int64_t in_dim) {
+    return a.nope % 2 == 0 && matvec_rows_supported(static_cast<int64_t>(a.heads) * (a.nope + a.rope), in_dim);
+}
+
+hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
+                                 int64_t pos, hipStream_t s) {
+    if (!query_rope_one_supported(a, in_dim)) {
+        return hipErrorInvalidValue;
+    }
+    const int64_t rows = static_cast<int64_t>(a.heads) * (a.nope + a.rope);
+    hipLaunchKernelGGL(query_rope_one_kernel, dim3(blocks_of(rows, 8)), dim3(256), 0, s, w, x, q, rows,
+                       static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions);
+    return hipGetLastError();
+}
+
+bool kv_one_supported(const AttnShape& a) {
+    return matvec_rows_supported(static_cast<int64_t>(a.heads) * (a.nope + a.vh), a.rank);
+}
+
+hipError_t launch_kv_one(const AttnShape& a, const KvCacheDev& c, const uint16_t* kv_b, const float* lat,
+                         const float* norm_w, float eps, int64_t slot, int64_t pos, hipStream_t s) {
+    if (!kv_one_supported(a)) {
+        return hipErrorInvalidValue;
+    }
+    const int64_t rows = static_cast<int64_t>(a.heads) * (a.nope + a.vh);
+    hipLaunchKernelGGL(kv_one_kernel, dim3(blocks_of(rows, 8)), dim3(256), 0, s, kv_b, lat, norm_w, c.key_nope,
+                       c.value, c.key_rope, a.heads, a.nope, a.vh, a.rank, a.rope, a.cap, slot, a.cos_t, a.sin_t,
+                       pos, a.max_positions, eps);
     return hipGetLastError();
 }
 

@@ -363,14 +363,8 @@ __global__ __launch_bounds__(256) void matvec_tokens_kernel(const uint16_t* __re
 }
 
 // The same dot product for one token (the projections of a decode step): 32
-// lanes per row, lane c running chain c (elements c, c + 32, ... in order, then
-// chains 0..7 over the 8-wide remainder), two rows per wave, so even a
-// 576-row projection spreads over 72 workgroups; the lanes' chains then reduce
-// by shuffles in the association above: (a[l] + a[8 + l]) + (a[16 + l] +
-// a[24 + l]), lanes j and j + 4, (h0 + h2) + (h1 + h3).  Each lane requests
-// kOneAhead elements of its chain before it adds the first.
-constexpr int kOneAhead = 16;
-
+// lanes per row (dot_bf16_lanes32), two rows per wave, so even a 576-row
+// projection spreads over 72 workgroups.
 __global__ __launch_bounds__(256) void matvec_one_kernel(const uint16_t* __restrict__ w, const float* __restrict__ x,
                                                          float* out, int64_t rows, int32_t in_dim, float scale,
                                                          int32_t accumulate) {
@@ -379,35 +373,7 @@ __global__ __launch_bounds__(256) void matvec_one_kernel(const uint16_t* __restr
     const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
     const bool live = row < rows;
     const uint16_t* wr = w + (live ? row : rows - 1) * in_dim;
-    const int steps = in_dim / 32;
-    float acc = 0.0f;
-    int k = 0;
-    for (; k + kOneAhead <= steps; k += kOneAhead) {
-        uint16_t wv[kOneAhead];
-        float xv[kOneAhead];
-#pragma unroll
-        for (int u = 0; u < kOneAhead; ++u) {
-            wv[u] = wr[32 * (k + u) + c];
-            xv[u] = x[32 * (k + u) + c];
-        }
-#pragma unroll
-        for (int u = 0; u < kOneAhead; ++u) {
-            acc = __builtin_fmaf(widen_bf16(wv[u]), xv[u], acc);
-        }
-    }
-    for (; k < steps; ++k) {
-        acc = __builtin_fmaf(widen_bf16(wr[32 * k + c]), x[32 * k + c], acc);
-    }
-    if (c < 8) {
-        for (int e = steps * 32 + c; e < in_dim; e += 8) {
-            acc = __builtin_fmaf(widen_bf16(wr[e]), x[e], acc);
-        }
-    }
-    const float t1 = acc + __shfl_xor(acc, 8);
-    const float t2 = t1 + __shfl_xor(t1, 16);
-    const float t3 = t2 + __shfl_xor(t2, 4);
-    const float t4 = t3 + __shfl_xor(t3, 2);
-    const float total = t4 + __shfl_xor(t4, 1);
+    const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
     if (live && c == 0) {
         out[row] = accumulate ? __builtin_fmaf(scale, total, out[row]) : total;
     }

@@ -248,21 +248,34 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     float* S = kvx + kvx_f;
     float* ctxv = S + s_f;
 
-    // queries (src/Attention.cpp:33-48)
-    if (ql == 0) {
-        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_proj, x, q, heads * qk, H, F, 1.0f, 0, stream));
-    } else {
+    // queries (src/Attention.cpp:33-48); for one token the rotary step rides
+    // on the projection's launch
+    const int64_t q_in = ql == 0 ? H : ql;
+    const bool q_fused = F == 1 && lm::query_rope_one_supported(a, q_in);
+    const float* q_x = x;
+    if (ql != 0) {
         LM_ATT_HIP(lm::launch_matvec_tokens(L.q_a, x, qlat, ql, H, F, 1.0f, 0, stream));
         LM_ATT_HIP(lm::launch_rms_norm(qlat, L.q_a_norm, qlat, F, static_cast<int32_t>(ql), c.rms_norm_eps, stream));
-        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_b, qlat, q, heads * qk, ql, F, 1.0f, 0, stream));
+        q_x = qlat;
     }
-    LM_ATT_HIP(lm::launch_rope_query(a, q, F, pos0, stream));
-    // compressed keys and values, appended at slots n0 .. n0 + F - 1 (:50-75)
+    const uint16_t* q_w = ql == 0 ? L.q_proj : L.q_b;
+    if (q_fused) {
+        LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream));
+    } else {
+        LM_ATT_HIP(lm::launch_matvec_tokens(q_w, q_x, q, heads * qk, q_in, F, 1.0f, 0, stream));
+        LM_ATT_HIP(lm::launch_rope_query(a, q, F, pos0, stream));
+    }
+    // compressed keys and values, appended at slots n0 .. n0 + F - 1 (:50-75);
+    // for one token the norm, kv_b and the append are one launch
     LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_a, x, lat, rank + rope, H, F, 1.0f, 0, stream));
-    LM_ATT_HIP(lm::launch_kv_prep(a, L.cache, lat, L.kv_a_norm, kvn, F, n0, pos0, c.rms_norm_eps, stream));
-    LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_b, kvn, kvx, heads * (c.qk_nope_head_dim + vh), rank, F, 1.0f, 0,
-                                        stream));
-    LM_ATT_HIP(lm::launch_kv_append(a, L.cache, kvx, F, n0, stream));
+    if (F == 1 && lm::kv_one_supported(a)) {
+        LM_ATT_HIP(lm::launch_kv_one(a, L.cache, L.kv_b, lat, L.kv_a_norm, c.rms_norm_eps, n0, pos0, stream));
+    } else {
+        LM_ATT_HIP(lm::launch_kv_prep(a, L.cache, lat, L.kv_a_norm, kvn, F, n0, pos0, c.rms_norm_eps, stream));
+        LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_b, kvn, kvx, heads * (c.qk_nope_head_dim + vh), rank, F, 1.0f, 0,
+                                            stream));
+        LM_ATT_HIP(lm::launch_kv_append(a, L.cache, kvx, F, n0, stream));
+    }
     // causal attention over the cache (:77-98), in groups of query tokens
     for (int64_t t0 = 0; t0 < F; t0 += core) {
         const int64_t n = std::min(core, F - t0);

@@ -230,6 +230,63 @@ hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int
 // tokens; conditions as matvec_rows_supported.
 hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim,
                                 int64_t tokens, float scale, int32_t accumulate, hipStream_t s);
+// gemm::dot_bf16 of one weight row over 32 lanes (lane c = 0..31 of a half
+// wave): lane c runs chain c (elements c, c + 32, ... in order, kOneAhead of
+// them requested before the first is added), then chains 0..7 over the 8-wide
+// remainder; the 32 lanes then reduce by shuffles in LiteMind's association,
+// (a[l] + a[8 + l]) + (a[16 + l] + a[24 + l]), lanes j and j + 4,
+// (h0 + h2) + (h1 + h3).  Every lane of the half wave returns the total.
+// `xat(e)` gives input element e.  in_dim % 8 == 0.  With `pre`, the lane's
+// weights of the first kOneAhead steps (elements 32 u + c) were loaded by the
+// caller, earlier (given only when in_dim >= 32 kOneAhead).
+constexpr int kOneAhead = 16;
+
+template <class X>
+__device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat, int in_dim, int c,
+                                         const uint16_t* pre = nullptr) {
+    const int steps = in_dim / 32;
+    float acc = 0.0f;
+    int k = 0;
+    if (pre != nullptr && steps >= kOneAhead) {
+        float xv[kOneAhead];
+#pragma unroll
+        for (int u = 0; u < kOneAhead; ++u) {
+            xv[u] = xat(32 * u + c);
+        }
+#pragma unroll
+        for (int u = 0; u < kOneAhead; ++u) {
+            acc = __builtin_fmaf(widen_bf16(pre[u]), xv[u], acc);
+        }
+        k = kOneAhead;
+    }
+    for (; k + kOneAhead <= steps; k += kOneAhead) {
+        uint16_t wv[kOneAhead];
+        float xv[kOneAhead];
+#pragma unroll
+        for (int u = 0; u < kOneAhead; ++u) {
+            wv[u] = wr[32 * (k + u) + c];
+            xv[u] = xat(32 * (k + u) + c);
+        }
+#pragma unroll
+        for (int u = 0; u < kOneAhead; ++u) {
+            acc = __builtin_fmaf(widen_bf16(wv[u]), xv[u], acc);
+        }
+    }
+    for (; k < steps; ++k) {
+        acc = __builtin_fmaf(widen_bf16(wr[32 * k + c]), xat(32 * k + c), acc);
+    }
+    if (c < 8) {
+        for (int e = steps * 32 + c; e < in_dim; e += 8) {
+            acc = __builtin_fmaf(widen_bf16(wr[e]), xat(e), acc);
+        }
+    }
+    const float t1 = acc + __shfl_xor(acc, 8);
+    const float t2 = t1 + __shfl_xor(t1, 16);
+    const float t3 = t2 + __shfl_xor(t2, 4);
+    const float t4 = t3 + __shfl_xor(t3, 2);
+    return t4 + __shfl_xor(t4, 1);
+}
+
 // ---- multi-head latent attention (k_attn.hip) ----
 // Shapes of one attention launch; cos_t / sin_t are the rotary tables
 // [max_positions, rope / 2] in HBM.
@@ -253,6 +310,18 @@ hipError_t launch_kv_prep(const AttnShape& a, const KvCacheDev& c, const float* 
                           int64_t T, int64_t slot0, int64_t pos0, float eps, hipStream_t s);
 hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float* kvx, int64_t T, int64_t slot0,
                             hipStream_t s);
+// One token (decode): the query projection (rows heads * (nope + rope), or
+// q_b's) with the rotary step of launch_rope_query applied to its output rows
+// in the same launch; nope % 2 == 0 and matvec_rows_supported.
+bool query_rope_one_supported(const AttnShape& a, int64_t in_dim);
+hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
+                                 int64_t pos, hipStream_t s);
+// One token: launch_kv_prep, kv_b's projection of its output and
+// launch_kv_append in one launch (every workgroup forms the normalised latent
+// itself); the cache slot `slot`, rotary position `pos`.
+bool kv_one_supported(const AttnShape& a);
+hipError_t launch_kv_one(const AttnShape& a, const KvCacheDev& c, const uint16_t* kv_b, const float* lat,
+                         const float* norm_w, float eps, int64_t slot, int64_t pos, hipStream_t s);
 // scores -> softmax -> context for T tokens in slots n0 .. n0 + T - 1 (already
 // appended); S holds T * heads * (n0 + T) floats, ctx [T, heads * vh].
 hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const float* q, float* S, float* ctx,

@@ -124,18 +124,43 @@ def test_prefill_batch_equals_sequential(over):
         m.close()
 
 
-def test_odd_widths_and_dot_tails():
-    """Three heads, qk_nope 22 and qk_rope 6 (dots with fused tails past the last
-    multiple of four), v_head 24 (a partial wave in the context kernel), prefill
-    of 5 then 4 tokens."""
-    d = small_dims(heads=3, qk_nope=22, qk_rope=6, v_head=24)
-    announce("attention odd widths")
+@pytest.mark.parametrize("nope", [22, 21])
+def test_odd_widths_and_dot_tails(nope):
+    """Three heads, qk_nope 22 or 21 and qk_rope 6 (dots with fused tails past
+    the last multiple of four; with 21 the rotary pairs do not fall on a row
+    pair of the single-token query launch, which then runs the projection and
+    the rotary step separately), v_head 24 (a partial wave in the context
+    kernel), prefill of 5 then 4 tokens, then three single-token steps."""
+    d = small_dims(heads=3, qk_nope=nope, qk_rope=6, v_head=24)
+    announce(f"attention odd widths nope={nope}")
     m = Mla(d, 121)
     try:
-        x = tokens(122, 9, d.hidden)
-        for lo, hi in ((0, 5), (5, 9)):
+        x = tokens(122, 12, d.hidden)
+        for lo, hi in ((0, 5), (5, 9), (9, 10), (10, 11), (11, 12)):
             y = m.forward(x[lo:hi], lo)
             want, _ = m.oracle(x[lo:hi], lo)
+            np.testing.assert_array_equal(bits(y), bits(want))
+        m.check_cache()
+    finally:
+        m.close()
+
+
+def test_decode_positions_past_the_rotary_table():
+    """Single-token steps at positions 20..25 with a 24-row rotary table (cache
+    slots 4..9 after four tokens at positions 16..19): the query and key
+    rotations of the single-token launches leave positions 24 and 25
+    unrotated (and in place), as RotaryEmbedding::apply does."""
+    d = small_dims(max_positions=24)
+    announce("attention decode past table")
+    m = Mla(d, 135)
+    try:
+        x = tokens(136, 10, d.hidden)
+        y = m.forward(x[:4], 16)
+        want, _ = m.oracle(x[:4], 16)
+        np.testing.assert_array_equal(bits(y), bits(want))
+        for t in range(4, 10):
+            y = m.forward(x[t:t + 1], 16 + t)
+            want, _ = m.oracle(x[t:t + 1], 16 + t)
             np.testing.assert_array_equal(bits(y), bits(want))
         m.check_cache()
     finally:
