@@ -167,20 +167,29 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
 // when nope is even, so each half takes the other's total by one shuffle and
 // stores its own output (the even one at nope + i, the odd one at nope + half
 // + i).  Positions at or past the table store the rows as they are.
+// Rows past the query's (rows2 of them, from w2 into out2) are a second
+// projection of the same input with no rotary step: kv_a's, in the same launch.
 __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __restrict__ w,
                                                              const float* __restrict__ x, float* __restrict__ q,
                                                              int64_t rows, int32_t in_dim, int32_t nope,
                                                              int32_t rope, const float* __restrict__ cos_t,
                                                              const float* __restrict__ sin_t, int64_t pos,
-                                                             int64_t max_positions) {
+                                                             int64_t max_positions, const uint16_t* __restrict__ w2,
+                                                             float* __restrict__ out2, int64_t rows2) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 31;
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
-    const bool live = row < rows;
-    const uint16_t* wr = w + (live ? row : rows - 1) * in_dim;
+    const int64_t row_all = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+    const bool second = row_all >= rows;  // uniform over each half wave (rows is even)
+    const int64_t row = second ? row_all - rows : row_all;
+    const bool live = second ? row < rows2 : true;
+    const uint16_t* wr = second ? w2 + (live ? row : rows2 - 1) * in_dim : w + row * in_dim;
     const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
     const float other = __shfl_xor(total, 32);  // the pair partner's total
     if (!live || c != 0) {
+        return;
+    }
+    if (second) {
+        out2[row] = total;
         return;
     }
     const int qk = nope + rope;
@@ -942,13 +951,17 @@ bool query_rope_one_supported(const AttnShape& a, int64_t in_dim) {
 }
 
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
-                                 int64_t pos, hipStream_t s) {
-    if (!query_rope_one_supported(a, in_dim)) {
+                                 int64_t pos, hipStream_t s, const uint16_t* w2, float* out2, int64_t rows2) {
+    if (!query_rope_one_supported(a, in_dim) || (w2 != nullptr && !matvec_rows_supported(rows2, in_dim))) {
         return hipErrorInvalidValue;
     }
     const int64_t rows = static_cast<int64_t>(a.heads) * (a.nope + a.rope);
-    hipLaunchKernelGGL(query_rope_one_kernel, dim3(blocks_of(rows, 8)), dim3(256), 0, s, w, x, q, rows,
-                       static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions);
+    if (w2 == nullptr) {
+        rows2 = 0;
+    }
+    hipLaunchKernelGGL(query_rope_one_kernel, dim3(blocks_of(rows + rows2, 8)), dim3(256), 0, s, w, x, q, rows,
+                       static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
+                       out2, rows2);
     return hipGetLastError();
 }
 

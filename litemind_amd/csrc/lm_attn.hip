@@ -259,7 +259,11 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
         q_x = qlat;
     }
     const uint16_t* q_w = ql == 0 ? L.q_proj : L.q_b;
-    if (q_fused) {
+    // without the q LoRA, kv_a projects the same x: one launch for both
+    const bool kv_a_with_q = q_fused && ql == 0 && lm::matvec_rows_supported(rank + rope, H);
+    if (kv_a_with_q) {
+        LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream, L.kv_a, lat, rank + rope));
+    } else if (q_fused) {
         LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream));
     } else {
         LM_ATT_HIP(lm::launch_matvec_tokens(q_w, q_x, q, heads * qk, q_in, F, 1.0f, 0, stream));
@@ -267,7 +271,9 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     }
     // compressed keys and values, appended at slots n0 .. n0 + F - 1 (:50-75);
     // for one token the norm, kv_b and the append are one launch
-    LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_a, x, lat, rank + rope, H, F, 1.0f, 0, stream));
+    if (!kv_a_with_q) {
+        LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_a, x, lat, rank + rope, H, F, 1.0f, 0, stream));
+    }
     if (F == 1 && lm::kv_one_supported(a)) {
         LM_ATT_HIP(lm::launch_kv_one(a, L.cache, L.kv_b, lat, L.kv_a_norm, c.rms_norm_eps, n0, pos0, stream));
     } else {
