@@ -5,6 +5,7 @@
     python bench.py --workload load       # SafeTensors shards of 4 layers into HBM
     python bench.py --workload head       # final norm + LM head + greedy token, T=1
     python bench.py --workload attention  # one MLA attention layer: decode near 512 / 4K cache tokens, prefill T=512
+    python bench.py --workload decoder    # 27 layers of attention + FFN: prefill of 512 tokens, then decode
 
 A step is one MoE-layer forward (router, permutation, routed + shared SwiGLU
 experts, combine) over one batch of T synthetic tokens whose inputs are already
@@ -172,6 +173,76 @@ def run_stack(steps_t1: int, steps_big: int, big_tokens: int, moe_layers: int) -
                         "value": round(T / (ms / 1e3), 1), "unit": "tokens/s"}
         dh.free()
         log(f"stack T={T}: {ms:.3f} ms per step")
+    ctx.close()
+    return out
+
+
+def run_decoder(steps: int, warmup: int, moe_layers: int, context: int) -> dict:
+    """DeepSeek-V2-Lite's layer loop as DeepSeekRunner::forward runs it
+    (src/DeepSeekRunner.cpp:251-291), without the embedding and the LM head:
+    per layer h += attention(rms_norm(h, input_norm)), then h += FFN(rms_norm(h,
+    post_norm)); layer 0 dense, layers 1..`moe_layers` MoE, every weight
+    synthetic and resident, through lm_decoder_forward.  Prefill: `context`
+    tokens from position 0 through every layer (one batched call, timed with
+    events, after one untimed run into a cleared cache).  Decode: `steps`
+    single-token calls after `warmup` untimed ones, continuing from that
+    prefill, so the KV caches hold context .. context + warmup + steps - 1
+    tokens."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = wl.V2_LITE
+    d = wl.V2_LITE_MLA
+    n = 1 + moe_layers
+    if context + warmup + steps > d.max_positions:
+        raise ValueError(f"decoder: {context} + {warmup} + {steps} tokens exceed the {d.max_positions}-token cache")
+    log(f"decoder: generating and uploading dense + {moe_layers} MoE layers with attention")
+    ctx = Context(dims.moe_config(num_layers=n))
+    ctx.attention_configure(wl.mla_config(d))
+    gate, up, down = wl.dense_ffn(wl.MASTER_SEED, 0, dims)
+    ctx.upload_dense(0, gate, up, down)
+    ctx.finalize_layer(0)
+    del gate, up, down
+    for l in range(1, n):
+        wl.upload_moe_layer(ctx, l, wl.moe_layer(wl.MASTER_SEED, l, dims))
+        log(f"decoder: MoE layer {l} resident")
+    for l in range(n):
+        wl.upload_mla_layer(ctx, l, wl.mla_layer(wl.MASTER_SEED + 31, l, d))
+        ctx.upload_input_norm(l, (1.0 + wl.normal_f32(wl.MASTER_SEED + 32, l, 0.1, (dims.hidden,))).astype(np.float32))
+        ctx.upload_norm(l, (1.0 + wl.normal_f32(wl.MASTER_SEED + 33, l, 0.1, (dims.hidden,))).astype(np.float32))
+    out = {"layers": n, "resident_gb": round(ctx.resident_bytes() / 1e9, 2), "context": context}
+    h0 = wl.tokens(wl.MASTER_SEED + 34, context + warmup + steps, dims.hidden)
+    dh = ctx.to_device(h0)
+    row = dims.hidden * 4
+    for rep in range(2):  # the first pass warms up; the second is timed
+        ctx.kv_cache_clear()
+        dh.upload(h0)
+        ctx.synchronize()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        ctx.decoder_forward(0, n - 1, dh, context, 0)
+        ctx.record(e1)
+        ctx.synchronize()
+    pre_ms = ctx.elapsed_ms(e0, e1)
+    out["prefill"] = {"tokens": context, "ms": round(pre_ms, 3), "tokens_per_s": round(context / pre_ms * 1e3, 1)}
+    log(f"decoder prefill T={context}: {pre_ms:.3f} ms")
+    pos = context
+    for _ in range(warmup):
+        ctx.decoder_forward(0, n - 1, dh.ptr + pos * row, 1, pos)
+        pos += 1
+    ctx.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(steps):
+        ctx.decoder_forward(0, n - 1, dh.ptr + pos * row, 1, pos)
+        pos += 1
+    ctx.record(e1)
+    ctx.synchronize()
+    us = ctx.elapsed_ms(e0, e1) * 1e3 / steps
+    out["decode"] = {"context": [context + warmup, context + warmup + steps - 1], "us_per_token": round(us, 2),
+                     "us_per_layer": round(us / n, 2), "tokens_per_s": round(1e6 / us, 1)}
+    log(f"decoder decode: {us:.2f} us per token ({us / n:.2f} per layer)")
+    dh.free()
     ctx.close()
     return out
 
@@ -482,6 +553,22 @@ def main() -> int:
                              "frac": main["hbm_frac"], "traffic": None, "avg_us": main["us_per_step"],
                              "algorithmic_bytes": main["bytes_per_step"]},
                 "attention": at}
+        print(json.dumps(line), flush=True)
+        return 0
+    if args.workload == "decoder":
+        if args.gpus != 1:
+            print("bench.py measures one GPU.", file=sys.stderr)
+            return 2
+        dc = run_decoder(args.steps if args.steps != 200 else 100, args.warmup, 26, 512)
+        line = {"metric": "DeepSeek-V2-Lite decoder layers, decode tokens/sec (27 layers of attention + FFN, "
+                          "KV cache near 512 tokens)",
+                "value": dc["decode"]["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+                "steps": args.steps if args.steps != 200 else 100, "warmup": args.warmup,
+                "ms_per_step": round(dc["decode"]["us_per_token"] / 1e3, 5), "higher_is_better": True,
+                "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)",
+                "config": {"workload": "decoder", "layers": dc["layers"], "resident_gb": dc["resident_gb"],
+                           "prefill_tokens": dc["context"]},
+                "decoder": dc}
         print(json.dumps(line), flush=True)
         return 0
     if args.workload == "head":

@@ -314,11 +314,12 @@ hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float
 // q_b's) with the rotary step of launch_rope_query applied to its output rows
 // in the same launch; nope % 2 == 0 and matvec_rows_supported.  With w2, a
 // second projection of the same x (rows2 rows, no rotary step, into out2)
-// runs in the same launch.
+// runs in the same launch.  With norm_w, x is normalised first inside the
+// launch, bit for bit as launch_rms_norm would (eps as there).
 bool query_rope_one_supported(const AttnShape& a, int64_t in_dim);
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
                                  int64_t pos, hipStream_t s, const uint16_t* w2 = nullptr, float* out2 = nullptr,
-                                 int64_t rows2 = 0);
+                                 int64_t rows2 = 0, const float* norm_w = nullptr, float eps = 0.0f);
 // One token: launch_kv_prep, kv_b's projection of its output and
 // launch_kv_append in one launch (every workgroup forms the normalised latent
 // itself); the cache slot `slot`, rotary position `pos`.
