@@ -99,21 +99,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const float* __restrict__ 
     __shared__ double part[4];
     const int64_t t = blockIdx.x;
     const float* row = lat + t * static_cast<int64_t>(rank + rope);
-    double sq = 0.0;
-    for (int c = threadIdx.x; c < rank; c += 256) {
-        const double v = static_cast<double>(row[c]);
-        sq = sq + v * v;
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        sq += __shfl_xor(sq, o);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        part[threadIdx.x >> 6] = sq;
-    }
-    __syncthreads();
-    const double total = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inverse =
-        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(rank) + static_cast<double>(eps)));
+    const float inverse = rms_inverse_256(row, rank, eps, part);
     for (int c = threadIdx.x; c < rank; c += 256) {
         const float scaled = row[c] * inverse;
         kvn[t * rank + c] = scaled * norm_w[c];
@@ -169,19 +155,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
 // + i).  Positions at or past the table store the rows as they are.
 // Rows past the query's (rows2 of them, from w2 into out2) are a second
 // projection of the same input with no rotary step: kv_a's, in the same launch.
-// With NORM the input is the raw hidden state and every workgroup normalises
-// it on the fly as rms_norm_kernel does (the inverse from the same
-// thread-strided double sums, then (x * inverse) * norm_w), having requested
-// its lanes' first weights before that reduction.
-template <bool NORM>
 __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __restrict__ w,
                                                              const float* __restrict__ x, float* __restrict__ q,
                                                              int64_t rows, int32_t in_dim, int32_t nope,
                                                              int32_t rope, const float* __restrict__ cos_t,
                                                              const float* __restrict__ sin_t, int64_t pos,
                                                              int64_t max_positions, const uint16_t* __restrict__ w2,
-                                                             float* __restrict__ out2, int64_t rows2,
-                                                             const float* __restrict__ norm_w, float eps) {
+                                                             float* __restrict__ out2, int64_t rows2) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 31;
     const int64_t row_all = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
@@ -189,37 +169,7 @@ __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __r
     const int64_t row = second ? row_all - rows : row_all;
     const bool live = second ? row < rows2 : true;
     const uint16_t* wr = second ? w2 + (live ? row : rows2 - 1) * in_dim : w + row * in_dim;
-    float total;
-    if (NORM) {
-        uint16_t pre[kOneAhead];
-        const bool use_pre = in_dim / 32 >= kOneAhead;
-        if (use_pre) {
-#pragma unroll
-            for (int u = 0; u < kOneAhead; ++u) {
-                pre[u] = wr[32 * u + c];
-            }
-        }
-        __shared__ double part[4];
-        double sq = 0.0;
-        for (int e = threadIdx.x; e < in_dim; e += 256) {
-            const double v = static_cast<double>(x[e]);
-            sq = sq + v * v;
-        }
-        for (int o = 32; o >= 1; o >>= 1) {
-            sq += __shfl_xor(sq, o);
-        }
-        if ((threadIdx.x & 63) == 0) {
-            part[threadIdx.x >> 6] = sq;
-        }
-        __syncthreads();
-        const double total_sq = (part[0] + part[1]) + (part[2] + part[3]);
-        const float inverse = static_cast<float>(
-            1.0 / __builtin_sqrt(total_sq / static_cast<double>(in_dim) + static_cast<double>(eps)));
-        total = dot_bf16_lanes32(wr, [&](int e) { return (x[e] * inverse) * norm_w[e]; }, in_dim, c,
-                                 use_pre ? pre : nullptr);
-    } else {
-        total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
-    }
+    const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
     const float other = __shfl_xor(total, 32);  // the pair partner's total
     if (!live || c != 0) {
         return;
@@ -271,29 +221,12 @@ __global__ __launch_bounds__(256) void kv_one_kernel(const uint16_t* __restrict_
     const uint16_t* wr = w + (live ? row : rows - 1) * rank;
     // the lane's first weights, requested before the norm's reduction so they
     // arrive while it runs
-    uint16_t pre[kOneAhead];
+    uint32_t pre[kOneAhead];
     const bool use_pre = rank / 32 >= kOneAhead;
     if (use_pre) {
-#pragma unroll
-        for (int u = 0; u < kOneAhead; ++u) {
-            pre[u] = wr[32 * u + c];
-        }
+        pre_weights(wr, c, pre);
     }
-    double sq = 0.0;
-    for (int e = threadIdx.x; e < rank; e += 256) {
-        const double v = static_cast<double>(lat[e]);
-        sq = sq + v * v;
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        sq += __shfl_xor(sq, o);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        part[threadIdx.x >> 6] = sq;
-    }
-    __syncthreads();
-    const double total_sq = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inverse =
-        static_cast<float>(1.0 / __builtin_sqrt(total_sq / static_cast<double>(rank) + static_cast<double>(eps)));
+    const float inverse = rms_inverse_256(lat, rank, eps, part);
     if (blockIdx.x == 0) {
         const int half = rope / 2;
         const float* tail = lat + rank;
@@ -311,8 +244,8 @@ __global__ __launch_bounds__(256) void kv_one_kernel(const uint16_t* __restrict_
             }
         }
     }
-    const float total = dot_bf16_lanes32(wr, [&](int e) { return (lat[e] * inverse) * norm_w[e]; }, rank, c,
-                                         use_pre ? pre : nullptr);
+    const auto xn = [&](int e) { return (lat[e] * inverse) * norm_w[e]; };
+    const float total = use_pre ? dot_bf16_lanes32(wr, xn, rank, c, pre) : dot_bf16_lanes32(wr, xn, rank, c);
     if (!live || c != 0) {
         return;
     }
@@ -987,8 +920,7 @@ bool query_rope_one_supported(const AttnShape& a, int64_t in_dim) {
 }
 
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
-                                 int64_t pos, hipStream_t s, const uint16_t* w2, float* out2, int64_t rows2,
-                                 const float* norm_w, float eps) {
+                                 int64_t pos, hipStream_t s, const uint16_t* w2, float* out2, int64_t rows2) {
     if (!query_rope_one_supported(a, in_dim) || (w2 != nullptr && !matvec_rows_supported(rows2, in_dim))) {
         return hipErrorInvalidValue;
     }
@@ -996,16 +928,9 @@ hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const fl
     if (w2 == nullptr) {
         rows2 = 0;
     }
-    const dim3 grid(blocks_of(rows + rows2, 8));
-    if (norm_w != nullptr) {
-        hipLaunchKernelGGL(query_rope_one_kernel<true>, grid, dim3(256), 0, s, w, x, q, rows,
-                           static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
-                           out2, rows2, norm_w, eps);
-    } else {
-        hipLaunchKernelGGL(query_rope_one_kernel<false>, grid, dim3(256), 0, s, w, x, q, rows,
-                           static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
-                           out2, rows2, norm_w, eps);
-    }
+    hipLaunchKernelGGL(query_rope_one_kernel, dim3(blocks_of(rows + rows2, 8)), dim3(256), 0, s, w, x, q, rows,
+                       static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
+                       out2, rows2);
     return hipGetLastError();
 }
 

@@ -198,24 +198,25 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* in, const fl
     __shared__ double part[4];
     const int64_t row = blockIdx.x;
     const float* x = in + row * cols;
-    double s = 0.0;
-    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
-        const double v = static_cast<double>(x[c]);
-        s = s + v * v;
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        s += __shfl_xor(s, o);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        part[threadIdx.x >> 6] = s;
-    }
-    __syncthreads();
-    const double total = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inverse =
-        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(cols) + static_cast<double>(eps)));
-    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float scaled = x[c] * inverse;
-        out[row * cols + c] = scaled * w[c];
+    const float inverse = rms_inverse_256(x, cols, eps, part);
+    // eight elements per thread per pass, loads first (one pass for 2048 columns)
+    for (int c0 = static_cast<int>(threadIdx.x); c0 < cols; c0 += 8 * 256) {
+        float v[8], wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + 256 * u;
+            const int cc = c < cols ? c : cols - 1;  // unconditional loads
+            v[u] = x[cc];
+            wv[u] = w[cc];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + 256 * u;
+            if (c < cols) {
+                const float scaled = v[u] * inverse;
+                out[row * cols + c] = scaled * wv[u];
+            }
+        }
     }
 }
 

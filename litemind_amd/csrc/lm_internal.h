@@ -230,6 +230,41 @@ hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int
 // tokens; conditions as matvec_rows_supported.
 hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim,
                                 int64_t tokens, float scale, int32_t accumulate, hipStream_t s);
+// gemm::rms_norm's inverse, 1 / sqrt(mean(x^2) + eps), for x[0 .. n) as
+// rms_norm_kernel forms it with 256 threads: thread t sums the exact squares of
+// elements t, t + 256, ... in double, in that order; the wave's butterfly;
+// then (w0 + w1) + (w2 + w3) over the four waves.  The loads are issued eight
+// at a time (a loop of one load per step waits a round trip per element).
+// Every thread of the 256-thread workgroup calls it; `part` is 4 doubles of
+// LDS.
+__device__ inline float rms_inverse_256(const float* __restrict__ x, int n, float eps, double* part) {
+    double sq = 0.0;
+    for (int e0 = static_cast<int>(threadIdx.x); e0 < n; e0 += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + 256 * u;
+            v[u] = x[e < n ? e : n - 1];  // unconditional (a conditional load becomes a branch and a wait)
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (e0 + 256 * u < n) {
+                const double d = static_cast<double>(v[u]);
+                sq = sq + d * d;
+            }
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        sq += __shfl_xor(sq, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = sq;
+    }
+    __syncthreads();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(n) + static_cast<double>(eps)));
+}
+
 // gemm::dot_bf16 of one weight row over 32 lanes (lane c = 0..31 of a half
 // wave): lane c runs chain c (elements c, c + 32, ... in order, kOneAhead of
 // them requested before the first is added), then chains 0..7 over the 8-wide
@@ -237,17 +272,29 @@ hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, i
 // (a[l] + a[8 + l]) + (a[16 + l] + a[24 + l]), lanes j and j + 4,
 // (h0 + h2) + (h1 + h3).  Every lane of the half wave returns the total.
 // `xat(e)` gives input element e.  in_dim % 8 == 0.  With `pre`, the lane's
-// weights of the first kOneAhead steps (elements 32 u + c) were loaded by the
-// caller, earlier (given only when in_dim >= 32 kOneAhead).
+// weights of the first kOneAhead steps were loaded by the caller, earlier
+// (only when in_dim >= 32 kOneAhead): word u is the aligned 32-bit word
+// holding element 32 u + c (pre_weights), so no instruction touches it before
+// the FMA that uses it.
 constexpr int kOneAhead = 16;
 
-template <class X>
-__device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat, int in_dim, int c,
-                                         const uint16_t* pre = nullptr) {
+// The words dot_bf16_lanes32 takes as `pre`: for u < kOneAhead, the aligned
+// 32-bit word of row wr holding element 32 u + c (wr 4-byte aligned).
+__device__ inline void pre_weights(const uint16_t* __restrict__ wr, int c, uint32_t (&pre)[kOneAhead]) {
+    const uint32_t* w32 = reinterpret_cast<const uint32_t*>(wr);
+#pragma unroll
+    for (int u = 0; u < kOneAhead; ++u) {
+        pre[u] = w32[(32 * u + c) >> 1];
+    }
+}
+
+template <bool PRE, class X>
+__device__ inline float dot_bf16_lanes32_impl(const uint16_t* __restrict__ wr, X xat, int in_dim, int c,
+                                              const uint32_t (&pre)[kOneAhead]) {
     const int steps = in_dim / 32;
     float acc = 0.0f;
     int k = 0;
-    if (pre != nullptr && steps >= kOneAhead) {
+    if (PRE) {
         float xv[kOneAhead];
 #pragma unroll
         for (int u = 0; u < kOneAhead; ++u) {
@@ -255,7 +302,8 @@ __device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat,
         }
 #pragma unroll
         for (int u = 0; u < kOneAhead; ++u) {
-            acc = __builtin_fmaf(widen_bf16(pre[u]), xv[u], acc);
+            const uint32_t word = pre[u];
+            acc = __builtin_fmaf(bits_float((c & 1) != 0 ? (word & 0xffff0000u) : (word << 16)), xv[u], acc);
         }
         k = kOneAhead;
     }
@@ -287,6 +335,19 @@ __device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat,
     return t4 + __shfl_xor(t4, 1);
 }
 
+template <class X>
+__device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat, int in_dim, int c) {
+    const uint32_t none[kOneAhead] = {};
+    return dot_bf16_lanes32_impl<false>(wr, xat, in_dim, c, none);
+}
+
+// The same with the first kOneAhead steps' weights already in registers.
+template <class X>
+__device__ inline float dot_bf16_lanes32(const uint16_t* __restrict__ wr, X xat, int in_dim, int c,
+                                         const uint32_t (&pre)[kOneAhead]) {
+    return dot_bf16_lanes32_impl<true>(wr, xat, in_dim, c, pre);
+}
+
 // ---- multi-head latent attention (k_attn.hip) ----
 // Shapes of one attention launch; cos_t / sin_t are the rotary tables
 // [max_positions, rope / 2] in HBM.
@@ -314,12 +375,11 @@ hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float
 // q_b's) with the rotary step of launch_rope_query applied to its output rows
 // in the same launch; nope % 2 == 0 and matvec_rows_supported.  With w2, a
 // second projection of the same x (rows2 rows, no rotary step, into out2)
-// runs in the same launch.  With norm_w, x is normalised first inside the
-// launch, bit for bit as launch_rms_norm would (eps as there).
+// runs in the same launch.
 bool query_rope_one_supported(const AttnShape& a, int64_t in_dim);
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
                                  int64_t pos, hipStream_t s, const uint16_t* w2 = nullptr, float* out2 = nullptr,
-                                 int64_t rows2 = 0, const float* norm_w = nullptr, float eps = 0.0f);
+                                 int64_t rows2 = 0);
 // One token: launch_kv_prep, kv_b's projection of its output and
 // launch_kv_append in one launch (every workgroup forms the normalised latent
 // itself); the cache slot `slot`, rotary position `pos`.
