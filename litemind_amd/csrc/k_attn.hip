@@ -491,34 +491,40 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
     }
 }
 
-// softmax_rows_kernel's arithmetic for one query token (decode, T = 1): one
-// workgroup per head.  All threads find the maximum and form expf(s - max)
-// into LDS; wave 0 adds them left to right in one chain, reading LDS with
-// broadcast loads a batch of 64 ahead (a VGPR operand: no lane-to-SGPR hand-off
-// per step); then every thread writes e * (1 / total).  n <= kSoftmaxLds.
+// softmax_rows_kernel's arithmetic for one query token (decode, T = 1), for
+// one head's row of n <= kSoftmaxLds scores, by a workgroup of NT threads:
+// all threads find the maximum and form expf(s - max) into e (LDS); wave 0 adds
+// them left to right in one chain, reading LDS with broadcast loads a batch of
+// 64 ahead (a VGPR operand: no lane-to-SGPR hand-off per step).  Returns
+// 1 / total to every thread (after a barrier); e then holds the exponentials,
+// zero past n up to the next multiple of 128.  red: NT / 64 floats of LDS,
+// inverse_lds: one, tab: expf's 2^(i/32) table in LDS.  Its barriers order LDS
+// only, so loads the caller has in flight stay in flight; after_max() runs on
+// every thread once the scores are in.
 constexpr int kSoftmaxLds = 8192;  // a multiple of 128
 
-__global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n, int64_t n_stride) {
-    constexpr int kPer = kSoftmaxLds / 256;  // scores per thread
-    __shared__ __align__(16) float e[kSoftmaxLds];
-    __shared__ float red[4];
-    __shared__ uint64_t exp_tab[32];  // expf's 2^(i/32) table: one LDS read in place of a select tree
-    if (threadIdx.x < 32) {
-        exp_tab[threadIdx.x] = exp2_table(threadIdx.x);
+// (In two parts: softmax_row_load requests the thread's scores, so a caller
+// can issue them before other loads, whose results come back after them.)
+template <int NT>
+constexpr int softmax_per() { return (kSoftmaxLds + NT - 1) / NT; }  // scores per thread
+
+template <int NT>
+__device__ inline void softmax_row_load(const float* s, int nn, float (&v)[softmax_per<NT>()]) {
+#pragma unroll
+    for (int k = 0; k < softmax_per<NT>(); ++k) {
+        const int c = static_cast<int>(threadIdx.x) + NT * k;
+        v[k] = c < nn ? s[c] : -__builtin_inff();
     }
-    __shared__ float inverse_lds;
+}
+
+template <int NT, class AfterMax>
+__device__ inline float softmax_row_lds(const float (&v)[softmax_per<NT>()], int nn, float* e, float* red,
+                                        float* inverse_lds, const uint64_t* tab, AfterMax after_max) {
+    constexpr int kPer = softmax_per<NT>();
+    constexpr int kW = NT / 64;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    float* s = S + static_cast<int64_t>(blockIdx.x) * n_stride;
-    const int nn = static_cast<int>(n);
-    // every score of the thread requested at once
-    float v[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int c = tid + 256 * k;
-        v[k] = c < nn ? s[c] : -__builtin_inff();
-    }
     float m = -__builtin_inff();
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -531,27 +537,32 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
     if (lane == 0) {
         red[wave] = m;
     }
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    lds_barrier();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) {
+        m = fmaxf(m, red[w]);
+    }
+    after_max();  // every thread, once its scores are in
     // e past n is 0 up to the next multiple of 128: adding those exact zeros to
     // the (non-negative) total changes nothing, and the chain below runs in
     // whole pairs of batches without a bounds test
     const int n64 = (nn + 127) / 128 * 128;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-        const int c = tid + 256 * k;
+        const int c = tid + NT * k;
         if (c < nn) {
-            e[c] = expf_with(v[k] - m, [&](uint32_t i) { return exp_tab[i]; });
+            e[c] = expf_with(v[k] - m, [&](uint32_t i) { return tab[i]; });
         } else if (c < n64) {
             e[c] = 0.0f;
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
         // one batch of 64 values (16 broadcast reads) requested ahead of the
-        // batch being added, so the chain does not wait for LDS
-        // a native 4-float vector, so each read stays one 16-byte LDS read
-        // (HIP's float4 struct is split into four)
+        // batch being added, so the chain does not wait for LDS; a native
+        // 4-float vector, so each read stays one 16-byte LDS read (HIP's float4
+        // struct is split into four)
         typedef float f4v __attribute__((ext_vector_type(4)));
         const f4v* e4 = reinterpret_cast<const f4v*>(e);
         const int nb = n64 / 64;  // even
@@ -584,17 +595,30 @@ __global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n
             add16(b);
         }
         if (lane == 0) {
-            inverse_lds = total > 0.0f ? 1.0f / total : 0.0f;
+            *inverse_lds = total > 0.0f ? 1.0f / total : 0.0f;
         }
     }
-    __syncthreads();
-    const float inverse = inverse_lds;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int c = tid + 256 * k;
-        if (c < nn) {
-            s[c] = e[c] * inverse;
-        }
+    lds_barrier();
+    return *inverse_lds;
+}
+
+// The decode softmax as its own launch (one workgroup per head), for the
+// context kernel's unfused form: P = e * (1 / total) back into S.
+__global__ __launch_bounds__(256) void softmax_decode_kernel(float* S, int64_t n, int64_t n_stride) {
+    __shared__ __align__(16) float e[kSoftmaxLds];
+    __shared__ float red[4];
+    __shared__ float inverse_lds;
+    __shared__ uint64_t exp_tab[32];  // expf's 2^(i/32) table: one LDS read in place of a select tree
+    if (threadIdx.x < 32) {
+        exp_tab[threadIdx.x] = exp2_table(threadIdx.x);
+    }
+    float* s = S + static_cast<int64_t>(blockIdx.x) * n_stride;
+    const int nn = static_cast<int>(n);
+    float v[softmax_per<256>()];
+    softmax_row_load<256>(s, nn, v);
+    const float inverse = softmax_row_lds<256>(v, nn, e, red, &inverse_lds, exp_tab, [] {});
+    for (int c = threadIdx.x; c < nn; c += 256) {
+        s[c] = e[c] * inverse;
     }
 }
 
@@ -723,22 +747,33 @@ constexpr int kCtxDepth = 8;
 constexpr int kCtxLoaders = 4;  // waves 1 .. 4 issue the loads, wave 0 only adds
 constexpr int kCtxThreads = (kCtxLoaders + 1) * 64;
 constexpr int kCtxTokPerLoad = 64 * 4 / kCtxCh;  // tokens per 1 KB value load
-constexpr int kCtxLoads = kCtxChunk / kCtxTokPerLoad / kCtxLoaders + kCtxChunk / 64 / kCtxLoaders;  // per loader
+constexpr int kCtxDepthFused = 7;  // slots when the probability row also sits in LDS
+constexpr int kCtxValueLoads = kCtxChunk / kCtxTokPerLoad / kCtxLoaders;  // per loader and chunk
 static_assert(kCtxChunk % (kCtxTokPerLoad * kCtxLoaders) == 0 && kCtxChunk % (64 * kCtxLoaders) == 0,
               "even shares");
-static_assert((kCtxDepth - 1) * kCtxLoads < 64, "vmcnt immediate");
+static_assert((kCtxDepth - 1) * (kCtxValueLoads + kCtxChunk / 64 / kCtxLoaders) < 64, "vmcnt immediate");
 
+// FUSED: the softmax of the head's row of scores runs inside the launch
+// (softmax_row_lds, every workgroup of the head the same) while the loader
+// waves already stream the first value chunks; its probabilities stay in LDS
+// (the whole row, n <= kSoftmaxLds) and the ring carries values only, in
+// kCtxDepthFused slots.  Otherwise P holds the probabilities (a separate
+// softmax launch) and each slot carries its chunk's share of them.
+template <bool FUSED>
 __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float* __restrict__ P,
                                                                         const float* __restrict__ value,
                                                                         float* __restrict__ ctx, int32_t vh,
                                                                         int64_t cap, int64_t n, int64_t n_stride) {
-    // slot = [token][16 channels] values, then the chunk's probabilities: one
-    // array per slot (eight LDS objects are what the compiler's wait insertion
-    // tells apart)
-    constexpr int kSlot = kCtxChunk * kCtxCh + kCtxChunk;
+    constexpr int kDepth = FUSED ? kCtxDepthFused : kCtxDepth;
+    constexpr int kLoads = kCtxValueLoads + (FUSED ? 0 : kCtxChunk / 64 / kCtxLoaders);  // per loader and chunk
+    // slot = [token][16 channels] values, then (unfused) the chunk's
+    // probabilities: one array per slot (separate LDS objects are what the
+    // compiler's wait insertion tells apart)
+    constexpr int kSlot = kCtxChunk * kCtxCh + (FUSED ? 0 : kCtxChunk);
     __shared__ __align__(16) float s0[kSlot], s1[kSlot], s2[kSlot], s3[kSlot], s4[kSlot], s5[kSlot], s6[kSlot],
-        s7[kSlot];
-    float* const ring[kCtxDepth] = {s0, s1, s2, s3, s4, s5, s6, s7};
+        s7[FUSED ? 4 : kSlot];
+    __shared__ __align__(16) float prob[FUSED ? kSoftmaxLds : 4];
+    float* const ring[8] = {s0, s1, s2, s3, s4, s5, s6, s7};
     const int lane = threadIdx.x & 63;
     // wave-uniform as far as the compiler knows, so the branches on it stay
     // scalar and its wait insertion keeps track of each slot's loads
@@ -751,7 +786,7 @@ __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float
     const int h = static_cast<int>(blockIdx.x) % heads;
     const int c0 = (static_cast<int>(blockIdx.x) / heads) * kCtxCh;
     const float* vbase = value + static_cast<int64_t>(h) * cap * vh + c0;
-    const float* prow = P + static_cast<int64_t>(h) * n_stride;
+    const float* prow = P + static_cast<int64_t>(h) * n_stride;  // scores (FUSED) or probabilities
     const int64_t nchunks = (n + kCtxChunk - 1) / kCtxChunk;
     // loader wave w = wave - 1's share of chunk c (clamped to the last chunk,
     // so every step issues the same count): value load i (i = w, w + 4, ...)
@@ -773,7 +808,7 @@ __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float
     auto issue = [&](int64_t c, float* slot) {
         c = c < nchunks ? c : nchunks - 1;
 #pragma unroll
-        for (int k = 0; k < kCtxChunk / kCtxTokPerLoad / kCtxLoaders; ++k) {
+        for (int k = 0; k < kCtxValueLoads; ++k) {
             const int i = k * kCtxLoaders + lw;
             int64_t tok = c * kCtxChunk + kCtxTokPerLoad * i + (lane >> 2);
             tok = tok < n ? tok : n - 1;
@@ -781,7 +816,7 @@ __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float
                                                      static_cast<unsigned>((tok * vh + 4 * (lane & 3)) * 4), 0, 0, 0);
         }
 #pragma unroll
-        for (int k = 0; k < kCtxChunk / 64 / kCtxLoaders; ++k) {
+        for (int k = 0; k < (FUSED ? 0 : kCtxChunk / 64 / kCtxLoaders); ++k) {
             const int i = k * kCtxLoaders + lw;
             int64_t tok = c * kCtxChunk + 64 * i + lane;
             tok = tok < n ? tok : n - 1;
@@ -789,34 +824,58 @@ __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float
                                                      static_cast<unsigned>(tok * 4), 0, 0, 0);
         }
     };
-    if (wave != 0) {
+    auto first_chunks = [&] {
+        if (wave != 0) {
 #pragma unroll
-        for (int d = 0; d < kCtxDepth - 1; ++d) {
-            issue(d, ring[d]);
+            for (int d = 0; d < kDepth - 1; ++d) {
+                issue(d, ring[d]);
+            }
         }
+    };
+    if constexpr (FUSED) {
+        // the head's probabilities into LDS; the first chunks are requested
+        // once the scores are in (results return in issue order), and arrive
+        // while the exponentials and the total are formed
+        __shared__ float red[kCtxThreads / 64];
+        __shared__ float inverse_lds;
+        __shared__ uint64_t exp_tab[32];
+        if (threadIdx.x < 32) {
+            exp_tab[threadIdx.x] = exp2_table(threadIdx.x);
+        }
+        const int nn = static_cast<int>(n);
+        float scores[softmax_per<kCtxThreads>()];
+        softmax_row_load<kCtxThreads>(prow, nn, scores);
+        const float inverse =
+            softmax_row_lds<kCtxThreads>(scores, nn, prob, red, &inverse_lds, exp_tab, first_chunks);
+        for (int t = threadIdx.x; t < nn; t += kCtxThreads) {
+            prob[t] = prob[t] * inverse;
+        }
+        lds_barrier();
+    } else {
+        first_chunks();
     }
-    // chunk c is in once at most the kCtxDepth - 2 chunks issued after it are
-    // in flight
-    constexpr int kVm = (kCtxDepth - 2) * kCtxLoads;
+    // chunk c is in once at most the kDepth - 2 chunks issued after it are in
+    // flight
+    constexpr int kVm = (kDepth - 2) * kLoads;
     constexpr int kWait = 0x0070 | 0x0F00 | (kVm & 15) | ((kVm >> 4) << 14);
     const int ch = lane < kCtxCh ? lane : kCtxCh - 1;  // lanes past the group repeat its last channel
     float acc = 0.0f;
-    for (int64_t cb = 0; cb < nchunks; cb += kCtxDepth) {
+    for (int64_t cb = 0; cb < nchunks; cb += kDepth) {
         // no early exit: the loop unrolls over the slots (steps past the last
         // chunk wait and reload as the others and add nothing)
 #pragma unroll
-        for (int j = 0; j < kCtxDepth; ++j) {
+        for (int j = 0; j < kDepth; ++j) {
             const int64_t c = cb + j;
             __builtin_amdgcn_s_waitcnt(kWait);
             // every loader's share of chunk c is in; wave 0 has read the slot
             // refilled next (chunk c - 1) and used all of it
             __builtin_amdgcn_s_barrier();
             if (wave != 0) {
-                issue(c + kCtxDepth - 1, ring[(j + kCtxDepth - 1) % kCtxDepth]);
+                issue(c + kDepth - 1, ring[(j + kDepth - 1) % kDepth]);
                 continue;
             }
             const float* vs = ring[j];
-            const float* ps = ring[j] + kCtxChunk * kCtxCh;
+            const float* ps = FUSED ? prob + c * kCtxChunk : ring[j] + kCtxChunk * kCtxCh;
             const int64_t rem = n - c * kCtxChunk;
             const int cnt = static_cast<int>(rem < kCtxChunk ? (rem > 0 ? rem : 0) : kCtxChunk);
             if (cnt == kCtxChunk) {
@@ -979,22 +1038,31 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
         return err;
     }
     const int64_t rows = T * a.heads;
-    if (T == 1 && n0 + 1 <= kSoftmaxLds) {
-        hipLaunchKernelGGL(softmax_decode_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, S, n0 + 1,
-                           n_stride);
-    } else {
-        hipLaunchKernelGGL(softmax_rows_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, S, rows, a.heads, n0,
-                           n_stride);
-    }
-    err = hipGetLastError();
-    if (err != hipSuccess) {
-        return err;
+    // one token: the context kernel by channel groups (32-bit buffer offsets),
+    // with the softmax inside it while the row fits its LDS
+    const bool ctx_decode = T == 1 && a.vh % kCtxCh == 0 && a.cap * a.vh < (int64_t{1} << 29);
+    const bool fused = ctx_decode && n0 + 1 <= kSoftmaxLds;
+    if (!fused) {
+        if (T == 1 && n0 + 1 <= kSoftmaxLds) {
+            hipLaunchKernelGGL(softmax_decode_kernel, dim3(static_cast<unsigned>(a.heads)), dim3(256), 0, s, S,
+                               n0 + 1, n_stride);
+        } else {
+            hipLaunchKernelGGL(softmax_rows_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, S, rows, a.heads, n0,
+                               n_stride);
+        }
+        err = hipGetLastError();
+        if (err != hipSuccess) {
+            return err;
+        }
     }
     const unsigned threads = static_cast<unsigned>((a.vh + 63) / 64 * 64);
-    if (T == 1 && a.vh % kCtxCh == 0 && a.cap * a.vh < (int64_t{1} << 29)) {  // 32-bit buffer offsets
-        hipLaunchKernelGGL(context_decode_kernel, dim3(static_cast<unsigned>(a.heads * (a.vh / kCtxCh))),
-                           dim3(kCtxThreads), 0, s,
-                           S, c.value, ctx, a.vh, a.cap, n0 + 1, n_stride);
+    const dim3 ctx_grid(static_cast<unsigned>(a.heads * (a.vh / kCtxCh)));
+    if (fused) {
+        hipLaunchKernelGGL(context_decode_kernel<true>, ctx_grid, dim3(kCtxThreads), 0, s, S, c.value, ctx, a.vh,
+                           a.cap, n0 + 1, n_stride);
+    } else if (ctx_decode) {
+        hipLaunchKernelGGL(context_decode_kernel<false>, ctx_grid, dim3(kCtxThreads), 0, s, S, c.value, ctx, a.vh,
+                           a.cap, n0 + 1, n_stride);
     } else if (T == 1) {
         hipLaunchKernelGGL(context_kernel<1>, dim3(a.heads, 1), dim3(threads), 0, s, S, c.value, ctx, a.heads, a.vh,
                            a.cap, n0, T, n_stride);

@@ -265,12 +265,15 @@ def test_v2_lite_shapes_prefill_and_decode(q_lora):
         m.close()
 
 
-@pytest.mark.parametrize("prefill", [255, 2303])
+@pytest.mark.parametrize("prefill", [255, 2303, 8191])
 def test_decode_across_value_chunks(prefill):
     """Decode steps whose cached lengths cross the single-token context
     kernel's 256-token chunks: n = 256, 257, 258 (one full chunk, then a
     partial one) and n = 2304, 2305, 2306 (nine chunks, more than its LDS
-    ring holds, so slots are refilled), after a batched prefill."""
+    ring holds, so slots are refilled), after a batched prefill; and n = 8192
+    (the longest row whose softmax runs inside the context launch), 8193 and
+    8194 (the softmax as its own launch, the context kernel with the
+    probabilities in its ring)."""
     d = small_dims(max_positions=prefill + 8)
     announce(f"attention prefill T={prefill} + decode x3 small")
     m = Mla(d, 181)
