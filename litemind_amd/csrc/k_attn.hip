@@ -155,13 +155,19 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
 // + i).  Positions at or past the table store the rows as they are.
 // Rows past the query's (rows2 of them, from w2 into out2) are a second
 // projection of the same input with no rotary step: kv_a's, in the same launch.
+// With NORM (in_dim <= 2048) x is the raw hidden state: each thread loads its
+// rms_norm_kernel elements once, the workgroup forms the inverse from them in
+// that kernel's order and writes (x * inverse) * norm_w into LDS, which the
+// dot products then read.
+template <bool NORM>
 __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __restrict__ w,
                                                              const float* __restrict__ x, float* __restrict__ q,
                                                              int64_t rows, int32_t in_dim, int32_t nope,
                                                              int32_t rope, const float* __restrict__ cos_t,
                                                              const float* __restrict__ sin_t, int64_t pos,
                                                              int64_t max_positions, const uint16_t* __restrict__ w2,
-                                                             float* __restrict__ out2, int64_t rows2) {
+                                                             float* __restrict__ out2, int64_t rows2,
+                                                             const float* __restrict__ norm_w, float eps) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 31;
     const int64_t row_all = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
@@ -169,7 +175,32 @@ __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __r
     const int64_t row = second ? row_all - rows : row_all;
     const bool live = second ? row < rows2 : true;
     const uint16_t* wr = second ? w2 + (live ? row : rows2 - 1) * in_dim : w + row * in_dim;
-    const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
+    float total;
+    if constexpr (NORM) {
+        __shared__ __align__(16) float xs[2048];
+        __shared__ double part[4];
+        float v[8], nw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = static_cast<int>(threadIdx.x) + 256 * u;
+            const int ec = e < in_dim ? e : in_dim - 1;  // unconditional loads
+            v[u] = x[ec];
+            nw[u] = norm_w[ec];
+        }
+        const float inverse = rms_inverse_256_regs(v, in_dim, eps, part);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = static_cast<int>(threadIdx.x) + 256 * u;
+            if (e < in_dim) {
+                const float scaled = v[u] * inverse;
+                xs[e] = scaled * nw[u];
+            }
+        }
+        lds_barrier();
+        total = dot_bf16_lanes32(wr, [&](int e) { return xs[e]; }, in_dim, c);
+    } else {
+        total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
+    }
     const float other = __shfl_xor(total, 32);  // the pair partner's total
     if (!live || c != 0) {
         return;
@@ -979,17 +1010,26 @@ bool query_rope_one_supported(const AttnShape& a, int64_t in_dim) {
 }
 
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
-                                 int64_t pos, hipStream_t s, const uint16_t* w2, float* out2, int64_t rows2) {
-    if (!query_rope_one_supported(a, in_dim) || (w2 != nullptr && !matvec_rows_supported(rows2, in_dim))) {
+                                 int64_t pos, hipStream_t s, const uint16_t* w2, float* out2, int64_t rows2,
+                                 const float* norm_w, float eps) {
+    if (!query_rope_one_supported(a, in_dim) || (w2 != nullptr && !matvec_rows_supported(rows2, in_dim)) ||
+        (norm_w != nullptr && in_dim > 2048)) {
         return hipErrorInvalidValue;
     }
     const int64_t rows = static_cast<int64_t>(a.heads) * (a.nope + a.rope);
     if (w2 == nullptr) {
         rows2 = 0;
     }
-    hipLaunchKernelGGL(query_rope_one_kernel, dim3(blocks_of(rows + rows2, 8)), dim3(256), 0, s, w, x, q, rows,
-                       static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
-                       out2, rows2);
+    const dim3 grid(blocks_of(rows + rows2, 8));
+    if (norm_w != nullptr) {
+        hipLaunchKernelGGL(query_rope_one_kernel<true>, grid, dim3(256), 0, s, w, x, q, rows,
+                           static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
+                           out2, rows2, norm_w, eps);
+    } else {
+        hipLaunchKernelGGL(query_rope_one_kernel<false>, grid, dim3(256), 0, s, w, x, q, rows,
+                           static_cast<int32_t>(in_dim), a.nope, a.rope, a.cos_t, a.sin_t, pos, a.max_positions, w2,
+                           out2, rows2, norm_w, eps);
+    }
     return hipGetLastError();
 }
 

@@ -215,8 +215,9 @@ int ensure_buffer(float** buf, size_t* have, hipStream_t stream, size_t floats) 
 
 // Attention::forward for F tokens that all fit the cache; out = o_proj ctx or
 // out += o_proj ctx.  x [F, H] must not overlap out, except with in_norm: x is
-// then the raw hidden state, normalised here by in_norm into xn_buf [F, H]
-// before anything else reads it, so out may be x itself.
+// then the raw hidden state, normalised here by in_norm (into xn_buf [F, H], or
+// inside the first projection's launch for one token) before anything else
+// reads it, so out may be x itself.
 int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const float* x, int64_t F, int64_t pos0,
                      float* out, int32_t accumulate, const float* in_norm = nullptr, float* xn_buf = nullptr) {
     const lm_mla_config& c = st->cfg;
@@ -256,7 +257,10 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     const bool q_fused = F == 1 && lm::query_rope_one_supported(a, q_in);
     // without the q LoRA, kv_a projects the same x: one launch for both
     const bool kv_a_with_q = q_fused && ql == 0 && lm::matvec_rows_supported(rank + rope, H);
-    if (in_norm != nullptr) {
+    // the input norm inside that launch when it takes the whole row (nothing
+    // else reads x then)
+    const float* norm_in_launch = kv_a_with_q && H <= 2048 ? in_norm : nullptr;
+    if (in_norm != nullptr && norm_in_launch == nullptr) {
         LM_ATT_HIP(lm::launch_rms_norm(x, in_norm, xn_buf, F, static_cast<int32_t>(H), c.rms_norm_eps, stream));
         x = xn_buf;
     }
@@ -268,7 +272,8 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     }
     const uint16_t* q_w = ql == 0 ? L.q_proj : L.q_b;
     if (kv_a_with_q) {
-        LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream, L.kv_a, lat, rank + rope));
+        LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream, L.kv_a, lat, rank + rope,
+                                             norm_in_launch, c.rms_norm_eps));
     } else if (q_fused) {
         LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream));
     } else {

@@ -237,6 +237,28 @@ hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, i
 // at a time (a loop of one load per step waits a round trip per element).
 // Every thread of the 256-thread workgroup calls it; `part` is 4 doubles of
 // LDS.
+// The same inverse from a thread's elements already in registers: v[u] is
+// element threadIdx.x + 256 u (n <= 2048; past n ignored).
+__device__ inline float rms_inverse_256_regs(const float (&v)[8], int n, float eps, double* part) {
+    double sq = 0.0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        if (static_cast<int>(threadIdx.x) + 256 * u < n) {
+            const double d = static_cast<double>(v[u]);
+            sq = sq + d * d;
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        sq += __shfl_xor(sq, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = sq;
+    }
+    __syncthreads();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(n) + static_cast<double>(eps)));
+}
+
 __device__ inline float rms_inverse_256(const float* __restrict__ x, int n, float eps, double* part) {
     double sq = 0.0;
     for (int e0 = static_cast<int>(threadIdx.x); e0 < n; e0 += 8 * 256) {
@@ -375,11 +397,12 @@ hipError_t launch_kv_append(const AttnShape& a, const KvCacheDev& c, const float
 // q_b's) with the rotary step of launch_rope_query applied to its output rows
 // in the same launch; nope % 2 == 0 and matvec_rows_supported.  With w2, a
 // second projection of the same x (rows2 rows, no rotary step, into out2)
-// runs in the same launch.
+// runs in the same launch.  With norm_w (in_dim <= 2048), x is normalised
+// inside the launch first, bit for bit as launch_rms_norm would (eps as there).
 bool query_rope_one_supported(const AttnShape& a, int64_t in_dim);
 hipError_t launch_query_rope_one(const AttnShape& a, const uint16_t* w, const float* x, float* q, int64_t in_dim,
                                  int64_t pos, hipStream_t s, const uint16_t* w2 = nullptr, float* out2 = nullptr,
-                                 int64_t rows2 = 0);
+                                 int64_t rows2 = 0, const float* norm_w = nullptr, float eps = 0.0f);
 // One token: launch_kv_prep, kv_b's projection of its output and
 // launch_kv_append in one launch (every workgroup forms the normalised latent
 // itself); the cache slot `slot`, rotary position `pos`.
