@@ -457,6 +457,82 @@ __global__ __launch_bounds__(kKeyTile) void scores_grouped_kernel(const float* _
     }
 }
 
+// scores_grouped_kernel's sums for one query token (decode), qk_nope +
+// qk_rope <= kScoreTileCh, in tiles of 64 keys: the four waves each load a
+// quarter of the tile's key channels (one round trip, ~48 loads in flight per
+// lane) into LDS as [key][channel], then wave 0 runs each key's two chains
+// (lane = key) in scores_grouped_kernel's order, reading four channels per LDS
+// read.  Four times the workgroups of the 256-key tiles, which at a few hundred
+// cached tokens leave most lanes waiting on several round trips each; used up
+// to kScoreTileMaxKeys keys.
+constexpr int kScoreTile = 64;
+constexpr int kScoreTileCh = 192;
+constexpr int kScoreTileStride = kScoreTileCh + 4;  // floats per key row (16-byte aligned, banks spread)
+constexpr int64_t kScoreTileMaxKeys = 1024;         // longer rows take scores_grouped_kernel<1>
+
+__global__ __launch_bounds__(256) void scores_tile_kernel(const float* __restrict__ q,
+                                                          const float* __restrict__ key_nope,
+                                                          const float* __restrict__ key_rope, float* __restrict__ S,
+                                                          int32_t nope, int32_t rope, int64_t cap, int64_t n,
+                                                          float scale) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float ks[kScoreTile * kScoreTileStride];
+    __shared__ __align__(16) float qs[kScoreTileCh];
+    const int qk = nope + rope;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t key = static_cast<int64_t>(blockIdx.x) * kScoreTile + lane;
+    const int64_t kc = key < n ? key : n - 1;  // lanes past the last key read a valid one
+    if (threadIdx.x < qk) {
+        qs[threadIdx.x] = q[static_cast<int64_t>(h) * qk + threadIdx.x];
+    }
+    const float* kn = key_nope + static_cast<int64_t>(h) * nope * cap + kc;
+    const float* kr = key_rope + kc;
+    // channel d of this lane's key (d < nope: the head's key_nope, else the
+    // shared rotary key); wave w takes channels w, w + 4, ...
+    constexpr int kPer = kScoreTileCh / 4;
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int d = 4 * i + wave;
+        const int dc = d < qk ? d : qk - 1;
+        v[i] = dc < nope ? kn[static_cast<int64_t>(dc) * cap] : kr[static_cast<int64_t>(dc - nope) * cap];
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        ks[lane * kScoreTileStride + 4 * i + wave] = v[i];
+    }
+    lds_barrier();
+    if (wave != 0) {
+        return;
+    }
+    const f4v* k4 = reinterpret_cast<const f4v*>(ks + lane * kScoreTileStride);
+    const f4v* q4 = reinterpret_cast<const f4v*>(qs);
+    float a = 0.0f, b = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < nope / 4; ++i) {
+        const f4v kv = k4[i];
+        const f4v w = q4[i];
+        a = a + w.x * kv.x;
+        a = a + w.y * kv.y;
+        a = a + w.z * kv.z;
+        a = a + w.w * kv.w;
+    }
+#pragma unroll 8
+    for (int i = nope / 4; i < qk / 4; ++i) {
+        const f4v kv = k4[i];
+        const f4v w = q4[i];
+        b = b + w.x * kv.x;
+        b = b + w.y * kv.y;
+        b = b + w.z * kv.z;
+        b = b + w.w * kv.w;
+    }
+    if (key < n) {
+        S[static_cast<int64_t>(h) * n + key] = scale * (a + b);
+    }
+}
+
 // gemm::softmax (src/Gemm.cpp:209-223) on each row (token t, head h) of S,
 // n0 + t + 1 entries: the maximum, expf(s - max) in place with the total
 // accumulated left to right in one chain (each chunk of 64 is added in lane
@@ -1058,7 +1134,12 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
     const int qk = a.nope + a.rope;
     const unsigned tiles = blocks_of(n_stride, kKeyTile);
     const bool grouped = a.nope % kScoreGroup == 0 && a.rope % kScoreGroup == 0 && qk > 0;
-    if (T == 1 && grouped) {
+    // the 64-key tiles where the row is short (measured: 0.5 us faster than the
+    // 256-key tiles near 512 keys, 2.3 us slower near 4K)
+    if (T == 1 && grouped && qk <= kScoreTileCh && n_stride <= kScoreTileMaxKeys) {
+        hipLaunchKernelGGL(scores_tile_kernel, dim3(blocks_of(n_stride, kScoreTile), a.heads), dim3(256), 0, s, q,
+                           c.key_nope, c.key_rope, S, a.nope, a.rope, a.cap, n_stride, scale);
+    } else if (T == 1 && grouped) {
         hipLaunchKernelGGL(scores_grouped_kernel<1>, dim3(tiles, a.heads, 1), dim3(kKeyTile), sizeof(float) * qk, s,
                            q, c.key_nope, c.key_rope, S, a.heads, a.nope, a.rope, a.cap, n0, T, n_stride, scale);
     } else if (grouped) {
