@@ -366,6 +366,12 @@ __global__ __launch_bounds__(kKeyTile) void scores_kernel(const float* __restric
 // chain keeps scores_kernel's order: products rounded, added from channel 0
 // up.  grid: x = key tiles, y = heads, z = token blocks of KQ.
 constexpr int kScoreGroup = 16;
+// scores_tile_kernel's shape (below), and the query width up to which the
+// batched kernel stages its rows in one batch of loads
+constexpr int kScoreTile = 64;
+constexpr int kScoreTileCh = 192;
+constexpr int kScoreTileStride = kScoreTileCh + 4;  // floats per key row (16-byte aligned, banks spread)
+constexpr int64_t kScoreTileMaxKeys = 1024;         // longer rows take scores_grouped_kernel<1>
 
 template <int KQ>
 __global__ __launch_bounds__(kKeyTile) void scores_grouped_kernel(const float* __restrict__ q,
@@ -385,10 +391,30 @@ __global__ __launch_bounds__(kKeyTile) void scores_grouped_kernel(const float* _
     if (key0 >= n_hi) {
         return;  // uniform over the block
     }
-    for (int j = threadIdx.x; j < KQ * qk; j += kKeyTile) {
-        const int iq = j / qk;
-        const int d = j - iq * qk;
-        qs[j] = iq < nq ? q[((i0 + iq) * heads + h) * qk + d] : 0.0f;
+    {
+        // the block's query rows, unconditional loads (tokens past the last
+        // read the last) so a thread's are in flight together
+        constexpr int kPerThread = (KQ * kScoreTileCh + kKeyTile - 1) / kKeyTile;
+        float v[kPerThread];
+#pragma unroll
+        for (int u = 0; u < kPerThread; ++u) {
+            const int j = static_cast<int>(threadIdx.x) + kKeyTile * u;
+            const int jc = j < KQ * qk ? j : KQ * qk - 1;
+            const int iq = jc / qk;
+            const int64_t t = i0 + (iq < nq ? iq : nq - 1);
+            v[u] = q[(t * heads + h) * qk + (jc - iq * qk)];
+        }
+#pragma unroll
+        for (int u = 0; u < kPerThread; ++u) {
+            const int j = static_cast<int>(threadIdx.x) + kKeyTile * u;
+            if (j < KQ * qk) {
+                qs[j] = j / qk < nq ? v[u] : 0.0f;
+            }
+        }
+        for (int j = static_cast<int>(threadIdx.x) + kKeyTile * kPerThread; j < KQ * qk; j += kKeyTile) {
+            const int iq = j / qk;  // rows wider than kScoreTileCh
+            qs[j] = iq < nq ? q[((i0 + iq) * heads + h) * qk + (j - iq * qk)] : 0.0f;
+        }
     }
     __syncthreads();
     const int64_t key = key0 + threadIdx.x;
@@ -465,10 +491,6 @@ __global__ __launch_bounds__(kKeyTile) void scores_grouped_kernel(const float* _
 // read.  Four times the workgroups of the 256-key tiles, which at a few hundred
 // cached tokens leave most lanes waiting on several round trips each; used up
 // to kScoreTileMaxKeys keys.
-constexpr int kScoreTile = 64;
-constexpr int kScoreTileCh = 192;
-constexpr int kScoreTileStride = kScoreTileCh + 4;  // floats per key row (16-byte aligned, banks spread)
-constexpr int64_t kScoreTileMaxKeys = 1024;         // longer rows take scores_grouped_kernel<1>
 
 __global__ __launch_bounds__(256) void scores_tile_kernel(const float* __restrict__ q,
                                                           const float* __restrict__ key_nope,
@@ -554,9 +576,20 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
     }
     const int64_t n = n0 + row / heads + 1;
     float* s = S + row * n_stride;
+    // the maximum with eight loads in flight per lane (a duplicate of the last
+    // score past the end leaves the maximum unchanged)
     float m = -__builtin_inff();
-    for (int64_t c = lane; c < n; c += 64) {
-        m = fmaxf(m, s[c]);
+    for (int64_t cb = lane; cb < n; cb += 8 * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t c = cb + 64 * u;
+            v[u] = s[c < n ? c : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            m = fmaxf(m, v[u]);
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -593,8 +626,21 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(float* S, int64_t row
         }
     }
     const float inverse = total > 0.0f ? 1.0f / total : 0.0f;
-    for (int64_t c = lane; c < n; c += 64) {
-        s[c] = s[c] * inverse;
+    // each lane rescales the values it wrote, eight loads in flight
+    for (int64_t cb = lane; cb < n; cb += 8 * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t c = cb + 64 * u;
+            v[u] = s[c < n ? c : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t c = cb + 64 * u;
+            if (c < n) {
+                s[c] = v[u] * inverse;
+            }
+        }
     }
 }
 
@@ -758,16 +804,28 @@ __global__ __launch_bounds__(256) void context_kernel(const float* __restrict__ 
         acc[iq] = 0.0f;
     }
     for (int64_t c0 = 0; c0 < n_hi; c0 += kChunk) {
-        __syncthreads();
-        for (int j = threadIdx.x; j < KQ * kChunk; j += blockDim.x) {
-            const int iq = j / kChunk;
-            const int64_t key = c0 + (j - iq * kChunk);
-            ps[iq][j - iq * kChunk] =
-                iq < nq && key <= n0 + i0 + iq ? P[((i0 + iq) * heads + h) * n_stride + key] : 0.0f;
-        }
-        __syncthreads();
         const int cend = static_cast<int>(std::min<int64_t>(kChunk, n_hi - c0));
         const int ng = (cend + kG - 1) / kG;
+        __syncthreads();
+        // the chunk's probabilities of the block's tokens, zero where a token
+        // does not see the key, up to the groups' end; the loads are
+        // unconditional (keys < n_hi are inside every row; tokens past the
+        // last read the last) so each thread's eight are in flight together
+        for (int k = threadIdx.x; k < ng * kG; k += blockDim.x) {
+            const int64_t key = c0 + k;
+            const int64_t kc = key < n_hi ? key : n_hi - 1;
+            float v[KQ];
+#pragma unroll
+            for (int iq = 0; iq < KQ; ++iq) {
+                const int64_t t = i0 + (iq < nq ? iq : nq - 1);
+                v[iq] = P[(t * heads + h) * n_stride + kc];
+            }
+#pragma unroll
+            for (int iq = 0; iq < KQ; ++iq) {
+                ps[iq][k] = iq < nq && key <= n0 + i0 + iq ? v[iq] : 0.0f;
+            }
+        }
+        __syncthreads();
         // group g's 16 values; groups past the last reload it and keys past
         // the last read the last (every step issues the same loads)
         auto load = [&](int g, float (&x)[kG]) {
