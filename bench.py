@@ -171,8 +171,22 @@ def run_stack(steps_t1: int, steps_big: int, big_tokens: int, moe_layers: int) -
         ms = ctx.elapsed_ms(e0, e1) / steps
         out[f"t{T}"] = {"tokens": T, "steps": steps, "ms_per_step": round(ms, 4),
                         "value": round(T / (ms / 1e3), 1), "unit": "tokens/s"}
-        dh.free()
         log(f"stack T={T}: {ms:.3f} ms per step")
+        if T > 1:
+            # the same pass replayed from a captured HIP graph
+            graph = ctx.stack_graph_create(0, n - 1, dh, T)
+            ctx.stack_graph_launch(graph)
+            ctx.synchronize()
+            ctx.record(e0)
+            for _ in range(steps):
+                ctx.stack_graph_launch(graph)
+            ctx.record(e1)
+            ctx.synchronize()
+            gms = ctx.elapsed_ms(e0, e1) / steps
+            ctx.stack_graph_destroy(graph)
+            out[f"t{T}"]["graph_ms_per_step"] = round(gms, 4)
+            log(f"stack T={T} as a graph: {gms:.3f} ms per step")
+        dh.free()
     ctx.close()
     return out
 

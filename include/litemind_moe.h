@@ -216,6 +216,21 @@ int lm_permute(lm_context* ctx, const int32_t* topk_index_dev, int64_t tokens, i
  * FFN_l = dense SwiGLU or the MoE block.  hidden_dev [T, H] fp32 is updated in place. */
 int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
                      int32_t path);
+/* The same pass captured once as a HIP graph and replayed (no LiteMind
+ * counterpart; the survey's stack glue "run as a graph"): lm_stack_graph_create
+ * records lm_stack_forward(ctx, first, last, hidden_dev, tokens, path) without
+ * running it, lm_stack_graph_launch replays it on the context's stream (each
+ * replay updates hidden_dev in place, like one lm_stack_forward call), and
+ * lm_stack_graph_destroy frees it.  Only for token counts whose layers all take
+ * the batched path (T >= 2 beyond the single-token kernel's batches; the
+ * single-token kernel tags its hand-offs per launch from the host, which a
+ * replay would repeat) and with stage timing off.  While a graph exists the
+ * context keeps its workspace: a call needing a larger one fails with LM_EINVAL. */
+typedef struct lm_stack_graph lm_stack_graph;
+int lm_stack_graph_create(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev,
+                          int64_t tokens, int32_t path, lm_stack_graph** graph);
+int lm_stack_graph_launch(lm_stack_graph* graph);
+int lm_stack_graph_destroy(lm_stack_graph* graph);
 /* gemm::rms_norm over T rows (src/Gemm.cpp:197-207); out may equal in. */
 int lm_rms_norm(lm_context* ctx, const float* in_dev, const float* weight_dev, float* out_dev, int64_t tokens,
                 int32_t hidden, float epsilon);

@@ -110,6 +110,9 @@ PROTOTYPES = {
     "lm_router_select": [_P, _P, _I64, _P, _P],
     "lm_permute": [_P, _P, _I64, _P, _P, _P, _P],
     "lm_stack_forward": [_P, _I32, _I32, _P, _I64, _I32],
+    "lm_stack_graph_create": [_P, _I32, _I32, _P, _I64, _I32, C.POINTER(C.c_void_p)],
+    "lm_stack_graph_launch": [_P],
+    "lm_stack_graph_destroy": [_P],
     "lm_rms_norm": [_P, _P, _P, _P, _I64, _I32, _F],
     "lm_dense_forward": [_P, _I32, _P, _I64, _P, _I32],
     "lm_gemm_matvec_bf16": [_P, _P, _P, _P, _SZ, _SZ, _F, _I32],
@@ -454,6 +457,20 @@ class Context:
 
     def stack_forward(self, first, last, hidden, tokens, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_stack_forward(self.handle, first, last, _ptr(hidden), tokens, path))
+
+    def stack_graph_create(self, first, last, hidden, tokens, path=PATH_AUTO) -> int:
+        """lm_stack_graph_create: the stack pass recorded as a HIP graph (a handle for
+        stack_graph_launch / stack_graph_destroy)."""
+        out = C.c_void_p()
+        self._check(self.lib.lm_stack_graph_create(self.handle, first, last, _ptr(hidden), tokens, path,
+                                                   C.byref(out)))
+        return out.value
+
+    def stack_graph_launch(self, graph: int) -> None:
+        self._check(self.lib.lm_stack_graph_launch(C.c_void_p(graph)))
+
+    def stack_graph_destroy(self, graph: int) -> None:
+        self._check(self.lib.lm_stack_graph_destroy(C.c_void_p(graph)))
 
     def rms_norm(self, x, weight, out, tokens, hidden, eps) -> None:
         self._check(self.lib.lm_rms_norm(self.handle, _ptr(x), _ptr(weight), _ptr(out), tokens, hidden, eps))

@@ -195,6 +195,7 @@ struct lm_context {
     float* head_logits = nullptr;
     lm::HeadBest* head_partial = nullptr;  // per-block candidates of the greedy choice
     lm::AttnState* attention = nullptr;  // lm_attention_configure: MLA weights, rotary tables, KV caches
+    int32_t graphs = 0;  // live lm_stack_graph captures (they hold the workspace's pointers)
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -332,6 +333,10 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
     Workspace& w = ctx->ws;
     if (w.tokens >= tokens && w.idx != nullptr) {
         return LM_OK;
+    }
+    if (ctx->graphs > 0) {
+        return fail(LM_EINVAL, "a captured stack graph holds the workspace (sized for " + std::to_string(w.tokens) +
+                                   " tokens); destroy it before a call with " + std::to_string(tokens));
     }
     LM_HIP(hipStreamSynchronize(ctx->stream));
     void** ptrs[] = {reinterpret_cast<void**>(&w.idx),     reinterpret_cast<void**>(&w.wts),
@@ -1581,13 +1586,42 @@ int lm_dense_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t
     LM_GUARD_END
 }
 
-int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
-                     int32_t path) {
-    LM_GUARD_BEGIN
+namespace {
+
+// lm_stack_forward's layer loop, the workspace already sized.  Between two
+// batched layers the first one's combine also applies the second one's RMSNorm
+// (and its fp16 copy): bit for bit the separate kernels' results, one pass over
+// the hidden state instead of three.
+int stack_pass(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
+               int32_t path) {
+    bool prenormed = false;
+    for (int32_t l = first_layer; l <= last_layer; ++l) {
+        const bool fuse_next = l < last_layer && lm::combine_norm_supported(ctx->H, ctx->Hp) &&
+                               batched_layer(ctx, l, tokens, path) && batched_layer(ctx, l + 1, tokens, path);
+        const float* next_norm = fuse_next ? ctx->layers[static_cast<size_t>(l + 1)].norm : nullptr;
+        const int rc = ffn_sublayer_fused(ctx, l, hidden_dev, tokens, path, next_norm, prenormed);
+        if (rc != LM_OK) {
+            return rc;
+        }
+        prenormed = fuse_next;
+    }
+    return LM_OK;
+}
+
+int check_stack_args(lm_context* ctx, int32_t first_layer, int32_t last_layer) {
     int rc = check_layer(ctx, first_layer);
     if (rc == LM_OK) {
         rc = check_layer(ctx, last_layer);
     }
+    return rc;
+}
+
+}  // namespace
+
+int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
+                     int32_t path) {
+    LM_GUARD_BEGIN
+    int rc = check_stack_args(ctx, first_layer, last_layer);
     if (rc != LM_OK) {
         return rc;
     }
@@ -1598,20 +1632,89 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
     if (rc != LM_OK) {
         return rc;
     }
-    // Between two batched layers the first one's combine also applies the
-    // second one's RMSNorm (and its fp16 copy): bit for bit the separate
-    // kernels' results, one pass over the hidden state instead of three.
-    bool prenormed = false;
-    for (int32_t l = first_layer; l <= last_layer; ++l) {
-        const bool fuse_next = l < last_layer && lm::combine_norm_supported(ctx->H, ctx->Hp) &&
-                               batched_layer(ctx, l, tokens, path) && batched_layer(ctx, l + 1, tokens, path);
-        const float* next_norm = fuse_next ? ctx->layers[static_cast<size_t>(l + 1)].norm : nullptr;
-        rc = ffn_sublayer_fused(ctx, l, hidden_dev, tokens, path, next_norm, prenormed);
-        if (rc != LM_OK) {
-            return rc;
-        }
-        prenormed = fuse_next;
+    return stack_pass(ctx, first_layer, last_layer, hidden_dev, tokens, path);
+    LM_GUARD_END
+}
+
+struct lm_stack_graph {
+    lm_context* ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int lm_stack_graph_create(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev,
+                          int64_t tokens, int32_t path, lm_stack_graph** graph) {
+    LM_GUARD_BEGIN
+    if (graph == nullptr) {
+        return fail(LM_EINVAL, "null graph output");
     }
+    *graph = nullptr;
+    int rc = check_stack_args(ctx, first_layer, last_layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (first_layer > last_layer || tokens <= 0 || hidden_dev == nullptr) {
+        return fail(LM_EINVAL, "empty layer range, bad token count or null hidden state");
+    }
+    if (ctx->timing) {
+        return fail(LM_EINVAL, "lm_stack_graph_create: stage timing is on (its events are host state a replay "
+                               "would not update)");
+    }
+    for (int32_t l = first_layer; l <= last_layer; ++l) {
+        const Layer& L = ctx->layers[static_cast<size_t>(l)];
+        if (!L.dense && takes_decode_path(ctx, L, tokens, path)) {
+            return fail(LM_EINVAL, "lm_stack_graph_create: at " + std::to_string(tokens) + " tokens layer " +
+                                       std::to_string(l) +
+                                       " runs the single-token kernel, whose hand-off words carry a tag the host "
+                                       "advances per launch (a replay would repeat it)");
+        }
+    }
+    rc = ensure_workspace(ctx, tokens);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    LM_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    rc = stack_pass(ctx, first_layer, last_layer, hidden_dev, tokens, path);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(ctx->stream, &g);
+    if (rc != LM_OK || end != hipSuccess) {
+        if (g != nullptr) {
+            (void)hipGraphDestroy(g);
+        }
+        return rc != LM_OK ? rc : fail(LM_EHIP, std::string("stack capture: ") + hipGetErrorString(end));
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (inst != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(LM_EHIP, std::string("stack graph instantiate: ") + hipGetErrorString(inst));
+    }
+    *graph = new lm_stack_graph{ctx, g, exec};
+    ++ctx->graphs;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_stack_graph_launch(lm_stack_graph* graph) {
+    LM_GUARD_BEGIN
+    if (graph == nullptr) {
+        return fail(LM_EINVAL, "null graph");
+    }
+    LM_HIP(hipGraphLaunch(graph->exec, graph->ctx->stream));
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_stack_graph_destroy(lm_stack_graph* graph) {
+    LM_GUARD_BEGIN
+    if (graph == nullptr) {
+        return LM_OK;
+    }
+    LM_HIP(hipStreamSynchronize(graph->ctx->stream));  // no replay may still read the workspace
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    --graph->ctx->graphs;
+    delete graph;
     return LM_OK;
     LM_GUARD_END
 }

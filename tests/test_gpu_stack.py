@@ -230,3 +230,46 @@ def test_stack_fused_norm_is_bit_exact(stack_ctx, T, path_name):
         ones = np.ones(dims.hidden, np.float32)
         for l in range(1 + MOE_LAYERS):
             ctx.upload_norm(l, ones)
+
+
+@pytest.mark.parametrize("T", [48, 300])
+def test_stack_graph_replays_match_eager(stack_ctx, T):
+    """lm_stack_graph_create records a whole stack pass as a HIP graph; three
+    replays, with eager uploads, an eager pass and synchronisations between
+    them, each give the eager pass's bits.  While the graph exists a call that
+    needs a larger workspace fails instead of moving memory the graph uses; a
+    token count whose layers take the single-token kernel is refused."""
+    from litemind_amd import LmError
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    announce(f"stack graph T={T}: replays against the eager pass")
+    h0 = wl.tokens(wl.MASTER_SEED + 91 + T, T, dims.hidden)
+    h1 = wl.tokens(wl.MASTER_SEED + 92 + T, T, dims.hidden)
+    eager = _run(ctx, h0)
+    eager_other = _run(ctx, h1)
+    dh = ctx.to_device(h0)
+    graph = ctx.stack_graph_create(0, MOE_LAYERS, dh, T)
+    try:
+        for rep in range(3):
+            dh.upload(h0)
+            ctx.synchronize()
+            ctx.stack_graph_launch(graph)
+            ctx.synchronize()
+            got = dh.download()
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {rep}"
+            # eager work on the same workspace between the replays
+            assert np.array_equal(_run(ctx, h1).view(np.uint32), eager_other.view(np.uint32))
+        big = np.zeros((8192, dims.hidden), np.float32)
+        dbig = ctx.to_device(big)
+        with pytest.raises(LmError):
+            ctx.stack_forward(0, MOE_LAYERS, dbig, 8192)
+        dbig.free()
+    finally:
+        ctx.stack_graph_destroy(graph)
+        dh.free()
+    d1 = ctx.to_device(h0[:1])
+    with pytest.raises(LmError):
+        ctx.stack_graph_create(0, MOE_LAYERS, d1, 1)
+    d1.free()
+
