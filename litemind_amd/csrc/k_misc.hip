@@ -7,7 +7,11 @@ namespace {
 // y[t] = sum over ranks r of w[t,r] * down[slot(t,r)], accumulated in rank order
 // as out += w * dot (src/DeepSeekRunner.cpp:277-284, src/Gemm.cpp:172, which GCC
 // fuses), then + shared (:285-288), optionally + residual (gemm::axpy, :290).
-// A gather in a fixed order per token: deterministic, no float atomics.
+// A gather in a fixed order per token: deterministic, no float atomics.  With
+// K > 0 (the top-k known when compiling) the K rows' loads are all in flight
+// before the first addition; K = 0 reads the top-k at run time, one row at a
+// time.  The additions are the same either way.
+template <int K>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int quads = a.hidden / 4;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -17,14 +21,32 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int64_t t = i / quads;
     const int c = static_cast<int>(i - t * quads) * 4;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int r = 0; r < a.top_k; ++r) {
-        const int64_t s = a.slot_of[t * a.top_k + r];
-        const float w = a.wts[t * a.top_k + r];
-        const float4 d = *reinterpret_cast<const float4*>(a.down_out + s * a.hidden + c);
-        acc.x = __builtin_fmaf(w, d.x, acc.x);
-        acc.y = __builtin_fmaf(w, d.y, acc.y);
-        acc.z = __builtin_fmaf(w, d.z, acc.z);
-        acc.w = __builtin_fmaf(w, d.w, acc.w);
+    if constexpr (K > 0) {
+        float4 d[K];
+        float w[K];
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+            const int64_t s = a.slot_of[t * K + r];
+            w[r] = a.wts[t * K + r];
+            d[r] = *reinterpret_cast<const float4*>(a.down_out + s * a.hidden + c);
+        }
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+            acc.x = __builtin_fmaf(w[r], d[r].x, acc.x);
+            acc.y = __builtin_fmaf(w[r], d[r].y, acc.y);
+            acc.z = __builtin_fmaf(w[r], d[r].z, acc.z);
+            acc.w = __builtin_fmaf(w[r], d[r].w, acc.w);
+        }
+    } else {
+        for (int r = 0; r < a.top_k; ++r) {
+            const int64_t s = a.slot_of[t * a.top_k + r];
+            const float w = a.wts[t * a.top_k + r];
+            const float4 d = *reinterpret_cast<const float4*>(a.down_out + s * a.hidden + c);
+            acc.x = __builtin_fmaf(w, d.x, acc.x);
+            acc.y = __builtin_fmaf(w, d.y, acc.y);
+            acc.z = __builtin_fmaf(w, d.z, acc.z);
+            acc.w = __builtin_fmaf(w, d.w, acc.w);
+        }
     }
     if (a.has_shared) {
         const int64_t s = a.tokens * a.top_k + t;
@@ -53,60 +75,115 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 // forms it (16-byte loads, thread t owning columns 4 t .. 4 t + 3 of every
 // 1024-column step) and staged in LDS, where thread t then adds the squares of
 // columns t, t + 256, ... in rms_norm_kernel's order.  hidden % 4 == 0 and
-// hidden <= kCombineNormMax.
+// hidden <= kCombineNormMax.  With K > 0 (the top-k known when compiling) and
+// STEPS * 1024 >= hidden_p, every rank's slot and weight is read first and all
+// rows' loads (ranks, shared, residual; clamped to column 0 past the row's
+// end) are in flight together before the first addition; K = 0 reads the top-k
+// at run time, one rank's loads at a time.  The additions are the same either
+// way.
 constexpr int kCombineNormMax = 8192;
 constexpr int kCombineNormSteps = kCombineNormMax / 1024;
 
+template <int K, int STEPS>
 __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
-    __shared__ float row[kCombineNormMax];
+    __shared__ float row[STEPS * 1024];
     __shared__ double part[4];
     const int64_t t = blockIdx.x;
     const int H = a.hidden;
     const int tid = threadIdx.x;
     const float* __restrict__ dout = a.down_out;
-    float4 y[kCombineNormSteps];
+    float4 y[STEPS];
 #pragma unroll
-    for (int k = 0; k < kCombineNormSteps; ++k) {
+    for (int k = 0; k < STEPS; ++k) {
         y[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     // every load is issued before any store (y may be the residual)
-    for (int r = 0; r < a.top_k; ++r) {
-        const int64_t slot = a.slot_of[t * a.top_k + r];
-        const float w = a.wts[t * a.top_k + r];
+    if constexpr (K > 0) {
+        int64_t slot[K];
+        float wt[K];
 #pragma unroll
-        for (int k = 0; k < kCombineNormSteps; ++k) {
+        for (int r = 0; r < K; ++r) {
+            slot[r] = a.slot_of[t * K + r];
+            wt[r] = a.wts[t * K + r];
+        }
+        const float* shared_row = a.has_shared ? dout + (a.tokens * K + t) * H : dout;
+        const float* residual_row = a.residual != nullptr ? a.residual + t * H : dout;
+        float4 d[K][STEPS], sh[STEPS], res[STEPS];
+#pragma unroll
+        for (int k = 0; k < STEPS; ++k) {
             const int c = 1024 * k + 4 * tid;
-            if (c < H) {
-                const float4 d = *reinterpret_cast<const float4*>(dout + slot * H + c);
-                y[k].x = __builtin_fmaf(w, d.x, y[k].x);
-                y[k].y = __builtin_fmaf(w, d.y, y[k].y);
-                y[k].z = __builtin_fmaf(w, d.z, y[k].z);
-                y[k].w = __builtin_fmaf(w, d.w, y[k].w);
+            const int cc = c < H ? c : 0;
+#pragma unroll
+            for (int r = 0; r < K; ++r) {
+                d[r][k] = *reinterpret_cast<const float4*>(dout + slot[r] * H + cc);
+            }
+            sh[k] = *reinterpret_cast<const float4*>(shared_row + cc);
+            res[k] = *reinterpret_cast<const float4*>(residual_row + cc);
+        }
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                y[k].x = __builtin_fmaf(wt[r], d[r][k].x, y[k].x);
+                y[k].y = __builtin_fmaf(wt[r], d[r][k].y, y[k].y);
+                y[k].z = __builtin_fmaf(wt[r], d[r][k].z, y[k].z);
+                y[k].w = __builtin_fmaf(wt[r], d[r][k].w, y[k].w);
             }
         }
-    }
 #pragma unroll
-    for (int k = 0; k < kCombineNormSteps; ++k) {
-        const int c = 1024 * k + 4 * tid;
-        if (c < H) {
+        for (int k = 0; k < STEPS; ++k) {
             if (a.has_shared) {
-                const float4 d = *reinterpret_cast<const float4*>(dout + (a.tokens * a.top_k + t) * H + c);
-                y[k].x = y[k].x + d.x;
-                y[k].y = y[k].y + d.y;
-                y[k].z = y[k].z + d.z;
-                y[k].w = y[k].w + d.w;
+                y[k].x = y[k].x + sh[k].x;
+                y[k].y = y[k].y + sh[k].y;
+                y[k].z = y[k].z + sh[k].z;
+                y[k].w = y[k].w + sh[k].w;
             }
             if (a.residual != nullptr) {
-                const float4 h = *reinterpret_cast<const float4*>(a.residual + t * H + c);
-                y[k].x = h.x + y[k].x;
-                y[k].y = h.y + y[k].y;
-                y[k].z = h.z + y[k].z;
-                y[k].w = h.w + y[k].w;
+                y[k].x = res[k].x + y[k].x;
+                y[k].y = res[k].y + y[k].y;
+                y[k].z = res[k].z + y[k].z;
+                y[k].w = res[k].w + y[k].w;
+            }
+        }
+    } else {
+        for (int r = 0; r < a.top_k; ++r) {
+            const int64_t slot = a.slot_of[t * a.top_k + r];
+            const float w = a.wts[t * a.top_k + r];
+#pragma unroll
+            for (int k = 0; k < STEPS; ++k) {
+                const int c = 1024 * k + 4 * tid;
+                if (c < H) {
+                    const float4 d = *reinterpret_cast<const float4*>(dout + slot * H + c);
+                    y[k].x = __builtin_fmaf(w, d.x, y[k].x);
+                    y[k].y = __builtin_fmaf(w, d.y, y[k].y);
+                    y[k].z = __builtin_fmaf(w, d.z, y[k].z);
+                    y[k].w = __builtin_fmaf(w, d.w, y[k].w);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < STEPS; ++k) {
+            const int c = 1024 * k + 4 * tid;
+            if (c < H) {
+                if (a.has_shared) {
+                    const float4 d = *reinterpret_cast<const float4*>(dout + (a.tokens * a.top_k + t) * H + c);
+                    y[k].x = y[k].x + d.x;
+                    y[k].y = y[k].y + d.y;
+                    y[k].z = y[k].z + d.z;
+                    y[k].w = y[k].w + d.w;
+                }
+                if (a.residual != nullptr) {
+                    const float4 h = *reinterpret_cast<const float4*>(a.residual + t * H + c);
+                    y[k].x = h.x + y[k].x;
+                    y[k].y = h.y + y[k].y;
+                    y[k].z = h.z + y[k].z;
+                    y[k].w = h.w + y[k].w;
+                }
             }
         }
     }
 #pragma unroll
-    for (int k = 0; k < kCombineNormSteps; ++k) {
+    for (int k = 0; k < STEPS; ++k) {
         const int c = 1024 * k + 4 * tid;
         if (c < H) {
             *reinterpret_cast<float4*>(a.y + t * H + c) = y[k];
@@ -140,7 +217,7 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
         if (c < H) {
             float4 yy = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int kk = 0; kk < kCombineNormSteps; ++kk) {
+            for (int kk = 0; kk < STEPS; ++kk) {
                 if (kk == k) {
                     yy = y[kk];
                 }
@@ -464,11 +541,21 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
         if (a.xnorm == nullptr || !combine_norm_supported(a.hidden, a.hidden_p)) {
             return hipErrorInvalidValue;
         }
-        hipLaunchKernelGGL(combine_norm_kernel, dim3(static_cast<unsigned>(a.tokens)), dim3(256), 0, s, a);
+        if (a.top_k == 6 && a.hidden_p <= 2048) {
+            hipLaunchKernelGGL((combine_norm_kernel<6, 2>), dim3(static_cast<unsigned>(a.tokens)), dim3(256), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((combine_norm_kernel<0, kCombineNormSteps>), dim3(static_cast<unsigned>(a.tokens)),
+                               dim3(256), 0, s, a);
+        }
         return hipGetLastError();
     }
     const int64_t n = a.tokens * (a.hidden / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    if (a.top_k == 6) {
+        hipLaunchKernelGGL(combine_kernel<6>, grid, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(combine_kernel<0>, grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
