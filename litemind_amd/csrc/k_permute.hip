@@ -120,8 +120,14 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
     if (arrived != static_cast<uint32_t>(G - 1) || threadIdx.x >= 64) {
         return;
     }
-    // The last workgroup: lane e scans expert e's counts over the segments (in
-    // batches of 8 loads), then the totals over the experts in expert order.
+    // The last workgroup: lane e scans expert e's counts over the segments,
+    // then the totals over the experts in expert order.  Up to kScanRegs
+    // segments the counts are loaded at once (clamped, unconditional loads) and
+    // the bases kept in registers, so every base is stored once, offset
+    // included; beyond that in batches of 8 loads, the relative bases stored
+    // and then offset.
+    constexpr int kScanRegs = 32;
+    const bool in_regs = G <= kScanRegs;
     int carry = 0, carry_active = 0;
     const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
@@ -129,7 +135,22 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
         const int e = lane + 64 * j;
         const bool valid = e < E;
         int tot = 0;
-        for (int g0 = 0; g0 < G; g0 += 8) {
+        int rel[kScanRegs];
+        if (in_regs) {
+            // lanes past E read words of their own column that no one wrote
+            // (inside the segment table) and count them as zero
+            int c[kScanRegs];
+#pragma unroll
+            for (int q = 0; q < kScanRegs; ++q) {
+                c[q] = load_agent(seg + (q < G ? q : G - 1) * NE + e);
+            }
+#pragma unroll
+            for (int q = 0; q < kScanRegs; ++q) {
+                rel[q] = tot;
+                tot += valid && q < G ? c[q] : 0;
+            }
+        }
+        for (int g0 = 0; !in_regs && g0 < G; g0 += 8) {
             int c[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -152,10 +173,19 @@ __global__ __launch_bounds__(kThreads) void permute_count_kernel(PermuteArgs a) 
             }
         }
         const int off = carry + incl - tot;
-        if (valid) {
+        if (valid && in_regs) {
+#pragma unroll
+            for (int q = 0; q < kScanRegs; ++q) {
+                if (q < G) {
+                    seg[q * NE + e] = rel[q] + off;
+                }
+            }
+        } else if (valid) {
             for (int sg = 0; sg < G; ++sg) {
                 seg[sg * NE + e] += off;
             }
+        }
+        if (valid) {
             a.rb.counts[e] = tot;
             a.rb.offsets[e] = off;
         }
