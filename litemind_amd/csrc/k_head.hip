@@ -365,6 +365,11 @@ __global__ __launch_bounds__(256) void matvec_tokens_kernel(const uint16_t* __re
 // The same dot product for one token (the projections of a decode step): 32
 // lanes per row (dot_bf16_lanes32), two rows per wave, so even a 576-row
 // projection spreads over 72 workgroups.
+// STEPS > 0: in_dim == 32 STEPS, and every step's weight word and activation
+// is loaded before the first multiply-add (the whole matrix in flight at once
+// when there are few rows); the chain and the lane reduction are
+// dot_bf16_lanes32's.
+template <int STEPS>
 __global__ __launch_bounds__(256) void matvec_one_kernel(const uint16_t* __restrict__ w, const float* __restrict__ x,
                                                          float* out, int64_t rows, int32_t in_dim, float scale,
                                                          int32_t accumulate) {
@@ -373,7 +378,29 @@ __global__ __launch_bounds__(256) void matvec_one_kernel(const uint16_t* __restr
     const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
     const bool live = row < rows;
     const uint16_t* wr = w + (live ? row : rows - 1) * in_dim;
-    const float total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
+    float total;
+    if constexpr (STEPS > 0) {
+        uint32_t word[STEPS];
+        float xv[STEPS];
+        const uint32_t* w32 = reinterpret_cast<const uint32_t*>(wr) + (c >> 1);
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {
+            word[u] = w32[16 * u];
+            xv[u] = x[32 * u + c];
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < STEPS; ++u) {
+            acc = __builtin_fmaf(bits_float((c & 1) != 0 ? (word[u] & 0xffff0000u) : (word[u] << 16)), xv[u], acc);
+        }
+        const float t1 = acc + __shfl_xor(acc, 8);
+        const float t2 = t1 + __shfl_xor(t1, 16);
+        const float t3 = t2 + __shfl_xor(t2, 4);
+        const float t4 = t3 + __shfl_xor(t3, 2);
+        total = t4 + __shfl_xor(t4, 1);
+    } else {
+        total = dot_bf16_lanes32(wr, [&](int e) { return x[e]; }, in_dim, c);
+    }
     if (live && c == 0) {
         out[row] = accumulate ? __builtin_fmaf(scale, total, out[row]) : total;
     }
@@ -460,8 +487,13 @@ hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, i
         return hipErrorInvalidValue;
     }
     if (tokens == 1) {
-        hipLaunchKernelGGL(matvec_one_kernel, dim3(static_cast<unsigned>((rows + 7) / 8)), dim3(256), 0, s, w, x, out,
-                           rows, static_cast<int32_t>(in_dim), scale, accumulate);
+        if (in_dim == 2048) {
+            hipLaunchKernelGGL(matvec_one_kernel<64>, dim3(static_cast<unsigned>((rows + 7) / 8)), dim3(256), 0, s, w,
+                               x, out, rows, static_cast<int32_t>(in_dim), scale, accumulate);
+        } else {
+            hipLaunchKernelGGL(matvec_one_kernel<0>, dim3(static_cast<unsigned>((rows + 7) / 8)), dim3(256), 0, s, w, x,
+                               out, rows, static_cast<int32_t>(in_dim), scale, accumulate);
+        }
         return hipGetLastError();
     }
     if (tokens > kHeadTokens && in_dim % 64 == 0) {
