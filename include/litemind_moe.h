@@ -70,8 +70,13 @@ int lm_version(int32_t* major, int32_t* minor);
 /* Replaces DeepSeekRunner::load's MoeRouter(config) / ExpertCache::configure
  * (src/DeepSeekRunner.cpp:361-362): one context per GPU owns the resident weights. */
 int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** out);
+/* LM_EINVAL (nothing freed) while stack graphs captured on the context are
+ * alive: lm_stack_graph_destroy each of them first. */
 int lm_context_destroy(lm_context* ctx);
 int lm_synchronize(lm_context* ctx);
+/* The context's HIP stream (a hipStream_t), so a caller can order its own work
+ * with the context's (events, stream waits).  No LiteMind counterpart. */
+int lm_context_stream(lm_context* ctx, void** out_stream);
 /* The configuration the context was created with. */
 int lm_context_config(lm_context* ctx, lm_moe_config* out);
 
@@ -180,18 +185,24 @@ int lm_moe_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t t
                    float* logits_dev, int32_t path);
 
 /* No counterpart in LiteMind: lm_moe_forward for callers that cannot allocate
- * device memory (code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc).  The same MoE block, each token through the
- * single-token kernel in turn (the LM_PATH_AUTO kernel of one to three
- * tokens), with every scratch word in one fixed device array of 2 MiB per
- * GPU instead of the context's workspace: the call makes no hipMalloc, hipFree
- * or other allocating call.  The array belongs to the GPU, not to the context:
- * calls on one GPU that overlap (other threads, other contexts' streams) race,
- * and a wait that gave up is reported by the next lm_synchronize or
- * lm_copy_d2h of any context on that GPU.  LM_EINVAL for a layer whose shape
- * has no single-token kernel (lm_moe_forward runs those) or whose scratch
- * would not fit the array.  topk_index_dev, topk_weight_dev and logits_dev may
- * be NULL.  Asynchronous. */
+ * device memory (tight serving loops, harnesses that forbid hipMalloc).  The
+ * same MoE block, each token through the single-token kernel in turn (the
+ * LM_PATH_AUTO kernel of one to three tokens), with every scratch word in one
+ * fixed device array of 2 MiB per GPU instead of the context's workspace: the
+ * call makes no hipMalloc, hipFree or other allocating call.  The array belongs
+ * to the GPU, not to the context: every call on one GPU makes its context's
+ * stream wait for the previous call's launches (a per-GPU event created at the
+ * first lm_context_create on the GPU), so calls from several contexts run one
+ * after another on the GPU.  Each call overwrites the array, which holds only
+ * scratch (and the selection when topk_index_dev / topk_weight_dev are NULL);
+ * outputs go to the caller's buffers.  A wait that gave up
+ * is reported by the next lm_synchronize or lm_copy_d2h of any context on that
+ * GPU.  Graph capture is not supported: the kernel's hand-off words carry a
+ * parity and a tag the host advances per launch, which a replay would repeat;
+ * a call while the context's stream is being captured returns LM_EINVAL.
+ * LM_EINVAL too for a layer whose shape has no single-token kernel
+ * (lm_moe_forward runs those) or whose scratch would not fit the array.
+ * topk_index_dev, topk_weight_dev and logits_dev may be NULL.  Asynchronous. */
 int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, float* y_dev,
                            const float* logit_bias_dev, int32_t* topk_index_dev, float* topk_weight_dev,
                            float* logits_dev);
@@ -204,6 +215,19 @@ int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens
 /* MoeRouter::select alone on given logits [T, E] (src/MoeRouter.cpp:54-107). */
 int lm_router_select(lm_context* ctx, const float* logits_dev, int64_t tokens, int32_t* topk_index_dev,
                      float* topk_weight_dev);
+/* The grouped SwiGLU alone: feed_forward (src/DeepSeekRunner.cpp:228-240) of
+ * every (token, expert) assignment of the routing topk_index_dev [T, k], and
+ * of the fused shared expert, without routing weights or combine.
+ *   out_dev [T*k + T, H] fp32: row t*k + r = W_down(silu(W_gate x_t) * (W_up x_t))
+ *           of expert topk_index[t, r]; row T*k + t the shared expert's output
+ *           for token t (zero when the layer has no shared expert).
+ * The tokens are grouped by lm_permute's canonical permutation; path
+ * LM_PATH_GEMV (fp32 activations) or LM_PATH_MFMA (fp16 operands, fp32
+ * accumulation); LM_PATH_AUTO picks as lm_moe_forward's batched path does.
+ * Every expert id is checked on the host first (a synchronous copy of the T*k
+ * ids; LM_EINVAL for one outside [0, E)); the rest is asynchronous. */
+int lm_grouped_swiglu(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens,
+                      const int32_t* topk_index_dev, float* out_dev, int32_t path);
 /* Canonical expert-major permutation of the T*k selections (no LiteMind
  * counterpart: LiteMind visits one token's selections in rank order,
  * src/DeepSeekRunner.cpp:277-284).  counts [E], offsets [E+1], perm [T*k]
@@ -221,7 +245,10 @@ int lm_stack_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, f
  * records lm_stack_forward(ctx, first, last, hidden_dev, tokens, path) without
  * running it, lm_stack_graph_launch replays it on the context's stream (each
  * replay updates hidden_dev in place, like one lm_stack_forward call), and
- * lm_stack_graph_destroy frees it.  Only for token counts whose layers all take
+ * lm_stack_graph_destroy frees it.  Destroy every graph before its context
+ * (lm_context_destroy refuses while one is alive).  A replay reads the layers'
+ * current weights; lm_stack_graph_launch returns LM_ENOTRES when a layer of its
+ * range was uploaded since and not finalized again.  Only for token counts whose layers all take
  * the batched path (T >= 2 beyond the single-token kernel's batches; the
  * single-token kernel tags its hand-offs per launch from the host, which a
  * replay would repeat) and with stage timing off.  While a graph exists the

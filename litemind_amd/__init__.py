@@ -109,6 +109,8 @@ PROTOTYPES = {
     "lm_router": [_P, _I32, _P, _I64, _P, _P, _P, _P],
     "lm_router_select": [_P, _P, _I64, _P, _P],
     "lm_permute": [_P, _P, _I64, _P, _P, _P, _P],
+    "lm_grouped_swiglu": [_P, _I32, _P, _I64, _P, _P, _I32],
+    "lm_context_stream": [_P, _P],
     "lm_stack_forward": [_P, _I32, _I32, _P, _I64, _I32],
     "lm_stack_graph_create": [_P, _I32, _I32, _P, _I64, _I32, C.POINTER(C.c_void_p)],
     "lm_stack_graph_launch": [_P],
@@ -454,6 +456,17 @@ class Context:
     def permute(self, idx, tokens, counts, offsets, perm, slot_of) -> None:
         self._check(self.lib.lm_permute(self.handle, _ptr(idx), tokens, _ptr(counts), _ptr(offsets), _ptr(perm),
                                         _ptr(slot_of)))
+
+    def grouped_swiglu(self, layer, x, tokens, idx, out, path=PATH_AUTO) -> None:
+        """lm_grouped_swiglu: per-assignment FFN outputs [T*k + T, H] (routed rows in
+        assignment order, then the shared rows) for the routing idx [T, k]."""
+        self._check(self.lib.lm_grouped_swiglu(self.handle, layer, _ptr(x), tokens, _ptr(idx), _ptr(out), path))
+
+    def stream(self) -> int:
+        """The context's hipStream_t (lm_context_stream)."""
+        out = C.c_void_p()
+        self._check(self.lib.lm_context_stream(self.handle, C.byref(out)))
+        return out.value or 0
 
     def stack_forward(self, first, last, hidden, tokens, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_stack_forward(self.handle, first, last, _ptr(hidden), tokens, path))

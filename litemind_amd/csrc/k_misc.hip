@@ -496,6 +496,28 @@ __global__ __launch_bounds__(256) void transpose_u16_kernel(const uint16_t* __re
     }
 }
 
+// out[a] = down_out[slot_of[a]] for the T*K routed assignments (assignment
+// order), then the T shared rows as they are; float4 per thread, H % 4 == 0.
+// The shared rows are zero when the layer has none.
+__global__ __launch_bounds__(256) void gather_slots_kernel(const float* __restrict__ down_out,
+                                                           const int32_t* __restrict__ slot_of, float* __restrict__ out,
+                                                           int64_t assignments, int64_t rows, int32_t hidden,
+                                                           int32_t has_shared) {
+    const int64_t q = hidden / 4;
+    const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i >= rows * q) {
+        return;
+    }
+    const int64_t r = i / q, c = i % q;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (r < assignments) {
+        v = reinterpret_cast<const float4*>(down_out + static_cast<int64_t>(slot_of[r]) * hidden)[c];
+    } else if (has_shared) {
+        v = reinterpret_cast<const float4*>(down_out + r * hidden)[c];
+    }
+    reinterpret_cast<float4*>(out + r * hidden)[c] = v;
+}
+
 }  // namespace
 
 hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
@@ -526,6 +548,21 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
     const int64_t units = n / 8;
     hipLaunchKernelGGL(to_f16_rows_kernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0, s, x, x16,
                        rows, cols, cols_p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_slots(const float* down_out, const int32_t* slot_of, float* out, int64_t assignments,
+                               int64_t tokens, int32_t hidden, int32_t has_shared, hipStream_t s) {
+    const int64_t rows = assignments + tokens;
+    if (rows <= 0) {
+        return hipSuccess;
+    }
+    if (hidden % 4 != 0) {
+        return hipErrorInvalidValue;
+    }
+    const int64_t n = rows * (hidden / 4);
+    hipLaunchKernelGGL(gather_slots_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, down_out,
+                       slot_of, out, assignments, rows, hidden, has_shared);
     return hipGetLastError();
 }
 

@@ -136,10 +136,14 @@ static_assert(kStaticAct < kStaticPart && kStaticPart < kStaticWords, "static sc
 static __device__ __align__(256) uint32_t scratch[kStaticWords];
 
 constexpr int kMaxDevices = 64;
-// Per device: the array's address and the state the single-token kernel keeps
-// across launches on these words.  Every call on one GPU shares them.
+// Per device: the array's address, the state the single-token kernel keeps
+// across launches on these words, and an event recorded after the last call's
+// launches.  Every call on one GPU shares them: each call makes its context's
+// stream wait for that event before its first launch, so calls from different
+// contexts (streams) run one after another on the GPU, never interleaved.
 struct StaticScratch {
     uint32_t* ptr = nullptr;
+    hipEvent_t last = nullptr;
     int32_t parity = 0;
     uint32_t seq = 0;
     bool pending = false;
@@ -435,11 +439,9 @@ lm::RouteBufs route_bufs(lm_context* ctx, int32_t* idx, float* wts) {
     return rb;
 }
 
-// Expert kernels + combine for a layer whose routing is in rb (or a dense FFN).
-// next_norm: the next stack layer's RMSNorm weight; the combine then also
-// writes that layer's input (ws.xnorm, and ws.x16 when the MFMA path follows).
-int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, int64_t T, const lm::RouteBufs& rb,
-                float* y, const float* residual, bool mfma, const float* next_norm = nullptr) {
+// The expert kernels' arguments for a layer whose routing is in rb (or a dense FFN).
+lm::ExpertArgs expert_args(lm_context* ctx, const Layer& L, const float* x, const _Float16* x16, int64_t T,
+                           const lm::RouteBufs& rb) {
     lm::ExpertArgs ea{};
     ea.groups.gu = reinterpret_cast<const uint16_t* const*>(L.table);
     const int ng = L.dense ? 1 : ctx->E + 1;
@@ -468,6 +470,12 @@ int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, 
         ea.shared_inter_p = L.shared_present ? ctx->Sp : 0;
         ea.has_shared = L.shared_present ? 1 : 0;
     }
+    return ea;
+}
+
+// Gate/up then down of every group into ws.down_out (one row per slot, then
+// the shared rows), with stage marks 2 and 3 before each launch.
+int launch_expert_kernels(lm_context* ctx, const Layer& L, const lm::ExpertArgs& ea, int64_t T, bool mfma) {
     const int64_t max_active = L.dense ? 0 : std::min<int64_t>(ctx->E, T * ctx->K);
     stage_mark(ctx, 2);
     if (mfma) {
@@ -478,6 +486,19 @@ int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, 
         LM_HIP(lm::launch_gemv_gateup(ea, max_active, ctx->stream));
         stage_mark(ctx, 3);
         LM_HIP(lm::launch_gemv_down(ea, max_active, ctx->stream));
+    }
+    return LM_OK;
+}
+
+// Expert kernels + combine for a layer whose routing is in rb (or a dense FFN).
+// next_norm: the next stack layer's RMSNorm weight; the combine then also
+// writes that layer's input (ws.xnorm, and ws.x16 when the MFMA path follows).
+int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, int64_t T, const lm::RouteBufs& rb,
+                float* y, const float* residual, bool mfma, const float* next_norm = nullptr) {
+    const lm::ExpertArgs ea = expert_args(ctx, L, x, x16, T, rb);
+    const int rc = launch_expert_kernels(ctx, L, ea, T, mfma);
+    if (rc != LM_OK) {
+        return rc;
     }
     stage_mark(ctx, 4);
     lm::CombineArgs ca{};
@@ -784,36 +805,47 @@ int ensure_gemm_scratch(lm_context* ctx, size_t floats) {
     return LM_OK;
 }
 
-// After the stream has drained: a bounded wait inside a single-launch decode
-// that ran out has set the error word; report it once and clear it.
+// Reads a single-token error word after its launches have finished; a set
+// word is cleared on the context's stream (a fill kernel, not a memset, so the
+// clear is an ordinary kernel on every path).  Sets *failed.
+int consume_decode_error(lm_context* ctx, uint32_t* sync, bool* failed) {
+    uint32_t error = 0;
+    uint32_t* word = sync + lm::kDecodeErrorWord;
+    LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
+    if (error != 0) {
+        hipLaunchKernelGGL(fill_words_kernel, dim3(1), dim3(64), 0, ctx->stream, word, int64_t{1}, 0u);
+        LM_HIP(hipGetLastError());
+        LM_HIP(hipStreamSynchronize(ctx->stream));
+        *failed = true;
+    }
+    return LM_OK;
+}
+
+// After the context's stream has drained: a bounded wait inside a
+// single-launch decode that ran out has set the error word; report it once and
+// clear it.  The fixed array's word (lm_moe_forward_noalloc, any context on
+// this GPU) is read only after the last such call has finished on the GPU
+// (its event), with the lock held so that no new call is enqueued meanwhile.
 int check_decode_error(lm_context* ctx) {
-    uint32_t* words[2] = {nullptr, nullptr};
+    bool failed = false;
     if (ctx->decode_pending) {
         ctx->decode_pending = false;
-        words[0] = ctx->ws.decode_sync;
+        const int rc = consume_decode_error(ctx, ctx->ws.decode_sync, &failed);
+        if (rc != LM_OK) {
+            return rc;
+        }
     }
     if (ctx->device < kMaxDevices) {
-        // lm_moe_forward_noalloc's launches on this device (any context)
         std::lock_guard<std::mutex> lock(g_static_mutex);
         StaticScratch& st = g_static[ctx->device];
         if (st.pending) {
             st.pending = false;
-            words[1] = st.ptr;
-        }
-    }
-    bool failed = false;
-    for (uint32_t* sync : words) {
-        if (sync == nullptr) {
-            continue;
-        }
-        uint32_t error = 0;
-        uint32_t* word = sync + lm::kDecodeErrorWord;
-        LM_HIP(hipMemcpy(&error, word, sizeof error, hipMemcpyDeviceToHost));
-        if (error != 0) {
-            hipLaunchKernelGGL(fill_words_kernel, dim3(1), dim3(64), 0, ctx->stream, word, int64_t{1}, 0u);
-            LM_HIP(hipGetLastError());
-            LM_HIP(hipStreamSynchronize(ctx->stream));
-            failed = true;
+            LM_HIP(hipEventSynchronize(st.last));
+            const int rc = consume_decode_error(ctx, st.ptr, &failed);
+            if (rc != LM_OK) {
+                return rc;
+            }
+            LM_HIP(hipEventRecord(st.last, ctx->stream));  // after the clear, if one ran
         }
     }
     if (failed) {
@@ -835,11 +867,15 @@ int static_scratch_setup(lm_context* ctx) {
     }
     void* ptr = nullptr;
     LM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    hipEvent_t ev = nullptr;
+    LM_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     hipLaunchKernelGGL(fill_words_kernel, dim3(64), dim3(256), 0, ctx->stream, static_cast<uint32_t*>(ptr),
                        static_cast<int64_t>(kStaticWords), 0u);
     LM_HIP(hipGetLastError());
+    LM_HIP(hipEventRecord(ev, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     st.ptr = static_cast<uint32_t*>(ptr);
+    st.last = ev;
     return LM_OK;
 }
 
@@ -988,6 +1024,11 @@ int lm_context_destroy(lm_context* ctx) {
     LM_GUARD_BEGIN
     if (ctx == nullptr) {
         return LM_OK;
+    }
+    if (ctx->graphs > 0) {
+        return fail(LM_EINVAL, "lm_context_destroy: " + std::to_string(ctx->graphs) +
+                                   " stack graph(s) captured on this context are still alive; "
+                                   "lm_stack_graph_destroy them first");
     }
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
@@ -1435,14 +1476,24 @@ int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, i
     if (ctx->device >= kMaxDevices) {
         return fail(LM_EINVAL, "lm_moe_forward_noalloc: device index beyond the fixed scratch table");
     }
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    LM_HIP(hipStreamIsCapturing(ctx->stream, &capture));
+    if (capture != hipStreamCaptureStatusNone) {
+        // The single-token kernel's hand-off words carry a parity and a tag that
+        // the host advances per launch; a replayed capture would repeat them.
+        return fail(LM_EINVAL, "lm_moe_forward_noalloc: the context's stream is being captured; graph capture "
+                               "and replay of this entry point are not supported");
+    }
     if (tokens == 0) {
         return LM_OK;
     }
     std::lock_guard<std::mutex> lock(g_static_mutex);
     StaticScratch& st = g_static[ctx->device];
-    if (st.ptr == nullptr) {
+    if (st.ptr == nullptr || st.last == nullptr) {
         return fail(LM_EHIP, "lm_moe_forward_noalloc: the fixed scratch was not set up on this device");
     }
+    // After the previous call on this GPU, whichever stream it ran on.
+    LM_HIP(hipStreamWaitEvent(ctx->stream, st.last, 0));
     float* words = reinterpret_cast<float*>(st.ptr);
     const DecodeScratch sc{st.ptr, words + kStaticLogits, words + kStaticAct, words + kStaticPart, nullptr, &st.parity, &st.seq,
                            &st.pending};
@@ -1453,10 +1504,13 @@ int lm_moe_forward_noalloc(lm_context* ctx, int32_t layer, const float* x_dev, i
         rc = decode_layer(ctx, L, sc, x_dev + t * H, y_dev + t * H, nullptr, logit_bias_dev, idx, wts,
                           logits_dev != nullptr ? logits_dev + t * ctx->E : nullptr, nullptr);
         if (rc != LM_OK) {
-            return rc;
+            break;
         }
     }
-    return LM_OK;
+    // The next call on this GPU waits for these launches (also after a failed
+    // launch: whatever was enqueued still runs on the array).
+    LM_HIP(hipEventRecord(st.last, ctx->stream));
+    return rc;
     LM_GUARD_END
 }
 
@@ -1564,6 +1618,87 @@ int lm_permute(lm_context* ctx, const int32_t* topk_index_dev, int64_t tokens, i
     LM_GUARD_END
 }
 
+int lm_grouped_swiglu(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens,
+                      const int32_t* topk_index_dev, float* out_dev, int32_t path) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (tokens < 0 || (tokens > 0 && (x_dev == nullptr || topk_index_dev == nullptr || out_dev == nullptr))) {
+        return fail(LM_EINVAL, "bad token count or null x / topk_index / out");
+    }
+    if (path < LM_PATH_AUTO || path > LM_PATH_MFMA) {
+        return fail(LM_EINVAL, "unknown path");
+    }
+    Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.allocated || L.dense || L.router_t == nullptr || !L.finalized) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " has no finalized MoE weights");
+    }
+    if (tokens == 0) {
+        return LM_OK;
+    }
+    rc = set_device(ctx);
+    if (rc == LM_OK) {
+        rc = ensure_workspace(ctx, tokens);
+    }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    // The routing comes from the caller: every expert id must name a routed
+    // expert, or the permutation would leave its slot unset.
+    const int64_t TK = tokens * ctx->K;
+    std::vector<int32_t> host_idx(static_cast<size_t>(TK));
+    LM_HIP(hipMemcpyAsync(host_idx.data(), topk_index_dev, sizeof(int32_t) * host_idx.size(), hipMemcpyDeviceToHost,
+                          ctx->stream));
+    LM_HIP(hipStreamSynchronize(ctx->stream));
+    for (int64_t a = 0; a < TK; ++a) {
+        if (host_idx[static_cast<size_t>(a)] < 0 || host_idx[static_cast<size_t>(a)] >= ctx->E) {
+            return fail(LM_EINVAL, "lm_grouped_swiglu: topk_index[" + std::to_string(a) + "] = " +
+                                       std::to_string(host_idx[static_cast<size_t>(a)]) + " is not an expert of [0, " +
+                                       std::to_string(ctx->E) + ")");
+        }
+    }
+    // Same path choice as lm_moe_forward's batched path (this entry has no
+    // single-token form).
+    const bool mfma = path == LM_PATH_MFMA || (path == LM_PATH_AUTO && tokens > kMfmaCrossover);
+    lm::RouteBufs rb = route_bufs(ctx, const_cast<int32_t*>(topk_index_dev), ctx->ws.wts);
+    lm::PermuteArgs pa{};
+    pa.idx = topk_index_dev;
+    pa.tokens = tokens;
+    pa.top_k = ctx->K;
+    pa.experts = ctx->E;
+    pa.rb = rb;
+    pa.scratch = ctx->ws.permute_scratch;
+    // Stage timing: no router; the fp16 copy counts with the permutation, the
+    // gather with the combine.
+    stage_mark(ctx, 0);
+    stage_mark(ctx, 1);
+    LM_HIP(lm::launch_permute(pa, ctx->stream));
+    if (mfma) {
+        LM_HIP(lm::launch_to_f16_rows(x_dev, ctx->ws.x16, tokens, ctx->H, ctx->Hp, ctx->stream));
+    }
+    const lm::ExpertArgs ea = expert_args(ctx, L, x_dev, ctx->ws.x16, tokens, rb);
+    rc = launch_expert_kernels(ctx, L, ea, tokens, mfma);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    stage_mark(ctx, 4);
+    LM_HIP(lm::launch_gather_slots(ctx->ws.down_out, rb.slot_of, out_dev, TK, tokens, ctx->H, ea.has_shared,
+                                   ctx->stream));
+    stage_mark(ctx, 5);
+    return stage_finish(ctx);
+    LM_GUARD_END
+}
+
+int lm_context_stream(lm_context* ctx, void** out_stream) {
+    if (ctx == nullptr || out_stream == nullptr) {
+        return fail(LM_EINVAL, "null context or output pointer");
+    }
+    *out_stream = static_cast<void*>(ctx->stream);
+    return LM_OK;
+}
+
 int lm_rms_norm(lm_context* ctx, const float* in_dev, const float* weight_dev, float* out_dev, int64_t tokens,
                 int32_t hidden, float epsilon) {
     if (ctx == nullptr || in_dev == nullptr || weight_dev == nullptr || out_dev == nullptr || hidden <= 0) {
@@ -1640,6 +1775,7 @@ struct lm_stack_graph {
     lm_context* ctx = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    int32_t first = 0, last = -1;
 };
 
 int lm_stack_graph_create(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev,
@@ -1689,7 +1825,7 @@ int lm_stack_graph_create(lm_context* ctx, int32_t first_layer, int32_t last_lay
         (void)hipGraphDestroy(g);
         return fail(LM_EHIP, std::string("stack graph instantiate: ") + hipGetErrorString(inst));
     }
-    *graph = new lm_stack_graph{ctx, g, exec};
+    *graph = new lm_stack_graph{ctx, g, exec, first_layer, last_layer};
     ++ctx->graphs;
     return LM_OK;
     LM_GUARD_END
@@ -1699,6 +1835,15 @@ int lm_stack_graph_launch(lm_stack_graph* graph) {
     LM_GUARD_BEGIN
     if (graph == nullptr) {
         return fail(LM_EINVAL, "null graph");
+    }
+    // The graph reads each layer's slab through the pointers of the capture.  An
+    // upload into a layer since then (without lm_finalize_layer) leaves its fp16
+    // copy stale, which the eager path refuses too.
+    for (int32_t l = graph->first; l <= graph->last; ++l) {
+        if (!graph->ctx->layers[static_cast<size_t>(l)].finalized) {
+            return fail(LM_ENOTRES, "lm_stack_graph_launch: layer " + std::to_string(l) +
+                                        " was uploaded since the capture and is not finalized (lm_finalize_layer)");
+        }
     }
     LM_HIP(hipGraphLaunch(graph->exec, graph->ctx->stream));
     return LM_OK;

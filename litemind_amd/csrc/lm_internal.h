@@ -438,6 +438,11 @@ hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t
 hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
+// out [T*K + T, H]: the down projection of each routed assignment in
+// assignment order (down_out[slot_of[a]]), then the T shared rows (zero
+// without a shared expert).  hidden % 4 == 0.
+hipError_t launch_gather_slots(const float* down_out, const int32_t* slot_of, float* out, int64_t assignments,
+                               int64_t tokens, int32_t hidden, int32_t has_shared, hipStream_t s);
 // True when launch_combine can apply the next layer's norm (CombineArgs::next_norm).
 bool combine_norm_supported(int32_t hidden, int32_t hidden_p);
 // dst = fp16 panels of the BF16 matrix src [rows, cols] (cols % kPanel == 0);

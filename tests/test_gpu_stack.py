@@ -273,3 +273,40 @@ def test_stack_graph_replays_match_eager(stack_ctx, T):
         ctx.stack_graph_create(0, MOE_LAYERS, d1, 1)
     d1.free()
 
+
+
+def test_stack_graph_lifetime(stack_ctx):
+    """A live graph holds its context: lm_context_destroy refuses (and frees
+    nothing) until the graph is destroyed.  An upload into a layer of the
+    graph's range leaves that layer unfinalized, and a replay is refused until
+    lm_finalize_layer runs again; then the replay gives the eager bits."""
+    import litemind_amd as lm
+    from litemind_amd import LmError
+    from litemind_amd import workload as wl
+
+    ctx, layers, dims = stack_ctx
+    T = 48
+    announce(f"stack graph T={T}: context destroy refused, stale layer refused")
+    h0 = wl.tokens(wl.MASTER_SEED + 95, T, dims.hidden)
+    eager = _run(ctx, h0)
+    dh = ctx.to_device(h0)
+    graph = ctx.stack_graph_create(0, MOE_LAYERS, dh, T)
+    try:
+        status = ctx.lib.lm_context_destroy(ctx.handle)
+        assert status == -1 and b"still alive" in ctx.lib.lm_last_error()
+        moe = layers[1][1]
+        ctx.upload_expert(1, 0, moe.gate[0], moe.up[0], moe.down[0])  # same weights, layer left unfinalized
+        with pytest.raises(LmError) as err:
+            ctx.stack_graph_launch(graph)
+        assert err.value.status == -4
+        ctx.finalize_layer(1)
+        dh.upload(h0)
+        ctx.synchronize()
+        ctx.stack_graph_launch(graph)
+        ctx.synchronize()
+        got = dh.download()
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+    finally:
+        ctx.stack_graph_destroy(graph)
+        dh.free()
+    assert lm.LM_OK == 0

@@ -84,3 +84,72 @@ def test_noalloc_rejects_shapes_without_the_kernel():
         dx, y = ctx.to_device(wl.tokens(5, 1, 1024)), ctx.empty((1, 1024))
         with pytest.raises(LmError, match="no single-token kernel"):
             ctx.moe_forward_noalloc(0, dx, 1, y)
+
+
+def test_noalloc_two_contexts_alternate(v2_ctx, v2_layer):
+    """Two contexts (two streams) on one GPU share the fixed array.  Calls
+    issued alternately from both, with no synchronisation between them, run one
+    after another on the GPU (each waits for the previous call's event), so
+    every call's outputs equal lm_moe_forward's for its tokens bit for bit."""
+    from litemind_amd import PATH_AUTO, Context
+    from litemind_amd import workload as wl
+
+    ctx_a, _ = v2_ctx
+    announce("second context on the same GPU for alternating noalloc calls")
+    with Context(wl.V2_LITE.moe_config(num_layers=1)) as ctx_b:
+        wl.upload_moe_layer(ctx_b, 0, v2_layer)
+        E, K, H = 64, ctx_a.config.num_experts_per_tok, 2048
+        calls = []
+        for i in range(6):
+            ctx = ctx_a if i % 2 == 0 else ctx_b
+            T = 2 if i % 3 else 1
+            x = wl.tokens(wl.MASTER_SEED + 7800 + i, T, H)
+            bufs = (ctx.to_device(x), ctx.empty((T, H)), ctx.empty((T, K), np.int32), ctx.empty((T, K)),
+                    ctx.empty((T, E)))
+            calls.append((ctx, x, bufs))
+        announce("alternating lm_moe_forward_noalloc calls on two contexts, no synchronisation between them")
+        for ctx, x, (dx, y, idx, w, lg) in calls:
+            ctx.moe_forward_noalloc(0, dx, x.shape[0], y, idx=idx, w=w, logits=lg)
+        ctx_a.synchronize()
+        ctx_b.synchronize()
+        for n, (ctx, x, (dx, y, idx, w, lg)) in enumerate(calls):
+            got = (y.download(), idx.download(), w.download(), lg.download())
+            ref = [_run(ctx_a, ctx_a.moe_forward, x[t:t + 1], path=PATH_AUTO) for t in range(x.shape[0])]
+            ref = tuple(np.concatenate([r[i] for r in ref]) for i in range(4))
+            for a, b, name in zip(got, ref, ("y", "idx", "weights", "logits")):
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"call {n}: {name} differ"
+            for b in (dx, y, idx, w, lg):
+                b.free()
+
+
+def test_noalloc_refuses_graph_capture(v2_ctx):
+    """While the context's stream is being captured the call returns LM_EINVAL
+    (its hand-off tags would repeat on replay); nothing is launched, so the
+    capture ends with an empty graph."""
+    import ctypes as C
+
+    from litemind_amd import LmError
+    from litemind_amd import workload as wl
+
+    ctx, _ = v2_ctx
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    hip.hipGraphDestroy.argtypes = [C.c_void_p]
+    dx, y = ctx.to_device(wl.tokens(wl.MASTER_SEED + 7900, 1, 2048)), ctx.empty((1, 2048))
+    ctx.synchronize()
+    stream = C.c_void_p(ctx.stream())
+    announce("lm_moe_forward_noalloc while the context stream is captured (refused before any launch)")
+    assert hip.hipStreamBeginCapture(stream, 2) == 0  # hipStreamCaptureModeRelaxed
+    try:
+        with pytest.raises(LmError, match="being captured"):
+            ctx.moe_forward_noalloc(0, dx, 1, y)
+    finally:
+        graph = C.c_void_p()
+        assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+    ctx.moe_forward_noalloc(0, dx, 1, y)  # and works again afterwards
+    ctx.synchronize()
+    for b in (dx, y):
+        b.free()
