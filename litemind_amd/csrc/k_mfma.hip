@@ -16,22 +16,33 @@
 // Every operand is stored in panel layout (32-column panels of [rows, 32]), so
 // the K slice of a stage is one contiguous block per operand: 64 bytes per row,
 // consecutive rows adjacent.  Loads go from global memory straight into LDS
-// with global_load_lds_dwordx4 (no staging registers); each wave instruction
-// fills 1 KB of LDS, 16 rows of 64 bytes, lane l writing bytes [16 l, 16 l + 16).
-// The lane chooses which 16-byte chunk of its row it loads, so rows are stored
-// in LDS with their chunks permuted (row_swizzle), which keeps the MFMA fragment
-// reads free of bank conflicts.
+// with buffer_load_dwordx4 ... lds (no staging registers; a buffer load, unlike
+// a global load to LDS, does not make the compiler wait for every LDS read);
+// each wave instruction fills 1 KB of LDS, 16 rows of 64 bytes, lane l writing
+// bytes [16 l, 16 l + 16).  The lane chooses which 16-byte chunk of its row it
+// loads, so rows are stored in LDS with their chunks permuted (row_swizzle),
+// which keeps the MFMA fragment reads free of bank conflicts.
 //
 // Per workgroup: a WM x WN grid of waves, each computing MI x NJ MFMA blocks of
 // 32 x 32, over a BM x 256 tile (BM = 32 WM MI), K step 32, and a STAGES-deep
-// pipeline: while stage k is multiplied, stages k + 1 .. k + STAGES - 1 are in
+// pipeline: while stage k is multiplied, stages k + 1 .. k + STAGES - 2 are in
 // flight, each in its own LDS array so the compiler can track the asynchronous
-// writes per buffer.  Rows past the end of a group (tokens) or of a matrix
-// (weight rows) load a clamped row and are never stored.  Two shapes:
+// writes per buffer.  Two workgroups share a CU, so one's memory waits are
+// covered by the other's MFMAs.  Rows past the end of a group (tokens) or of a
+// matrix (weight rows) load a clamped row and are never stored.  Two shapes:
 //   128 x 256, 2 x 2 waves of 64 x 128, 3 stages (24 KB each): large groups;
 //    64 x 256, 1 x 4 waves of 64 x 64, 4 stages (20 KB each): groups of a few
 //    dozen rows, where the kernel streams weights and the bytes in flight
 //    per CU (two workgroups x (STAGES - 1) x 16 KB of weights) set its rate.
+//
+// Measured alternatives, not kept (T = 2048 skewed / T = 4096 MoE layer, gate/up
+// µs on one box): 256 x 256 or 192 x 256 tiles of one workgroup per CU with the
+// next half step's fragments prefetched, four or five stages (1.17 against
+// 0.94 PFLOP/s for this kernel's previous version on a dense 4096^3 GEMM, but
+// 307-343 against 284 on the grouped layer, where one workgroup per CU cannot
+// cover the memory waits of gathered token rows); those tiles for the groups
+// of 96 rows and more with the small groups in a separate 64-row launch
+// (343: the second launch's tail).
 #include "lm_internal.h"
 
 namespace lm {
@@ -39,7 +50,6 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(1))) const void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int BN = 256;
@@ -47,6 +57,7 @@ constexpr int BK = kPanel;                   // halves: 64-byte rows, 4 chunks o
 constexpr int kRowBytes = BK * 2;
 constexpr int kBBytes = BN * kRowBytes;      // 16 KB
 constexpr int kXcds = 8;
+constexpr int kBufferWord3 = 0x00020000;     // buffer descriptor word 3: raw 32-bit access
 
 template <int WM, int WN, int MI, int NJ, int STAGES>
 struct Shape {
@@ -54,13 +65,18 @@ struct Shape {
     static constexpr int kThreads = 64 * WAVES;
     static constexpr int BM = 32 * WM * MI;
     static constexpr int kABytes = BM * kRowBytes;
-    static constexpr int kALoads = kABytes / 1024 / WAVES;  // wave instructions per stage
-    static constexpr int kBLoads = kBBytes / 1024 / WAVES;
-    static constexpr int kLoadsPerStage = kALoads + kBLoads;
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int AL = kABytes / 1024 / WAVES;  // A loads (1 KB wave instructions) per wave per stage
+    static constexpr int BL = kBBytes / 1024 / WAVES;
+    static constexpr int L = AL + BL;
+    static constexpr int NR = MI + NJ;                 // fragment reads per half step
+    static constexpr int NP = MI * NJ / 2;             // MFMA pairs per half step
     static_assert(32 * WN * NJ == BN, "the waves cover the 256 columns");
-    static_assert(kALoads * 1024 * WAVES == kABytes && kALoads >= 1, "whole A instructions per wave");
+    static_assert(AL * 1024 * WAVES == kABytes && AL >= 1, "whole A instructions per wave");
     static_assert(NJ % 2 == 0, "gate/up column blocks come in pairs");
-    static_assert((STAGES - 2) * kLoadsPerStage < 16, "vmcnt immediate");
+    static_assert(NR <= 2 * NP && L <= 4 * NP, "reads and loads spread over the MFMA pairs");
+    static_assert(STAGES >= 3 && STAGES <= 4 && (STAGES - 2) * L < 64, "pipeline depth, vmcnt");
+    static_assert(STAGES * kStageBytes <= 80 * 1024, "two workgroups per CU");
 };
 
 // Launches whose average routed group fits one 64-row tile (T k <= 64 E; a
@@ -90,7 +106,10 @@ struct TileInfo {
 // it (gate/up: every tile has the same K) XCD x takes the x-th of eight
 // contiguous, equal ranges of all tiles; dealing column blocks round robin over
 // the XCDs instead (every XCD a share of every expert) measured 8% slower at
-// T = 2048 and 5% at T = 4096.  M tiles of a column block share one L2.
+// T = 2048 and 5% at T = 4096, and spreading the tiles of single-tile groups
+// (weight streams) evenly among each XCD's other tiles changed nothing
+// (273 against 272 us for gate/up at T = 2048).  M tiles of a column block
+// share one L2.
 // s_info: 3 ints of LDS for the hand-off from wave 0 (the caller lends a
 // pipeline buffer that no load writes before every wave has passed a later
 // barrier).
@@ -98,21 +117,22 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
                             TileInfo& ti, int* s_info) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
+        auto inclusive = [&](int v) {
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int u = __shfl_up(v, o);
+                if (lane >= o) {
+                    v += u;
+                }
+            }
+            return v;
+        };
         // Tiles of the routed groups in expert order, 64 experts per pass.
-        int routed_total = 0;
+        int64_t routed_total = 0;
         for (int g0 = 0; g0 < a.experts; g0 += 64) {
             const int g = g0 + lane;
             const int n = g < a.experts ? a.rb.counts[g] : 0;
-            const int tiles = (n + BM - 1) / BM * nt_routed;
-            int incl = tiles;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int v = __shfl_up(incl, o);
-                if (lane >= o) {
-                    incl += v;
-                }
-            }
-            routed_total += __shfl(incl, 63);
+            routed_total += __shfl(inclusive((n + BM - 1) / BM * nt_routed), 63);
         }
         const int mts_s = a.has_shared ? static_cast<int>((a.tokens + BM - 1) / BM) : 0;
         const int64_t shared_total = static_cast<int64_t>(mts_s) * nt_shared;
@@ -142,26 +162,19 @@ __device__ bool decode_tile(const ExpertArgs& a, int BM, int64_t blk, int nt_rou
         }
         int found = -1, local = 0, found_mts = 0;
         if (tile >= 0 && tile < routed_total) {
-            int carry = 0;
+            int64_t carry = 0;
             for (int g0 = 0; g0 < a.experts; g0 += 64) {
                 const int g = g0 + lane;
                 const int n = g < a.experts ? a.rb.counts[g] : 0;
                 const int mts = (n + BM - 1) / BM;
                 const int tiles = mts * nt_routed;
-                int incl = tiles;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int v = __shfl_up(incl, o);
-                    if (lane >= o) {
-                        incl += v;
-                    }
-                }
-                const int excl = carry + incl - tiles;
+                const int incl = inclusive(tiles);
+                const int64_t excl = carry + incl - tiles;
                 const uint64_t hit = __ballot(tile >= excl && tile < carry + incl && tiles > 0);
                 if (hit != 0) {
                     const int gl = static_cast<int>(__builtin_ctzll(hit));
                     found = g0 + gl;
-                    local = static_cast<int>(tile) - __shfl(excl, gl);
+                    local = static_cast<int>(tile - __shfl(excl, gl));
                     found_mts = __shfl(mts, gl);
                     break;
                 }
@@ -210,34 +223,128 @@ __device__ inline int row_swizzle(int r) { return ((r >> 2) & 3) ^ (r & 2); }
 // LDS byte offset of the 16-byte chunk c of row r.
 __device__ inline int chunk_offset(int r, int c) { return r * kRowBytes + ((c ^ row_swizzle(r)) << 4); }
 
+// s_waitcnt with only vmcnt (expcnt and lgkmcnt at their maxima)
+#define LM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x0F70)
+
+// The per-wave state of a tile and the steps of its pipeline.  One type per
+// kernel instantiation (MODE is a parameter): hipcc's host pass left out the
+// launch stub of a second kernel whose body instantiated the same member
+// functions.
+template <int MODE, int WM, int WN, int MI, int NJ, int STAGES>
+struct Tile {
+    using Z = Shape<WM, WN, MI, NJ, STAGES>;
+    __amdgpu_buffer_rsrc_t ra, rb;  // operand A (token rows / activations), operand B (weight rows)
+    unsigned va[Z::AL], vb[Z::BL];  // this lane's byte offset of its row chunk in stage 0
+    unsigned a_step, b_step;        // bytes between consecutive K panels
+    int lane, wave, wm, wn;
+    half8 fa[2][MI], fb[2][NJ];     // fragments of the two half steps of a stage
+    floatx16 acc[MI][NJ];
+
+    // Load q of this wave's stage loads (A first, then B): 1 KB, 16 rows of 64
+    // bytes, into LDS by a buffer load (the stage offset is a scalar).
+    __device__ void load1(int ks, char* buf, int q) {
+        if (q < Z::AL) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(buf + (Z::WAVES * q + wave) * 1024), 16, va[q],
+                                                     static_cast<unsigned>(ks) * a_step, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (lds_void*)(buf + Z::kABytes + (Z::WAVES * (q - Z::AL) + wave) * 1024), 16, vb[q - Z::AL],
+                static_cast<unsigned>(ks) * b_step, 0, 0);
+        }
+    }
+    // Fragment r of half step kk: A blocks 0..MI-1, then B blocks 0..NJ-1.
+    __device__ void read1(const char* buf, int kk, int r) {
+        const int c = 2 * kk + (lane >> 5);
+        if (r < MI) {
+            fa[kk][r] = *reinterpret_cast<const half8*>(buf + chunk_offset(wm * 32 * MI + 32 * r + (lane & 31), c));
+        } else {
+            fb[kk][r - MI] = *reinterpret_cast<const half8*>(
+                buf + Z::kABytes + chunk_offset(wn * 32 * NJ + 32 * (r - MI) + (lane & 31), c));
+        }
+    }
+    // MFMAs t and t + 1 of half step kk (one A block: NJ is even).
+    __device__ void mma2(int t, int kk) {
+        const int i = t / NJ, j = t % NJ;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+        acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j + 1], acc[i][j + 1], 0, 0, 0);
+    }
+    // s_waitcnt vmcnt(n L): n later stages of this wave's loads may stay in flight.
+    __device__ void wait_stages(int n) {
+        if (n >= 2) {
+            LM_WAIT_VM(2 * Z::L);
+        } else if (n == 1) {
+            LM_WAIT_VM(Z::L);
+        } else {
+            LM_WAIT_VM(0);
+        }
+    }
+    // Stage ks: wait for this wave's loads of it (`behind` later stages stay in
+    // flight), barrier (every wave's loads visible; the buffer of stage ks - 1,
+    // which the loads of stage ks + STAGES - 1 overwrite, read by every wave),
+    // the first half step's fragments, then its MFMAs with the second half
+    // step's fragment reads and the stage's loads between them, then the second
+    // half step's MFMAs with the remaining loads.  With one read or load
+    // between two MFMAs the wave's MFMA issue never waits for a run of memory
+    // instructions to be accepted (measured on a dense 4096^3 GEMM: 1,150 cycles
+    // per stage against 1,561 with the loads and reads issued in runs).
+    __device__ void stage(int ks, const char* cur, char* tgt, bool issue, int behind) {
+        wait_stages(behind);
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int r = 0; r < Z::NR; ++r) {
+            read1(cur, 0, r);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < 2 * Z::NP; ++p) {
+            if (p < Z::NP) {
+#pragma unroll
+                for (int r = 2 * p; r < 2 * p + 2; ++r) {
+                    if (r < Z::NR) {
+                        read1(cur, 1, r);
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = p * Z::L / (2 * Z::NP); q < (p + 1) * Z::L / (2 * Z::NP); ++q) {
+                if (issue) {
+                    load1(ks + STAGES - 1, tgt, q);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mma2(2 * (p % Z::NP), p / Z::NP);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
 template <int MODE, int WM, int WN, int MI, int NJ, int STAGES>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_grouped_kernel(
     ExpertArgs a) {
-    using S = Shape<WM, WN, MI, NJ, STAGES>;
-    constexpr int WAVES = S::WAVES;
-    constexpr int BM = S::BM;
-    // One LDS array per stage (A tile, then B tile): the compiler tracks the
-    // asynchronous LDS writes per array and only a few arrays individually.
-    constexpr int kA = S::kABytes;
-    constexpr int kStage = kA + kBBytes;
-    constexpr int kStage3 = STAGES > 3 ? kStage : 16;
-    __shared__ __attribute__((aligned(1024))) char s0[kStage], s1[kStage], s2[kStage], s3[kStage3];
-    char* const As[4] = {s0, s1, s2, s3};
-    char* const Bs[4] = {s0 + kA, s1 + kA, s2 + kA, s3 + kA};
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
+    using Z = Shape<WM, WN, MI, NJ, STAGES>;
+    constexpr int BM = Z::BM;
+    // One LDS array per stage: the compiler tracks the asynchronous LDS writes
+    // per array.
+    constexpr int kStage3 = STAGES > 3 ? Z::kStageBytes : 16;
+    __shared__ __attribute__((aligned(1024))) char s0[Z::kStageBytes], s1[Z::kStageBytes], s2[Z::kStageBytes],
+        s3[kStage3];
+    char* const bufs[4] = {s0, s1, s2, s3};
+    Tile<MODE, WM, WN, MI, NJ, STAGES> t;
+    t.lane = threadIdx.x & 63;
+    t.wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    t.wm = t.wave / WN;
+    t.wn = t.wave % WN;
+    const int lane = t.lane, wave = t.wave;
 
     const int inter_p = a.inter_p;
     const int n_routed = MODE == kGateUp ? 2 * inter_p : a.hidden;  // weight rows
     const int n_shared = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
     TileInfo ti;
     // The last stage buffer holds the tile hand-off: the prologue never loads
-    // into it, and the first load that does follows the main loop's first
-    // barrier, after every wave has read its tile.
+    // into it, and its first load follows the first stage's barrier, after
+    // every wave has read its tile.
     if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, MODE == kDown, ti,
-                     reinterpret_cast<int*>(As[STAGES - 1]))) {
+                     reinterpret_cast<int*>(bufs[STAGES - 1]))) {
         return;
     }
     const bool shared = ti.g >= a.experts;
@@ -250,131 +357,73 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     const int64_t act_slot0 = shared ? 0 : ti.slot0;
     _Float16* const act_base = a.act16 + (shared ? TK * static_cast<int64_t>(inter_p) : 0);
 
-    // Rows this lane loads: A block q covers rows 16 (WAVES q + wave) + lane / 4,
-    // B block q likewise over the 256 B rows.  The chunk follows the permutation.
-    const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);  // the lane's row is 16 k + lane / 4
-    const _Float16* pa[S::kALoads];
-    const _Float16* pb[S::kBLoads];
-    // Halves between consecutive K panels of each operand.
-    const int64_t a_step = (MODE == kGateUp ? a.tokens : act_rows) * kPanel;
-    const int64_t b_step = static_cast<int64_t>(n_rows) * kPanel;
-#pragma unroll
-    for (int q = 0; q < S::kALoads; ++q) {
-        const int r = 16 * (WAVES * q + wave) + (lane >> 2);
-        int m = ti.mt * BM + r;
-        m = m < ti.rows ? m : ti.rows - 1;  // padding rows repeat the last row; never stored
-        if (MODE == kGateUp) {
-            const int64_t token = shared ? m : a.rb.perm[ti.slot0 + m] / a.top_k;
-            pa[q] = a.x16 + token * kPanel + chunk * 8;
-        } else {
-            pa[q] = act_base + (act_slot0 + m) * kPanel + chunk * 8;
-        }
-    }
+    // Operand A: token rows (gate/up, gathered through the permutation) or the
+    // slots' activations (down); operand B: the group's weight rows.  Lane l of
+    // a load covers row 16 k + l / 4 and loads the chunk of it that the row's
+    // LDS swizzle puts at byte 16 (l % 4) of the row.  Rows past the end of a
+    // group (tokens) or of a matrix (weight rows) load a clamped row and are
+    // never stored.  32-bit offsets: the launcher checks the operand sizes.
+    const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);
+    const _Float16* const a_base = MODE == kGateUp ? a.x16 : act_base;
+    const int64_t a_rows = MODE == kGateUp ? a.tokens : act_rows;
+    t.ra = __builtin_amdgcn_make_buffer_rsrc((void*)a_base, 0, static_cast<int>(a_rows * K * 2), kBufferWord3);
     const _Float16* const wbase = MODE == kGateUp ? a.groups.gu_h[ti.g] : a.groups.down_h[ti.g];
+    t.rb = __builtin_amdgcn_make_buffer_rsrc((void*)wbase, 0, static_cast<int>(static_cast<int64_t>(n_rows) * K * 2),
+                                             kBufferWord3);
 #pragma unroll
-    for (int q = 0; q < S::kBLoads; ++q) {
-        const int r = 16 * (WAVES * q + wave) + (lane >> 2);
-        int row = ti.nt * BN + r;
-        row = row < n_rows ? row : n_rows - 1;  // rows past the matrix: never stored
-        pb[q] = wbase + static_cast<int64_t>(row) * kPanel + chunk * 8;
+    for (int q = 0; q < Z::AL; ++q) {
+        int m = ti.mt * BM + 16 * (Z::WAVES * q + wave) + (lane >> 2);
+        m = m < ti.rows ? m : ti.rows - 1;  // padding rows repeat the last row; never stored
+        int64_t row;
+        if (MODE == kGateUp) {
+            row = shared ? m : a.rb.perm[ti.slot0 + m] / a.top_k;
+        } else {
+            row = act_slot0 + m;
+        }
+        t.va[q] = static_cast<unsigned>((row * kPanel + chunk * 8) * 2);
     }
-
-    auto issue = [&](int ks, char* as, char* bs) {
 #pragma unroll
-        for (int q = 0; q < S::kALoads; ++q) {
-            __builtin_amdgcn_global_load_lds((global_void*)(pa[q] + ks * a_step),
-                                             (lds_void*)(as + (WAVES * q + wave) * 1024), 16, 0, 0);
-        }
-#pragma unroll
-        for (int q = 0; q < S::kBLoads; ++q) {
-            __builtin_amdgcn_global_load_lds((global_void*)(pb[q] + ks * b_step),
-                                             (lds_void*)(bs + (WAVES * q + wave) * 1024), 16, 0, 0);
-        }
-    };
-
-    floatx16 acc[MI][NJ];
+    for (int q = 0; q < Z::BL; ++q) {
+        int n = ti.nt * BN + 16 * (Z::WAVES * q + wave) + (lane >> 2);
+        n = n < n_rows ? n : n_rows - 1;  // rows past the matrix: never stored
+        t.vb[q] = static_cast<unsigned>((static_cast<int64_t>(n) * kPanel + chunk * 8) * 2);
+    }
+    t.a_step = static_cast<unsigned>(a_rows * kRowBytes);
+    t.b_step = static_cast<unsigned>(n_rows) * kRowBytes;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            acc[i][j] = floatx16{};
+            t.acc[i][j] = floatx16{};
         }
     }
-    auto compute = [&](const char* as, const char* bs) {
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            const int c = 2 * kk + (lane >> 5);
-            half8 af[MI], bf[NJ];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const int r = wm * (32 * MI) + i * 32 + (lane & 31);
-                af[i] = *reinterpret_cast<const half8*>(as + chunk_offset(r, c));
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int r = wn * (32 * NJ) + j * 32 + (lane & 31);
-                bf[j] = *reinterpret_cast<const half8*>(bs + chunk_offset(r, c));
-            }
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-    };
-    // Stage ks lives in buffer ks % STAGES and was issued STAGES - 1 steps
-    // earlier.  Before multiplying it, wait for this wave's loads of it (the
-    // loads of the stages after it may remain in flight) and for its own LDS
-    // reads of the previous step; the barrier then makes every wave's part
-    // visible and guarantees that buffer (ks - 1) % STAGES, read in the previous
-    // step, is free for stage ks + STAGES - 1.
-    constexpr int L = S::kLoadsPerStage;
+    // Stages 0 .. STAGES - 2 in flight before the first stage; stage ks lives in
+    // buffer ks % STAGES and the loads of stage ks + STAGES - 1 go to buffer
+    // (ks - 1) % STAGES.  A K shorter than STAGES - 1 stages reloads the last
+    // stage into buffers that are never read, so every path has the same loads
+    // in flight.
     const int nk = K / BK;
-    auto step_full = [&](int ks, char* as, char* bs, char* an, char* bn) {
-        __builtin_amdgcn_s_waitcnt(0x0070 | ((STAGES - 2) * L));  // vmcnt((STAGES - 2) L) lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
-        issue(ks + STAGES - 1, an, bn);
-        compute(as, bs);
-    };
-    // The last steps: fewer stages remain in flight behind stage ks.
-    auto step_tail = [&](int ks, char* as, char* bs, char* an, char* bn) {
-        const int later = nk - 1 - ks;
-        if (STAGES > 3 && later >= 2) {
-            __builtin_amdgcn_s_waitcnt(0x0070 | (2 * L));
-        } else if (later >= 1) {
-            __builtin_amdgcn_s_waitcnt(0x0070 | L);
-        } else {
-            __builtin_amdgcn_s_waitcnt(0x0070);
-        }
-        __builtin_amdgcn_s_barrier();
-        if (ks + STAGES - 1 < nk) {
-            issue(ks + STAGES - 1, an, bn);
-        }
-        compute(as, bs);
-    };
-    // The prologue always issues STAGES - 1 stages (a stage past the end
-    // reloads the last one into a buffer that is never read), so every path
-    // into the main loop has the same loads in flight and the compiler's own
-    // wait tracking needs no extra vmcnt(0).
 #pragma unroll
     for (int d = 0; d < STAGES - 1; ++d) {
-        issue(d < nk ? d : nk - 1, As[d], Bs[d]);
+#pragma unroll
+        for (int q = 0; q < Z::L; ++q) {
+            t.load1(d < nk ? d : nk - 1, bufs[d], q);
+        }
     }
-    // Main loop: every step has STAGES - 2 stages behind it and issues one.
     int ks = 0;
     for (; ks + 2 * STAGES - 1 <= nk; ks += STAGES) {
 #pragma unroll
         for (int j = 0; j < STAGES; ++j) {
-            step_full(ks + j, As[j], Bs[j], As[(j + STAGES - 1) % STAGES], Bs[(j + STAGES - 1) % STAGES]);
+            t.stage(ks + j, bufs[j], bufs[(j + STAGES - 1) % STAGES], true, STAGES - 2);
         }
     }
 #pragma unroll
     for (int j = 0; j < 2 * STAGES - 1; ++j) {
-        if (ks + j < nk) {
-            step_tail(ks + j, As[j % STAGES], Bs[j % STAGES], As[(j + STAGES - 1) % STAGES],
-                      Bs[(j + STAGES - 1) % STAGES]);
+        const int kj = ks + j;
+        if (kj < nk) {
+            const int later = nk - 1 - kj;
+            t.stage(kj, bufs[j % STAGES], bufs[(j + STAGES - 1) % STAGES], kj + STAGES - 1 < nk,
+                    later < STAGES - 2 ? later : STAGES - 2);
         }
     }
 
@@ -385,8 +434,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     for (int i = 0; i < MI; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m_local = wm * (32 * MI) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const int m = ti.mt * BM + m_local;
+            const int m = ti.mt * BM + t.wm * (32 * MI) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m >= ti.rows) {
                 continue;
             }
@@ -394,24 +442,25 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
                 // Blocks (2p, 2p + 1) are the gate and up of one 32-column group.
 #pragma unroll
                 for (int p = 0; p < NJ / 2; ++p) {
-                    const int jcol = (ti.nt * BN) / 2 + wn * (16 * NJ) + p * 32 + n;
+                    const int jcol = (ti.nt * BN) / 2 + t.wn * (16 * NJ) + p * 32 + n;
                     if (jcol < width_p) {
-                        const float h = silu_fast(acc[i][2 * p][r], acc[i][2 * p + 1][r]);
+                        const float h = silu_fast(t.acc[i][2 * p][r], t.acc[i][2 * p + 1][r]);
                         act_base[panel_index(act_slot0 + m, jcol, act_rows)] = static_cast<_Float16>(h);
                     }
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    const int h = ti.nt * BN + wn * (32 * NJ) + j * 32 + n;
+                    const int h = ti.nt * BN + t.wn * (32 * NJ) + j * 32 + n;
                     if (h < a.hidden) {
-                        a.down_out[(ti.slot0 + m) * a.hidden + h] = acc[i][j][r];
+                        a.down_out[(ti.slot0 + m) * a.hidden + h] = t.acc[i][j][r];
                     }
                 }
             }
         }
     }
 }
+#undef LM_WAIT_VM
 
 // Upper bound of the workgroups the tile walk needs (the kernel maps
 // workgroups onto the tiles that exist and the rest return at once): per XCD
@@ -435,12 +484,23 @@ hipError_t launch_shape(const ExpertArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Operands the kernels' 32-bit buffer offsets reach: the fp16 token copy
+// [T, Hp], the activations [T K Ip + T Sp] and the widest gate/up matrix.
+bool offsets_fit(const ExpertArgs& a) {
+    const int64_t limit = 0x7fffffff;
+    const int64_t widest = a.inter_p > a.shared_inter_p ? a.inter_p : a.shared_inter_p;
+    const int64_t TK = a.tokens * a.top_k;
+    return a.tokens * a.hidden_p * 2 <= limit && (TK * a.inter_p + a.tokens * a.shared_inter_p) * 2 <= limit &&
+           2 * widest * a.hidden_p * 2 <= limit && static_cast<int64_t>(a.hidden) * widest * 2 <= limit;
+}
+
 template <int MODE>
 hipError_t launch(const ExpertArgs& a, hipStream_t s) {
     if (a.tokens <= 0) {
         return hipSuccess;
     }
-    if (a.hidden_p % BK != 0 || a.inter_p % BK != 0 || (a.has_shared && a.shared_inter_p % BK != 0)) {
+    if (a.hidden_p % BK != 0 || a.inter_p % BK != 0 || (a.has_shared && a.shared_inter_p % BK != 0) ||
+        !offsets_fit(a)) {
         return hipErrorInvalidValue;
     }
     // A layer without routed experts (the dense FFN) is one group of T rows.
