@@ -237,6 +237,7 @@ struct Tile {
     unsigned va[Z::AL], vb[Z::BL];  // this lane's byte offset of its row chunk in stage 0
     unsigned a_step, b_step;        // bytes between consecutive K panels
     int lane, wave, wm, wn;
+    int blocks;                     // this wave's 32-row blocks holding group rows (0..MI); the rest skip their MFMAs
     half8 fa[2][MI], fb[2][NJ];     // fragments of the two half steps of a stage
     floatx16 acc[MI][NJ];
 
@@ -262,11 +263,14 @@ struct Tile {
                 buf + Z::kABytes + chunk_offset(wn * 32 * NJ + 32 * (r - MI) + (lane & 31), c));
         }
     }
-    // MFMAs t and t + 1 of half step kk (one A block: NJ is even).
+    // MFMAs t and t + 1 of half step kk (one A block: NJ is even), skipped for
+    // a block past the group's rows (its accumulators are never stored).
     __device__ void mma2(int t, int kk) {
         const int i = t / NJ, j = t % NJ;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
-        acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j + 1], acc[i][j + 1], 0, 0, 0);
+        if (i < blocks) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+            acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j + 1], acc[i][j + 1], 0, 0, 0);
+        }
     }
     // s_waitcnt vmcnt(n L): n later stages of this wave's loads may stay in flight.
     __device__ void wait_stages(int n) {
@@ -390,6 +394,10 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     }
     t.a_step = static_cast<unsigned>(a_rows * kRowBytes);
     t.b_step = static_cast<unsigned>(n_rows) * kRowBytes;
+    {
+        const int left = ti.rows - (ti.mt * BM + t.wm * 32 * MI);
+        t.blocks = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : (left >= 32 * MI ? MI : (left + 31) / 32));
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
 #pragma unroll
