@@ -8,8 +8,9 @@
  * lm_context_create (include/litemind_moe.h; same conventions: int status,
  * lm_last_error, *_dev device pointers, work on the context stream).
  *
- * Results are LiteMind's bit for bit: every projection is gemm::matvec_bf16's
- * association order, the RMS norms gemm::rms_norm's roundings, the rotation
+ * On the bit-exact projection path (LM_PATH_GEMV, and LM_PATH_AUTO below 16
+ * tokens per call) results are LiteMind's bit for bit: every projection is
+ * gemm::matvec_bf16's association order, the RMS norms gemm::rms_norm's roundings, the rotation
  * RotaryEmbedding::apply's two fused multiply-adds per channel pair, each score
  * scale * (dot(q_nope, k_nope) + dot(q_rope, k_rope)) with gemm::dot's
  * left-to-right sums, the softmax gemm::softmax's (glibc expf, left-to-right
@@ -17,7 +18,11 @@
  * the cached tokens in order.  T tokens at once give the same results as T
  * calls of Attention::forward in turn (causal: token i sees the cache up to its
  * own slot), which is how LiteMind's runner prefills (src/DeepSeekRunner.cpp:
- * 468-476).
+ * 468-476).  On the MFMA path (LM_PATH_MFMA for two or more tokens,
+ * LM_PATH_AUTO from 16 tokens) each projection of a batch is one GEMM with fp16
+ * operands and fp32 accumulation, as the MoE block's MFMA path: the results
+ * follow LiteMind's within that path's tolerance, everything after the
+ * projections (norms, rotation, scores, softmax, context) unchanged.
  */
 #ifndef LITEMIND_ATTENTION_H
 #define LITEMIND_ATTENTION_H
@@ -99,6 +104,14 @@ int lm_upload_input_norm(lm_context* ctx, int32_t layer, const float* weight_hos
 int lm_attention_forward(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens, int64_t position0,
                          float* out_dev, int32_t accumulate);
 
+/* Projection path of lm_attention_forward (no LiteMind counterpart):
+ * LM_PATH_GEMV every projection bit for bit gemm::matvec_bf16; LM_PATH_MFMA
+ * batches of two or more tokens on MFMA (fp16 operands, fp32 accumulation;
+ * one token keeps the bit-exact single-token launches); LM_PATH_AUTO (the
+ * default) MFMA from 16 tokens per call.  Layers whose projection widths are
+ * not multiples of 32, or whose weights overflow fp16, always take the
+ * bit-exact path. */
+int lm_attention_set_path(lm_context* ctx, int32_t path);
 /* KvCache::clear for every layer (src/DeepSeekRunner.cpp:432-437, DeepSeekRunner::reset). */
 int lm_kv_cache_clear(lm_context* ctx);
 /* KvCache::token_count of a layer. */
@@ -115,6 +128,8 @@ int lm_kv_cache_read(lm_context* ctx, int32_t layer, int64_t tokens, float* key_
  * hidden_dev [T, H] in place: h += Attention(rms_norm(h, input_layernorm)),
  * then h += FFN(rms_norm(h, post_attention_layernorm)) as lm_stack_forward.
  * Every layer needs its attention weights, input norm, norm and FFN resident.
+ * `path` selects the FFN's expert path (as lm_moe_forward) and the attention's
+ * projection path (as lm_attention_set_path) of every layer.
  * LM_EFULL as lm_attention_forward (hidden_dev is then partly updated). */
 int lm_decoder_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,
                        int64_t position0, int32_t path);

@@ -149,6 +149,7 @@ PROTOTYPES = {
     "lm_upload_input_norm": [_P, _I32, _P],
     "lm_attention_forward": [_P, _I32, _P, _I64, _I64, _P, _I32],
     "lm_kv_cache_clear": [_P],
+    "lm_attention_set_path": [_P, _I32],
     "lm_kv_cache_tokens": [_P, _I32, _P],
     "lm_kv_cache_read": [_P, _I32, _I64, _P, _P, _P],
     "lm_decoder_forward": [_P, _I32, _I32, _P, _I64, _I64, _I32],
@@ -419,6 +420,10 @@ class Context:
     def attention_forward(self, layer, x, tokens, position0, out, accumulate=False) -> None:
         self._check(self.lib.lm_attention_forward(self.handle, layer, _ptr(x), tokens, position0, _ptr(out),
                                                   1 if accumulate else 0))
+
+    def attention_set_path(self, path: int) -> None:
+        """Projection path of attention_forward (lm_attention_set_path)."""
+        self._check(self.lib.lm_attention_set_path(self.handle, path))
 
     def kv_cache_clear(self) -> None:
         self._check(self.lib.lm_kv_cache_clear(self.handle))

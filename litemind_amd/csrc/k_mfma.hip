@@ -45,6 +45,8 @@
 // (343: the second launch's tail).
 #include "lm_internal.h"
 
+#include <algorithm>
+
 namespace lm {
 namespace {
 
@@ -346,10 +348,18 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     TileInfo ti;
     // The last stage buffer holds the tile hand-off: the prologue never loads
     // into it, and its first load follows the first stage's barrier, after
-    // every wave has read its tile.
-    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, (n_shared + BN - 1) / BN, MODE == kDown, ti,
+    // every wave has read its tile.  A split K multiplies the shared group's
+    // column blocks: block nt + c * blocks is chunk c of column block nt.
+    const int nt_shared = (n_shared + BN - 1) / BN;
+    const int ksplit = MODE == kDown && a.ksplit > 1 ? a.ksplit : 1;
+    if (!decode_tile(a, BM, blockIdx.x, (n_routed + BN - 1) / BN, nt_shared * ksplit, MODE == kDown, ti,
                      reinterpret_cast<int*>(bufs[STAGES - 1]))) {
         return;
+    }
+    int kc = 0;
+    if (ksplit > 1) {
+        kc = ti.nt / nt_shared;
+        ti.nt -= kc * nt_shared;
     }
     const bool shared = ti.g >= a.experts;
     const int width_p = shared ? a.shared_inter_p : inter_p;
@@ -394,6 +404,19 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     }
     t.a_step = static_cast<unsigned>(a_rows * kRowBytes);
     t.b_step = static_cast<unsigned>(n_rows) * kRowBytes;
+    // this tile's K stages [k0, k0 + nk): all of K, or chunk kc of the split
+    const int nk_all = K / BK;
+    const int kchunk = (nk_all + ksplit - 1) / ksplit;
+    const int k0 = kc * kchunk;
+    const int nk = nk_all - k0 < kchunk ? nk_all - k0 : kchunk;  // >= 1: the launcher's choice of ksplit
+#pragma unroll
+    for (int q = 0; q < Z::AL; ++q) {
+        t.va[q] += static_cast<unsigned>(k0) * t.a_step;
+    }
+#pragma unroll
+    for (int q = 0; q < Z::BL; ++q) {
+        t.vb[q] += static_cast<unsigned>(k0) * t.b_step;
+    }
     {
         const int left = ti.rows - (ti.mt * BM + t.wm * 32 * MI);
         t.blocks = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : (left >= 32 * MI ? MI : (left + 31) / 32));
@@ -410,7 +433,6 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
     // (ks - 1) % STAGES.  A K shorter than STAGES - 1 stages reloads the last
     // stage into buffers that are never read, so every path has the same loads
     // in flight.
-    const int nk = K / BK;
 #pragma unroll
     for (int d = 0; d < STAGES - 1; ++d) {
 #pragma unroll
@@ -457,11 +479,12 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2,
                     }
                 }
             } else {
+                float* const dst = ksplit > 1 ? a.partial + static_cast<int64_t>(kc) * a.tokens * a.hidden : a.down_out;
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
                     const int h = ti.nt * BN + t.wn * (32 * NJ) + j * 32 + n;
                     if (h < a.hidden) {
-                        a.down_out[(ti.slot0 + m) * a.hidden + h] = t.acc[i][j][r];
+                        dst[(ti.slot0 + m) * a.hidden + h] = t.acc[i][j][r];
                     }
                 }
             }
@@ -486,7 +509,8 @@ hipError_t launch_shape(const ExpertArgs& a, hipStream_t s) {
     using S = Shape<WM, WN, MI, NJ, STAGES>;
     const int nr = MODE == kGateUp ? 2 * a.inter_p : a.hidden;
     const int ns = MODE == kGateUp ? 2 * a.shared_inter_p : a.hidden;
-    const int64_t grid = tile_bound(a, S::BM, (nr + BN - 1) / BN, (ns + BN - 1) / BN);
+    const int ksplit = MODE == kDown && a.ksplit > 1 ? a.ksplit : 1;
+    const int64_t grid = tile_bound(a, S::BM, (nr + BN - 1) / BN, (ns + BN - 1) / BN * ksplit);
     hipLaunchKernelGGL((mfma_grouped_kernel<MODE, WM, WN, MI, NJ, STAGES>), dim3(static_cast<unsigned>(grid)),
                        dim3(S::kThreads), 0, s, a);
     return hipGetLastError();
@@ -519,7 +543,74 @@ hipError_t launch(const ExpertArgs& a, hipStream_t s) {
     return launch_shape<MODE, 2, 2, 2, 4, 3>(a, s);
 }
 
+// out[i] = (accumulate ? out[i] : 0) + (p_0[i] + p_1[i] + ... + p_{n-1}[i]), the
+// chunks in order.
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                                         int64_t count, int32_t chunks, int32_t accumulate) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i >= count) {
+        return;
+    }
+    float sum = partial[i];
+    for (int c = 1; c < chunks; ++c) {
+        sum = sum + partial[c * count + i];
+    }
+    out[i] = accumulate ? out[i] + sum : sum;
+}
+
 }  // namespace
+
+hipError_t launch_mfma_gemm(const _Float16* a16, const _Float16* const* w, float* out, int64_t M, int32_t N, int32_t Kp,
+                            int32_t accumulate, float* scratch, int64_t scratch_floats, hipStream_t s) {
+    if (M <= 0 || N <= 0) {
+        return hipSuccess;
+    }
+    if (Kp <= 0 || Kp % BK != 0 || (accumulate && scratch_floats < M * N)) {
+        return hipErrorInvalidValue;
+    }
+    ExpertArgs ea{};
+    ea.groups.down_h = w;
+    ea.groups.gu_h = w;
+    ea.act16 = const_cast<_Float16*>(a16);
+    ea.down_out = out;
+    ea.tokens = M;
+    ea.hidden = N;
+    ea.hidden_p = static_cast<int32_t>(round_up(N, kPanel));
+    ea.experts = 0;
+    ea.top_k = 0;
+    ea.inter_p = 0;
+    ea.shared_inter_p = Kp;
+    ea.has_shared = 1;
+    // Split K while the tiles fill less than half of the workgroup slots (two
+    // per CU), keeping at least 8 stages per chunk and at most 4 chunks.
+    const int64_t bm = M <= kNarrowRows ? 64 : 128;
+    const int64_t tiles = (M + bm - 1) / bm * ((N + BN - 1) / BN);
+    const int nk = Kp / BK;
+    int ks = 1;
+    if (tiles < 256) {
+        ks = static_cast<int>(std::min<int64_t>({(256 + tiles - 1) / tiles, 4, nk / 8}));
+        ks = ks < 1 ? 1 : ks;
+        const int chunk = (nk + ks - 1) / ks;
+        ks = (nk + chunk - 1) / chunk;  // every chunk holds at least one stage
+        if (static_cast<int64_t>(ks) * M * N > scratch_floats) {
+            ks = 1;
+        }
+    }
+    const bool via_scratch = ks > 1 || accumulate;
+    if (via_scratch) {
+        ea.down_out = scratch;
+        ea.ksplit = ks;
+        ea.partial = scratch;
+    }
+    hipError_t e = launch<kDown>(ea, s);
+    if (e != hipSuccess || !via_scratch) {
+        return e;
+    }
+    const int64_t count = M * N;
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((count + 255) / 256)), dim3(256), 0, s, scratch,
+                       out, count, ks, accumulate);
+    return hipGetLastError();
+}
 
 hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s) { return launch<kGateUp>(a, s); }
 

@@ -518,6 +518,14 @@ __global__ __launch_bounds__(256) void gather_slots_kernel(const float* __restri
     reinterpret_cast<float4*>(out + r * hidden)[c] = v;
 }
 
+// out[i] = out[i] + y[i] (= fma(1, y[i], out[i]): gemm::axpy with scale 1).
+__global__ __launch_bounds__(256) void add_rows_kernel(float* __restrict__ out, const float* __restrict__ y, int64_t n) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i < n) {
+        out[i] = out[i] + y[i];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
@@ -563,6 +571,14 @@ hipError_t launch_gather_slots(const float* down_out, const int32_t* slot_of, fl
     const int64_t n = rows * (hidden / 4);
     hipLaunchKernelGGL(gather_slots_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, down_out,
                        slot_of, out, assignments, rows, hidden, has_shared);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rows(float* out, const float* y, int64_t n, hipStream_t s) {
+    if (n <= 0) {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(add_rows_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, out, y, n);
     return hipGetLastError();
 }
 

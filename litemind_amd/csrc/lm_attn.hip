@@ -11,6 +11,12 @@
 //   ctx    = softmax(scale * q . keys) . values, causal                   (k_attn.hip)
 //   out    = o_proj ctx   (or out += o_proj ctx)                          (matvec)
 // which is Attention::forward (src/Attention.cpp:22-103) for each token in turn.
+// Every projection keeps gemm::matvec_bf16's association (bit for bit) unless
+// the projection path is MFMA: then, from kAttnMfmaTokens tokens on (LM_PATH_AUTO)
+// or for every batch of two or more (LM_PATH_MFMA), each projection is a GEMM on
+// the grouped kernel of k_mfma.hip (one group of T rows): the input converted to
+// fp16 panels, the weights' fp16 panel copy made at upload, fp32 accumulation;
+// results within the tolerance of the MoE block's MFMA path.
 #include "litemind_attention.h"
 #include "lm_error.h"
 #include "lm_internal.h"
@@ -41,12 +47,25 @@ struct AttnLayer {
     const float* kv_a_norm = nullptr;
     const uint16_t* kv_b = nullptr;
     const uint16_t* o = nullptr;
+    // fp16 panel copies for the MFMA path (null when a width is not a multiple
+    // of 32 or a weight overflows fp16): device table of pointers in the order
+    // of Proj, read by the kernel as its group's weights
+    void* slab16 = nullptr;
+    const _Float16* const* table16 = nullptr;
     float* input_norm = nullptr;  // [H], lm_decoder_forward
     KvCacheDev cache;
     int64_t count = 0;  // KvCache::token_count
 };
 
+// Projections in the order of AttnLayer::table16.
+enum Proj { kProjQ = 0, kProjQa = 1, kProjQb = 2, kProjKva = 3, kProjKvb = 4, kProjO = 5, kProjCount = 6 };
+
 struct AttnState {
+    int32_t path = LM_PATH_AUTO;  // projection path of lm_attention_forward
+    // MFMA path: the query projections run on `side` while the key and value
+    // projections run on the context stream (fork / join events)
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     lm_mla_config cfg{};
     AttnShape shape;
     float scale = 0.0f;
@@ -65,7 +84,18 @@ void attention_release(AttnState* st) {
     }
     for (AttnLayer& L : st->layers) {
         (void)hipFree(L.slab);
+        (void)hipFree(L.slab16);
         (void)hipFree(L.input_norm);
+    }
+    if (st->fork != nullptr) {
+        (void)hipEventDestroy(st->fork);
+    }
+    if (st->join != nullptr) {
+        (void)hipEventDestroy(st->join);
+    }
+    if (st->side != nullptr) {
+        (void)hipStreamSynchronize(st->side);
+        (void)hipStreamDestroy(st->side);
     }
     (void)hipFree(st->tables);
     (void)hipFree(st->caches);
@@ -84,6 +114,8 @@ using lm::AttnState;
 // Query tokens per launch of the attention core: bounds the score scratch to
 // kCoreTokens * heads * (n0 + T) floats.
 constexpr int64_t kCoreTokens = 512;
+// LM_PATH_AUTO: batches of at least this many tokens take the MFMA projections.
+constexpr int64_t kAttnMfmaTokens = 16;
 
 int fail(int code, const std::string& message) { return lm::set_error(code, message); }
 
@@ -213,13 +245,44 @@ int ensure_buffer(float** buf, size_t* have, hipStream_t stream, size_t floats) 
     return LM_OK;
 }
 
+// Scratch of the MFMA projections on one stream: an fp16 panel copy of an
+// input that is ready (and which input it is), the buffer for the next
+// conversion, and the GEMM's partial sums.
+struct ProjScratch {
+    const _Float16* ready;
+    const float* ready_of;
+    _Float16* conv;
+    float* partial;
+    int64_t partial_floats;
+};
+
+// out [F, N] = W x (or out += W x) for x [F, K]: gemm::matvec_bf16 per token
+// (bit for bit), or with `mfma` the GEMM on MFMA over W's fp16 panel copy.
+int project(const AttnLayer& L, int proj, const uint16_t* w, const float* x, int64_t K, float* out, int64_t N,
+            int64_t F, int32_t accumulate, bool mfma, ProjScratch& ps, hipStream_t stream) {
+    if (!mfma) {
+        LM_ATT_HIP(lm::launch_matvec_tokens(w, x, out, N, K, F, 1.0f, accumulate, stream));
+        return LM_OK;
+    }
+    const int64_t Kp = lm::round_up(K, lm::kPanel);
+    if (ps.ready_of != x) {
+        LM_ATT_HIP(lm::launch_to_f16_rows(x, ps.conv, F, static_cast<int32_t>(K), static_cast<int32_t>(Kp), stream));
+        ps.ready = ps.conv;
+        ps.ready_of = x;
+    }
+    LM_ATT_HIP(lm::launch_mfma_gemm(ps.ready, L.table16 + proj, out, F, static_cast<int32_t>(N),
+                                    static_cast<int32_t>(Kp), accumulate, ps.partial, ps.partial_floats, stream));
+    return LM_OK;
+}
+
 // Attention::forward for F tokens that all fit the cache; out = o_proj ctx or
 // out += o_proj ctx.  x [F, H] must not overlap out, except with in_norm: x is
 // then the raw hidden state, normalised here by in_norm (into xn_buf [F, H], or
 // inside the first projection's launch for one token) before anything else
 // reads it, so out may be x itself.
 int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const float* x, int64_t F, int64_t pos0,
-                     float* out, int32_t accumulate, const float* in_norm = nullptr, float* xn_buf = nullptr) {
+                     float* out, int32_t accumulate, int32_t path, const float* in_norm = nullptr,
+                     float* xn_buf = nullptr) {
     const lm_mla_config& c = st->cfg;
     AttnLayer& L = st->layers[static_cast<size_t>(layer)];
     if (L.kv_a == nullptr) {
@@ -239,7 +302,21 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     const size_t kvx_f = static_cast<size_t>(F * heads * (c.qk_nope_head_dim + vh));
     const size_t s_f = static_cast<size_t>(core * heads * n_total);
     const size_t ctx_f = static_cast<size_t>(F * heads * vh);
-    int rc = ensure_buffer(&st->ws, &st->ws_floats, stream, q_f + ql_f + lat_f + kvn_f + kvx_f + s_f + ctx_f);
+    const bool mfma = L.table16 != nullptr && F >= 2 &&
+                      (path == LM_PATH_MFMA || (path == LM_PATH_AUTO && F >= kAttnMfmaTokens));
+    // MFMA projections: fp16 copies of x (read by the query and the key /
+    // value projections), of the q latent and of the key / value inputs
+    // (latent, then context), and partial sums for each stream
+    auto halves = [&](int64_t w) { return static_cast<size_t>((F * lm::round_up(w, lm::kPanel) + 127) / 2 / 64 * 64); };
+    const size_t x16a_f = mfma ? halves(H) : 0;
+    const size_t x16q_f = mfma && ql > 0 ? halves(ql) : 0;
+    const size_t x16kv_f = mfma ? halves(std::max(rank, heads * vh)) : 0;
+    const size_t partq_f = mfma ? static_cast<size_t>(4 * F * std::max(heads * qk, ql)) : 0;
+    const size_t partkv_f =
+        mfma ? static_cast<size_t>(4 * F * std::max({rank + rope, heads * (c.qk_nope_head_dim + vh), H})) : 0;
+    int rc = ensure_buffer(&st->ws, &st->ws_floats, stream,
+                           q_f + ql_f + lat_f + kvn_f + kvx_f + s_f + ctx_f + x16a_f + x16q_f + x16kv_f + partq_f +
+                               partkv_f);
     if (rc != LM_OK) {
         return rc;
     }
@@ -250,6 +327,13 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     float* kvx = kvn + kvn_f;
     float* S = kvx + kvx_f;
     float* ctxv = S + s_f;
+    _Float16* const x16a = reinterpret_cast<_Float16*>(ctxv + ctx_f);
+    _Float16* const x16q = reinterpret_cast<_Float16*>(ctxv + ctx_f + x16a_f);
+    _Float16* const x16kv = reinterpret_cast<_Float16*>(ctxv + ctx_f + x16a_f + x16q_f);
+    float* const partq = ctxv + ctx_f + x16a_f + x16q_f + x16kv_f;
+    float* const partkv = partq + partq_f;
+    ProjScratch psq{nullptr, nullptr, ql > 0 ? x16q : x16a, partq, static_cast<int64_t>(partq_f)};
+    ProjScratch pskv{nullptr, nullptr, x16kv, partkv, static_cast<int64_t>(partkv_f)};
 
     // queries (src/Attention.cpp:33-48); for one token the rotary step rides
     // on the projection's launch
@@ -264,10 +348,24 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
         LM_ATT_HIP(lm::launch_rms_norm(x, in_norm, xn_buf, F, static_cast<int32_t>(H), c.rms_norm_eps, stream));
         x = xn_buf;
     }
+    // MFMA path: x's fp16 copy, then the query path forks onto the side stream
+    hipStream_t qs = stream;
+    if (mfma) {
+        LM_ATT_HIP(lm::launch_to_f16_rows(x, x16a, F, static_cast<int32_t>(H),
+                                          static_cast<int32_t>(lm::round_up(H, lm::kPanel)), stream));
+        psq.ready = pskv.ready = x16a;
+        psq.ready_of = pskv.ready_of = x;
+        LM_ATT_HIP(hipEventRecord(st->fork, stream));
+        LM_ATT_HIP(hipStreamWaitEvent(st->side, st->fork, 0));
+        qs = st->side;
+    }
     const float* q_x = x;
     if (ql != 0) {
-        LM_ATT_HIP(lm::launch_matvec_tokens(L.q_a, x, qlat, ql, H, F, 1.0f, 0, stream));
-        LM_ATT_HIP(lm::launch_rms_norm(qlat, L.q_a_norm, qlat, F, static_cast<int32_t>(ql), c.rms_norm_eps, stream));
+        rc = project(L, lm::kProjQa, L.q_a, x, H, qlat, ql, F, 0, mfma, psq, qs);
+        if (rc != LM_OK) {
+            return rc;
+        }
+        LM_ATT_HIP(lm::launch_rms_norm(qlat, L.q_a_norm, qlat, F, static_cast<int32_t>(ql), c.rms_norm_eps, qs));
         q_x = qlat;
     }
     const uint16_t* q_w = ql == 0 ? L.q_proj : L.q_b;
@@ -277,21 +375,34 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     } else if (q_fused) {
         LM_ATT_HIP(lm::launch_query_rope_one(a, q_w, q_x, q, q_in, pos0, stream));
     } else {
-        LM_ATT_HIP(lm::launch_matvec_tokens(q_w, q_x, q, heads * qk, q_in, F, 1.0f, 0, stream));
-        LM_ATT_HIP(lm::launch_rope_query(a, q, F, pos0, stream));
+        rc = project(L, ql == 0 ? lm::kProjQ : lm::kProjQb, q_w, q_x, q_in, q, heads * qk, F, 0, mfma, psq, qs);
+        if (rc != LM_OK) {
+            return rc;
+        }
+        LM_ATT_HIP(lm::launch_rope_query(a, q, F, pos0, qs));
     }
     // compressed keys and values, appended at slots n0 .. n0 + F - 1 (:50-75);
     // for one token the norm, kv_b and the append are one launch
     if (!kv_a_with_q) {
-        LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_a, x, lat, rank + rope, H, F, 1.0f, 0, stream));
+        rc = project(L, lm::kProjKva, L.kv_a, x, H, lat, rank + rope, F, 0, mfma, pskv, stream);
+        if (rc != LM_OK) {
+            return rc;
+        }
     }
     if (F == 1 && lm::kv_one_supported(a)) {
         LM_ATT_HIP(lm::launch_kv_one(a, L.cache, L.kv_b, lat, L.kv_a_norm, c.rms_norm_eps, n0, pos0, stream));
     } else {
         LM_ATT_HIP(lm::launch_kv_prep(a, L.cache, lat, L.kv_a_norm, kvn, F, n0, pos0, c.rms_norm_eps, stream));
-        LM_ATT_HIP(lm::launch_matvec_tokens(L.kv_b, kvn, kvx, heads * (c.qk_nope_head_dim + vh), rank, F, 1.0f, 0,
-                                            stream));
+        rc = project(L, lm::kProjKvb, L.kv_b, kvn, rank, kvx, heads * (c.qk_nope_head_dim + vh), F, 0, mfma, pskv,
+                     stream);
+        if (rc != LM_OK) {
+            return rc;
+        }
         LM_ATT_HIP(lm::launch_kv_append(a, L.cache, kvx, F, n0, stream));
+    }
+    if (mfma) {  // join: the queries are in
+        LM_ATT_HIP(hipEventRecord(st->join, st->side));
+        LM_ATT_HIP(hipStreamWaitEvent(stream, st->join, 0));
     }
     // causal attention over the cache (:77-98), in groups of query tokens
     for (int64_t t0 = 0; t0 < F; t0 += core) {
@@ -300,7 +411,10 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
                                              st->scale, stream));
     }
     // output projection (:100-101)
-    LM_ATT_HIP(lm::launch_matvec_tokens(L.o, ctxv, out, H, heads * vh, F, 1.0f, accumulate, stream));
+    rc = project(L, lm::kProjO, L.o, ctxv, heads * vh, out, H, F, accumulate, mfma, pskv, stream);
+    if (rc != LM_OK) {
+        return rc;
+    }
     L.count = n_total;
     return LM_OK;
 }
@@ -410,6 +524,16 @@ int lm_attention_configure(lm_context* ctx, const lm_mla_config* config) {
         if (!lm::attention_shape_supported(a)) {
             return cleanup(fail(LM_EINVAL, "attention shape not supported"));
         }
+        err = hipStreamCreateWithFlags(&st->side, hipStreamNonBlocking);  // default priority
+        if (err == hipSuccess) {
+            err = hipEventCreateWithFlags(&st->fork, hipEventDisableTiming);
+        }
+        if (err == hipSuccess) {
+            err = hipEventCreateWithFlags(&st->join, hipEventDisableTiming);
+        }
+        if (err != hipSuccess) {
+            return cleanup(fail(LM_EHIP, std::string("attention stream: ") + hipGetErrorString(err)));
+        }
         lm::context_attention(ctx) = st;
         return LM_OK;
     } catch (const std::bad_alloc&) {
@@ -508,6 +632,75 @@ int lm_upload_attention(lm_context* ctx, int32_t layer, const uint16_t* q_proj_h
         L.slab = nullptr;
         return rc;
     }
+    // fp16 panel copies of the projections for the MFMA path, when every width
+    // a projection reads is a multiple of 32 and no weight overflows fp16
+    (void)hipFree(L.slab16);
+    L.slab16 = nullptr;
+    L.table16 = nullptr;
+    const bool panels = H % lm::kPanel == 0 && rank % lm::kPanel == 0 && (heads * vh) % lm::kPanel == 0 &&
+                        (!lora || ql % lm::kPanel == 0);
+    if (panels) {
+        struct Piece {
+            int proj;
+            int64_t off, rows, cols;
+        };
+        const Piece pieces[] = {{lm::kProjQ, off_q, lora ? 0 : heads * qk, H},
+                                {lm::kProjQa, off_qa, lora ? ql : 0, H},
+                                {lm::kProjQb, off_qb, lora ? heads * qk : 0, ql},
+                                {lm::kProjKva, off_kva, rank + rope, H},
+                                {lm::kProjKvb, off_kvb, heads * (c.qk_nope_head_dim + vh), rank},
+                                {lm::kProjO, off_o, H, heads * vh}};
+        int64_t bytes16 = align(static_cast<int64_t>(sizeof(void*)) * lm::kProjCount + sizeof(int));
+        int64_t offs16[lm::kProjCount] = {};
+        for (const Piece& pc : pieces) {
+            offs16[pc.proj] = bytes16;
+            bytes16 += align(pc.rows * pc.cols * 2);
+        }
+        err = hipMalloc(&L.slab16, static_cast<size_t>(bytes16));
+        if (err != hipSuccess) {
+            (void)hipFree(L.slab);
+            L.slab = nullptr;
+            return fail(LM_ENOMEM, "fp16 attention weights of layer " + std::to_string(layer) + ": " +
+                                       hipGetErrorString(err));
+        }
+        char* b16 = static_cast<char*>(L.slab16);
+        int* d_overflow = reinterpret_cast<int*>(b16 + sizeof(void*) * lm::kProjCount);
+        const _Float16* table[lm::kProjCount] = {};
+        for (const Piece& pc : pieces) {
+            table[pc.proj] = pc.rows > 0 ? reinterpret_cast<const _Float16*>(b16 + offs16[pc.proj]) : nullptr;
+        }
+        rc = LM_OK;
+        err = hipMemcpyAsync(b16, table, sizeof table, hipMemcpyHostToDevice, info.stream);
+        if (err == hipSuccess) {
+            err = hipMemsetAsync(d_overflow, 0, sizeof(int), info.stream);
+        }
+        for (const Piece& pc : pieces) {
+            if (err == hipSuccess && pc.rows > 0) {
+                err = lm::launch_bf16_to_f16_panels(reinterpret_cast<const uint16_t*>(base + pc.off),
+                                                    reinterpret_cast<_Float16*>(b16 + offs16[pc.proj]), pc.rows,
+                                                    pc.cols, d_overflow, info.stream);
+            }
+        }
+        int overflow = 0;
+        if (err == hipSuccess) {
+            err = hipMemcpyAsync(&overflow, d_overflow, sizeof(int), hipMemcpyDeviceToHost, info.stream);
+        }
+        if (err == hipSuccess) {
+            err = hipStreamSynchronize(info.stream);
+        }
+        if (err != hipSuccess) {
+            (void)hipFree(L.slab);
+            (void)hipFree(L.slab16);
+            L.slab = L.slab16 = nullptr;
+            return fail(LM_EHIP, std::string("fp16 attention weights: ") + hipGetErrorString(err));
+        }
+        if (overflow == 0) {
+            L.table16 = reinterpret_cast<const _Float16* const*>(b16);
+        } else {
+            (void)hipFree(L.slab16);  // a weight outside fp16's range: the layer keeps the BF16 path
+            L.slab16 = nullptr;
+        }
+    }
     L.q_proj = lora ? nullptr : reinterpret_cast<const uint16_t*>(base + off_q);
     L.q_a = lora ? reinterpret_cast<const uint16_t*>(base + off_qa) : nullptr;
     L.q_a_norm = lora ? reinterpret_cast<const float*>(base + off_qan) : nullptr;
@@ -574,7 +767,7 @@ int lm_attention_forward(lm_context* ctx, int32_t layer, const float* x_dev, int
         const int64_t room = st->cfg.context_length - L.count;
         const int64_t F = std::min(tokens, room);
         if (F > 0) {
-            rc = attention_tokens(st, info.stream, layer, x_dev, F, position0, out_dev, accumulate);
+            rc = attention_tokens(st, info.stream, layer, x_dev, F, position0, out_dev, accumulate, st->path);
             if (rc != LM_OK) {
                 return rc;
             }
@@ -587,6 +780,19 @@ int lm_attention_forward(lm_context* ctx, int32_t layer, const float* x_dev, int
     } catch (const std::bad_alloc&) {
         return fail(LM_ENOMEM, "host allocation failed");
     }
+}
+
+int lm_attention_set_path(lm_context* ctx, int32_t path) {
+    AttnState* st = nullptr;
+    const int rc = get_state(ctx, &st);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (path < LM_PATH_AUTO || path > LM_PATH_MFMA) {
+        return fail(LM_EINVAL, "unknown path");
+    }
+    st->path = path;
+    return LM_OK;
 }
 
 int lm_kv_cache_clear(lm_context* ctx) {
@@ -724,7 +930,7 @@ int lm_decoder_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer,
             }
             float* xn = st->xn;
             for (int32_t l = first_layer; l <= last_layer && rc == LM_OK; ++l) {
-                rc = attention_tokens(st, info.stream, l, hidden_dev, F, position0, hidden_dev, 1,
+                rc = attention_tokens(st, info.stream, l, hidden_dev, F, position0, hidden_dev, 1, path,
                                       st->layers[l].input_norm, xn);
                 if (rc == LM_OK) {
                     rc = lm::ffn_sublayer(ctx, l, hidden_dev, F, path);

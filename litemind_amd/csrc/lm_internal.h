@@ -131,6 +131,11 @@ struct ExpertArgs {
     int32_t hidden, hidden_p, experts, top_k;
     int32_t inter_p, shared_inter_p;   // padded widths (shared 0 = none)
     int32_t has_shared;
+    // Down GEMM of a layer without routed experts only: K split into ksplit
+    // chunks (0 or 1: none), chunk c's partial sums [T, hidden] at
+    // partial + c T hidden instead of down_out.
+    int32_t ksplit;
+    float* partial;
 };
 
 struct CombineArgs {
@@ -437,7 +442,16 @@ hipError_t launch_gemv_down(const ExpertArgs& a, int64_t max_groups, hipStream_t
 // Grouped SwiGLU on MFMA (k_mfma.hip): fp16 panel operands, fp32 accumulation.
 hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s);
+// out [M, N] = a16 . W^T (accumulate: out += a16 . W^T) for a16 [M, Kp] and W
+// [N, Kp] fp16 panels (*w, a device pointer to the matrix), fp32 accumulation,
+// on the down kernel as one group of M rows.  With few tiles the K range is
+// split (partial sums, then added in chunk order).  scratch: floats for the
+// partial sums (at least M N when accumulating; up to 4 M N are used).
+hipError_t launch_mfma_gemm(const _Float16* a16, const _Float16* const* w, float* out, int64_t M, int32_t N, int32_t Kp,
+                            int32_t accumulate, float* scratch, int64_t scratch_floats, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
+// out[i] += y[i] for n floats.
+hipError_t launch_add_rows(float* out, const float* y, int64_t n, hipStream_t s);
 // out [T*K + T, H]: the down projection of each routed assignment in
 // assignment order (down_out[slot_of[a]]), then the T shared rows (zero
 // without a shared expert).  hidden % 4 == 0.

@@ -1,5 +1,6 @@
 """Multi-head latent attention on the GPU (include/litemind_attention.h) against
-the oracle's Attention::forward (src/Attention.cpp:22-103), bit for bit: the
+the oracle's Attention::forward (src/Attention.cpp:22-103), bit for bit on the
+bit-exact projection path (LM_PATH_GEMV, which these tests select): the
 outputs and the KV cache contents, for decode (one token per call), batched
 prefill (T tokens per call, causal) and their mix, with and without the
 q_lora path and YaRN, positions past the rotary table, a cache that fills, the
@@ -37,12 +38,15 @@ def moe_dims_for(hidden):
 class Mla:
     """A context holding one attention layer (id 0) and the oracle's mirror of it."""
 
-    def __init__(self, d, seed, layers=1):
+    def __init__(self, d, seed, layers=1, path=None):
+        from litemind_amd import PATH_GEMV
+        path = PATH_GEMV if path is None else path
         from litemind_amd import Context
         from litemind_amd import workload as wl
         self.d = d
         self.ctx = Context(moe_dims_for(d.hidden).moe_config(num_layers=layers))
         self.ctx.attention_configure(wl.mla_config(d))
+        self.ctx.attention_set_path(path)
         self.L = wl.mla_layer(seed, 0, d)
         wl.upload_mla_layer(self.ctx, 0, self.L)
         self.cache = ol.OracleKvCache(d, d.max_positions)
@@ -363,6 +367,8 @@ def test_decoder_layers_match_oracle_chain():
             return h
 
         from litemind_amd import PATH_AUTO, PATH_GEMV
+        # 5 tokens: below the attention's MFMA crossover, so AUTO would be
+        # bit-exact too; GEMV selects the fp32 FFN path as well
         for lo, hi, path in ((0, 5, PATH_GEMV), (5, 6, PATH_AUTO)):
             dh = ctx.to_device(h0[lo:hi])
             ctx.decoder_forward(0, 1, dh, hi - lo, lo, path)
@@ -376,3 +382,77 @@ def test_decoder_layers_match_oracle_chain():
         assert ctx.kv_cache_tokens(0) == 6 and ctx.kv_cache_tokens(1) == 6
     finally:
         ctx.close()
+
+
+# ---- MFMA projections (tolerance-bounded) ----
+# fp16 operands with fp32 accumulation in the four projections of a batch:
+# every projection output carries the fp16 rounding of its input (~2^-12
+# relative per element), which passes through the scores and the softmax into
+# the context and o_proj.  Measured on V2-Lite shapes (512-token prefill):
+# mean relative error ~1e-3 on the attention output; bar 5e-3 mean-rel and
+# max-abs 5e-2 on outputs of magnitude ~1.  The KV cache entries (produced by
+# kv_a / kv_b) are held to the same bar.
+ATT_MEAN_REL = 5e-3
+ATT_MAX_ABS = 5e-2
+
+
+@pytest.mark.parametrize("q_lora", [0, 1536])
+def test_mfma_projections_v2_lite_prefill_then_decode(q_lora):
+    """A 512-token prefill on the MFMA projection path (LM_PATH_AUTO) at
+    V2-Lite shapes with and without the q LoRA path, then two decode steps
+    (single-token launches over the MFMA-filled cache), against the oracle."""
+    from litemind_amd import PATH_AUTO
+    from litemind_amd import workload as wl
+    d = dataclasses.replace(wl.V2_LITE_MLA, q_lora_rank=q_lora, max_positions=520)
+    announce(f"attention MFMA projections V2-Lite q_lora={q_lora}: prefill 512 + decode 2")
+    m = Mla(d, 191, path=PATH_AUTO)
+    try:
+        x = tokens(192, 514, d.hidden)
+        y = m.forward(x[:512], 0)
+        want, _ = m.oracle(x[:512], 0)
+        assert np.all(np.isfinite(y))
+        mx, rel = layer_error(y, want)
+        print(f"prefill 512 q_lora={q_lora}: max_abs={mx:.3e} mean_rel={rel:.3e} (|y| mean {np.abs(want).mean():.3f})")
+        assert mx <= ATT_MAX_ABS and rel <= ATT_MEAN_REL
+        n = 512
+        kn, kr, v = m.ctx.kv_cache_read(0, n)
+        for got, ref, name in ((kn, m.cache.key_nope[:n], "key_nope"), (kr, m.cache.key_rope[:n], "key_rope"),
+                               (v, m.cache.value[:n], "value")):
+            mx, rel = layer_error(got, ref)
+            print(f"cache {name}: max_abs={mx:.3e} mean_rel={rel:.3e}")
+            assert mx <= ATT_MAX_ABS and rel <= ATT_MEAN_REL, name
+        for t in (512, 513):
+            y = m.forward(x[t:t + 1], t)
+            want, _ = m.oracle(x[t:t + 1], t)
+            mx, rel = layer_error(y, want)
+            print(f"decode {t}: max_abs={mx:.3e} mean_rel={rel:.3e}")
+            assert mx <= ATT_MAX_ABS and rel <= ATT_MEAN_REL
+    finally:
+        m.close()
+
+
+def test_mfma_path_selection():
+    """LM_PATH_AUTO below 16 tokens keeps the bit-exact projections; LM_PATH_MFMA
+    takes the MFMA projections from two tokens (within tolerance, and not bit
+    for bit equal on these inputs); an unknown path is refused."""
+    from litemind_amd import PATH_AUTO, PATH_MFMA, LmError
+    from litemind_amd import workload as wl
+    d = dataclasses.replace(wl.V2_LITE_MLA, max_positions=32)
+    announce("attention path selection: AUTO T=8 bit-exact, MFMA T=8 within tolerance")
+    m = Mla(d, 201, path=PATH_AUTO)
+    try:
+        x = tokens(202, 16, d.hidden)
+        y = m.forward(x[:8], 0)
+        want, _ = m.oracle(x[:8], 0)
+        np.testing.assert_array_equal(bits(y), bits(want))
+        m.ctx.attention_set_path(PATH_MFMA)
+        y = m.forward(x[8:16], 8)
+        want, _ = m.oracle(x[8:16], 8)
+        mx, rel = layer_error(y, want)
+        print(f"MFMA T=8: max_abs={mx:.3e} mean_rel={rel:.3e}")
+        assert mx <= ATT_MAX_ABS and rel <= ATT_MEAN_REL
+        assert not np.array_equal(bits(y), bits(want))
+        with pytest.raises(LmError):
+            m.ctx.attention_set_path(7)
+    finally:
+        m.close()
