@@ -112,6 +112,30 @@ int lm_attention_forward(lm_context* ctx, int32_t layer, const float* x_dev, int
  * not multiples of 32, or whose weights overflow fp16, always take the
  * bit-exact path. */
 int lm_attention_set_path(lm_context* ctx, int32_t path);
+/* With MFMA projections the attention core (scores, softmax, context) also
+ * runs on MFMA when qk_nope and qk_rope are multiples of 32, v_head_dim of 8
+ * and heads * v_head_dim of 32: per head S = Q K^T and ctx = P V with fp16
+ * operands over fp16 copies of the cache made once per call, P the causal
+ * softmax in fp32 rounded to fp16; within the MFMA path's tolerance.
+ *
+ * The core takes the call's query tokens in groups sized from a byte budget
+ * for its scratch (no LiteMind counterpart): the fp32 scores, and for the MFMA
+ * core the fp16 copies of the keys, values, queries and probabilities.  A
+ * group holds as many tokens as fit the budget, at least one and at most 512;
+ * the MFMA core is used while its key / value copies take at most half of it.
+ * bytes = 0 restores the default of 1 GiB. */
+int lm_attention_set_score_budget(lm_context* ctx, int64_t bytes);
+typedef struct lm_attention_core_plan {
+    int64_t query_group;   /* query tokens per core launch */
+    int64_t scratch_bytes; /* the core's scratch at that group size */
+    int32_t mfma_core;     /* 1: scores and context on MFMA */
+    int32_t reserved;
+} lm_attention_core_plan;
+/* The sizing lm_attention_forward chooses for `tokens` new tokens after
+ * `cached` ones on a layer with fp16 weight copies, for a path and a budget
+ * (0: the default); host only, no context or GPU. */
+int lm_attention_plan_core(const lm_mla_config* config, int64_t cached, int64_t tokens, int32_t path,
+                           int64_t budget_bytes, lm_attention_core_plan* out);
 /* KvCache::clear for every layer (src/DeepSeekRunner.cpp:432-437, DeepSeekRunner::reset). */
 int lm_kv_cache_clear(lm_context* ctx);
 /* KvCache::token_count of a layer. */

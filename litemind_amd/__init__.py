@@ -150,6 +150,8 @@ PROTOTYPES = {
     "lm_attention_forward": [_P, _I32, _P, _I64, _I64, _P, _I32],
     "lm_kv_cache_clear": [_P],
     "lm_attention_set_path": [_P, _I32],
+    "lm_attention_set_score_budget": [_P, _I64],
+    "lm_attention_plan_core": [_P, _I64, _I64, _I32, _I64, _P],
     "lm_kv_cache_tokens": [_P, _I32, _P],
     "lm_kv_cache_read": [_P, _I32, _I64, _P, _P, _P],
     "lm_decoder_forward": [_P, _I32, _I32, _P, _I64, _I64, _I32],
@@ -246,6 +248,28 @@ def rope_tables(config: MlaConfig, positions: int):
     sin = np.zeros((positions, half), np.float32)
     _check_status(lib, lib.lm_rope_tables(C.byref(config), positions, _ptr(cos), _ptr(sin)))
     return cos, sin
+
+
+class AttentionCorePlan(C.Structure):
+    """lm_attention_core_plan: the attention core's query group and scratch for one call."""
+
+    _fields_ = [
+        ("query_group", C.c_int64),
+        ("scratch_bytes", C.c_int64),
+        ("mfma_core", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
+def attention_plan_core(config: MlaConfig, cached: int, tokens: int, path: int = 0,
+                        budget_bytes: int = 0) -> AttentionCorePlan:
+    """The query grouping lm_attention_forward takes after `cached` tokens (lm_attention_plan_core,
+    host only)."""
+    lib = load_library()
+    out = AttentionCorePlan()
+    _check_status(lib, lib.lm_attention_plan_core(C.byref(config), cached, tokens, path, budget_bytes,
+                                                  C.byref(out)))
+    return out
 
 
 def mla_softmax_scale(config: MlaConfig) -> float:
@@ -424,6 +448,10 @@ class Context:
     def attention_set_path(self, path: int) -> None:
         """Projection path of attention_forward (lm_attention_set_path)."""
         self._check(self.lib.lm_attention_set_path(self.handle, path))
+
+    def attention_set_score_budget(self, nbytes: int) -> None:
+        """Byte budget of the attention core's scratch (lm_attention_set_score_budget; 0: default)."""
+        self._check(self.lib.lm_attention_set_score_budget(self.handle, nbytes))
 
     def kv_cache_clear(self) -> None:
         self._check(self.lib.lm_kv_cache_clear(self.handle))

@@ -1100,6 +1100,192 @@ __global__ __launch_bounds__(kCtxThreads) void context_decode_kernel(const float
     }
 }
 
+// ---- attention core on MFMA (fp16 operands, fp32 accumulation) ----
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+//
+// The projection path's tolerance path for batches of query tokens: per head,
+// S = Q K^T and ctx = P V are GEMMs of the grouped MFMA kernel (one group per
+// head), over fp16 copies of the cache in panel layout made once per call:
+//   keys16    [heads][Kp rows][qk]    row j = [key_nope(h, :, j) | key_rope(:, j)]
+//   values16  [heads][vh rows][Kp]    value(h, j, :) transposed, the K of P V
+// with Kp = keys rounded up to 32 and zeros past the last key (P is zero
+// there too, so no padding value reaches a sum).
+
+// keys16 from the fp32 cache: workgroup (key block of 64, 32-channel panel,
+// head) reads 32 channel rows of 64 keys (256 B each, coalesced), transposes
+// them in LDS and writes the panel's 64 rows of 64 bytes (contiguous).
+__global__ __launch_bounds__(256) void pack_keys16_kernel(const float* __restrict__ key_nope,
+                                                          const float* __restrict__ key_rope,
+                                                          _Float16* __restrict__ k16, int32_t nope, int32_t qk,
+                                                          int64_t cap, int64_t keys, int64_t kp) {
+    __shared__ float tile[32][65];
+    const int tid = threadIdx.x;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int p = blockIdx.y;
+    const int h = blockIdx.z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int e = tid + 256 * i;
+        const int ch = e >> 6, kk = e & 63;
+        const int c = p * 32 + ch;
+        const int64_t j = j0 + kk;
+        float v = 0.0f;
+        if (j < keys) {
+            v = c < nope ? key_nope[(static_cast<int64_t>(h) * nope + c) * cap + j]
+                         : key_rope[static_cast<int64_t>(c - nope) * cap + j];
+        }
+        tile[ch][kk] = v;
+    }
+    __syncthreads();
+    const int kk = tid >> 2, part = tid & 3;
+    const int64_t j = j0 + kk;
+    if (j < kp) {
+        half8 out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            out[e] = static_cast<_Float16>(tile[part * 8 + e][kk]);
+        }
+        _Float16* const dst = k16 + static_cast<int64_t>(h) * kp * qk + (static_cast<int64_t>(p) * kp + j) * kPanel;
+        *reinterpret_cast<half8*>(dst + part * 8) = out;
+    }
+}
+
+// values16 from the fp32 cache: workgroup (panel of 32 keys, head) reads the
+// 32 keys' value rows (coalesced over channels), transposes them in LDS
+// (32 x (vh + 1) floats, dynamic) and writes vh rows of 64 bytes (contiguous).
+__global__ __launch_bounds__(256) void pack_values16_kernel(const float* __restrict__ value,
+                                                            _Float16* __restrict__ v16, int32_t vh, int64_t cap,
+                                                            int64_t keys, int64_t kp) {
+    extern __shared__ float vtile[];  // [32][vh + 1]
+    const int tid = threadIdx.x;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * kPanel;
+    const int h = blockIdx.y;
+    const int stride = vh + 1;
+    for (int e = tid; e < 32 * vh; e += 256) {
+        const int kk = e / vh, c = e - kk * vh;
+        const int64_t j = j0 + kk;
+        vtile[kk * stride + c] = j < keys ? value[(static_cast<int64_t>(h) * cap + j) * vh + c] : 0.0f;
+    }
+    __syncthreads();
+    _Float16* const dst = v16 + static_cast<int64_t>(h) * vh * kp + static_cast<int64_t>(blockIdx.x) * vh * kPanel;
+    for (int e = tid; e < 4 * vh; e += 256) {
+        const int c = e >> 2, part = e & 3;
+        half8 out;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            out[i] = static_cast<_Float16>(vtile[(part * 8 + i) * stride + c]);
+        }
+        *reinterpret_cast<half8*>(dst + c * kPanel + part * 8) = out;
+    }
+}
+
+// q [T][heads][qk] fp32 -> q16 [heads T rows][qk] panels, row h T + t (the
+// query rows of head h are group h).  Thread i converts 8 channels.
+__global__ __launch_bounds__(256) void pack_queries16_kernel(const float* __restrict__ q, _Float16* __restrict__ q16,
+                                                             int32_t heads, int32_t qk, int64_t T) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int per_row = qk / 8;
+    const int64_t rows = heads * T;
+    if (i >= rows * per_row) {
+        return;
+    }
+    const int64_t r = i / per_row;
+    const int c0 = static_cast<int>(i - r * per_row) * 8;
+    const int64_t h = r / T, t = r - h * T;
+    const float4* src = reinterpret_cast<const float4*>(q + (t * heads + h) * qk + c0);
+    const float4 a = src[0], b = src[1];
+    const half8 out = {static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+                       static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+                       static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
+    *reinterpret_cast<half8*>(q16 + panel_index(r, c0, rows)) = out;
+}
+
+// Causal softmax of the raw scores S [heads T rows][Kp] (row h T + t sees keys
+// 0 .. n0 + t) into P [heads T rows][Kp] fp16 panels: p = exp(s scale - max)
+// / total, zero past the row's last key.  One wave per row; lane l owns the
+// 8 columns 512 k + 8 l .. + 7 of each 512-column step (two 16-byte loads, one
+// 16-byte store into the panel of those columns).
+__global__ __launch_bounds__(256) void softmax_p16_kernel(const float* __restrict__ S, _Float16* __restrict__ P,
+                                                          int64_t rows, int64_t T, int64_t n0, int64_t kp,
+                                                          float scale) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= rows) {
+        return;
+    }
+    const int64_t valid = n0 + r % T + 1;
+    const float* const row = S + r * kp;
+    float m = -INFINITY;
+    for (int64_t j = 8 * lane; j < valid; j += 512) {
+        const float4 a = *reinterpret_cast<const float4*>(row + j);
+        const float4 b = *reinterpret_cast<const float4*>(row + j + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (j + e < valid) {
+                m = fmaxf(m, v[e] * scale);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o));
+    }
+    float total = 0.0f;
+    for (int64_t j = 8 * lane; j < valid; j += 512) {
+        const float4 a = *reinterpret_cast<const float4*>(row + j);
+        const float4 b = *reinterpret_cast<const float4*>(row + j + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (j + e < valid) {
+                total += __expf(v[e] * scale - m);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        total += __shfl_xor(total, o);
+    }
+    const float inv = 1.0f / total;
+    for (int64_t j = 8 * lane; j < kp; j += 512) {
+        half8 out = {};
+        if (j < valid) {
+            const float4 a = *reinterpret_cast<const float4*>(row + j);
+            const float4 b = *reinterpret_cast<const float4*>(row + j + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                out[e] = static_cast<_Float16>(j + e < valid ? __expf(v[e] * scale - m) * inv : 0.0f);
+            }
+        }
+        *reinterpret_cast<half8*>(P + panel_index(r, j, rows)) = out;
+    }
+}
+
+// c32 [heads T rows][vh] (row h T + t) -> ctx16 [ctx_rows][heads vh] panels at
+// row row0 + t, column h vh + c: the output projection's fp16 input.  Thread i
+// converts 8 channels.
+__global__ __launch_bounds__(256) void unpack_context16_kernel(const float* __restrict__ c32,
+                                                               _Float16* __restrict__ ctx16, int32_t heads,
+                                                               int32_t vh, int64_t T, int64_t row0,
+                                                               int64_t ctx_rows) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int per_row = vh / 8;
+    if (i >= heads * T * per_row) {
+        return;
+    }
+    const int64_t r = i / per_row;
+    const int c0 = static_cast<int>(i - r * per_row) * 8;
+    const int64_t h = r / T, t = r - h * T;
+    const float4* src = reinterpret_cast<const float4*>(c32 + r * vh + c0);
+    const float4 a = src[0], b = src[1];
+    const half8 out = {static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+                       static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+                       static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
+    *reinterpret_cast<half8*>(ctx16 + panel_index(row0 + t, h * vh + c0, ctx_rows)) = out;
+}
+
 unsigned blocks_of(int64_t n, int64_t per) { return static_cast<unsigned>((n + per - 1) / per); }
 
 }  // namespace
@@ -1249,6 +1435,71 @@ hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const 
         hipLaunchKernelGGL(context_kernel<kQueries>, dim3(a.heads, blocks_of(T, kQueries)), dim3(threads), 0, s, S,
                            c.value, ctx, a.heads, a.vh, a.cap, n0, T, n_stride);
     }
+    return hipGetLastError();
+}
+
+bool attention_mfma_supported(const AttnShape& a) {
+    // whole panels of channels for the queries and keys and for the context's
+    // fp16 copy [T, heads vh] (no padding columns to clear); 8-channel stores
+    return a.nope % kPanel == 0 && a.rope % kPanel == 0 && a.nope + a.rope > 0 && a.vh % 8 == 0 && a.vh <= 256 &&
+           (a.heads * a.vh) % kPanel == 0;
+}
+
+hipError_t launch_pack_kv16(const AttnShape& a, const KvCacheDev& c, int64_t keys, _Float16* k16, _Float16* v16,
+                            hipStream_t s) {
+    if (keys <= 0) {
+        return hipSuccess;
+    }
+    const int64_t kp = round_up(keys, kPanel);
+    const int qk = a.nope + a.rope;
+    hipLaunchKernelGGL(pack_keys16_kernel, dim3(blocks_of(kp, 64), static_cast<unsigned>(qk / kPanel), a.heads),
+                       dim3(256), 0, s, c.key_nope, c.key_rope, k16, a.nope, qk, a.cap, keys, kp);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL(pack_values16_kernel, dim3(static_cast<unsigned>(kp / kPanel), a.heads), dim3(256),
+                       sizeof(float) * kPanel * (a.vh + 1), s, c.value, v16, a.vh, a.cap, keys, kp);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_core_mfma(const AttnShape& a, const float* q, const AttnMfmaBufs& b, int64_t T,
+                                      int64_t n0, int64_t keys, float scale, _Float16* ctx16, int64_t row0,
+                                      int64_t ctx_rows, hipStream_t s) {
+    if (T <= 0) {
+        return hipSuccess;
+    }
+    if (n0 + T > keys || row0 + T > ctx_rows) {
+        return hipErrorInvalidValue;
+    }
+    const int qk = a.nope + a.rope;
+    const int64_t kp = round_up(keys, kPanel);
+    const int64_t rows = a.heads * T;
+    hipLaunchKernelGGL(pack_queries16_kernel, dim3(blocks_of(rows * (qk / 8), 256)), dim3(256), 0, s, q, b.q16,
+                       a.heads, qk, T);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    // S = Q K^T per head: rows h T + t, Kp columns (keys past the last are zero rows)
+    err = launch_mfma_heads(b.q16, b.k16, kp * qk, b.S, a.heads, T, static_cast<int32_t>(kp), qk, b.meta, s);
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL(softmax_p16_kernel, dim3(blocks_of(rows, 4)), dim3(256), 0, s, b.S, b.p16, rows, T, n0, kp,
+                       scale);
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    // ctx = P V per head: K = Kp (zero probabilities and zero values past the last key)
+    err = launch_mfma_heads(b.p16, b.v16, static_cast<int64_t>(a.vh) * kp, b.c32, a.heads, T, a.vh,
+                            static_cast<int32_t>(kp), b.meta, s);
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL(unpack_context16_kernel, dim3(blocks_of(rows * (a.vh / 8), 256)), dim3(256), 0, s, b.c32,
+                       ctx16, a.heads, a.vh, T, row0, ctx_rows);
     return hipGetLastError();
 }
 

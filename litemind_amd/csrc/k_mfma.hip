@@ -612,6 +612,57 @@ hipError_t launch_mfma_gemm(const _Float16* a16, const _Float16* const* w, float
     return hipGetLastError();
 }
 
+namespace {
+// The group table of launch_mfma_heads: every head a group of `rows` rows.
+__global__ __launch_bounds__(64) void heads_table_kernel(int32_t* counts, int32_t* offsets, const _Float16** ptrs,
+                                                         const _Float16* w16, int64_t w_stride, int32_t heads,
+                                                         int32_t rows) {
+    const int g = blockIdx.x * 64 + threadIdx.x;
+    if (g < heads) {
+        counts[g] = rows;
+        offsets[g] = g * rows;
+        ptrs[g] = w16 + g * w_stride;
+    } else if (g == heads) {
+        offsets[g] = heads * rows;
+    }
+}
+}  // namespace
+
+hipError_t launch_mfma_heads(const _Float16* a16, const _Float16* w16, int64_t w_stride, float* out, int32_t heads,
+                             int64_t rows, int32_t N, int32_t Kp, void* meta, hipStream_t s) {
+    if (rows <= 0 || heads <= 0 || N <= 0) {
+        return hipSuccess;
+    }
+    if (Kp <= 0 || Kp % BK != 0 || heads * rows > 0x7fffffff) {
+        return hipErrorInvalidValue;
+    }
+    int32_t* const counts = static_cast<int32_t*>(meta);
+    int32_t* const offsets = counts + heads;
+    const _Float16** const ptrs =
+        reinterpret_cast<const _Float16**>(static_cast<char*>(meta) + round_up(4 * (2 * heads + 1), 8));
+    hipLaunchKernelGGL(heads_table_kernel, dim3(static_cast<unsigned>(heads / 64 + 1)), dim3(64), 0, s, counts,
+                       offsets, ptrs, w16, w_stride, heads, static_cast<int32_t>(rows));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return e;
+    }
+    ExpertArgs ea{};
+    ea.groups.down_h = ptrs;
+    ea.rb.counts = counts;
+    ea.rb.offsets = offsets;
+    ea.act16 = const_cast<_Float16*>(a16);
+    ea.down_out = out;
+    ea.tokens = rows;
+    ea.top_k = heads;  // the kernel's routed rows: tokens * top_k = every head's rows
+    ea.experts = heads;
+    ea.hidden = N;
+    ea.hidden_p = static_cast<int32_t>(round_up(N, kPanel));
+    ea.inter_p = Kp;
+    ea.shared_inter_p = 0;
+    ea.has_shared = 0;
+    return launch<kDown>(ea, s);
+}
+
 hipError_t launch_mfma_gateup(const ExpertArgs& a, hipStream_t s) { return launch<kGateUp>(a, s); }
 
 hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s) { return launch<kDown>(a, s); }

@@ -16,7 +16,15 @@
 // or for every batch of two or more (LM_PATH_MFMA), each projection is a GEMM on
 // the grouped kernel of k_mfma.hip (one group of T rows): the input converted to
 // fp16 panels, the weights' fp16 panel copy made at upload, fp32 accumulation;
-// results within the tolerance of the MoE block's MFMA path.
+// results within the tolerance of the MoE block's MFMA path.  With MFMA
+// projections the attention core is MFMA as well where the shape allows it
+// (k_attn.hip): per head S = Q K^T and ctx = P V on the same grouped kernel,
+// over fp16 copies of the cache made once per call.
+//
+// Query tokens are processed by the core in groups sized from a byte budget
+// (lm_attention_set_score_budget, default 1 GiB) for the scores (and the MFMA
+// core's fp16 copies), so a long cache takes smaller groups instead of failing
+// to allocate.
 #include "litemind_attention.h"
 #include "lm_error.h"
 #include "lm_internal.h"
@@ -76,6 +84,7 @@ struct AttnState {
     size_t ws_floats = 0;
     float* xn = nullptr;      // lm_decoder_forward: normalised rows [T, H]
     size_t xn_floats = 0;
+    int64_t score_budget = 0; // bytes of the attention core's scratch (0: the default)
 };
 
 void attention_release(AttnState* st) {
@@ -111,13 +120,59 @@ namespace {
 using lm::AttnLayer;
 using lm::AttnState;
 
-// Query tokens per launch of the attention core: bounds the score scratch to
-// kCoreTokens * heads * (n0 + T) floats.
+// Query tokens per launch of the attention core, at most.
 constexpr int64_t kCoreTokens = 512;
+// Default byte budget of the attention core's scratch.
+constexpr int64_t kScoreBudget = int64_t{1} << 30;
 // LM_PATH_AUTO: batches of at least this many tokens take the MFMA projections.
 constexpr int64_t kAttnMfmaTokens = 16;
 
 int fail(int code, const std::string& message) { return lm::set_error(code, message); }
+
+// Sizing of the attention core for F tokens after `cached` ones.
+struct CorePlan {
+    int64_t group = 0;  // query tokens per core launch
+    bool mfma = false;  // scores and context on MFMA
+    int64_t kp = 0;     // keys rounded up to 32 (MFMA core)
+    int64_t bytes = 0;  // the core's scratch
+};
+
+// A query group of as many tokens as the budget holds (at least one, at most
+// kCoreTokens).  The MFMA core when the projections are MFMA, the shape allows
+// it, its fp16 copies of the keys and values fit in half the budget and its
+// operands stay within the grouped kernel's 32-bit buffer offsets; its scratch
+// per query token is heads (6 Kp + 2 qk) bytes (fp32 scores, fp16
+// probabilities and query), the VALU core's heads keys 4 bytes.
+CorePlan plan_core(const lm::AttnShape& a, int64_t cached, int64_t F, bool mfma_proj, int64_t budget) {
+    CorePlan p;
+    if (F <= 0) {
+        return p;
+    }
+    const int64_t keys = cached + F;
+    const int64_t heads = a.heads, qk = a.nope + a.rope, vh = a.vh;
+    const int64_t limit = 0x7fffffff;
+    if (mfma_proj && F >= 2 && lm::attention_mfma_supported(a)) {
+        const int64_t kp = lm::round_up(keys, lm::kPanel);
+        const int64_t fixed = heads * kp * (qk + vh) * 2;
+        const int64_t per = heads * (6 * kp + 2 * qk);
+        const int64_t group = std::min({(budget - fixed) / per, kCoreTokens, F, limit / (2 * heads * kp)});
+        if (fixed <= budget / 2 && group >= 1 && 4 * kp * std::max(qk, lm::round_up(vh, lm::kPanel)) <= limit) {
+            p.group = group;
+            p.mfma = true;
+            p.kp = kp;
+            p.bytes = fixed + group * per;
+            return p;
+        }
+    }
+    const int64_t per = heads * keys * 4;
+    p.group = std::max<int64_t>(1, std::min({budget / per, kCoreTokens, F}));
+    p.bytes = p.group * per;
+    return p;
+}
+
+bool mfma_projections(int32_t path, int64_t F) {
+    return F >= 2 && (path == LM_PATH_MFMA || (path == LM_PATH_AUTO && F >= kAttnMfmaTokens));
+}
 
 // yarn_get_mscale (src/Rope.cpp:13-18, src/Config.cpp:12-17):
 // 0.1 * mscale * log(scale) + 1, which LiteMind's GCC build fuses into one
@@ -293,47 +348,60 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
     const int64_t rank = c.kv_lora_rank, rope = c.qk_rope_head_dim, vh = c.v_head_dim, ql = c.q_lora_rank;
     const int64_t n0 = L.count;
     const int64_t n_total = n0 + F;
-    const int64_t core = std::min(F, kCoreTokens);
-    // scratch: q | q latent | kv latent | kv normalised | kv expanded | scores | context
-    const size_t q_f = static_cast<size_t>(F * heads * qk);
-    const size_t ql_f = static_cast<size_t>(F * ql);
-    const size_t lat_f = static_cast<size_t>(F * (rank + rope));
-    const size_t kvn_f = static_cast<size_t>(F * rank);
-    const size_t kvx_f = static_cast<size_t>(F * heads * (c.qk_nope_head_dim + vh));
-    const size_t s_f = static_cast<size_t>(core * heads * n_total);
-    const size_t ctx_f = static_cast<size_t>(F * heads * vh);
-    const bool mfma = L.table16 != nullptr && F >= 2 &&
-                      (path == LM_PATH_MFMA || (path == LM_PATH_AUTO && F >= kAttnMfmaTokens));
-    // MFMA projections: fp16 copies of x (read by the query and the key /
-    // value projections), of the q latent and of the key / value inputs
-    // (latent, then context), and partial sums for each stream
-    auto halves = [&](int64_t w) { return static_cast<size_t>((F * lm::round_up(w, lm::kPanel) + 127) / 2 / 64 * 64); };
-    const size_t x16a_f = mfma ? halves(H) : 0;
-    const size_t x16q_f = mfma && ql > 0 ? halves(ql) : 0;
-    const size_t x16kv_f = mfma ? halves(std::max(rank, heads * vh)) : 0;
-    const size_t partq_f = mfma ? static_cast<size_t>(4 * F * std::max(heads * qk, ql)) : 0;
-    const size_t partkv_f =
-        mfma ? static_cast<size_t>(4 * F * std::max({rank + rope, heads * (c.qk_nope_head_dim + vh), H})) : 0;
-    int rc = ensure_buffer(&st->ws, &st->ws_floats, stream,
-                           q_f + ql_f + lat_f + kvn_f + kvx_f + s_f + ctx_f + x16a_f + x16q_f + x16kv_f + partq_f +
-                               partkv_f);
+    const bool mfma = L.table16 != nullptr && mfma_projections(path, F);
+    const CorePlan plan = plan_core(a, n0, F, mfma, st->score_budget > 0 ? st->score_budget : kScoreBudget);
+    const int64_t core = plan.group;
+    // Scratch, each region a multiple of 64 floats: q | q latent | kv latent |
+    // kv normalised | kv expanded | scores | context; with MFMA projections
+    // fp16 copies of x (read by the query and the key / value projections), of
+    // the q latent and of the key / value inputs (latent, then context), and
+    // partial sums for each stream; with the MFMA core fp16 copies of the keys,
+    // values, queries and probabilities and the per-head group table.
+    size_t total_f = 0;
+    auto region = [&](int64_t floats) {
+        const size_t at = total_f;
+        total_f += static_cast<size_t>((floats + 63) / 64 * 64);
+        return at;
+    };
+    auto halves = [](int64_t n) { return (n + 1) / 2; };
+    const int64_t kp = plan.kp;
+    const size_t q_at = region(F * heads * qk);
+    const size_t ql_at = region(F * ql);
+    const size_t lat_at = region(F * (rank + rope));
+    const size_t kvn_at = region(F * rank);
+    const size_t kvx_at = region(F * heads * (c.qk_nope_head_dim + vh));
+    const size_t s_at = region(plan.mfma ? core * heads * kp : core * heads * n_total);
+    const size_t ctx_at = region(F * heads * vh);
+    const size_t x16a_at = region(mfma ? halves(F * lm::round_up(H, lm::kPanel)) : 0);
+    const size_t x16q_at = region(mfma && ql > 0 ? halves(F * lm::round_up(ql, lm::kPanel)) : 0);
+    const size_t x16kv_at = region(mfma ? halves(F * lm::round_up(std::max(rank, heads * vh), lm::kPanel)) : 0);
+    const int64_t partq_f = mfma ? 4 * F * std::max(heads * qk, ql) : 0;
+    const int64_t partkv_f = mfma ? 4 * F * std::max({rank + rope, heads * (c.qk_nope_head_dim + vh), H}) : 0;
+    const size_t partq_at = region(partq_f);
+    const size_t partkv_at = region(partkv_f);
+    const size_t k16_at = region(plan.mfma ? halves(heads * kp * qk) : 0);
+    const size_t v16_at = region(plan.mfma ? halves(heads * vh * kp) : 0);
+    const size_t q16_at = region(plan.mfma ? halves(heads * core * qk) : 0);
+    const size_t p16_at = region(plan.mfma ? halves(heads * core * kp) : 0);
+    const size_t meta_at = region(plan.mfma ? (lm::mfma_heads_meta_bytes(heads) + 3) / 4 : 0);
+    int rc = ensure_buffer(&st->ws, &st->ws_floats, stream, total_f);
     if (rc != LM_OK) {
         return rc;
     }
-    float* q = st->ws;
-    float* qlat = q + q_f;
-    float* lat = qlat + ql_f;
-    float* kvn = lat + lat_f;
-    float* kvx = kvn + kvn_f;
-    float* S = kvx + kvx_f;
-    float* ctxv = S + s_f;
-    _Float16* const x16a = reinterpret_cast<_Float16*>(ctxv + ctx_f);
-    _Float16* const x16q = reinterpret_cast<_Float16*>(ctxv + ctx_f + x16a_f);
-    _Float16* const x16kv = reinterpret_cast<_Float16*>(ctxv + ctx_f + x16a_f + x16q_f);
-    float* const partq = ctxv + ctx_f + x16a_f + x16q_f + x16kv_f;
-    float* const partkv = partq + partq_f;
-    ProjScratch psq{nullptr, nullptr, ql > 0 ? x16q : x16a, partq, static_cast<int64_t>(partq_f)};
-    ProjScratch pskv{nullptr, nullptr, x16kv, partkv, static_cast<int64_t>(partkv_f)};
+    float* const ws = st->ws;
+    auto h16 = [&](size_t at) { return reinterpret_cast<_Float16*>(ws + at); };
+    float* q = ws + q_at;
+    float* qlat = ws + ql_at;
+    float* lat = ws + lat_at;
+    float* kvn = ws + kvn_at;
+    float* kvx = ws + kvx_at;
+    float* S = ws + s_at;
+    float* ctxv = ws + ctx_at;
+    _Float16* const x16a = h16(x16a_at);
+    _Float16* const x16q = h16(x16q_at);
+    _Float16* const x16kv = h16(x16kv_at);
+    ProjScratch psq{nullptr, nullptr, ql > 0 ? x16q : x16a, ws + partq_at, partq_f};
+    ProjScratch pskv{nullptr, nullptr, x16kv, ws + partkv_at, partkv_f};
 
     // queries (src/Attention.cpp:33-48); for one token the rotary step rides
     // on the projection's launch
@@ -405,10 +473,25 @@ int attention_tokens(AttnState* st, hipStream_t stream, int32_t layer, const flo
         LM_ATT_HIP(hipStreamWaitEvent(stream, st->join, 0));
     }
     // causal attention over the cache (:77-98), in groups of query tokens
-    for (int64_t t0 = 0; t0 < F; t0 += core) {
-        const int64_t n = std::min(core, F - t0);
-        LM_ATT_HIP(lm::launch_attention_core(a, L.cache, q + t0 * heads * qk, S, ctxv + t0 * heads * vh, n, n0 + t0,
-                                             st->scale, stream));
+    if (plan.mfma) {
+        // the context lands in fp16 panels [F, heads vh] in x16kv (free once
+        // kv_b has run), the output projection's input; ctxv holds the
+        // per-head context of one group
+        const lm::AttnMfmaBufs b{h16(k16_at), h16(v16_at), h16(q16_at), S, h16(p16_at), ctxv, ws + meta_at};
+        LM_ATT_HIP(lm::launch_pack_kv16(a, L.cache, n_total, b.k16, b.v16, stream));
+        for (int64_t t0 = 0; t0 < F; t0 += core) {
+            const int64_t n = std::min(core, F - t0);
+            LM_ATT_HIP(lm::launch_attention_core_mfma(a, q + t0 * heads * qk, b, n, n0 + t0, n_total, st->scale,
+                                                      x16kv, t0, F, stream));
+        }
+        pskv.ready = x16kv;
+        pskv.ready_of = ctxv;
+    } else {
+        for (int64_t t0 = 0; t0 < F; t0 += core) {
+            const int64_t n = std::min(core, F - t0);
+            LM_ATT_HIP(lm::launch_attention_core(a, L.cache, q + t0 * heads * qk, S, ctxv + t0 * heads * vh, n,
+                                                 n0 + t0, st->scale, stream));
+        }
     }
     // output projection (:100-101)
     rc = project(L, lm::kProjO, L.o, ctxv, heads * vh, out, H, F, accumulate, mfma, pskv, stream);
@@ -792,6 +875,45 @@ int lm_attention_set_path(lm_context* ctx, int32_t path) {
         return fail(LM_EINVAL, "unknown path");
     }
     st->path = path;
+    return LM_OK;
+}
+
+int lm_attention_set_score_budget(lm_context* ctx, int64_t bytes) {
+    AttnState* st = nullptr;
+    const int rc = get_state(ctx, &st);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (bytes < 0) {
+        return fail(LM_EINVAL, "negative score budget");
+    }
+    st->score_budget = bytes;
+    return LM_OK;
+}
+
+int lm_attention_plan_core(const lm_mla_config* config, int64_t cached, int64_t tokens, int32_t path,
+                           int64_t budget_bytes, lm_attention_core_plan* out) {
+    int rc = check_config(config);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (out == nullptr || cached < 0 || tokens < 0 || budget_bytes < 0) {
+        return fail(LM_EINVAL, "null plan or negative size");
+    }
+    if (path < LM_PATH_AUTO || path > LM_PATH_MFMA) {
+        return fail(LM_EINVAL, "unknown path");
+    }
+    lm::AttnShape a;
+    a.heads = config->num_heads;
+    a.nope = config->qk_nope_head_dim;
+    a.rope = config->qk_rope_head_dim;
+    a.vh = config->v_head_dim;
+    const CorePlan p = plan_core(a, cached, tokens, mfma_projections(path, tokens),
+                                 budget_bytes > 0 ? budget_bytes : kScoreBudget);
+    out->query_group = p.group;
+    out->scratch_bytes = p.bytes;
+    out->mfma_core = p.mfma ? 1 : 0;
+    out->reserved = 0;
     return LM_OK;
 }
 

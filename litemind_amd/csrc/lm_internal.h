@@ -418,6 +418,28 @@ hipError_t launch_kv_one(const AttnShape& a, const KvCacheDev& c, const uint16_t
 // appended); S holds T * heads * (n0 + T) floats, ctx [T, heads * vh].
 hipError_t launch_attention_core(const AttnShape& a, const KvCacheDev& c, const float* q, float* S, float* ctx,
                                  int64_t T, int64_t n0, float scale, hipStream_t s);
+// The attention core on MFMA (fp16 operands, fp32 accumulation) for T query
+// tokens at cache slots n0 .. n0 + T - 1 over the first `keys` cached tokens
+// (n0 + T <= keys), Kp = keys rounded up to 32.  Buffers:
+struct AttnMfmaBufs {
+    _Float16* k16;   // [heads][Kp][qk] panels (launch_pack_kv16)
+    _Float16* v16;   // [heads][vh][Kp] panels (launch_pack_kv16)
+    _Float16* q16;   // [heads T][qk] panels
+    float* S;        // [heads T][Kp] raw scores
+    _Float16* p16;   // [heads T][Kp] panels, probabilities
+    float* c32;      // [heads T][vh] context per head
+    void* meta;      // mfma_heads_meta_bytes(heads): the per-head group table
+};
+bool attention_mfma_supported(const AttnShape& a);
+// fp16 panel copies of keys 0 .. keys - 1 (zero rows / columns up to Kp).
+hipError_t launch_pack_kv16(const AttnShape& a, const KvCacheDev& c, int64_t keys, _Float16* k16, _Float16* v16,
+                            hipStream_t s);
+// q [T][heads][qk] (rotary applied) -> the context in fp16 panels
+// ctx16 [ctx_rows][heads vh], rows row0 .. row0 + T - 1 (the output
+// projection's input).
+hipError_t launch_attention_core_mfma(const AttnShape& a, const float* q, const AttnMfmaBufs& b, int64_t T,
+                                      int64_t n0, int64_t keys, float scale, _Float16* ctx16, int64_t row0,
+                                      int64_t ctx_rows, hipStream_t s);
 
 // ---- services of the context (lm_capi.hip) to the attention translation unit ----
 struct AttnState;
@@ -449,6 +471,14 @@ hipError_t launch_mfma_down(const ExpertArgs& a, hipStream_t s);
 // partial sums (at least M N when accumulating; up to 4 M N are used).
 hipError_t launch_mfma_gemm(const _Float16* a16, const _Float16* const* w, float* out, int64_t M, int32_t N, int32_t Kp,
                             int32_t accumulate, float* scratch, int64_t scratch_floats, hipStream_t s);
+// Per-head GEMMs on the grouped MFMA kernel: out[g rows + m, n] =
+// a16[g rows + m] . w16[g w_stride + n] for heads groups of `rows` rows; a16
+// [heads rows][Kp] and each w16 block [N][Kp] in panel layout, out fp32
+// [heads rows][N].  meta: device scratch of mfma_heads_meta_bytes(heads) for the
+// group table (written by a kernel on s before the GEMM).
+inline int64_t mfma_heads_meta_bytes(int64_t heads) { return round_up(4 * (2 * heads + 1), 8) + 8 * heads; }
+hipError_t launch_mfma_heads(const _Float16* a16, const _Float16* w16, int64_t w_stride, float* out, int32_t heads,
+                             int64_t rows, int32_t N, int32_t Kp, void* meta, hipStream_t s);
 hipError_t launch_combine(const CombineArgs& a, hipStream_t s);
 // out[i] += y[i] for n floats.
 hipError_t launch_add_rows(float* out, const float* y, int64_t n, hipStream_t s);

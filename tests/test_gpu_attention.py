@@ -456,3 +456,65 @@ def test_mfma_path_selection():
             m.ctx.attention_set_path(7)
     finally:
         m.close()
+
+
+# ---- query groups sized from the score budget ----
+
+def test_small_score_budget_groups_bit_exact():
+    """A score budget of five query tokens' scores: the 20-token call after 6
+    cached tokens runs the attention core in four groups, still bit for bit
+    LiteMind's sequential calls (bit-exact path)."""
+    from litemind_amd import PATH_GEMV, attention_plan_core
+    from litemind_amd import workload as wl
+    d = small_dims(max_positions=32)
+    budget = 5 * d.heads * 26 * 4  # five tokens of scores over 26 keys
+    plan = attention_plan_core(wl.mla_config(d), 6, 20, PATH_GEMV, budget)
+    assert plan.query_group == 5 and plan.mfma_core == 0
+    announce("attention prefill 6 + 20 with a five-token score budget (bit-exact path)")
+    m = Mla(d, 221)
+    try:
+        m.ctx.attention_set_score_budget(budget)
+        x = tokens(222, 26, d.hidden)
+        for lo, hi in ((0, 6), (6, 26)):
+            y = m.forward(x[lo:hi], lo)
+            want, n = m.oracle(x[lo:hi], lo)
+            assert n == hi - lo
+            np.testing.assert_array_equal(bits(y), bits(want))
+        m.check_cache()
+    finally:
+        m.close()
+
+
+def test_mfma_core_small_budget_two_groups():
+    """V2-Lite on the MFMA core: 40 tokens, then 96 with a budget that holds 77
+    query tokens (two core launches, the second of 19 rows per head on the
+    narrow tile); the outputs equal those of one 96-token group bit for bit
+    (every score and context element has the same K order either way) and meet
+    the oracle within the MFMA tolerance."""
+    from litemind_amd import PATH_AUTO, attention_plan_core
+    from litemind_amd import workload as wl
+    d = dataclasses.replace(wl.V2_LITE_MLA, max_positions=160)
+    budget = 3_300_000
+    plan = attention_plan_core(wl.mla_config(d), 40, 96, PATH_AUTO, budget)
+    assert plan.mfma_core == 1 and plan.query_group == 77
+    assert attention_plan_core(wl.mla_config(d), 40, 96, PATH_AUTO).query_group == 96
+    announce("attention MFMA core V2-Lite 40 + 96 tokens, score budget of 77 query tokens vs default")
+    x = tokens(232, 136, d.hidden)
+    outs = []
+    for b in (budget, 0):
+        m = Mla(d, 231, path=PATH_AUTO)
+        try:
+            m.ctx.attention_set_score_budget(b)
+            y0 = m.forward(x[:40], 0)
+            y1 = m.forward(x[40:], 40)
+            if b:
+                for y, lo, hi in ((y0, 0, 40), (y1, 40, 136)):
+                    want, _ = m.oracle(x[lo:hi], lo)
+                    mx, rel = layer_error(y, want)
+                    print(f"MFMA core {lo}..{hi}: max_abs={mx:.3e} mean_rel={rel:.3e}")
+                    assert mx <= ATT_MAX_ABS and rel <= ATT_MEAN_REL
+            outs.append((y0, y1))
+        finally:
+            m.close()
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(bits(a), bits(b))
