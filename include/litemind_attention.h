@@ -146,6 +146,22 @@ int lm_kv_cache_tokens(lm_context* ctx, int32_t layer, int64_t* out_tokens);
  * NULL).  Synchronous. */
 int lm_kv_cache_read(lm_context* ctx, int32_t layer, int64_t tokens, float* key_nope_host, float* key_rope_host,
                      float* value_host);
+/* Entries [token0, token0 + tokens) in the same layout (KvCache's read-only
+ * accessors, include/KvCache.hpp:60-69).  Synchronous. */
+int lm_kv_cache_read_range(lm_context* ctx, int32_t layer, int64_t token0, int64_t tokens, float* key_nope_host,
+                           float* key_rope_host, float* value_host);
+/* Stores entries [token0, token0 + tokens) from host buffers in KvCache's layout
+ * (what LiteMind writes through KvCache's writable accessors,
+ * include/KvCache.hpp:49-58): token0 at most the cached count (no gap),
+ * token0 + tokens at most the capacity; the count becomes at least
+ * token0 + tokens.  Every buffer of a non-empty part is required.
+ * Synchronous. */
+int lm_kv_cache_write(lm_context* ctx, int32_t layer, int64_t token0, int64_t tokens, const float* key_nope_host,
+                      const float* key_rope_host, const float* value_host);
+/* Keeps the first `tokens` entries of one layer (at most its count); the next
+ * call appends at slot `tokens`.  KvCache::clear (include/KvCache.hpp:31) for
+ * one layer is tokens = 0. */
+int lm_kv_cache_truncate(lm_context* ctx, int32_t layer, int64_t tokens);
 
 /* DeepSeekRunner::Impl::forward's layer loop (src/DeepSeekRunner.cpp:251-291)
  * for T tokens at positions position0 .. + T - 1, layers first..last, on

@@ -154,6 +154,9 @@ PROTOTYPES = {
     "lm_attention_plan_core": [_P, _I64, _I64, _I32, _I64, _P],
     "lm_kv_cache_tokens": [_P, _I32, _P],
     "lm_kv_cache_read": [_P, _I32, _I64, _P, _P, _P],
+    "lm_kv_cache_read_range": [_P, _I32, _I64, _I64, _P, _P, _P],
+    "lm_kv_cache_write": [_P, _I32, _I64, _I64, _P, _P, _P],
+    "lm_kv_cache_truncate": [_P, _I32, _I64],
     "lm_decoder_forward": [_P, _I32, _I32, _P, _I64, _I64, _I32],
 }
 _RESTYPE = {"lm_last_error": C.c_char_p}
@@ -470,6 +473,25 @@ class Context:
         v = np.zeros((tokens, c.num_heads, c.v_head_dim), np.float32)
         self._check(self.lib.lm_kv_cache_read(self.handle, layer, tokens, _ptr(kn), _ptr(kr), _ptr(v)))
         return kn, kr, v
+
+    def kv_cache_read_range(self, layer: int, token0: int, tokens: int):
+        """Entries [token0, token0 + tokens) in KvCache's layout (lm_kv_cache_read_range)."""
+        c = self.mla_config
+        kn = np.zeros((tokens, c.num_heads, c.qk_nope_head_dim), np.float32)
+        kr = np.zeros((tokens, c.qk_rope_head_dim), np.float32)
+        v = np.zeros((tokens, c.num_heads, c.v_head_dim), np.float32)
+        self._check(self.lib.lm_kv_cache_read_range(self.handle, layer, token0, tokens, _ptr(kn), _ptr(kr), _ptr(v)))
+        return kn, kr, v
+
+    def kv_cache_write(self, layer: int, token0: int, key_nope, key_rope, value) -> None:
+        """Stores entries token0 .. token0 + len - 1 from KvCache-layout arrays (lm_kv_cache_write)."""
+        kn = np.ascontiguousarray(key_nope, np.float32)
+        kr = np.ascontiguousarray(key_rope, np.float32)
+        v = np.ascontiguousarray(value, np.float32)
+        self._check(self.lib.lm_kv_cache_write(self.handle, layer, token0, kn.shape[0], _ptr(kn), _ptr(kr), _ptr(v)))
+
+    def kv_cache_truncate(self, layer: int, tokens: int) -> None:
+        self._check(self.lib.lm_kv_cache_truncate(self.handle, layer, tokens))
 
     def decoder_forward(self, first, last, hidden, tokens, position0, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_decoder_forward(self.handle, first, last, _ptr(hidden), tokens, position0, path))

@@ -107,9 +107,11 @@ def build_oracle() -> None:
 
 
 def build_ref_tests() -> None:
-    """LiteMind's own KernelTest / MoeRouterSamplerTest linked against the GPU drop-in."""
+    """LiteMind's own KernelTest / MoeRouterSamplerTest / AttentionTest / RopeTest and its whole runner
+    (DeepSeekRunner through oracle/runner_driver.cpp) linked against the GPU drop-in, and the runner over
+    LiteMind's own sources as the CPU reference."""
     if os.path.isdir(os.path.join(REFERENCE, "tests")):
-        _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-B", "ref-tests", f"REF={REFERENCE}"])
+        _run(["make", "-s", "-j4", "-C", os.path.join(ROOT, "oracle"), "-B", "ref-tests", f"REF={REFERENCE}"])
 
 
 def build_all() -> None:

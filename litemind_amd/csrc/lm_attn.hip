@@ -507,6 +507,126 @@ int upload(hipStream_t stream, void* dst, const void* src, size_t bytes) {
     return LM_OK;
 }
 
+// Copies cached entries [token0, token0 + tokens) of a layer between the
+// device cache and host buffers in KvCache's layout (key_nope [tokens, heads,
+// qk_nope], key_rope [tokens, qk_rope], value [tokens, heads, v_head]).
+// Reading needs token0 + tokens <= the layer's count; writing needs token0 <=
+// count (no gap) and token0 + tokens <= capacity, every buffer of a non-empty
+// part given, and extends the count to token0 + tokens.  Both wait for the
+// context stream first and finish before returning.
+int kv_cache_copy(lm_context* ctx, int32_t layer, int64_t token0, int64_t tokens, float* key_nope_host,
+                  float* key_rope_host, float* value_host, bool to_device) {
+    try {
+        AttnState* st = nullptr;
+        int rc = get_state(ctx, &st);
+        if (rc == LM_OK) {
+            rc = check_attn_layer(st, layer);
+        }
+        if (rc != LM_OK) {
+            return rc;
+        }
+        AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+        const int64_t cap = st->cfg.context_length, heads = st->cfg.num_heads, nope = st->cfg.qk_nope_head_dim,
+                      rope = st->cfg.qk_rope_head_dim, vh = st->cfg.v_head_dim;
+        if (token0 < 0 || tokens < 0) {
+            return fail(LM_EINVAL, "negative token range");
+        }
+        if (!to_device && token0 + tokens > L.count) {
+            return fail(LM_EINVAL, "tokens must be within the cache's " + std::to_string(L.count));
+        }
+        if (to_device) {
+            if (token0 > L.count || token0 + tokens > cap) {
+                return fail(LM_EINVAL, "write of entries " + std::to_string(token0) + ".." +
+                                           std::to_string(token0 + tokens) + " to a cache holding " +
+                                           std::to_string(L.count) + " of " + std::to_string(cap));
+            }
+            if (tokens > 0 && ((nope > 0 && key_nope_host == nullptr) || (rope > 0 && key_rope_host == nullptr) ||
+                               value_host == nullptr)) {
+                return fail(LM_EINVAL, "a cache write needs the keys, the rotary keys and the values");
+            }
+        }
+        if (tokens == 0) {
+            return LM_OK;
+        }
+        const lm::ContextInfo info = lm::context_info(ctx);
+        LM_ATT_HIP(hipSetDevice(info.device));
+        LM_ATT_HIP(hipStreamSynchronize(info.stream));
+        const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+        // one 2-D copy per part between the device rows (stride cap) and a
+        // staging buffer with the host layout's transpose
+        auto copy2d = [&](float* dev, size_t dev_pitch, float* host, size_t width, size_t height) {
+            return to_device ? hipMemcpy2DAsync(dev, dev_pitch, host, width, width, height, kind, info.stream)
+                             : hipMemcpy2DAsync(host, width, dev, dev_pitch, width, height, kind, info.stream);
+        };
+        const size_t tb = sizeof(float) * static_cast<size_t>(tokens);
+        std::vector<float> kn, kr, v;
+        if (key_nope_host != nullptr && nope > 0) {
+            kn.resize(static_cast<size_t>(heads * nope * tokens));
+            if (to_device) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    for (int64_t hd = 0; hd < heads * nope; ++hd) {
+                        kn[static_cast<size_t>(hd * tokens + t)] = key_nope_host[t * heads * nope + hd];
+                    }
+                }
+            }
+            LM_ATT_HIP(copy2d(L.cache.key_nope + token0, sizeof(float) * cap, kn.data(), tb,
+                              static_cast<size_t>(heads * nope)));
+        }
+        if (key_rope_host != nullptr && rope > 0) {
+            kr.resize(static_cast<size_t>(rope * tokens));
+            if (to_device) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    for (int64_t d = 0; d < rope; ++d) {
+                        kr[static_cast<size_t>(d * tokens + t)] = key_rope_host[t * rope + d];
+                    }
+                }
+            }
+            LM_ATT_HIP(copy2d(L.cache.key_rope + token0, sizeof(float) * cap, kr.data(), tb, static_cast<size_t>(rope)));
+        }
+        if (value_host != nullptr) {
+            v.resize(static_cast<size_t>(heads * tokens * vh));
+            if (to_device) {
+                for (int64_t h = 0; h < heads; ++h) {
+                    for (int64_t t = 0; t < tokens; ++t) {
+                        std::copy_n(value_host + (t * heads + h) * vh, vh, v.data() + (h * tokens + t) * vh);
+                    }
+                }
+            }
+            LM_ATT_HIP(copy2d(L.cache.value + token0 * vh, sizeof(float) * cap * vh, v.data(), tb * vh,
+                              static_cast<size_t>(heads)));
+        }
+        LM_ATT_HIP(hipStreamSynchronize(info.stream));
+        if (to_device) {
+            L.count = std::max(L.count, token0 + tokens);
+            return LM_OK;
+        }
+        if (!kn.empty()) {
+            for (int64_t hd = 0; hd < heads * nope; ++hd) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    key_nope_host[t * heads * nope + hd] = kn[static_cast<size_t>(hd * tokens + t)];
+                }
+            }
+        }
+        if (!kr.empty()) {
+            for (int64_t d = 0; d < rope; ++d) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    key_rope_host[t * rope + d] = kr[static_cast<size_t>(d * tokens + t)];
+                }
+            }
+        }
+        if (!v.empty()) {
+            for (int64_t h = 0; h < heads; ++h) {
+                for (int64_t t = 0; t < tokens; ++t) {
+                    std::copy_n(v.data() + (h * tokens + t) * vh, vh, value_host + (t * heads + h) * vh);
+                }
+            }
+        }
+        return LM_OK;
+    } catch (const std::bad_alloc&) {
+        return fail(LM_ENOMEM, "host allocation failed");
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -949,66 +1069,35 @@ int lm_kv_cache_tokens(lm_context* ctx, int32_t layer, int64_t* out_tokens) {
 
 int lm_kv_cache_read(lm_context* ctx, int32_t layer, int64_t tokens, float* key_nope_host, float* key_rope_host,
                      float* value_host) {
-    try {
-        AttnState* st = nullptr;
-        int rc = get_state(ctx, &st);
-        if (rc == LM_OK) {
-            rc = check_attn_layer(st, layer);
-        }
-        if (rc != LM_OK) {
-            return rc;
-        }
-        const AttnLayer& L = st->layers[static_cast<size_t>(layer)];
-        if (tokens < 0 || tokens > L.count) {
-            return fail(LM_EINVAL, "tokens must be within the cache's " + std::to_string(L.count));
-        }
-        if (tokens == 0) {
-            return LM_OK;
-        }
-        const lm::ContextInfo info = lm::context_info(ctx);
-        LM_ATT_HIP(hipSetDevice(info.device));
-        LM_ATT_HIP(hipStreamSynchronize(info.stream));
-        const int64_t cap = st->cfg.context_length, heads = st->cfg.num_heads, nope = st->cfg.qk_nope_head_dim,
-                      rope = st->cfg.qk_rope_head_dim, vh = st->cfg.v_head_dim;
-        const size_t tb = sizeof(float) * static_cast<size_t>(tokens);
-        std::vector<float> tmp;
-        if (key_nope_host != nullptr && nope > 0) {
-            tmp.resize(static_cast<size_t>(heads * nope * tokens));
-            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb, L.cache.key_nope, sizeof(float) * cap, tb,
-                                   static_cast<size_t>(heads * nope), hipMemcpyDeviceToHost));
-            for (int64_t h = 0; h < heads; ++h) {
-                for (int64_t d = 0; d < nope; ++d) {
-                    const float* src = tmp.data() + (h * nope + d) * tokens;
-                    for (int64_t t = 0; t < tokens; ++t) {
-                        key_nope_host[(t * heads + h) * nope + d] = src[t];
-                    }
-                }
-            }
-        }
-        if (key_rope_host != nullptr && rope > 0) {
-            tmp.resize(static_cast<size_t>(rope * tokens));
-            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb, L.cache.key_rope, sizeof(float) * cap, tb,
-                                   static_cast<size_t>(rope), hipMemcpyDeviceToHost));
-            for (int64_t d = 0; d < rope; ++d) {
-                for (int64_t t = 0; t < tokens; ++t) {
-                    key_rope_host[t * rope + d] = tmp[static_cast<size_t>(d * tokens + t)];
-                }
-            }
-        }
-        if (value_host != nullptr) {
-            tmp.resize(static_cast<size_t>(heads * tokens * vh));
-            LM_ATT_HIP(hipMemcpy2D(tmp.data(), tb * vh, L.cache.value, sizeof(float) * cap * vh, tb * vh,
-                                   static_cast<size_t>(heads), hipMemcpyDeviceToHost));
-            for (int64_t h = 0; h < heads; ++h) {
-                for (int64_t t = 0; t < tokens; ++t) {
-                    std::copy_n(tmp.data() + (h * tokens + t) * vh, vh, value_host + (t * heads + h) * vh);
-                }
-            }
-        }
-        return LM_OK;
-    } catch (const std::bad_alloc&) {
-        return fail(LM_ENOMEM, "host allocation failed");
+    return kv_cache_copy(ctx, layer, 0, tokens, key_nope_host, key_rope_host, value_host, false);
+}
+
+int lm_kv_cache_read_range(lm_context* ctx, int32_t layer, int64_t token0, int64_t tokens, float* key_nope_host,
+                           float* key_rope_host, float* value_host) {
+    return kv_cache_copy(ctx, layer, token0, tokens, key_nope_host, key_rope_host, value_host, false);
+}
+
+int lm_kv_cache_write(lm_context* ctx, int32_t layer, int64_t token0, int64_t tokens, const float* key_nope_host,
+                      const float* key_rope_host, const float* value_host) {
+    return kv_cache_copy(ctx, layer, token0, tokens, const_cast<float*>(key_nope_host),
+                         const_cast<float*>(key_rope_host), const_cast<float*>(value_host), true);
+}
+
+int lm_kv_cache_truncate(lm_context* ctx, int32_t layer, int64_t tokens) {
+    AttnState* st = nullptr;
+    int rc = get_state(ctx, &st);
+    if (rc == LM_OK) {
+        rc = check_attn_layer(st, layer);
     }
+    if (rc != LM_OK) {
+        return rc;
+    }
+    AttnLayer& L = st->layers[static_cast<size_t>(layer)];
+    if (tokens < 0 || tokens > L.count) {
+        return fail(LM_EINVAL, "tokens must be within the cache's " + std::to_string(L.count));
+    }
+    L.count = tokens;  // later calls append from here; queued work keeps the counts it was given
+    return LM_OK;
 }
 
 int lm_decoder_forward(lm_context* ctx, int32_t first_layer, int32_t last_layer, float* hidden_dev, int64_t tokens,

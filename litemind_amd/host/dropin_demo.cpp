@@ -15,6 +15,26 @@
 //       hand-off waits made to give up at once (lm_decode_wait_test): forward
 //       must throw with the library's LM_EKERNEL message, and a second forward
 //       with normal waits must succeed.  Exit status 0 when both hold.
+//   dropin_demo attention <case_dir>
+//       Drives one Attention (configured as DeepSeekRunner does, with a
+//       RotaryEmbedding and one KvCache per cache id) through the commands of
+//       script.txt, one per line:
+//         fwd <cache> <weights> <position> <x_row>   Attention::forward of row
+//             x_row of x.f32; appends the output row to out.f32 and 1 / 0 (the
+//             return value; a refused call leaves its row NaN) to results.txt
+//         clear <cache>                                KvCache::clear
+//         copy <dst> <src>                             dst.clear(), then src's
+//             entries written into dst through KvCache's writable accessors
+//             and appended, as a caller filling a cache by hand does
+//         dump <cache>                                 the entries in KvCache's
+//             layout to cache<c>_{kn,kr,v}.f32 and the count to cache<c>.txt
+//       case.txt: hidden heads q_lora_rank kv_lora_rank qk_nope qk_rope v_head
+//                 layers capacity rms_norm_eps rope_theta yarn factor
+//                 beta_fast beta_slow mscale mscale_all_dim original_max
+//                 weight_sets caches rows
+//       Weights of set i: w<i>_q.bf16 (q_lora_rank 0) or w<i>_qa.bf16,
+//       w<i>_qan.f32, w<i>_qb.bf16; w<i>_kva.bf16, w<i>_kvan.f32, w<i>_kvb.bf16,
+//       w<i>_o.bf16.  The rotary table has `capacity` positions.
 //   dropin_demo cache-trace <budget> <block_bytes> <layer expert>...
 //       Replays touches on an ExpertCache with byte-less views and prints its
 //       counters after each touch and after clear(): resident_bytes,
@@ -26,13 +46,17 @@
 // Inputs: router.f32 [E,H], gate.bf16 / up.bf16 [E,I,H], down.bf16 [E,H,I],
 //         shared_{gate,up}.bf16 [S,H], shared_down.bf16 [H,S] (when S > 0),
 //         x.f32 [T,H].
+#include "Attention.hpp"
 #include "ExpertCache.hpp"
 #include "Gemm.hpp"
+#include "KvCache.hpp"
+#include "Rope.hpp"
 #include "MoeRouter.hpp"
 #include "Threading.hpp"
 #include "litemind_gpu.hpp"
 #include "litemind_moe.h"
 
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -40,6 +64,8 @@
 #include <exception>
 #include <fstream>
 #include <iostream>
+#include <limits>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -238,6 +264,135 @@ int run_moe_timeout(const std::string& dir) {
     return 0;
 }
 
+int run_attention(const std::string& dir) {
+    std::ifstream cfg(dir + "/case.txt");
+    std::size_t H = 0, heads = 0, ql = 0, rank = 0, nope = 0, rope_dim = 0, vh = 0, layers = 0, cap = 0;
+    std::size_t sets = 0, caches = 0, rows = 0, original_max = 0;
+    int yarn = 0;
+    float eps = 0.0F, theta = 0.0F;
+    double factor = 0, beta_fast = 0, beta_slow = 0, mscale = 0, mscale_all = 0;
+    if (!(cfg >> H >> heads >> ql >> rank >> nope >> rope_dim >> vh >> layers >> cap >> eps >> theta >> yarn >>
+          factor >> beta_fast >> beta_slow >> mscale >> mscale_all >> original_max >> sets >> caches >> rows)) {
+        throw std::runtime_error("bad case.txt");
+    }
+    Config config;
+    config.hidden_size = H;
+    config.num_hidden_layers = layers;
+    config.num_attention_heads = heads;
+    config.q_lora_rank = ql;
+    config.kv_lora_rank = rank;
+    config.qk_nope_head_dim = nope;
+    config.qk_rope_head_dim = rope_dim;
+    config.v_head_dim = vh;
+    config.rms_norm_eps = eps;
+    config.rope_theta = theta;
+    config.rope_scaling.enabled = yarn != 0;
+    config.rope_scaling.factor = factor;
+    config.rope_scaling.beta_fast = beta_fast;
+    config.rope_scaling.beta_slow = beta_slow;
+    config.rope_scaling.mscale = mscale;
+    config.rope_scaling.mscale_all_dim = mscale_all;
+    config.rope_scaling.original_max_position_embeddings = original_max;
+
+    // weights, held for the whole run (the views borrow them)
+    const std::size_t qk = nope + rope_dim;
+    std::vector<std::vector<std::uint16_t>> bf16;
+    std::vector<AttentionWeights> weights(sets);
+    auto load_view = [&](const std::string& name, std::size_t count) {
+        bf16.push_back(read_array<std::uint16_t>(dir + "/" + name, count));
+        return view_of(bf16.back(), 0, count);
+    };
+    bf16.reserve(sets * 6);
+    for (std::size_t i = 0; i < sets; ++i) {
+        const std::string w = "w" + std::to_string(i) + "_";
+        AttentionWeights& aw = weights[i];
+        if (ql == 0U) {
+            aw.q_proj = load_view(w + "q.bf16", heads * qk * H);
+        } else {
+            aw.q_a_proj = load_view(w + "qa.bf16", ql * H);
+            aw.q_a_layernorm = read_array<float>(dir + "/" + w + "qan.f32", ql);
+            aw.q_b_proj = load_view(w + "qb.bf16", heads * qk * ql);
+        }
+        aw.kv_a_proj = load_view(w + "kva.bf16", (rank + rope_dim) * H);
+        aw.kv_a_layernorm = read_array<float>(dir + "/" + w + "kvan.f32", rank);
+        aw.kv_b_proj = load_view(w + "kvb.bf16", heads * (nope + vh) * rank);
+        aw.o_proj = load_view(w + "o.bf16", H * heads * vh);
+    }
+    const auto x = read_array<float>(dir + "/x.f32", rows * H);
+
+    // src/DeepSeekRunner.cpp:358-360 and :416-420
+    ThreadPool pool(1);
+    RotaryEmbedding rope;
+    rope.build(config, cap);
+    Attention attention;
+    attention.configure(config, pool, rope);
+    std::vector<KvCache> cache(caches);
+    for (KvCache& c : cache) {
+        c.configure(heads, nope, rope_dim, vh, cap);
+    }
+
+    std::ifstream script(dir + "/script.txt");
+    std::ofstream out(dir + "/out.f32", std::ios::binary);
+    std::ofstream results(dir + "/results.txt");
+    std::vector<float> y(H);
+    std::string line;
+    while (std::getline(script, line)) {
+        std::istringstream cmd(line);
+        std::string op;
+        if (!(cmd >> op)) {
+            continue;
+        }
+        if (op == "fwd") {
+            std::size_t c = 0, w = 0, pos = 0, row = 0;
+            cmd >> c >> w >> pos >> row;
+            std::fill(y.begin(), y.end(), std::numeric_limits<float>::quiet_NaN());
+            const bool ok = attention.forward(x.data() + row * H, weights.at(w), cache.at(c), pos, y.data());
+            out.write(reinterpret_cast<const char*>(y.data()), static_cast<std::streamsize>(H * sizeof(float)));
+            results << (ok ? 1 : 0) << "\n";
+        } else if (op == "clear") {
+            std::size_t c = 0;
+            cmd >> c;
+            cache.at(c).clear();
+        } else if (op == "copy") {
+            std::size_t dst = 0, src = 0;
+            cmd >> dst >> src;
+            KvCache& d = cache.at(dst);
+            const KvCache& s = cache.at(src);
+            d.clear();
+            for (std::size_t t = 0; t < s.token_count(); ++t) {
+                const std::size_t slot = d.append();
+                for (std::size_t h = 0; h < heads; ++h) {
+                    std::copy_n(s.key_nope(t, h), nope, d.key_nope(slot) + h * nope);
+                    std::copy_n(s.value(t, h), vh, d.value(slot) + h * vh);
+                }
+                std::copy_n(s.key_rope(t), rope_dim, d.key_rope(slot));
+            }
+        } else if (op == "dump") {
+            std::size_t c = 0;
+            cmd >> c;
+            const KvCache& k = cache.at(c);
+            const std::size_t n = k.token_count();
+            std::vector<float> kn(n * heads * nope), kr(n * rope_dim), v(n * heads * vh);
+            for (std::size_t t = 0; t < n; ++t) {
+                for (std::size_t h = 0; h < heads; ++h) {
+                    std::copy_n(k.key_nope(t, h), nope, kn.data() + (t * heads + h) * nope);
+                    std::copy_n(k.value(t, h), vh, v.data() + (t * heads + h) * vh);
+                }
+                std::copy_n(k.key_rope(t), rope_dim, kr.data() + t * rope_dim);
+            }
+            const std::string base = dir + "/cache" + std::to_string(c);
+            write_array(base + "_kn.f32", kn);
+            write_array(base + "_kr.f32", kr);
+            write_array(base + "_v.f32", v);
+            std::ofstream(base + ".txt") << n << "\n";
+        } else {
+            throw std::runtime_error("unknown script command: " + line);
+        }
+    }
+    std::printf("attention case %s: %s\n", dir.c_str(), rope.summary().c_str());
+    return 0;
+}
+
 int run_cache_trace(int argc, char** argv) {
     if (argc < 4 || (argc - 4) % 2 != 0) {
         throw std::runtime_error("usage: cache-trace <budget> <block_bytes> <layer expert>...");
@@ -278,10 +433,14 @@ int main(int argc, char** argv) {
         if (argc >= 3 && std::strcmp(argv[1], "moe-timeout") == 0) {
             return run_moe_timeout(argv[2]);
         }
+        if (argc >= 3 && std::strcmp(argv[1], "attention") == 0) {
+            return run_attention(argv[2]);
+        }
         if (argc >= 2 && std::strcmp(argv[1], "cache-trace") == 0) {
             return run_cache_trace(argc, argv);
         }
-        std::fprintf(stderr, "usage: dropin_demo moe|moe-timeout <case_dir> | cache-trace <budget> <block_bytes> <l e>...\n");
+        std::fprintf(stderr, "usage: dropin_demo moe|moe-timeout|attention <case_dir> | cache-trace <budget> "
+                             "<block_bytes> <l e>...\n");
         return 2;
     } catch (const std::exception& error) {
         std::fprintf(stderr, "dropin_demo: %s\n", error.what());

@@ -17,6 +17,7 @@
 
 struct lm_context;
 struct lm_moe_config;
+struct lm_mla_config;
 
 namespace litemind::gpu {
 
@@ -26,11 +27,22 @@ void check(int status, const char* what);
 /** The process-wide context used by gemm:: and ExpertCache (created on first use). */
 lm_context* session();
 
+/** The device the drop-in uses: 0, or the one LITEMIND_DEVICE names. */
+int device();
+
+/** A new context of `num_layers` layers of width `hidden` for callers that use
+ * only its non-MoE services (attention); the caller destroys it. */
+lm_context* create_context(std::size_t hidden, int num_layers);
+
 /** A context whose routing policy matches `config` (cached per policy). */
 lm_context* router_session(const lm_moe_config& config);
 
 /** lm_moe_config for a LiteMind Config (its MoE subset). */
 lm_moe_config moe_config(const Config& config, int num_layers);
+
+/** lm_mla_config for a LiteMind Config (its attention subset), with `positions`
+ * rotary table rows and KV cache capacity per layer. */
+lm_mla_config mla_config(const Config& config, std::int64_t positions);
 
 /**
  * The MoE block of DeepSeekRunner::Impl::forward (src/DeepSeekRunner.cpp:273-290)

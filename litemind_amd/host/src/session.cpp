@@ -1,6 +1,7 @@
 // GPU session management and the batched MoE block for the drop-in layer.
 #include "litemind_gpu.hpp"
 
+#include "litemind_attention.h"
 #include "litemind_moe.h"
 
 #include <cstdlib>
@@ -58,6 +59,17 @@ void check(int status, const char* what) {
     }
 }
 
+int device() { return device_from_env(); }
+
+lm_context* create_context(std::size_t hidden, int num_layers) {
+    lm_moe_config c = minimal_config();
+    c.hidden_size = static_cast<int32_t>(hidden);
+    c.num_layers = num_layers > 0 ? num_layers : 1;
+    lm_context* ctx = nullptr;
+    check(lm_context_create(device_from_env(), &c, &ctx), "lm_context_create");
+    return ctx;
+}
+
 lm_context* session() {
     Sessions& s = sessions();
     std::lock_guard<std::mutex> lock(s.mutex);
@@ -112,6 +124,28 @@ lm_moe_config moe_config(const Config& config, int num_layers) {
     c.topk_group = grouped ? static_cast<int32_t>(config.topk_group > 1U ? config.topk_group : 1U) : 1;
     c.rms_norm_eps = config.rms_norm_eps;
     c.num_layers = num_layers;
+    return c;
+}
+
+lm_mla_config mla_config(const Config& config, std::int64_t positions) {
+    lm_mla_config c{};
+    c.hidden_size = static_cast<int32_t>(config.hidden_size);
+    c.num_heads = static_cast<int32_t>(config.num_attention_heads);
+    c.q_lora_rank = static_cast<int32_t>(config.q_lora_rank);
+    c.kv_lora_rank = static_cast<int32_t>(config.kv_lora_rank);
+    c.qk_nope_head_dim = static_cast<int32_t>(config.qk_nope_head_dim);
+    c.qk_rope_head_dim = static_cast<int32_t>(config.qk_rope_head_dim);
+    c.v_head_dim = static_cast<int32_t>(config.v_head_dim);
+    c.rms_norm_eps = config.rms_norm_eps;
+    c.rope_theta = static_cast<double>(config.rope_theta);
+    c.yarn = config.rope_scaling.enabled ? 1 : 0;
+    c.factor = config.rope_scaling.factor;
+    c.beta_fast = config.rope_scaling.beta_fast;
+    c.beta_slow = config.rope_scaling.beta_slow;
+    c.mscale = config.rope_scaling.mscale;
+    c.mscale_all_dim = config.rope_scaling.mscale_all_dim;
+    c.original_max_positions = static_cast<int64_t>(config.rope_scaling.original_max_position_embeddings);
+    c.context_length = positions;
     return c;
 }
 

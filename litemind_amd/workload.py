@@ -401,3 +401,147 @@ def upload_mla_layer(ctx, layer_id: int, L: MlaLayer) -> None:
     ctx.upload_attention(layer_id, q_proj=L.q_proj, q_a_proj=L.q_a_proj, q_a_layernorm=L.q_a_layernorm,
                          q_b_proj=L.q_b_proj, kv_a_proj=L.kv_a_proj, kv_a_layernorm=L.kv_a_layernorm,
                          kv_b_proj=L.kv_b_proj, o_proj=L.o_proj)
+
+
+# ---- whole checkpoints for LiteMind's runner (DeepSeekRunner::load) ----
+
+# LiteMind's tiny test model (tools/make_test_model.py:28-70): every code path
+# of the runner at a few hundred KB.
+TINY_MODEL = dict(hidden_size=32, num_hidden_layers=3, num_attention_heads=2, vocab_size=300,
+                  max_position_embeddings=4096, rms_norm_eps=1e-06, tie_word_embeddings=False, kv_lora_rank=16,
+                  q_lora_rank=None, qk_nope_head_dim=8, qk_rope_head_dim=4, v_head_dim=8, intermediate_size=64,
+                  moe_intermediate_size=16, n_routed_experts=4, n_shared_experts=1, num_experts_per_tok=2,
+                  first_k_dense_replace=1, moe_layer_freq=1, norm_topk_prob=False, routed_scaling_factor=1.0,
+                  scoring_func="softmax", topk_method="greedy", n_group=1, topk_group=1, rope_theta=10000,
+                  rope_scaling=dict(type="yarn", factor=40, beta_fast=32, beta_slow=1, mscale=0.707,
+                                    mscale_all_dim=0.707, original_max_position_embeddings=4096),
+                  bos_token_id=290, eos_token_id=291, torch_dtype="bfloat16")
+
+# A second shape: the q LoRA path, group-limited routing over 16 experts in 4
+# groups, normalised and scaled top-k weights, two shared experts.
+LORA_MODEL = dict(TINY_MODEL, hidden_size=256, num_hidden_layers=4, num_attention_heads=4, vocab_size=512,
+                  kv_lora_rank=64, q_lora_rank=48, qk_nope_head_dim=32, qk_rope_head_dim=16, v_head_dim=32,
+                  intermediate_size=512, moe_intermediate_size=64, n_routed_experts=16, n_shared_experts=2,
+                  num_experts_per_tok=4, norm_topk_prob=True, routed_scaling_factor=2.5,
+                  topk_method="group_limited_greedy", n_group=4, topk_group=2,
+                  rope_scaling=dict(type="yarn", factor=4, beta_fast=32, beta_slow=1, mscale=0.707,
+                                    mscale_all_dim=0.707, original_max_position_embeddings=32),
+                  bos_token_id=510, eos_token_id=511)
+
+
+_LCG_A, _LCG_C, _LCG_BLOCK = 1664525, 1013904223, 4096
+_lcg_jump = None
+
+
+def _lcg_bf16(state: list, count: int, scale: float = 0.08) -> np.ndarray:
+    """The test model's values (tools/make_test_model.py:73-93): Numerical
+    Recipes LCG steps s, value ((s / 0xFFFFFFFF) * 2 - 1) * scale rounded to fp32
+    and truncated to BF16.  Blocks of 4096 steps at once: step k of a block from
+    its start s0 is (A_k s0 + C_k) mod 2^32 with A_k = a^k, C_k = c (a^(k-1) +
+    ... + 1)."""
+    global _lcg_jump
+    if _lcg_jump is None:
+        A = np.empty(_LCG_BLOCK, np.uint64)
+        Cs = np.empty(_LCG_BLOCK, np.uint64)
+        a, c = 1, 0
+        for k in range(_LCG_BLOCK):
+            a, c = (a * _LCG_A) & 0xFFFFFFFF, (c * _LCG_A + _LCG_C) & 0xFFFFFFFF
+            A[k], Cs[k] = a, c
+        _lcg_jump = (A, Cs)
+    A, Cs = _lcg_jump
+    steps = np.empty(count, np.uint64)
+    s = state[0]
+    for b in range(0, count, _LCG_BLOCK):
+        n = min(_LCG_BLOCK, count - b)
+        block = (A[:n] * np.uint64(s) + Cs[:n]) & np.uint64(0xFFFFFFFF)
+        steps[b:b + n] = block
+        s = int(block[-1])
+    state[0] = s
+    f = ((steps.astype(np.float64) / 0xFFFFFFFF) * 2.0 - 1.0) * scale
+    return (f.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def write_runner_model(directory: str, cfg: dict = TINY_MODEL, seed: int = 20240816) -> None:
+    """config.json, a byte-level tokenizer and model.safetensors for
+    DeepSeekRunner::load.  Tensors in the order of tools/make_test_model.py:101-
+    173 (names as src/DeepSeekRunner.cpp:105-226 resolves them), BF16 values
+    from the test model's LCG, norm weights one; with q_lora_rank the query
+    path is q_a_proj / q_a_layernorm / q_b_proj.  The tokenizer maps every byte
+    to its own id, has four merges and adds the BOS / EOS tokens."""
+    import json
+
+    os.makedirs(directory, exist_ok=True)
+    H, heads = cfg["hidden_size"], cfg["num_attention_heads"]
+    nope, rope, vh = cfg["qk_nope_head_dim"], cfg["qk_rope_head_dim"], cfg["v_head_dim"]
+    rank, ql = cfg["kv_lora_rank"], cfg["q_lora_rank"] or 0
+    qk = nope + rope
+    state = [seed & 0xFFFFFFFF]
+    ones = lambda n: np.full(n, 0x3F80, np.uint16)  # BF16 1.0
+    t = {"model.embed_tokens.weight": _lcg_bf16(state, cfg["vocab_size"] * H).reshape(cfg["vocab_size"], H)}
+    for layer in range(cfg["num_hidden_layers"]):
+        p = f"model.layers.{layer}."
+        t[p + "input_layernorm.weight"] = ones(H)
+        t[p + "post_attention_layernorm.weight"] = ones(H)
+        a = p + "self_attn."
+        if ql == 0:
+            t[a + "q_proj.weight"] = _lcg_bf16(state, heads * qk * H).reshape(heads * qk, H)
+        else:
+            t[a + "q_a_proj.weight"] = _lcg_bf16(state, ql * H).reshape(ql, H)
+            t[a + "q_a_layernorm.weight"] = ones(ql)
+            t[a + "q_b_proj.weight"] = _lcg_bf16(state, heads * qk * ql).reshape(heads * qk, ql)
+        t[a + "kv_a_proj_with_mqa.weight"] = _lcg_bf16(state, (rank + rope) * H).reshape(rank + rope, H)
+        t[a + "kv_a_layernorm.weight"] = ones(rank)
+        t[a + "kv_b_proj.weight"] = _lcg_bf16(state, heads * (nope + vh) * rank).reshape(heads * (nope + vh), rank)
+        t[a + "o_proj.weight"] = _lcg_bf16(state, H * heads * vh).reshape(H, heads * vh)
+        if layer < cfg["first_k_dense_replace"]:
+            inter = cfg["intermediate_size"]
+            t[p + "mlp.gate_proj.weight"] = _lcg_bf16(state, inter * H).reshape(inter, H)
+            t[p + "mlp.up_proj.weight"] = _lcg_bf16(state, inter * H).reshape(inter, H)
+            t[p + "mlp.down_proj.weight"] = _lcg_bf16(state, H * inter).reshape(H, inter)
+            continue
+        E, I = cfg["n_routed_experts"], cfg["moe_intermediate_size"]
+        t[p + "mlp.gate.weight"] = _lcg_bf16(state, E * H).reshape(E, H)
+        for e in range(E):
+            x = p + f"mlp.experts.{e}."
+            t[x + "gate_proj.weight"] = _lcg_bf16(state, I * H).reshape(I, H)
+            t[x + "up_proj.weight"] = _lcg_bf16(state, I * H).reshape(I, H)
+            t[x + "down_proj.weight"] = _lcg_bf16(state, H * I).reshape(H, I)
+        S = I * cfg["n_shared_experts"]
+        x = p + "mlp.shared_experts."
+        t[x + "gate_proj.weight"] = _lcg_bf16(state, S * H).reshape(S, H)
+        t[x + "up_proj.weight"] = _lcg_bf16(state, S * H).reshape(S, H)
+        t[x + "down_proj.weight"] = _lcg_bf16(state, H * S).reshape(H, S)
+    t["model.norm.weight"] = ones(H)
+    t["lm_head.weight"] = _lcg_bf16(state, cfg["vocab_size"] * H).reshape(cfg["vocab_size"], H)
+    save_safetensors(os.path.join(directory, "model.safetensors"), t)
+
+    with open(os.path.join(directory, "config.json"), "w") as f:
+        json.dump(dict(cfg, architectures=["DeepseekV2ForCausalLM"], model_type="deepseek_v2"), f, indent=2)
+    # GPT-2's printable stand-ins for the 256 byte values
+    printable = [b for b in range(256) if 33 <= b <= 126 or 161 <= b <= 172 or b >= 174]
+    spelling, extra = {}, 256
+    for b in range(256):
+        if b in printable:
+            spelling[b] = chr(b)
+        else:
+            spelling[b] = chr(extra)
+            extra += 1
+    # a few merges (LiteMind's loader wants a non-empty table), each merged
+    # spelling a token of its own after the bytes
+    vocab = {spelling[b]: b for b in range(256)}
+    merges = [("t", "h"), ("th", "e"), ("i", "n"), ("e", "r")]
+    for a, b in merges:
+        vocab[a + b] = len(vocab)
+    special = lambda i, text: {"id": i, "content": text, "special": True, "single_word": False, "lstrip": False,
+                               "rstrip": False, "normalized": False}
+    tokenizer = {"version": "1.0",
+                 "added_tokens": [special(cfg["bos_token_id"], "<|begin_of_sentence|>"),
+                                  special(cfg["eos_token_id"], "<|end_of_sentence|>")],
+                 "pre_tokenizer": {"type": "ByteLevel", "add_prefix_space": False, "use_regex": True},
+                 "model": {"type": "BPE", "vocab": vocab, "merges": [f"{a} {b}" for a, b in merges]}}
+    with open(os.path.join(directory, "tokenizer.json"), "w", encoding="utf-8") as f:
+        json.dump(tokenizer, f, ensure_ascii=False)
+    with open(os.path.join(directory, "tokenizer_config.json"), "w") as f:
+        json.dump({"add_bos_token": True, "add_eos_token": False, "bos_token": "<|begin_of_sentence|>",
+                   "eos_token": "<|end_of_sentence|>", "model_max_length": 4096,
+                   "tokenizer_class": "LlamaTokenizerFast"}, f, indent=2)

@@ -518,3 +518,59 @@ def test_mfma_core_small_budget_two_groups():
             m.close()
     for a, b in zip(outs[0], outs[1]):
         np.testing.assert_array_equal(bits(a), bits(b))
+
+
+def test_kv_cache_write_read_range_truncate():
+    """lm_kv_cache_write / read_range / truncate through the C ABI: entries
+    written from KvCache's layout read back bit for bit (whole and by range),
+    appended after a prefill, decoding continues over them as over entries the
+    GPU made; a gap, a write past the capacity and a read past the count are
+    refused; truncate keeps the first entries and the next call appends there."""
+    from litemind_amd import LmError
+    d = small_dims(max_positions=32)
+    announce("KV cache write / read_range / truncate (small shapes)")
+    m = Mla(d, 241)
+    try:
+        x = tokens(242, 12, d.hidden)
+        m.forward(x[:6], 0)
+        m.oracle(x[:6], 0)
+        kn, kr, v = m.ctx.kv_cache_read(0, 6)
+        # the same six entries written again, and four more from random data
+        rng = np.random.default_rng(243)
+        kn4 = rng.standard_normal((4, d.heads, d.qk_nope)).astype(np.float32)
+        kr4 = rng.standard_normal((4, d.qk_rope)).astype(np.float32)
+        v4 = rng.standard_normal((4, d.heads, d.v_head)).astype(np.float32)
+        m.ctx.kv_cache_write(0, 6, kn4, kr4, v4)
+        assert m.ctx.kv_cache_tokens(0) == 10
+        rkn, rkr, rv = m.ctx.kv_cache_read_range(0, 6, 4)
+        for a, b in ((rkn, kn4), (rkr, kr4), (rv, v4)):
+            np.testing.assert_array_equal(bits(a), bits(b))
+        rkn, rkr, rv = m.ctx.kv_cache_read_range(0, 2, 3)
+        for a, b in ((rkn, kn[2:5]), (rkr, kr[2:5]), (rv, v[2:5])):
+            np.testing.assert_array_equal(bits(a), bits(b))
+        # the oracle's cache gets the same entries; decoding continues over them
+        n = int(m.cache.count.value)
+        m.cache.key_nope[n:n + 4], m.cache.key_rope[n:n + 4], m.cache.value[n:n + 4] = kn4, kr4, v4
+        m.cache.count.value = n + 4
+        y = m.forward(x[6:8], 10)
+        want, _ = m.oracle(x[6:8], 10)
+        np.testing.assert_array_equal(bits(y), bits(want))
+        m.check_cache()
+        with pytest.raises(LmError, match="write of entries"):
+            m.ctx.kv_cache_write(0, 13, kn4, kr4, v4)  # gap after the 12 entries
+        with pytest.raises(LmError, match="write of entries"):
+            m.ctx.kv_cache_write(0, 30, kn4, kr4, v4)  # past the capacity of 32
+        with pytest.raises(LmError, match="within the cache"):
+            m.ctx.kv_cache_read_range(0, 10, 3)
+        with pytest.raises(LmError, match="within the cache"):
+            m.ctx.kv_cache_truncate(0, 13)
+        # truncate to 6: the oracle's cache keeps its first 6 entries too
+        m.ctx.kv_cache_truncate(0, 6)
+        assert m.ctx.kv_cache_tokens(0) == 6
+        m.cache.count.value = 6
+        y = m.forward(x[8:12], 6)
+        want, _ = m.oracle(x[8:12], 6)
+        np.testing.assert_array_equal(bits(y), bits(want))
+        m.check_cache()
+    finally:
+        m.close()
