@@ -258,7 +258,10 @@ int lm_stack_graph_create(lm_context* ctx, int32_t first_layer, int32_t last_lay
                           int64_t tokens, int32_t path, lm_stack_graph** graph);
 int lm_stack_graph_launch(lm_stack_graph* graph);
 int lm_stack_graph_destroy(lm_stack_graph* graph);
-/* gemm::rms_norm over T rows (src/Gemm.cpp:197-207); out may equal in. */
+/* gemm::rms_norm over T rows (src/Gemm.cpp:197-207), bit for bit; out may
+ * equal in.  The kernel the stack and the attention normalise batches of
+ * tokens with: squares added in a thread-strided tree, and in LiteMind's order
+ * for the rare rows where the two orders could round the inverse differently. */
 int lm_rms_norm(lm_context* ctx, const float* in_dev, const float* weight_dev, float* out_dev, int64_t tokens,
                 int32_t hidden, float epsilon);
 /* Dense SwiGLU FFN of a resident dense layer: y = feed_forward(dense, x, scale 1)

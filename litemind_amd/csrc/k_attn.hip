@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void query_rope_one_kernel(const uint16_t* __r
             v[u] = x[ec];
             nw[u] = norm_w[ec];
         }
-        const float inverse = rms_inverse_256_regs(v, in_dim, eps, part);
+        const float inverse = rms_inverse_256_regs(v, in_dim, eps, part, xs);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int e = static_cast<int>(threadIdx.x) + 256 * u;

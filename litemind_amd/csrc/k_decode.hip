@@ -123,11 +123,12 @@ __device__ inline void load_act_coherent(const float* row, int width, int lane, 
 // RMSNorm of the token inside the launch (the stack's T = 1 step): the inverse
 // of gemm::rms_norm (src/Gemm.cpp:197-207) with the arithmetic of
 // rms_norm_kernel (thread-strided double sums of exact squares, wave
-// butterfly, then (w0 + w1) + (w2 + w3)), so the normalised token is the same
-// bits as the separate kernel's.  The token's elements are loaded first
+// butterfly, then (w0 + w1) + (w2 + w3), made LiteMind's by rms_inverse_exact),
+// so the normalised token is the same bits as the separate kernel's.  The token's elements are loaded first
 // (norm_load: issue them before any weight stream, so waiting for them waits
 // for nothing else) and reduced by norm_reduce, which every thread of the
-// workgroup calls; its barrier orders LDS only.
+// workgroup calls; its barrier orders LDS only.  `stage`: hidden floats of LDS
+// that are free during the call (the rare in-order sum copies the token there).
 static_assert(kWaves == 4, "norm_reduce combines four wave sums");
 template <int N>
 __device__ inline void norm_load(const DecodeArgs& a, float (&v)[N]) {
@@ -139,7 +140,7 @@ __device__ inline void norm_load(const DecodeArgs& a, float (&v)[N]) {
 }
 
 template <int N>
-__device__ inline float norm_reduce(const DecodeArgs& a, const float (&v)[N]) {
+__device__ inline float norm_reduce(const DecodeArgs& a, const float (&v)[N], float* stage) {
     __shared__ double part[kWaves];
     double s = 0.0;
 #pragma unroll
@@ -158,7 +159,18 @@ __device__ inline float norm_reduce(const DecodeArgs& a, const float (&v)[N]) {
     }
     lds_barrier();
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
-    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(a.hidden) + static_cast<double>(a.eps)));
+    return rms_inverse_exact(
+        total, a.hidden, a.eps, part, stage,
+        [&] {
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const int c = static_cast<int>(threadIdx.x) + k * kThreads;
+                if (c < a.hidden) {
+                    stage[c] = v[k];
+                }
+            }
+        },
+        [] { lds_barrier(); });
 }
 
 // Elements per thread of norm_load for a hidden width covered by GI 512-column steps.
@@ -245,7 +257,7 @@ __device__ __forceinline__ void router_slice(const DecodeArgs& a, int e0, float4
         }
     }
     if (a.norm != nullptr) {
-        inverse = norm_reduce(a, v);
+        inverse = norm_reduce(a, v, pf);  // the products are formed after it
     }
 #pragma unroll
     for (int blk = 0; blk < kBlocks; ++blk) {
@@ -394,7 +406,7 @@ __device__ __forceinline__ void gateup_item(const uint16_t* gu, const DecodeArgs
         }
     }
     load_rows<R, GI>(rows, a.hidden, lane, w);
-    const float inverse = a.norm != nullptr ? norm_reduce(a, nv) : 1.0f;
+    const float inverse = a.norm != nullptr ? norm_reduce(a, nv, xs) : 1.0f;
     float4* xs4 = reinterpret_cast<float4*>(xs);
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
@@ -497,7 +509,7 @@ __device__ __forceinline__ void shared_item(const DecodeArgs& a, int chunk, floa
     }
     load_rows<R, GI>(rows, a.hidden, lane, w);
     load_rows<kRpw, GI>(drows, a.hidden, lane, dw);
-    const float inverse = a.norm != nullptr ? norm_reduce(a, nv) : 1.0f;
+    const float inverse = a.norm != nullptr ? norm_reduce(a, nv, xs) : 1.0f;
     float4* xs4 = reinterpret_cast<float4*>(xs);
 #pragma unroll
     for (int i = 0; i < XS; ++i) {

@@ -68,7 +68,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 
 // combine_kernel's sum for one token row, then the next layer's RMSNorm of the
 // row just written (rms_norm_kernel's arithmetic: thread-strided double sums of
-// exact squares, wave butterfly, (w0 + w1) + (w2 + w3)) and its fp16 panel copy
+// exact squares, wave butterfly, (w0 + w1) + (w2 + w3), made LiteMind's by
+// rms_inverse_exact) and its fp16 panel copy
 // (to_f16_rows_kernel's conversion): the next layer's input is the same bits as
 // the separate kernels', without reading the hidden state again.  One
 // workgroup of 256 threads per token.  The row is formed as combine_kernel
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
     __syncthreads();
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
     const float inverse =
-        static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(H) + static_cast<double>(a.eps)));
+        rms_inverse_exact(total, H, a.eps, part, row, [] {}, [] { __syncthreads(); });
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     const int Hp = a.hidden_p;
     for (int k = 0; 1024 * k < Hp; ++k) {
@@ -268,8 +269,9 @@ __global__ __launch_bounds__(256) void bf16_to_f16_panels_kernel(const uint16_t*
 }
 
 // gemm::rms_norm per row (src/Gemm.cpp:197-207): sum of squares in double
-// (exact squares, tree order), inverse = float(1 / sqrt(mean + eps)), then
-// x * inverse * weight with two fp32 roundings.  One workgroup per row.
+// (exact squares, tree order, made LiteMind's by rms_inverse_exact), inverse =
+// float(1 / sqrt(mean + eps)), then x * inverse * weight with two fp32
+// roundings.  One workgroup per row.
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* in, const float* w, float* out, int32_t cols,
                                                        float eps) {
     __shared__ double part[4];

@@ -235,16 +235,75 @@ hipError_t launch_matvec_rows(const uint16_t* w, const float* x, float* out, int
 // tokens; conditions as matvec_rows_supported.
 hipError_t launch_matvec_tokens(const uint16_t* w, const float* x, float* out, int64_t rows, int64_t in_dim,
                                 int64_t tokens, float scale, int32_t accumulate, hipStream_t s);
-// gemm::rms_norm's inverse, 1 / sqrt(mean(x^2) + eps), for x[0 .. n) as
-// rms_norm_kernel forms it with 256 threads: thread t sums the exact squares of
-// elements t, t + 256, ... in double, in that order; the wave's butterfly;
-// then (w0 + w1) + (w2 + w3) over the four waves.  The loads are issued eight
-// at a time (a loop of one load per step waits a round trip per element).
-// Every thread of the 256-thread workgroup calls it; `part` is 4 doubles of
-// LDS.
+// gemm::rms_norm (src/Gemm.cpp:197-207) adds the exact double squares in
+// element order; the kernels add them in a thread-strided tree (below), whose
+// double sum can differ in its last bits, and the inverse float(1 / sqrt(sum /
+// n + eps)) then by one ulp for inputs whose double inverse lies near a float
+// rounding boundary (rows of a few large and many tiny elements reach it at
+// will).  Both sums lie within (n - 1) 2^-53 of the exact sum of the n
+// non-negative squares, so the two double inverses lie within a relative
+// (n + 8) 2^-53 of each other (half the sums' difference through the root,
+// plus the roundings of the division, root and reciprocal).  rms_inverse_exact
+// returns the tree's float inverse when it lies farther than (n + 64) 2^-52 of
+// itself from both rounding boundaries around it (then both round alike: all
+// but about one row in 10^5 of N(0, 1) data); otherwise every thread runs
+// stage() (which may copy the thread's elements to where src points) and
+// thread 0 adds the squares of src[0], src[1], ... in order, eight loads in
+// flight, and the inverse comes from that sum.  Either way the float is
+// gemm::rms_norm's, bit for bit.  Every thread of the workgroup calls it with
+// the same `total`; `barrier` orders LDS (`part`, 4 doubles, and the stage)
+// between its readers and writers.
+template <class Stage, class Barrier>
+__device__ inline float rms_inverse_exact(double total, int n, float eps, double* part, const float* src, Stage stage,
+                                          Barrier barrier) {
+    const double r = 1.0 / __builtin_sqrt(total / static_cast<double>(n) + static_cast<double>(eps));
+    const float f = static_cast<float>(r);
+    const double below = 0.5 * (static_cast<double>(f) + static_cast<double>(nextafterf(f, 0.0f)));
+    const double above = 0.5 * (static_cast<double>(f) + static_cast<double>(nextafterf(f, __builtin_inff())));
+    const double margin = r * (static_cast<double>(n) + 64.0) * 0x1p-52;
+    if (r - below >= margin && above - r >= margin) {
+        return f;
+    }
+    barrier();  // every thread has read the tree's parts
+    stage();
+    barrier();
+    if (threadIdx.x == 0) {
+        double sum = 0.0;
+        int i = 0;
+        for (; i + 8 <= n; i += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                v[u] = src[i + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const double d = static_cast<double>(v[u]);
+                sum = sum + d * d;
+            }
+        }
+        for (; i < n; ++i) {
+            const double d = static_cast<double>(src[i]);
+            sum = sum + d * d;
+        }
+        part[0] = sum;
+    }
+    barrier();
+    const double sum = part[0];
+    barrier();  // read before a later call writes `part` or the stage again
+    return static_cast<float>(1.0 / __builtin_sqrt(sum / static_cast<double>(n) + static_cast<double>(eps)));
+}
+
+// gemm::rms_norm's inverse for x[0 .. n) with 256 threads: thread t sums the
+// exact squares of elements t, t + 256, ... in double, in that order; the
+// wave's butterfly; then (w0 + w1) + (w2 + w3) over the four waves, made
+// LiteMind's by rms_inverse_exact.  The loads are issued eight at a time (a
+// loop of one load per step waits a round trip per element).  Every thread of
+// the 256-thread workgroup calls it; `part` is 4 doubles of LDS.
 // The same inverse from a thread's elements already in registers: v[u] is
-// element threadIdx.x + 256 u (n <= 2048; past n ignored).
-__device__ inline float rms_inverse_256_regs(const float (&v)[8], int n, float eps, double* part) {
+// element threadIdx.x + 256 u (n <= 2048; past n ignored); `stage_lds` (n
+// floats of LDS, free during the call) receives them for the rare in-order sum.
+__device__ inline float rms_inverse_256_regs(const float (&v)[8], int n, float eps, double* part, float* stage_lds) {
     double sq = 0.0;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -261,7 +320,18 @@ __device__ inline float rms_inverse_256_regs(const float (&v)[8], int n, float e
     }
     __syncthreads();
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
-    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(n) + static_cast<double>(eps)));
+    return rms_inverse_exact(
+        total, n, eps, part, stage_lds,
+        [&] {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int e = static_cast<int>(threadIdx.x) + 256 * u;
+                if (e < n) {
+                    stage_lds[e] = v[u];
+                }
+            }
+        },
+        [] { __syncthreads(); });
 }
 
 __device__ inline float rms_inverse_256(const float* __restrict__ x, int n, float eps, double* part) {
@@ -289,7 +359,7 @@ __device__ inline float rms_inverse_256(const float* __restrict__ x, int n, floa
     }
     __syncthreads();
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
-    return static_cast<float>(1.0 / __builtin_sqrt(total / static_cast<double>(n) + static_cast<double>(eps)));
+    return rms_inverse_exact(total, n, eps, part, x, [] {}, [] { __syncthreads(); });
 }
 
 // gemm::dot_bf16 of one weight row over 32 lanes (lane c = 0..31 of a half
