@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer tokens/sec at T=1 and T=2048; % HBM BW (T=1) / % bf16 MFMA (T=2048)"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2516.6  # dense bf16/fp16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk/CU
+PEAK_CLOCK_MHZ = 2400.0    # the engine clock that peak assumes
 
 EXPERT_BYTES = 3 * 1408 * 2048 * 2          # 17,301,504
 GATEUP_EXPERT_BYTES = 2 * 1408 * 2048 * 2   # 11,534,336
@@ -46,9 +47,68 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 # this benchmark, scaled by the counters' readings for a conversion kernel of
 # known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md and
 # profiles/mfma_grouped_kernel_prefill_t2048_skewed.md).
-MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 146_700_013,
-                    ("prefill_t2048_skewed", "gate_up"): 1_158_841_418,
-                    ("prefill_t2048_skewed", "down"): 702_495_046}
+MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 142_380_838,
+                    ("prefill_t2048_skewed", "gate_up"): 1_261_088_451,
+                    ("prefill_t2048_skewed", "down"): 708_908_194}
+
+
+class ClockSampler:
+    """The graphics clock while timed steps run: amdsmi's GPU metrics
+    (current_gfxclks, MHz per XCD, averaged over the XCDs) polled every 0.5 ms
+    from a thread.  summary() is None where amdsmi cannot read them."""
+
+    def __init__(self):
+        import threading
+        self.samples, self.stop, self.thread, self.handle = [], threading.Event(), None, None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self.amdsmi = amdsmi
+            self.handle = amdsmi.amdsmi_get_processor_handles()[0]
+            self._read()
+        except Exception as e:  # no metrics on this host: report none
+            log(f"clock sampler unavailable: {e}")
+            self.handle = None
+
+    def _read(self):
+        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.handle)
+        xcd = [v for v in (m.get("current_gfxclks") or []) if isinstance(v, (int, float)) and v > 0]
+        if xcd:
+            return float(np.mean(xcd))
+        v = m.get("current_gfxclk")
+        return float(v) if isinstance(v, (int, float)) and v > 0 else None
+
+    def _run(self):
+        while not self.stop.is_set():
+            try:
+                v = self._read()
+                if v is not None:
+                    self.samples.append(v)
+            except Exception:
+                pass
+            time.sleep(0.0005)
+
+    def __enter__(self):
+        import threading
+        if self.handle is not None:
+            self.stop.clear()
+            self.thread = threading.Thread(target=self._run, daemon=True)
+            self.thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self.thread is not None:
+            self.stop.set()
+            self.thread.join()
+            self.thread = None
+
+    def summary(self) -> dict | None:
+        if not self.samples:
+            return None
+        a = np.array(self.samples)
+        return {"mhz": round(float(np.median(a)), 1), "min_mhz": round(float(a.min()), 1),
+                "max_mhz": round(float(a.max()), 1), "samples": int(a.size),
+                "source": "amdsmi gpu metrics current_gfxclks (mean over XCDs), median over the timed steps"}
 
 
 def log(msg: str) -> None:
@@ -105,13 +165,15 @@ def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int)
     ctx.synchronize()
     start_ev, stop_ev = ctx.event(), ctx.event()
     ctx.synchronize()
-    t0 = time.perf_counter()
-    ctx.record(start_ev)
-    for i in range(steps):
-        step(i)
-    ctx.record(stop_ev)
-    ctx.synchronize()
-    wall = time.perf_counter() - t0
+    clock = ClockSampler()
+    with clock:
+        t0 = time.perf_counter()
+        ctx.record(start_ev)
+        for i in range(steps):
+            step(i)
+        ctx.record(stop_ev)
+        ctx.synchronize()
+        wall = time.perf_counter() - t0
     gpu_ms = ctx.elapsed_ms(start_ev, stop_ev)
     log(f"{workload_name}: {steps} steps wall {wall * 1e3:.3f} ms, events {gpu_ms:.3f} ms")
 
@@ -120,8 +182,10 @@ def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int)
     stages = {}
     if T > 1:
         ctx.stage_timing(True)
-        for i in range(steps):
-            step(i)
+        with clock:
+            for i in range(steps):
+                step(i)
+            ctx.synchronize()
         stages = ctx.stage_times()
         ctx.stage_timing(False)
 
@@ -130,7 +194,7 @@ def run_gpu(workload_name: str, steps: int, warmup: int, rotate: int, path: int)
     U = float(np.mean(distinct))
     ctx.close()
     return dict(T=T, wall_s=wall, gpu_ms=gpu_ms, steps=steps, stages=stages, distinct=U, layers=layers, x=x,
-                bias=bias, workload=workload_name)
+                bias=bias, workload=workload_name, clock=clock.summary())
 
 
 def run_stack(steps_t1: int, steps_big: int, big_tokens: int, moe_layers: int) -> dict:
@@ -353,6 +417,12 @@ def roofline(res: dict, mfma: bool) -> dict:
                algorithmic_bytes=by, algorithmic_flops=fl, hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     if mfma:
         out["mfma_frac"] = round(tfs / MFMA_PEAK_TFLOPS, 4)
+        clk = res.get("clock")
+        if clk:
+            # the same rate against the peak at the measured clock: the share
+            # of the matrix cores' issue slots the kernel fills
+            out["clock_mhz"] = clk["mhz"]
+            out["mfma_frac_at_clock"] = round(tfs / (MFMA_PEAK_TFLOPS * clk["mhz"] / PEAK_CLOCK_MHZ), 4)
     return out
 
 
@@ -364,8 +434,14 @@ def swiglu(res: dict) -> dict:
     fl = alg["gate_up_flops"] + alg["down_flops"]
     tf = fl / (us * 1e-6) / 1e12 if us else 0.0
     traffic = [MEASURED_TRAFFIC.get((res["workload"], k)) for k in ("gate_up", "down")]
-    return {"us": round(us, 2), "flops": fl, "achieved": round(tf, 2), "unit": "TFLOP/s", "peak": MFMA_PEAK_TFLOPS,
-            "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": None if None in traffic else sum(traffic)}
+    out = {"us": round(us, 2), "flops": fl, "achieved": round(tf, 2), "unit": "TFLOP/s", "peak": MFMA_PEAK_TFLOPS,
+           "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "traffic": None if None in traffic else sum(traffic)}
+    clk = res.get("clock")
+    out["clock"] = clk
+    if clk:
+        out["peak_at_clock"] = round(MFMA_PEAK_TFLOPS * clk["mhz"] / PEAK_CLOCK_MHZ, 1)
+        out["frac_at_clock"] = round(tf / out["peak_at_clock"], 4) if tf else 0.0
+    return out
 
 
 def run_load(moe_layers: int) -> dict:
@@ -636,6 +712,7 @@ def main() -> int:
                    "distinct_experts_per_step": res["distinct"]},
         "roofline": roofline(res, mfma_main),
         "layer_gpu_us": round(res["gpu_ms"] * 1e3 / res["steps"], 2),
+        "clock": res["clock"],
     }
     if res["stages"]:
         line["stage_us"] = {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res["stages"].items()}
@@ -673,6 +750,7 @@ def main() -> int:
             "expert_path": "mfma-fp16" if mfma2 else "gemv-fp32",
             "roofline": roofline(res2, mfma2),
             "stage_us": {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in res2["stages"].items()},
+            "clock": res2["clock"],
         }
         if mfma2:
             line["t2048" if w2.tokens == 2048 else args.second]["grouped_swiglu"] = swiglu(res2)
