@@ -623,6 +623,7 @@ struct FusedArgs {
     uint32_t* sync;     // [2][kSetWords] counters, then the error word
     uint64_t* approx;   // [E] fast (reassociated) logits for the speculative selection, tagged
     uint64_t* spec;     // [K] speculative experts by rank, tagged
+    uint64_t* spec_xcd; // [8][16] the same per XCD, one 128-byte L2 line each (kDecodeXcdSpecWord)
     uint32_t* mask;     // ranks whose speculative expert differs from the exact one
     int32_t parity;
     uint32_t seq;       // this launch's tag of the approx / spec words (nonzero, changes every launch)
@@ -747,6 +748,73 @@ __device__ inline void load_spec(const FusedArgs& f, uint32_t* error, int* spec_
         const uint32_t v = wait_tagged(f.spec, f.a.top_k, f.seq, error, f.max_spins);
         if (static_cast<int>(threadIdx.x) < f.a.top_k) {
             spec_lds[threadIdx.x] = static_cast<int>(v < static_cast<uint32_t>(f.a.experts) ? v : 0u);
+        }
+    }
+    __syncthreads();
+}
+
+// The XCD this workgroup runs on (HW_REG_XCC_ID, bits 0..3; eight per device).
+__device__ inline int xcd_id() { return static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 7); }
+
+// Per-XCD copies of the speculative experts.  The selectors (the first routed
+// workgroups, kXcdSelectors of them) each store the tagged words into the slot
+// of their own XCD with `sc0` stores: written through the CU's L1 into the
+// XCD's L2 and kept there.  The routed workgroups poll their XCD's slot with
+// `sc0` loads, which miss L1 and read that L2 (the scope the memory model
+// uses for a workgroup split over the CUs of one XCD), so the hand-off costs an
+// L2 round trip instead of a device-scope one through memory.  They poll the
+// device-scope words as well, alternately: a slot no selector of this launch
+// reached (workgroups placed on XCDs otherwise than round robin) never
+// delays them past the device-scope hand-off.  Slots hold words of earlier
+// launches, which their tags reject.
+constexpr int kXcdSelectors = 8;
+constexpr int kXcdSlotBytes = kDecodeXcdSlotWords * 4;
+constexpr int kAuxSc0 = 1;  // buffer instruction cache policy: sc0
+
+__device__ inline void publish_xcd(const FusedArgs& f, int rank, uint32_t bits) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(f.spec_xcd, 0, 8 * kXcdSlotBytes, 0x00020000);
+    const uint64_t word = (static_cast<uint64_t>(f.seq) << 32) | bits;
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = {static_cast<unsigned>(word), static_cast<unsigned>(word >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, xcd_id() * kXcdSlotBytes + rank * 8, 0, kAuxSc0);
+}
+
+__device__ inline void load_spec_xcd(const FusedArgs& f, uint32_t* error, int* spec_lds) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int n = f.a.top_k;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(f.spec_xcd, 0, 8 * kXcdSlotBytes, 0x00020000);
+        const int off = xcd_id() * kXcdSlotBytes + (lane < n ? lane : 0) * 8;
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        uint32_t spins = 0, v = 0;
+        for (;;) {
+            const u32x2 l = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kAuxSc0);
+            if (__ballot(lane < n && l.y != f.seq) == 0) {
+                v = l.x;
+                break;
+            }
+            // the device-scope words every 8th poll (a poll of them waits a
+            // round trip through memory; the slot's, one through L2)
+            if ((spins & 7) == 7) {
+                const uint64_t g = lane < n ? __hip_atomic_load(f.spec + lane, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT)
+                                            : static_cast<uint64_t>(f.seq) << 32;
+                if (__ballot(static_cast<uint32_t>(g >> 32) != f.seq) == 0) {
+                    v = static_cast<uint32_t>(g);
+                    break;
+                }
+                v = static_cast<uint32_t>(g);
+            }
+            if (++spins > f.max_spins) {
+                if (lane == 0) {
+                    __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane < n) {
+            spec_lds[lane] = static_cast<int>(v < static_cast<uint32_t>(f.a.experts) ? v : 0u);
         }
     }
     __syncthreads();
@@ -1115,15 +1183,20 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
     }
     b -= f.n_shared_gu;
     const int chunks = a.inter_p / kItemRows;
-    if (b == 0) {
-        // The first routed workgroup selects speculatively from the approximate
-        // logits and publishes the experts for the routed and down workgroups.
+    if (b < kXcdSelectors && b < f.n_routed) {
+        // The first routed workgroups select speculatively from the approximate
+        // logits and publish the experts into their XCD's slot; the first also
+        // into the device-scope words the down workgroups read.
         if (threadIdx.x < 64) {
             const bool valid = lane < a.experts;
             const float logit = bits_float(wait_tagged(f.approx, a.experts, f.seq, error, f.max_spins));
             const int rank = speculative_rank(valid ? logit : 0.0f, valid, lane, a.policy, sel);
             if (valid && rank < a.top_k) {
-                publish(f.spec + (f.perturb ? (rank + 1) % a.top_k : rank), f.seq, static_cast<uint32_t>(lane));
+                const int slot = f.perturb ? (rank + 1) % a.top_k : rank;
+                publish_xcd(f, slot, static_cast<uint32_t>(lane));
+                if (b == 0) {
+                    publish(f.spec + slot, f.seq, static_cast<uint32_t>(lane));
+                }
             }
         }
     }
@@ -1132,7 +1205,7 @@ __global__ __launch_bounds__(kThreads) void decode_fused_kernel(FusedArgs f) {
         // Routed gate/up of the speculative experts.
         const int item = b + f.n_routed;
         const int r = item / chunks;
-        load_spec(f, error, expert_of_rank);
+        load_spec_xcd(f, error, expert_of_rank);
         LM_TRACE(1);
         gateup_item<GI>(a.routed + static_cast<int64_t>(expert_of_rank[r]) * a.routed_stride, a,
                         item - r * chunks, a.act + static_cast<int64_t>(r) * a.inter_p,
@@ -1220,6 +1293,7 @@ hipError_t launch_decode(const DecodeLaunch& d, hipStream_t s) {
     f.sync = d.sync;
     f.approx = reinterpret_cast<uint64_t*>(d.sync + kDecodeApproxWord);
     f.spec = reinterpret_cast<uint64_t*>(d.sync + kDecodeSpecWord);
+    f.spec_xcd = reinterpret_cast<uint64_t*>(d.sync + kDecodeXcdSpecWord);
     f.seq = d.seq;
     f.mask = d.sync + kDecodeMaskWord;
     f.parity = d.parity & 1;

@@ -208,7 +208,10 @@ constexpr int kDecodeErrorWord = kDecodeCounterWords;
 constexpr int kDecodeApproxWord = kDecodeErrorWord + 16;
 constexpr int kDecodeSpecWord = kDecodeApproxWord + 2 * kMaxExperts;
 constexpr int kDecodeMaskWord = kDecodeSpecWord + 2 * kMaxTopK;
-constexpr int kDecodeSyncWords = kDecodeMaskWord + 16;
+// per-XCD copies of the speculative experts: 8 slots of 128 bytes (one L2 line each)
+constexpr int kDecodeXcdSpecWord = (kDecodeMaskWord + 16 + 31) / 32 * 32;
+constexpr int kDecodeXcdSlotWords = 32;
+constexpr int kDecodeSyncWords = kDecodeXcdSpecWord + 8 * kDecodeXcdSlotWords;
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 // LM head (k_head.hip): logits [tokens, rows] = w [rows, in_dim] . x [tokens, in_dim]
 // with gemm::dot_bf16's association, tokens <= kHeadTokens, in_dim % 8 == 0; and
