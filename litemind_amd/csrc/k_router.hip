@@ -669,21 +669,21 @@ __device__ void permute_one_token(const RouterArgs& a) {
     // Canonical permutation for T = 1: the k selections, bucketed by expert.
     const int E = a.experts, K = a.top_k;
     const int tid = threadIdx.x;
-    if (tid < E) {
+    for (int e = tid; e < E; e += static_cast<int>(blockDim.x)) {
         int count = 0;
         for (int r = 0; r < K; ++r) {
-            count += a.idx[r] == tid ? 1 : 0;
+            count += a.idx[r] == e ? 1 : 0;
         }
-        a.rb.counts[tid] = count;
+        a.rb.counts[e] = count;
         int offset = 0;
         for (int r = 0; r < K; ++r) {
-            offset += a.idx[r] < tid ? 1 : 0;
+            offset += a.idx[r] < e ? 1 : 0;
         }
-        a.rb.offsets[tid] = offset;
-        if (tid == 0) {
-            a.rb.offsets[E] = K;
-            a.rb.active[E] = K;
-        }
+        a.rb.offsets[e] = offset;
+    }
+    if (tid == 0) {
+        a.rb.offsets[E] = K;
+        a.rb.active[E] = K;
     }
     if (tid < K) {
         const int e = a.idx[tid];
@@ -769,6 +769,106 @@ __global__ __launch_bounds__(kSplitThreads) void router_single_kernel(RouterArgs
     }
 }
 
+// Raw logits (bias not added) of experts [e0, e0 + 8) for token blockIdx.y,
+// for any hidden width: the gate rows in chunks of kChunkRows, each chunk's
+// rounded products formed by all threads into one of two LDS buffers while
+// lanes 0..7 of wave 0 add the previous chunk's products to their expert's
+// chain, strictly left to right over the whole row (LiteMind's dot,
+// src/Gemm.cpp:183-189), as router_single_kernel does for a row that fits LDS
+// whole.  For more than 64 experts, where the per-token router gives one wave
+// every expert of a token (a chain per expert, one after another).  Grid
+// (E / 8, T); hidden % 4 == 0, E % 8 == 0.
+constexpr int kChunkRows = 512;
+__global__ __launch_bounds__(kSplitThreads) void router_chunked_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                        const float* __restrict__ wt) {
+    __shared__ float4 prod[2][kChunkRows / 4 * kSplitExperts];
+    const int tid = threadIdx.x;
+    const int H = a.hidden;
+    const int E = a.experts;
+    const int e0 = blockIdx.x * kSplitExperts;
+    const int64_t t = blockIdx.y;
+    const float* xt = x + t * H;
+    const int nchunks = (H + kChunkRows - 1) / kChunkRows;
+    constexpr int kPer = kChunkRows * (kSplitExperts / 4) / kSplitThreads;  // float4 loads per thread per chunk
+    float4 w[kPer];
+    float xv[kPer];
+    auto fetch = [&](int c) {
+        const int i0 = c * kChunkRows;
+        const int nf = (H - i0 < kChunkRows ? H - i0 : kChunkRows) * (kSplitExperts / 4);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int f = j * kSplitThreads + tid;
+            const int fl = f < nf ? f : nf - 1;
+            const int i = i0 + (fl >> 1);
+            w[j] = *reinterpret_cast<const float4*>(wt + static_cast<int64_t>(i) * E + e0 + 4 * (fl & 1));
+            xv[j] = xt[i];
+        }
+    };
+    auto store = [&](int c) {
+        const int i0 = c * kChunkRows;
+        const int nf = (H - i0 < kChunkRows ? H - i0 : kChunkRows) * (kSplitExperts / 4);
+        float4* buf = prod[c & 1];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int f = j * kSplitThreads + tid;
+            if (f < nf) {
+                const int i = f >> 1;  // row within the chunk
+                const int el = 4 * (f & 1);
+                float* base = reinterpret_cast<float*>(&buf[(i >> 2) * kSplitExperts]);
+                base[(el + 0) * 4 + (i & 3)] = w[j].x * xv[j];
+                base[(el + 1) * 4 + (i & 3)] = w[j].y * xv[j];
+                base[(el + 2) * 4 + (i & 3)] = w[j].z * xv[j];
+                base[(el + 3) * 4 + (i & 3)] = w[j].w * xv[j];
+            }
+        }
+    };
+    fetch(0);
+    store(0);
+    lds_barrier();
+    float acc = 0.0f;
+    for (int c = 0; c < nchunks; ++c) {
+        if (c + 1 < nchunks) {
+            fetch(c + 1);  // in flight while the chains run
+        }
+        if (tid < kSplitExperts) {
+            const float4* buf = prod[c & 1];
+            const int quads = (H - c * kChunkRows < kChunkRows ? H - c * kChunkRows : kChunkRows) / 4;
+            int q = 0;
+            for (; q + 8 <= quads; q += 8) {  // eight reads in flight, then their adds in order
+                float4 p[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    p[u] = buf[(q + u) * kSplitExperts + tid];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc = acc + p[u].x;
+                    acc = acc + p[u].y;
+                    acc = acc + p[u].z;
+                    acc = acc + p[u].w;
+                }
+            }
+            for (; q < quads; ++q) {
+                const float4 p = buf[q * kSplitExperts + tid];
+                acc = acc + p.x;
+                acc = acc + p.y;
+                acc = acc + p.z;
+                acc = acc + p.w;
+            }
+        }
+        if (c + 1 < nchunks) {
+            store(c + 1);  // the other buffer: its last readers passed the previous barrier
+        }
+        lds_barrier();
+    }
+    if (tid < kSplitExperts) {
+        a.logits_scratch[t * E + e0 + tid] = acc;
+    }
+}
+
+// The canonical permutation of one token's selection (any number of experts).
+__global__ __launch_bounds__(256) void permute_one_kernel(RouterArgs a) { permute_one_token(a); }
+
 // Selection and permutation for one token from the logits of router_single_kernel
 // (a separate launch: the kernel boundary orders the hand-off across XCDs).
 __global__ __launch_bounds__(64) void select_single_kernel(RouterArgs a) {
@@ -800,14 +900,42 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         if (a.experts > kMaxExpertsWide) {
             return hipErrorInvalidValue;
         }
-        if (a.experts <= 128) {
-            launch_multi<2>(a, s);
-        } else if (a.experts <= 256) {
-            launch_multi<4>(a, s);
-        } else {
-            launch_multi<8>(a, s);
+        RouterArgs k = a;
+        // few tokens: the logits over E / 8 workgroups per token first, then
+        // the per-token kernel selects from them (bias added there)
+        const bool split = a.do_matvec && a.tokens <= kRouterSplitTokens && a.experts % kSplitExperts == 0 &&
+                           a.hidden % 4 == 0 && a.logits_scratch != nullptr;
+        if (split) {
+            hipLaunchKernelGGL(router_chunked_kernel,
+                               dim3(static_cast<unsigned>(a.experts / kSplitExperts), static_cast<unsigned>(a.tokens)),
+                               dim3(kSplitThreads), 0, s, a, a.x, a.wt);
+            hipError_t err = hipGetLastError();
+            if (err != hipSuccess) {
+                return err;
+            }
+            k.do_matvec = 0;
+            k.x = a.logits_scratch;
+            k.x16 = nullptr;
         }
-        return hipGetLastError();
+        if (a.experts <= 128) {
+            launch_multi<2>(k, s);
+        } else if (a.experts <= 256) {
+            launch_multi<4>(k, s);
+        } else {
+            launch_multi<8>(k, s);
+        }
+        hipError_t err = hipGetLastError();
+        if (err == hipSuccess && split && a.x16 != nullptr) {
+            err = launch_to_f16_rows(a.x, a.x16, a.tokens, a.hidden, a.hidden_p, s);
+        }
+        if (err == hipSuccess && split && a.tokens == 1 && a.rb.counts != nullptr) {
+            hipLaunchKernelGGL(permute_one_kernel, dim3(1), dim3(256), 0, s, a);
+            err = hipGetLastError();
+            if (err == hipSuccess && permuted != nullptr) {
+                *permuted = true;
+            }
+        }
+        return err;
     }
     const size_t split_lds = sizeof(float) * static_cast<size_t>(a.hidden) * kSplitExperts;
     if (a.do_matvec && a.tokens == 1 && a.experts % kSplitExperts == 0 && a.logits_scratch != nullptr &&

@@ -96,7 +96,7 @@ struct Workspace {
     float* xnorm = nullptr;       // stack: normalised input
     float* ffn = nullptr;         // stack / dense: FFN output
     int32_t* zero = nullptr;      // a device int holding 0 (dense layers have no routed experts)
-    float* logit_scratch = nullptr;  // [E] single-token router hand-off
+    float* logit_scratch = nullptr;  // [kRouterSplitTokens, E] router hand-off of the few-token launches
     uint32_t* decode_sync = nullptr;  // single-launch decode counters (zeroed once) + error word
     float* decode_part = nullptr;     // single-launch decode: the shared items' partial down projections
     uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
@@ -376,7 +376,8 @@ int ensure_workspace(lm_context* ctx, int64_t tokens) {
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ffn), sizeof(float) * static_cast<size_t>(T * ctx->H)));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.zero), sizeof(int32_t) * 4));
     LM_HIP(hipMemsetAsync(w.zero, 0, sizeof(int32_t) * 4, ctx->stream));
-    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.logit_scratch), sizeof(float) * static_cast<size_t>(E)));
+    LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.logit_scratch),
+                     sizeof(float) * static_cast<size_t>(E) * lm::kRouterSplitTokens));
     LM_HIP(hipMalloc(reinterpret_cast<void**>(&w.ticket), sizeof(uint32_t) * 4));
     LM_HIP(hipMemsetAsync(w.ticket, 0, sizeof(uint32_t) * 4, ctx->stream));
     const size_t permute_bytes = sizeof(int32_t) * static_cast<size_t>(lm::permute_scratch_words(TK));

@@ -20,6 +20,10 @@ constexpr int kGroupRows = 32;
 constexpr int kPad = 64;
 constexpr int kMaxExperts = 64;   // one lane per expert: the single-token kernel and the fast router paths
 constexpr int kMaxExpertsWide = 512;  // the general router, selection and permutation (lane owns experts lane + 64 j)
+// Up to this many tokens, layers of more than 64 experts form their logits
+// over E / 8 workgroups per token (into the [tokens, E] logits scratch) before
+// the per-token selection.
+constexpr int kRouterSplitTokens = 16;
 constexpr int kMaxTopK = 16;
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

@@ -68,6 +68,11 @@ class Dims:
 
 
 V2_LITE = Dims()
+# DeepSeek-V2's MoE layers (config.json of deepseek-ai/DeepSeek-V2): 160 routed
+# experts in 8 groups of which 3 are kept, top-6, two shared experts, routed
+# weights scaled by 16.
+V2_FULL = Dims(hidden=5120, inter=1536, experts=160, top_k=6, n_shared=2, dense_inter=12288, layers=60,
+               routed_scaling_factor=16.0, group_limited=True, n_group=8, topk_group=3)
 
 _synth = None
 
