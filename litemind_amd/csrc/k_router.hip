@@ -655,6 +655,232 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs
 }
 
 // ---------------------------------------------------------------------------
+// More than 64 experts at batches above kRouterSplitTokens: router_wide_kernel's
+// direct-to-LDS ring, DEPTH slots deep (8 fill the CU's LDS where the grid has
+// one workgroup per CU, 4 let two share a CU), with lane l owning experts
+// l + 64 j (j < EPL).  The slots are separate LDS variables, each indexed by a
+// constant in the unrolled loop: the compiler can then tell the slot a read
+// uses from the ones the loads in flight fill, and waits only for its own
+// chunk (with one array it waits for every load in flight before each chunk's
+// first read).  A
+// chunk is R = 32 / 16 / 8 gate rows (EPL 2 / 4 / 8): their block of the
+// [H/4][E][4] layout, R / 4 x E x 16 bytes <= 16 KB and contiguous, loaded as
+// 16 wave instructions of 1 KB (those past the block reload its start into
+// LDS that is never read, so every chunk issues the same loads and the waits
+// stay exact), and the tokens' R activations each.  Each lane runs EPL x TPW
+// of LiteMind's sequential chains (src/Gemm.cpp:183-189), rows in order; then
+// select_token_multi per token.  H % R == 0.
+// ---------------------------------------------------------------------------
+template <int EPL>
+constexpr int wide_multi_rows() { return EPL <= 2 ? 32 : (EPL <= 4 ? 16 : 8); }
+constexpr int kWideMultiGate = 16 * 1024;  // gate bytes per ring slot
+constexpr int kWideMultiSlot = kWideMultiGate + kWideWaves * 1024;
+
+template <int EPL, int TPW, int DEPTH>
+__global__ __launch_bounds__(kWideWaves * 64) void router_wide_multi_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                             const float* __restrict__ wq4) {
+    static_assert(DEPTH == 4 || DEPTH == 8, "ring depth");
+    constexpr int R = wide_multi_rows<EPL>();
+    constexpr int kGateLoads = kWideMultiGate / 1024 / kWideWaves;  // 4 per wave
+    constexpr int kLoads = kGateLoads + 1;
+    constexpr int kHi = DEPTH > 4 ? kWideMultiSlot : 16;
+    __shared__ __attribute__((aligned(1024))) char r0[kWideMultiSlot], r1[kWideMultiSlot], r2[kWideMultiSlot],
+        r3[kWideMultiSlot];
+    __shared__ __attribute__((aligned(1024))) char r4[kHi], r5[kHi], r6[kHi], r7[kHi];
+    char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int H = a.hidden;
+    const int E = a.experts;
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * kWideWaves * TPW;
+    const int nchunks = H / R;
+    const int chunk_bytes = R / 4 * E * 16;
+
+    // activations: lane -> token (lane / (R / 4)) % TPW of the wave, rows 4 (lane % (R / 4)) .. + 3
+    int64_t xt = tb0 + wave * TPW + ((lane / (R / 4)) % TPW);
+    xt = xt < a.tokens ? xt : a.tokens - 1;
+    const float* xsrc = x + xt * H + 4 * (lane % (R / 4));
+    const char* wbase = reinterpret_cast<const char*>(wq4);
+    auto issue = [&](int c, char* buf) {
+        c = c < nchunks ? c : nchunks - 1;
+        const char* chunk = wbase + static_cast<int64_t>(c) * chunk_bytes;
+#pragma unroll
+        for (int j = 0; j < kGateLoads; ++j) {
+            const int n = j * kWideWaves + wave;  // 1 KB block n of the slot
+            const int off = n * 1024 + lane * 16;
+            __builtin_amdgcn_global_load_lds((router_global_void*)(chunk + (off < chunk_bytes ? off : 0)),
+                                             (router_lds_void*)(buf + n * 1024), 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + static_cast<int64_t>(c) * R),
+                                         (router_lds_void*)(buf + kWideMultiGate + wave * 1024), 16, 0, 0);
+    };
+
+    float acc[TPW][EPL];
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            acc[k][j] = 0.0f;
+        }
+    }
+    int ecl[EPL];  // this lane's experts, clamped for the reads (results past E are discarded)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        ecl[j] = lane + 64 * j < E ? lane + 64 * j : E - 1;
+    }
+    auto compute = [&](const char* buf) {
+        const float4* wb = reinterpret_cast<const float4*>(buf);
+        const float* xb = reinterpret_cast<const float*>(buf + kWideMultiGate + wave * 1024);
+#pragma unroll
+        for (int q = 0; q < R / 4; ++q) {
+            float4 w[EPL];
+            float4 xv[TPW];
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                w[j] = wb[q * E + ecl[j]];
+            }
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+                xv[k] = *reinterpret_cast<const float4*>(xb + k * R + 4 * q);
+            }
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    const float p0 = w[j].x * xv[k].x, p1 = w[j].y * xv[k].y;
+                    const float p2 = w[j].z * xv[k].z, p3 = w[j].w * xv[k].w;
+                    acc[k][j] = acc[k][j] + p0;
+                    acc[k][j] = acc[k][j] + p1;
+                    acc[k][j] = acc[k][j] + p2;
+                    acc[k][j] = acc[k][j] + p3;
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // chunk c in ring[c % DEPTH] with DEPTH - 2 chunks in flight behind it:
+    // wait for c, barrier (every wave is past c - 1), refill c - 1's slot with
+    // c + DEPTH - 1, compute c
+    constexpr int kVm = (DEPTH - 2) * kLoads;
+    static_assert(kVm < 64, "vmcnt field");
+    constexpr int kWait = 0x0070 | (kVm & 15) | ((kVm >> 4) << 14);  // vmcnt(kVm) lgkmcnt(0)
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) {
+        issue(d, ring[d]);
+    }
+    for (int c0 = 0; c0 < nchunks; c0 += DEPTH) {
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) {
+            __builtin_amdgcn_s_waitcnt(kWait);
+            __builtin_amdgcn_s_barrier();
+            issue(c0 + j + DEPTH - 1, ring[(j + DEPTH - 1) % DEPTH]);
+            if (c0 + j < nchunks) {
+                compute(ring[j]);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);  // drain the clamped reloads
+    __builtin_amdgcn_s_barrier();
+
+    const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
+    const int K = a.top_k < E ? a.top_k : E;
+    // one slot per wave (selected, not indexed: ring[] is only ever indexed by constants)
+    float* sh = reinterpret_cast<float*>(wave == 0 ? r0 : (wave == 1 ? r1 : (wave == 2 ? r2 : r3)));
+    static_assert(kWideWaves <= 4 && select_multi_words(EPL) * 4 <= kWideMultiSlot, "selection scratch in the ring");
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) {
+        const int64_t t = tb0 + wave * TPW + k;
+        if (t >= a.tokens) {
+            break;
+        }
+        float logit[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            logit[j] = acc[k][j];
+            if (a.bias != nullptr && e < E) {
+                logit[j] = logit[j] + a.bias[e];
+            }
+            if (a.logits != nullptr && e < E) {
+                a.logits[t * E + e] = logit[j];
+            }
+        }
+        int rank[EPL];
+        float weight[EPL];
+        select_token_multi<EPL>(logit, lane, p, sh, rank, weight);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            if (rank[j] < K) {
+                a.idx[t * a.top_k + rank[j]] = lane + 64 * j;
+                a.wts[t * a.top_k + rank[j]] = weight[j];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+#ifndef LM_RING_TPW2_TOKENS
+#define LM_RING_TPW2_TOKENS 2048
+#endif
+#ifndef LM_RING_TPW4_TOKENS
+#define LM_RING_TPW4_TOKENS 4096
+#endif
+// Tokens per wave: each gate value read from LDS feeds TPW chains.
+constexpr int64_t kRingTpw2Tokens = LM_RING_TPW2_TOKENS;
+constexpr int64_t kRingTpw4Tokens = LM_RING_TPW4_TOKENS;
+#ifndef LM_RING_DEEP_BLOCKS
+#define LM_RING_DEEP_BLOCKS 256
+#endif
+// Grids of up to this many workgroups (one per CU) take the 8-deep ring.
+constexpr int64_t kRingDeepBlocks = LM_RING_DEEP_BLOCKS;
+
+template <int EPL, int TPW>
+void launch_wide_multi_tpw(const RouterArgs& a, hipStream_t s) {
+    constexpr int64_t per_block = static_cast<int64_t>(kWideWaves) * TPW;
+    const int64_t blocks = (a.tokens + per_block - 1) / per_block;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if constexpr (TPW == 1) {  // more tokens per wave only above kRingTpw2Tokens: more than one workgroup per CU
+        if (blocks <= kRingDeepBlocks) {
+            hipLaunchKernelGGL((router_wide_multi_kernel<EPL, 1, 8>), grid, dim3(kWideWaves * 64), 0, s, a, a.x,
+                               a.wq4);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((router_wide_multi_kernel<EPL, TPW, 4>), grid, dim3(kWideWaves * 64), 0, s, a, a.x, a.wq4);
+}
+
+template <int EPL>
+void launch_wide_multi(const RouterArgs& a, hipStream_t s) {
+    if (a.tokens > kRingTpw4Tokens) {
+        launch_wide_multi_tpw<EPL, 4>(a, s);
+    } else if (a.tokens > kRingTpw2Tokens) {
+        launch_wide_multi_tpw<EPL, 2>(a, s);
+    } else {
+        launch_wide_multi_tpw<EPL, 1>(a, s);
+    }
+}
+
+// The ring router for 65..512 experts when the hidden size is a multiple of
+// a chunk's rows; false (nothing launched) otherwise.
+bool launch_ring_router(const RouterArgs& a, hipStream_t s) {
+    const int epl = (a.experts + 63) / 64;
+    const int rows = epl <= 2 ? wide_multi_rows<2>() : (epl <= 4 ? wide_multi_rows<4>() : wide_multi_rows<8>());
+    if (epl < 2 || epl > 8 || a.hidden % rows != 0) {
+        return false;
+    }
+    switch (epl) {
+        case 2: launch_wide_multi<2>(a, s); break;
+        case 3: launch_wide_multi<3>(a, s); break;
+        case 4: launch_wide_multi<4>(a, s); break;
+        case 5: launch_wide_multi<5>(a, s); break;
+        case 6: launch_wide_multi<6>(a, s); break;
+        case 7: launch_wide_multi<7>(a, s); break;
+        default: launch_wide_multi<8>(a, s); break;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // Single-token router (T = 1): the experts are split over kSplit workgroups so
 // each one loads its whole slice of the transposed gate (H x 8 fp32, 64 KB at
 // H = 2048) at once, forms every product fl(w * x) in parallel into LDS, and
@@ -917,15 +1143,20 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
             k.x = a.logits_scratch;
             k.x16 = nullptr;
         }
-        if (a.experts <= 128) {
-            launch_multi<2>(k, s);
-        } else if (a.experts <= 256) {
-            launch_multi<4>(k, s);
-        } else {
-            launch_multi<8>(k, s);
+        // larger batches: the direct-to-LDS ring (the per-token kernel waits a
+        // round trip per 16 gate rows: 694 us at T = 2048 on DeepSeek-V2's layer)
+        const bool wide = !split && a.do_matvec && a.wq4 != nullptr && launch_ring_router(a, s);
+        if (!wide) {
+            if (a.experts <= 128) {
+                launch_multi<2>(k, s);
+            } else if (a.experts <= 256) {
+                launch_multi<4>(k, s);
+            } else {
+                launch_multi<8>(k, s);
+            }
         }
         hipError_t err = hipGetLastError();
-        if (err == hipSuccess && split && a.x16 != nullptr) {
+        if (err == hipSuccess && (split || wide) && a.x16 != nullptr) {
             err = launch_to_f16_rows(a.x, a.x16, a.tokens, a.hidden, a.hidden_p, s);
         }
         if (err == hipSuccess && split && a.tokens == 1 && a.rb.counts != nullptr) {

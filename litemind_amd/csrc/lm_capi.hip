@@ -69,7 +69,7 @@ struct Layer {
     bool allocated = false;
     bool dense = false;
     bool finalized = false;
-    float* router_t = nullptr;         // [H, E], then [E/4][H][4], then [H/4][E][4]
+    float* router_t = nullptr;         // [H, E], then [ceil(E/4)][H][4], then [ceil(H/4)][E][4]
     float* norm = nullptr;             // [H]
     void* slab = nullptr;              // all FFN matrices of the layer (bf16 then fp16 shadow)
     size_t slab_bytes = 0;
@@ -219,6 +219,17 @@ int set_device(lm_context* ctx) {
 size_t ffn_bytes(int64_t inter_p, int64_t hidden, int64_t hidden_p) {
     // gu [2*inter_p, hidden_p] + down [hidden, inter_p], BF16
     return static_cast<size_t>((2 * inter_p * hidden_p + hidden * inter_p) * 2);
+}
+
+// Offsets (floats) of the gate's second and third layouts in Layer::router_t:
+// [H, E]; [ceil(E/4)][H][4] (the last slice zero-padded when E % 4 != 0);
+// [ceil(H/4)][E][4].
+size_t router_quad_expert_offset(const lm_context* ctx) {
+    return static_cast<size_t>(ctx->H) * static_cast<size_t>(ctx->E);
+}
+
+size_t router_quad_row_offset(const lm_context* ctx) {
+    return router_quad_expert_offset(ctx) + static_cast<size_t>(ctx->H) * static_cast<size_t>(lm::round_up(ctx->E, 4));
 }
 
 int check_layer(lm_context* ctx, int32_t layer) {
@@ -582,7 +593,7 @@ int decode_layer(lm_context* ctx, Layer& L, const DecodeScratch& sc, const float
     d.norm = norm;
     d.eps = ctx->cfg.rms_norm_eps;
     d.xnorm = sc.xnorm;
-    d.wq = L.router_t + static_cast<size_t>(ctx->H) * ctx->E;
+    d.wq = L.router_t + router_quad_expert_offset(ctx);
     d.bias = bias;
     d.logits = sc.logits;
     d.logits_out = logits_out;
@@ -672,7 +683,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     lm::RouterArgs ra{};
     ra.x = x;
     ra.wt = L.router_t;
-    ra.wq4 = L.router_t + 2 * static_cast<size_t>(ctx->H) * ctx->E;
+    ra.wq4 = L.router_t + router_quad_row_offset(ctx);
     ra.bias = bias;
     ra.logits = logits_out;
     ra.idx = idx;
@@ -1143,14 +1154,14 @@ int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host) {
         return fail(LM_EINVAL, "null router gate");
     }
     Layer& L = ctx->layers[static_cast<size_t>(layer)];
-    const size_t n = static_cast<size_t>(ctx->H) * static_cast<size_t>(ctx->E);
     // Three layouts of the gate: [H, E] for the per-wave router; [E/4][H][4]
     // (four experts' weights of one row side by side, each slice contiguous)
     // for the single-token router; [H/4][E][4] (four consecutive rows of one
-    // expert side by side) for the wide router.  H is padded to a multiple of
-    // 4 with zero rows in the last one.
-    const size_t n4 = static_cast<size_t>(lm::round_up(ctx->H, 4)) * static_cast<size_t>(ctx->E);
-    const size_t total = 2 * n + n4;
+    // expert side by side) for the ring routers.  E and H are padded to
+    // multiples of 4 with zeros in the last slice of the second and third.
+    const size_t o2 = router_quad_expert_offset(ctx);
+    const size_t o3 = router_quad_row_offset(ctx);
+    const size_t total = o3 + static_cast<size_t>(lm::round_up(ctx->H, 4)) * static_cast<size_t>(ctx->E);
     if (L.router_t == nullptr) {
         LM_HIP(hipMalloc(reinterpret_cast<void**>(&L.router_t), total * sizeof(float)));
         ctx->resident += total * sizeof(float);
@@ -1160,8 +1171,8 @@ int lm_upload_router(lm_context* ctx, int32_t layer, const float* gate_host) {
         for (int i = 0; i < ctx->H; ++i) {
             const float v = gate_host[static_cast<size_t>(e) * ctx->H + i];
             t[static_cast<size_t>(i) * ctx->E + e] = v;
-            t[n + (static_cast<size_t>(e / 4) * ctx->H + i) * 4 + e % 4] = v;
-            t[2 * n + (static_cast<size_t>(i / 4) * ctx->E + e) * 4 + i % 4] = v;
+            t[o2 + (static_cast<size_t>(e / 4) * ctx->H + i) * 4 + e % 4] = v;
+            t[o3 + (static_cast<size_t>(i / 4) * ctx->E + e) * 4 + i % 4] = v;
         }
     }
     LM_HIP(hipMemcpyAsync(L.router_t, t.data(), total * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
@@ -1536,7 +1547,7 @@ int lm_router(lm_context* ctx, int32_t layer, const float* x_dev, int64_t tokens
     lm::RouterArgs ra{};
     ra.x = x_dev;
     ra.wt = L.router_t;
-    ra.wq4 = L.router_t + 2 * static_cast<size_t>(ctx->H) * ctx->E;
+    ra.wq4 = L.router_t + router_quad_row_offset(ctx);
     ra.logits_scratch = ctx->ws.logit_scratch;
     ra.ticket = ctx->ws.ticket;
     ra.bias = logit_bias_dev;

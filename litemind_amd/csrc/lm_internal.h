@@ -23,7 +23,10 @@ constexpr int kMaxExpertsWide = 512;  // the general router, selection and permu
 // Up to this many tokens, layers of more than 64 experts form their logits
 // over E / 8 workgroups per token (into the [tokens, E] logits scratch) before
 // the per-token selection.
-constexpr int kRouterSplitTokens = 16;
+#ifndef LM_ROUTER_SPLIT_TOKENS
+#define LM_ROUTER_SPLIT_TOKENS 256
+#endif
+constexpr int kRouterSplitTokens = LM_ROUTER_SPLIT_TOKENS;
 constexpr int kMaxTopK = 16;
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

@@ -84,7 +84,8 @@ def test_wide_select_golden(name):
 @pytest.mark.parametrize("T", [1, 7, 300, 1500])
 def test_wide_router_bit_exact(wide_ctx, T):
     """Logits (each LiteMind's sequential fp32 chain), experts and weights at
-    one, a few and many tokens (two tokens per wave from 1024 on)."""
+    one and a few tokens (logits over E / 8 workgroups per token) and many
+    (the ring router: 8 deep at 300 tokens, 4 deep at 1500)."""
     from litemind_amd import workload as wl
 
     ctx, layer = wide_ctx
@@ -103,6 +104,63 @@ def test_wide_router_bit_exact(wide_ctx, T):
     assert all(len({e // per for e in row}) <= 3 for row in gidx)  # at most topk_group groups
     for b in (dx, lg, idx, w):
         b.free()
+
+
+# experts, top-k, group-limited, groups, kept, hidden, tokens, bias.  Above 256
+# tokens (or with E % 8 != 0) the batched ring router: every lane-ownership
+# width (two to eight experts per lane), the 8-deep ring (up to 256
+# workgroups) and the 4-deep one, one, two and four tokens per wave, expert
+# counts off multiples of 4 and 8, and a hidden size the ring's chunks do not
+# divide (the per-token kernel).  Up to 256 tokens with E % 8 == 0: logits
+# over E / 8 workgroups per token, then the selection.
+RING_CASES = {
+    "e100_epl2_deep": (100, 6, False, 1, 1, 512, 700, False),
+    "e256_epl4_tpw2": (256, 8, True, 8, 4, 1024, 2100, True),
+    "e512_epl8_deep": (512, 8, True, 16, 4, 512, 333, False),
+    "e130_epl3_deep": (130, 4, True, 2, 1, 768, 90, True),
+    "e160_epl3_tpw1": (160, 6, True, 8, 3, 512, 1300, False),
+    "e160_epl3_tpw4": (160, 6, True, 8, 3, 256, 4200, True),
+    "e100_h1040_fallback": (100, 5, False, 1, 1, 1040, 300, False),
+    "e300_epl5_deep": (300, 6, True, 4, 2, 256, 150, False),
+    "e384_epl6_tpw2": (384, 8, True, 8, 4, 320, 2060, True),
+    "e448_split": (448, 8, False, 1, 1, 256, 77, False),
+    "e160_split_256": (160, 6, True, 8, 3, 512, 256, True),
+}
+
+
+@pytest.mark.parametrize("name", sorted(RING_CASES))
+def test_wide_router_ring_shapes(name):
+    """The batched router above 16 tokens over more than 64 experts: logits,
+    experts and weights bit for bit against the oracle's chains and selection
+    (the logit bias added after the chain, as MoeRouter::route does)."""
+    from litemind_amd import Context
+
+    E, k, grouped, ng, tg, H, T, with_bias = RING_CASES[name]
+    dims = _dims(E, k, grouped, ng, tg, hidden=H, inter=16)
+    rng = np.random.default_rng(E * 7 + H)
+    gate = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32) if with_bias else None
+    announce(f"ring router {name}: E={E} H={H} T={T}")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        ctx.upload_router(0, gate)
+        dx = ctx.to_device(x)
+        db = ctx.to_device(bias) if with_bias else None
+        lg, idx, w = ctx.empty((T, E)), ctx.empty((T, k), np.int32), ctx.empty((T, k))
+        ctx.router(0, dx, T, idx, w, bias=db, logits=lg)
+        ctx.synchronize()
+        glg, gidx, gw = lg.download(), idx.download(), w.download()
+    olg = np.zeros((T, E), np.float32)
+    for t in range(T):
+        ol.oracle().orc_matvec_f32(ol.p(gate), ol.p(np.ascontiguousarray(x[t])), ol.p(olg[t]), E, H)
+    if with_bias:
+        olg = olg + bias[None, :]
+    cfg = ol.router_cfg(E, k, False, 1.0, grouped, ng, tg)
+    assert np.array_equal(glg.view(np.uint32), olg.view(np.uint32)), "logits differ"
+    for t in range(T):
+        oi, ow = ol.oracle_select(olg[t], cfg)
+        assert np.array_equal(gidx[t], oi), f"token {t}: experts differ"
+        assert np.array_equal(gw[t].view(np.uint32), ow.view(np.uint32)), f"token {t}: weights differ"
 
 
 def test_wide_permute(wide_ctx):
