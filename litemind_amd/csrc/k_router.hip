@@ -1059,7 +1059,42 @@ __global__ __launch_bounds__(kSplitThreads) void router_chunked_kernel(RouterArg
         if (tid < kSplitExperts) {
             const float4* buf = prod[c & 1];
             const int quads = (H - c * kChunkRows < kChunkRows ? H - c * kChunkRows : kChunkRows) / 4;
+            auto add8 = [&](const float4 (&p)[8]) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc = acc + p[u].x;
+                    acc = acc + p[u].y;
+                    acc = acc + p[u].z;
+                    acc = acc + p[u].w;
+                }
+            };
             int q = 0;
+            if (quads == kChunkRows / 4) {
+                // a whole chunk fully unrolled, two register sets in turn: one
+                // batch's reads are in flight while the other batch is added,
+                // so the chain (a dependent add every ~3.5 ns) never waits for
+                // LDS (a loop over the batches costs register copies and a
+                // full wait per batch)
+                constexpr int kBatches = kChunkRows / 32;
+                float4 p[2][8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    p[0][u] = buf[u * kSplitExperts + tid];
+                }
+#pragma unroll
+                for (int b = 0; b < kBatches; ++b) {
+                    if (b + 1 < kBatches) {
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            p[(b + 1) & 1][u] = buf[(8 * (b + 1) + u) * kSplitExperts + tid];
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the adds
+                    add8(p[b & 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                q = quads;
+            }
             for (; q + 8 <= quads; q += 8) {  // eight reads in flight, then their adds in order
                 float4 p[8];
 #pragma unroll
@@ -1092,8 +1127,95 @@ __global__ __launch_bounds__(kSplitThreads) void router_chunked_kernel(RouterArg
     }
 }
 
-// The canonical permutation of one token's selection (any number of experts).
-__global__ __launch_bounds__(256) void permute_one_kernel(RouterArgs a) { permute_one_token(a); }
+// One token over more than 64 experts, after router_chunked_kernel: the bias
+// added to the raw logits, the selection (lane owns experts lane + 64 j), the
+// token's permutation and its fp16 copy in one launch.
+template <int EPL>
+__global__ __launch_bounds__(64) void select_one_multi_kernel(RouterArgs a) {
+    __shared__ __align__(16) float sel[select_multi_words(EPL)];
+    __shared__ int ranked[kMaxTopK];  // the expert of each rank
+    const int lane = threadIdx.x;
+    const int E = a.experts;
+    float logit[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        logit[j] = e < E ? a.logits_scratch[e] : 0.0f;
+        if (a.bias != nullptr && e < E) {
+            logit[j] = logit[j] + a.bias[e];
+        }
+        if (a.logits != nullptr && e < E) {
+            a.logits[e] = logit[j];
+        }
+    }
+    const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
+    const int K = a.top_k < E ? a.top_k : E;
+    int rank[EPL];
+    float weight[EPL];
+    select_token_multi<EPL>(logit, lane, p, sel, rank, weight);
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        if (rank[j] < K) {
+            a.idx[rank[j]] = lane + 64 * j;
+            a.wts[rank[j]] = weight[j];
+            ranked[rank[j]] = lane + 64 * j;
+        }
+    }
+    if (a.rb.counts != nullptr) {
+        // permute_one_token's permutation from the ranks in LDS (the experts of
+        // one token are distinct): counts 0 / 1, offsets and positions count
+        // the selected experts below
+        __syncthreads();
+        int chosen[kMaxTopK];
+#pragma unroll
+        for (int r = 0; r < kMaxTopK; ++r) {
+            chosen[r] = r < K ? ranked[r] : 0x7fffffff;
+        }
+        for (int e = lane; e < E; e += 64) {
+            int count = 0, offset = 0;
+#pragma unroll
+            for (int r = 0; r < kMaxTopK; ++r) {
+                count += chosen[r] == e ? 1 : 0;
+                offset += chosen[r] < e ? 1 : 0;
+            }
+            a.rb.counts[e] = count;
+            a.rb.offsets[e] = offset;
+        }
+        if (lane == 0) {
+            a.rb.offsets[E] = K;
+            a.rb.active[E] = K;
+        }
+        if (lane < K) {
+            const int e = ranked[lane];
+            int pos = 0;
+#pragma unroll
+            for (int r = 0; r < kMaxTopK; ++r) {
+                pos += chosen[r] < e ? 1 : 0;
+            }
+            a.rb.perm[pos] = lane;
+            a.rb.slot_of[lane] = pos;
+            a.rb.active[pos] = e;
+        }
+    }
+    if (a.x16 != nullptr) {  // one token: the panel layout is the row itself
+        for (int c = lane; c < a.hidden_p; c += 64) {
+            a.x16[c] = c < a.hidden ? static_cast<_Float16>(a.x[c]) : static_cast<_Float16>(0.0f);
+        }
+    }
+}
+
+hipError_t launch_select_one_multi(const RouterArgs& a, hipStream_t s) {
+    switch ((a.experts + 63) / 64) {
+        case 2: hipLaunchKernelGGL(select_one_multi_kernel<2>, dim3(1), dim3(64), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(select_one_multi_kernel<3>, dim3(1), dim3(64), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(select_one_multi_kernel<4>, dim3(1), dim3(64), 0, s, a); break;
+        case 5: hipLaunchKernelGGL(select_one_multi_kernel<5>, dim3(1), dim3(64), 0, s, a); break;
+        case 6: hipLaunchKernelGGL(select_one_multi_kernel<6>, dim3(1), dim3(64), 0, s, a); break;
+        case 7: hipLaunchKernelGGL(select_one_multi_kernel<7>, dim3(1), dim3(64), 0, s, a); break;
+        default: hipLaunchKernelGGL(select_one_multi_kernel<8>, dim3(1), dim3(64), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
 
 // Selection and permutation for one token from the logits of router_single_kernel
 // (a separate launch: the kernel boundary orders the hand-off across XCDs).
@@ -1139,6 +1261,13 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
             if (err != hipSuccess) {
                 return err;
             }
+            if (a.tokens == 1) {
+                err = launch_select_one_multi(a, s);
+                if (err == hipSuccess && permuted != nullptr) {
+                    *permuted = a.rb.counts != nullptr;
+                }
+                return err;
+            }
             k.do_matvec = 0;
             k.x = a.logits_scratch;
             k.x16 = nullptr;
@@ -1158,13 +1287,6 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         hipError_t err = hipGetLastError();
         if (err == hipSuccess && (split || wide) && a.x16 != nullptr) {
             err = launch_to_f16_rows(a.x, a.x16, a.tokens, a.hidden, a.hidden_p, s);
-        }
-        if (err == hipSuccess && split && a.tokens == 1 && a.rb.counts != nullptr) {
-            hipLaunchKernelGGL(permute_one_kernel, dim3(1), dim3(256), 0, s, a);
-            err = hipGetLastError();
-            if (err == hipSuccess && permuted != nullptr) {
-                *permuted = true;
-            }
         }
         return err;
     }

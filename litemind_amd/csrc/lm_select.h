@@ -207,14 +207,13 @@ __device__ inline void select_token_lds(float logit, bool valid, int lane, const
 //
 // MoeRouter takes any expert count (DeepSeek-V2 routes over 160 experts in 8
 // groups, V3 over 256).  Above 64 experts a lane owns experts lane + 64 j,
-// j < EPL, and the all-to-all steps of the selection go through the wave's own
-// LDS scratch: every lane reads the E values in expert order, so the maximum
-// (std::max_element: the first of equal values, a NaN only at index 0) and
-// the softmax total (left to right) are LiteMind's bit for bit.
-// Per-wave scratch of select_token_multi, in 32-bit words: values [64 EPL],
-// keys [64 EPL] (64-bit), group maxima and group flags [64 EPL] each, picked
-// weights [kMaxTopK].
-__host__ __device__ constexpr int select_multi_words(int epl) { return 64 * epl * 5 + kMaxTopK; }
+// j < EPL.  The softmax total goes through the wave's own LDS scratch: every
+// lane reads the E values in expert order, so the sum runs left to right as
+// LiteMind's; the maximum and the top-k are wave reductions whose results do
+// not depend on the order (see below).
+// Per-wave scratch of select_token_multi, in 32-bit words: values, group
+// maxima and group flags [64 EPL] each, picked weights [kMaxTopK].
+__host__ __device__ constexpr int select_multi_words(int epl) { return 64 * epl * 3 + kMaxTopK; }
 
 template <int EPL>
 __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, const SelectPolicy& a, float* sh,
@@ -222,10 +221,9 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
     constexpr int NE = 64 * EPL;
     const int E = a.experts;
     float* val = sh;
-    uint64_t* keys = reinterpret_cast<uint64_t*>(sh + NE);  // 8-byte aligned: NE is even
-    float* gval = sh + 3 * NE;
-    int* gflag = reinterpret_cast<int*>(sh + 4 * NE);
-    float* picked = sh + 5 * NE;
+    float* gval = sh + NE;
+    int* gflag = reinterpret_cast<int*>(sh + 2 * NE);
+    float* picked = sh + 3 * NE;
     bool valid[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
@@ -235,12 +233,28 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
         }
     }
     __builtin_amdgcn_wave_barrier();
-    // softmax (src/Gemm.cpp:209-223)
-    float maximum = val[0];
-    for (int e = 1; e < E; ++e) {
-        const float v = val[e];
-        maximum = maximum < v ? v : maximum;
+    // softmax (src/Gemm.cpp:209-223).  std::max_element's maximum: only its
+    // value matters (the sign of a zero maximum cannot change logit - max),
+    // and a NaN takes part only at index 0, where it stays the maximum (no
+    // comparison with it holds); elsewhere a NaN never replaces it.  So the
+    // lanes' maxima of their other values, by compare and select (exact bit
+    // patterns, NaNs never enter), then a butterfly over the wave, then the
+    // rule for a NaN first value (a chain over the E values in LDS: 2.6 us at
+    // 160 experts).
+    float lane_max = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        if (valid[j]) {
+            lane_max = lane_max < logit[j] ? logit[j] : lane_max;
+        }
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float other = __shfl_xor(lane_max, o);
+        lane_max = lane_max < other ? other : lane_max;
+    }
+    const float first = val[0];
+    const float maximum = first != first ? first : lane_max;
     float s[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
@@ -255,6 +269,7 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
     }
     __builtin_amdgcn_wave_barrier();
     float total = 0.0f;
+#pragma unroll 8  // the eight reads of a step go out together; the adds stay in expert order
     for (int e = 0; e < E; ++e) {
         total = total + val[e];
     }
@@ -286,6 +301,7 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
         __builtin_amdgcn_wave_barrier();
         for (int g = lane; g < G; g += 64) {
             float best = val[g * per_group];
+#pragma unroll 8
             for (int q = 1; q < per_group; ++q) {
                 const float v = val[g * per_group + q];
                 best = best < v ? v : best;
@@ -297,6 +313,7 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
         for (int g = lane; g < G; g += 64) {
             const float mine = gval[g];
             int beaten = 0;
+#pragma unroll 8
             for (int h = 0; h < G; ++h) {
                 const float other = gval[h];
                 beaten += (other > mine || (other == mine && h < g)) ? 1 : 0;
@@ -312,6 +329,10 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
     // top_k_indices (src/MoeRouter.cpp:14-34): allowed first, then score
     // descending, then index ascending.  Scores are non-negative, so their bit
     // patterns order like the values; the index makes every key unique.
+    // The K largest keys in K rounds of a wave maximum over the keys not yet
+    // taken: round r's key has rank r, the others keep rank K (not
+    // selected).  Valid keys are non-zero and unique, and K <= E of them exist.
+    const int K = a.top_k < E ? a.top_k : E;
     uint64_t key[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
@@ -319,20 +340,20 @@ __device__ inline void select_token_multi(const float (&logit)[EPL], int lane, c
         key[j] = valid[j] ? ((allowed[j] ? (1ull << 62) : 0ull) | (static_cast<uint64_t>(float_bits(score[j])) << 16) |
                              static_cast<uint64_t>(0xffff - e))
                           : 0ull;
-        if (valid[j]) {
-            keys[e] = key[j];
-        }
-        rank[j] = 0;
+        rank[j] = K;
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int e = 0; e < E; ++e) {
-        const uint64_t k = keys[e];
+    for (int r = 0; r < K; ++r) {
+        uint64_t best = 0;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
-            rank[j] += k > key[j] ? 1 : 0;
+            best = rank[j] == K && key[j] > best ? key[j] : best;
+        }
+        best = wave_max_u64(best);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            rank[j] = rank[j] == K && key[j] == best ? r : rank[j];
         }
     }
-    const int K = a.top_k < E ? a.top_k : E;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
         if (valid[j] && rank[j] < K) {
