@@ -20,6 +20,8 @@
 //   scatter: every workgroup recounts its steps, adds the waves before it to
 //            its segment's base, and places every entry at its position plus
 //            its rank.
+// One segment (up to 1024 assignments) takes a single launch of one
+// workgroup that does all three.
 #include "lm_internal.h"
 
 namespace lm {
@@ -239,8 +241,78 @@ __global__ __launch_bounds__(kThreads) void permute_scatter_kernel(PermuteArgs a
     }
 }
 
+// One segment (T k <= 1024 assignments): the count, the scan and the scatter
+// in one workgroup and one launch (no ticket; the scratch is not touched).
+template <int EPL>
+__global__ __launch_bounds__(kThreads) void permute_single_kernel(PermuteArgs a) {
+    constexpr int NE = Wide<EPL>::NE;
+    __shared__ int wave_count[kWaves][NE];  // counts, then each wave's first position per expert
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int E = a.experts;
+    const int64_t i = wave * 64 + lane;
+    int v;
+    uint64_t m;
+    count_step<EPL>(a, i, lane, v, m, wave_count[wave]);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        int carry = 0, carry_active = 0;
+        const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + 64 * j;
+            const bool valid = e < E;
+            int tot = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                tot += valid ? wave_count[w][e] : 0;
+            }
+            int incl = tot;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int up = __shfl_up(incl, o);
+                if (lane >= o) {
+                    incl += up;
+                }
+            }
+            int run = carry + incl - tot;
+            if (valid) {
+                a.rb.counts[e] = tot;
+                a.rb.offsets[e] = run;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const int c = wave_count[w][e];
+                    wave_count[w][e] = run;
+                    run += c;
+                }
+            }
+            carry += __shfl(incl, 63);
+            const uint64_t has = __ballot(valid && tot > 0);
+            if (valid && tot > 0) {
+                a.rb.active[carry_active + __popcll(has & below)] = e;
+            }
+            carry_active += __popcll(has);
+        }
+        if (lane == 0) {
+            a.rb.offsets[E] = carry;
+            a.rb.active[E] = carry_active;
+        }
+    }
+    __syncthreads();
+    if (m != 0) {
+        const uint64_t below = (1ull << lane) - 1ull;
+        const int at = wave_count[wave][v] + __popcll(m & below);
+        a.rb.perm[at] = static_cast<int32_t>(i);
+        a.rb.slot_of[i] = at;
+    }
+}
+
 template <int EPL>
 hipError_t launch_epl(const PermuteArgs& a, int64_t segments, hipStream_t s) {
+    if (segments == 1) {
+        hipLaunchKernelGGL(permute_single_kernel<EPL>, dim3(1), dim3(kThreads), 0, s, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(permute_count_kernel<EPL>, dim3(static_cast<unsigned>(segments)), dim3(kThreads), 0, s, a);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) {

@@ -1127,6 +1127,41 @@ __global__ __launch_bounds__(kSplitThreads) void router_chunked_kernel(RouterArg
     }
 }
 
+// Token t's fp16 panel copy (x16 [tokens, hidden_p]) by one wave: lane l
+// writes columns 8 q .. 8 q + 7 (one 16-byte run of a panel row) from two
+// float4 loads, four chunks' loads in flight together (one element per lane
+// per step waited a load round trip per step).  hidden % 8 == 0,
+// hidden_p % 32 == 0.
+__device__ inline void store_f16_row(const RouterArgs& a, int64_t t, int lane) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const float* xt = a.x + t * a.hidden;
+    const int full = a.hidden / 8;  // chunks of the row; the rest of hidden_p is padding
+    for (int q0 = lane; q0 < full; q0 += 256) {
+        float4 v[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {  // every load first (clamped addresses), then the stores
+            const int q = q0 + 64 * u < full ? q0 + 64 * u : full - 1;
+            v[u][0] = *reinterpret_cast<const float4*>(xt + 8 * q);
+            v[u][1] = *reinterpret_cast<const float4*>(xt + 8 * q + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + 64 * u;
+            if (q < full) {
+                const h8 h = {static_cast<_Float16>(v[u][0].x), static_cast<_Float16>(v[u][0].y),
+                              static_cast<_Float16>(v[u][0].z), static_cast<_Float16>(v[u][0].w),
+                              static_cast<_Float16>(v[u][1].x), static_cast<_Float16>(v[u][1].y),
+                              static_cast<_Float16>(v[u][1].z), static_cast<_Float16>(v[u][1].w)};
+                *reinterpret_cast<h8*>(a.x16 + panel_index(t, 8 * q, a.tokens)) = h;
+            }
+        }
+    }
+    const h8 zero = {};
+    for (int q = full + lane; q < a.hidden_p / 8; q += 64) {
+        *reinterpret_cast<h8*>(a.x16 + panel_index(t, 8 * q, a.tokens)) = zero;
+    }
+}
+
 // One token over more than 64 experts, after router_chunked_kernel: the bias
 // added to the raw logits, the selection (lane owns experts lane + 64 j), the
 // token's permutation and its fp16 copy in one launch.
@@ -1197,10 +1232,31 @@ __global__ __launch_bounds__(64) void select_one_multi_kernel(RouterArgs a) {
             a.rb.active[pos] = e;
         }
     }
-    if (a.x16 != nullptr) {  // one token: the panel layout is the row itself
-        for (int c = lane; c < a.hidden_p; c += 64) {
-            a.x16[c] = c < a.hidden ? static_cast<_Float16>(a.x[c]) : static_cast<_Float16>(0.0f);
-        }
+    if (a.x16 != nullptr) {
+        store_f16_row(a, 0, lane);
+    }
+}
+
+// Up to 64 experts, after router_chunked_kernel: one wave per token adds the
+// bias to its raw logits, selects (route_token) and writes the token's fp16
+// panel copy.
+__global__ __launch_bounds__(256) void select_tokens_kernel(RouterArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (t >= a.tokens) {
+        return;
+    }
+    const bool valid = lane < a.experts;
+    float logit = valid ? a.logits_scratch[t * a.experts + lane] : 0.0f;
+    if (valid && a.bias != nullptr) {
+        logit = logit + a.bias[lane];
+    }
+    if (valid && a.logits != nullptr) {
+        a.logits[t * a.experts + lane] = logit;
+    }
+    route_token(logit, valid, lane, t, a);
+    if (a.x16 != nullptr) {
+        store_f16_row(a, t, lane);
     }
 }
 
@@ -1299,6 +1355,24 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         if (permuted != nullptr) {
             *permuted = a.rb.counts != nullptr;
         }
+        return hipGetLastError();
+    }
+#ifndef LM_SMALL_SPLIT_TOKENS
+#define LM_SMALL_SPLIT_TOKENS 64
+#endif
+    static_assert(LM_SMALL_SPLIT_TOKENS <= kRouterSplitTokens, "the logits scratch holds kRouterSplitTokens tokens");
+    // 2 .. 64 tokens: each token's logits over E / 8 workgroups (one chain
+    // per expert, ~3.5 ns per row), then one wave per token selects: the
+    // wide kernel below runs few workgroups there, each through every chunk
+    // of the gate in turn.  V2-Lite's router, T = 2 .. 32: 19.3-19.5 against
+    // 23.2-24.1 us; T = 64 21.1 against 24.4; T = 128 even; T = 256 36.8
+    // against 24.4.
+    if (a.do_matvec && a.tokens >= 2 && a.tokens <= LM_SMALL_SPLIT_TOKENS && a.experts % kSplitExperts == 0 &&
+        a.hidden % 4 == 0 && a.logits_scratch != nullptr) {
+        hipLaunchKernelGGL(router_chunked_kernel,
+                           dim3(static_cast<unsigned>(a.experts / kSplitExperts), static_cast<unsigned>(a.tokens)),
+                           dim3(kSplitThreads), 0, s, a, a.x, a.wt);
+        hipLaunchKernelGGL(select_tokens_kernel, dim3(static_cast<unsigned>((a.tokens + 3) / 4)), dim3(256), 0, s, a);
         return hipGetLastError();
     }
     // Every batch the wide kernel's shape allows: even a few tokens keep its

@@ -118,6 +118,7 @@ RING_CASES = {
     "e256_epl4_tpw2": (256, 8, True, 8, 4, 1024, 2100, True),
     "e512_epl8_deep": (512, 8, True, 16, 4, 512, 333, False),
     "e130_epl3_deep": (130, 4, True, 2, 1, 768, 90, True),
+    "e130_one_token": (130, 4, True, 2, 1, 768, 1, True),
     "e160_epl3_tpw1": (160, 6, True, 8, 3, 512, 1300, False),
     "e160_epl3_tpw4": (160, 6, True, 8, 3, 256, 4200, True),
     "e100_h1040_fallback": (100, 5, False, 1, 1, 1040, 300, False),
