@@ -336,6 +336,15 @@ int lm_event_elapsed_ms(lm_context* ctx, void* start, void* stop, float* out_ms)
  * 0 router, 1 permute, 2 gate/up, 3 down, 4 combine. */
 int lm_stage_timing(lm_context* ctx, int32_t enable);
 int lm_stage_times(lm_context* ctx, double* out_ms, int32_t* out_calls, int32_t stages);
+/* The core clock while the context's work runs (no counterpart in LiteMind: a
+ * measurement aid).  lm_clock_probe_start launches one wave on a stream of its
+ * own that reads the core clock counter and the 100 MHz real-time counter every
+ * 20 us for `seconds` (at most 2 s); work enqueued meanwhile on the context
+ * stream runs beside it.  lm_clock_probe_finish waits for it and returns the
+ * clock of its intervals in MHz: median, minimum, maximum and the count. */
+int lm_clock_probe_start(lm_context* ctx, double seconds);
+int lm_clock_probe_finish(lm_context* ctx, double* out_median_mhz, double* out_min_mhz, double* out_max_mhz,
+                          int32_t* out_intervals);
 
 #ifdef __cplusplus
 }

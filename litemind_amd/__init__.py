@@ -131,6 +131,8 @@ PROTOTYPES = {
     "lm_event_elapsed_ms": [_P, _P, _P, _P],
     "lm_stage_timing": [_P, _I32],
     "lm_stage_times": [_P, _P, _P, _I32],
+    "lm_clock_probe_start": [_P, C.c_double],
+    "lm_clock_probe_finish": [_P, _P, _P, _P, _P],
     "lm_context_config": [_P, _P],
     "lm_checkpoint_open": [C.c_char_p, _P],
     "lm_checkpoint_close": [_P],
@@ -580,3 +582,15 @@ class Context:
         calls = (C.c_int32 * len(STAGES))()
         self._check(self.lib.lm_stage_times(self.handle, ms, calls, len(STAGES)))
         return {name: (ms[i], calls[i]) for i, name in enumerate(STAGES)}
+
+    def clock_probe_start(self, seconds: float) -> None:
+        """lm_clock_probe_start: sample the core clock for `seconds` (<= 2) on a
+        stream of its own while work is enqueued on the context stream."""
+        self._check(self.lib.lm_clock_probe_start(self.handle, float(seconds)))
+
+    def clock_probe_finish(self) -> dict:
+        med, lo, hi = C.c_double(), C.c_double(), C.c_double()
+        n = C.c_int32()
+        self._check(self.lib.lm_clock_probe_finish(self.handle, C.byref(med), C.byref(lo), C.byref(hi), C.byref(n)))
+        return {"mhz": round(med.value, 1), "min_mhz": round(lo.value, 1), "max_mhz": round(hi.value, 1),
+                "intervals": n.value}

@@ -645,6 +645,44 @@ hipError_t launch_transpose_u16(const uint16_t* src, uint16_t* dst, int64_t rows
     return hipGetLastError();
 }
 
+// The core clock while other kernels run: one lane of one wave, on its own
+// stream, stores (100 MHz real-time counter, core clock counter) pairs every
+// `period` real-time ticks until `total` ticks have passed (the exit depends
+// on the real-time counter alone, so the kernel always ends).  out:
+// [2 * max_pairs] pairs, then the count.
+__global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t* out, int32_t max_pairs, int64_t period,
+                                                         int64_t total) {
+    if (threadIdx.x != 0) {
+        return;
+    }
+    const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+    uint64_t next = r0;
+    int32_t n = 0;
+    for (;;) {
+        const uint64_t r = __builtin_amdgcn_s_memrealtime();
+        if (r >= next) {
+            const uint64_t c = __builtin_amdgcn_s_memtime();
+            if (n < max_pairs) {
+                out[2 * n] = r;
+                out[2 * n + 1] = c;
+                ++n;
+            }
+            next += static_cast<uint64_t>(period);
+        }
+        if (r - r0 >= static_cast<uint64_t>(total)) {
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    out[2 * max_pairs] = static_cast<uint64_t>(n);
+}
+
+hipError_t launch_clock_probe(uint64_t* out, int32_t max_pairs, int64_t period_ticks, int64_t total_ticks,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, s, out, max_pairs, period_ticks, total_ticks);
+    return hipGetLastError();
+}
+
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
                            hipStream_t s) {
     if (rows <= 0) {

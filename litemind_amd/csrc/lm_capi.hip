@@ -200,6 +200,10 @@ struct lm_context {
     lm::HeadBest* head_partial = nullptr;  // per-block candidates of the greedy choice
     lm::AttnState* attention = nullptr;  // lm_attention_configure: MLA weights, rotary tables, KV caches
     int32_t graphs = 0;  // live lm_stack_graph captures (they hold the workspace's pointers)
+    // lm_clock_probe_*: its own stream (default priority) and sample buffer
+    hipStream_t probe_stream = nullptr;
+    uint64_t* probe_buf = nullptr;
+    bool probe_running = false;
     // stage timing
     bool timing = false;
     std::vector<EventSet> ring;
@@ -1081,6 +1085,11 @@ int lm_context_destroy(lm_context* ctx) {
             (void)hipEventDestroy(e);
         }
     }
+    if (ctx->probe_stream != nullptr) {
+        (void)hipStreamSynchronize(ctx->probe_stream);
+        (void)hipStreamDestroy(ctx->probe_stream);
+    }
+    (void)hipFree(ctx->probe_buf);
     if (ctx->stream != nullptr) {
         (void)hipStreamDestroy(ctx->stream);
     }
@@ -2059,6 +2068,73 @@ int lm_event_elapsed_ms(lm_context* ctx, void* start, void* stop, float* out_ms)
     LM_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
     LM_HIP(hipEventElapsedTime(out_ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
     return LM_OK;
+}
+
+namespace {
+constexpr int32_t kProbePairs = 100000;  // 2 s of 20 us intervals
+constexpr int64_t kProbePeriodTicks = 2000;  // 20 us of the 100 MHz counter
+}  // namespace
+
+int lm_clock_probe_start(lm_context* ctx, double seconds) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (!(seconds > 0.0) || seconds > 2.0) {
+        return fail(LM_EINVAL, "lm_clock_probe_start: seconds must be in (0, 2]");
+    }
+    if (ctx->probe_running) {
+        return fail(LM_EINVAL, "lm_clock_probe_start: a probe is running (lm_clock_probe_finish first)");
+    }
+    int rc = set_device(ctx);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (ctx->probe_stream == nullptr) {
+        LM_HIP(hipStreamCreateWithFlags(&ctx->probe_stream, hipStreamNonBlocking));
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->probe_buf), sizeof(uint64_t) * (2 * kProbePairs + 1)));
+    }
+    const int64_t total = static_cast<int64_t>(seconds * 1e8);
+    LM_HIP(lm::launch_clock_probe(ctx->probe_buf, kProbePairs, kProbePeriodTicks, total, ctx->probe_stream));
+    ctx->probe_running = true;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_clock_probe_finish(lm_context* ctx, double* out_median_mhz, double* out_min_mhz, double* out_max_mhz,
+                          int32_t* out_intervals) {
+    LM_GUARD_BEGIN
+    if (ctx == nullptr || out_median_mhz == nullptr || out_min_mhz == nullptr || out_max_mhz == nullptr ||
+        out_intervals == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    if (!ctx->probe_running) {
+        return fail(LM_EINVAL, "lm_clock_probe_finish: no probe running");
+    }
+    ctx->probe_running = false;
+    LM_HIP(hipStreamSynchronize(ctx->probe_stream));
+    std::vector<uint64_t> h(2 * kProbePairs + 1);
+    LM_HIP(hipMemcpy(h.data(), ctx->probe_buf, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    const int64_t n = std::min<int64_t>(static_cast<int64_t>(h[2 * kProbePairs]), kProbePairs);
+    std::vector<double> mhz;
+    for (int64_t i = 1; i < n; ++i) {
+        const uint64_t dr = h[2 * i] - h[2 * (i - 1)];
+        const uint64_t dc = h[2 * i + 1] - h[2 * (i - 1) + 1];
+        if (dr > 0) {
+            mhz.push_back(static_cast<double>(dc) / static_cast<double>(dr) * 100.0);
+        }
+    }
+    *out_intervals = static_cast<int32_t>(mhz.size());
+    if (mhz.empty()) {
+        *out_median_mhz = *out_min_mhz = *out_max_mhz = 0.0;
+        return LM_OK;
+    }
+    std::sort(mhz.begin(), mhz.end());
+    *out_median_mhz = mhz[mhz.size() / 2];
+    *out_min_mhz = mhz.front();
+    *out_max_mhz = mhz.back();
+    return LM_OK;
+    LM_GUARD_END
 }
 
 int lm_stage_timing(lm_context* ctx, int32_t enable) {

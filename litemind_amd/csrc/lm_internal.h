@@ -579,6 +579,8 @@ hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32
 // dst [cols, dst_stride] = src [rows, src_stride] transposed (16-bit elements).
 hipError_t launch_transpose_u16(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t cols, int64_t src_stride,
                                int64_t dst_stride, hipStream_t s);
+hipError_t launch_clock_probe(uint64_t* out, int32_t max_pairs, int64_t period_ticks, int64_t total_ticks,
+                              hipStream_t s);
 hipError_t launch_rms_norm(const float* in, const float* w, float* out, int64_t rows, int32_t cols, float eps,
                            hipStream_t s);
 hipError_t launch_matvec_f32_ref(const float* w, const float* x, float* out, int64_t out_dim, int64_t in_dim,
