@@ -833,6 +833,13 @@ constexpr int64_t kRingTpw4Tokens = LM_RING_TPW4_TOKENS;
 #endif
 // Grids of up to this many workgroups (one per CU) take the 8-deep ring.
 constexpr int64_t kRingDeepBlocks = LM_RING_DEEP_BLOCKS;
+#ifndef LM_SMALL_SPLIT_TOKENS
+#define LM_SMALL_SPLIT_TOKENS 64
+#endif
+// Up to 64 experts: batches of 2 .. kSmallSplitTokens tokens take the logits
+// over E / 8 workgroups per token (router_chunked_kernel).
+constexpr int64_t kSmallSplitTokens = LM_SMALL_SPLIT_TOKENS;
+static_assert(kSmallSplitTokens <= kRouterSplitTokens, "the logits scratch holds kRouterSplitTokens tokens");
 
 template <int EPL, int TPW>
 void launch_wide_multi_tpw(const RouterArgs& a, hipStream_t s) {
@@ -1357,17 +1364,13 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         }
         return hipGetLastError();
     }
-#ifndef LM_SMALL_SPLIT_TOKENS
-#define LM_SMALL_SPLIT_TOKENS 64
-#endif
-    static_assert(LM_SMALL_SPLIT_TOKENS <= kRouterSplitTokens, "the logits scratch holds kRouterSplitTokens tokens");
     // 2 .. 64 tokens: each token's logits over E / 8 workgroups (one chain
     // per expert, ~3.5 ns per row), then one wave per token selects: the
     // wide kernel below runs few workgroups there, each through every chunk
     // of the gate in turn.  V2-Lite's router, T = 2 .. 32: 19.3-19.5 against
     // 23.2-24.1 us; T = 64 21.1 against 24.4; T = 128 even; T = 256 36.8
     // against 24.4.
-    if (a.do_matvec && a.tokens >= 2 && a.tokens <= LM_SMALL_SPLIT_TOKENS && a.experts % kSplitExperts == 0 &&
+    if (a.do_matvec && a.tokens >= 2 && a.tokens <= kSmallSplitTokens && a.experts % kSplitExperts == 0 &&
         a.hidden % 4 == 0 && a.logits_scratch != nullptr) {
         hipLaunchKernelGGL(router_chunked_kernel,
                            dim3(static_cast<unsigned>(a.experts / kSplitExperts), static_cast<unsigned>(a.tokens)),
