@@ -39,19 +39,21 @@ def _oracle_route(layer, x, bias=None):
     return logits, idx, w
 
 
-@pytest.mark.parametrize("case", ["t1", "t5", "t32", "t100_ragged", "t512_uniform", "t2048_skewed", "t4096",
-                                  "t4100_ragged"])
+@pytest.mark.parametrize("case", ["t1", "t5", "t32", "t48_bias", "t64", "t100_ragged", "t512_uniform", "t2048_skewed",
+                                  "t4096", "t4100_ragged"])
 def test_router_bit_exact_v2lite(v2_ctx, case):
     """Every router kernel of the V2-Lite shape: the single-token split kernel,
-    and the wide kernel from a few tokens (one partly filled workgroup) up to
-    one, two and four tokens per wave, including partial last workgroups."""
+    the logits over 8 workgroups per token with a wave per token selecting
+    (2 to 64 tokens, with and without a logit bias), and the wide kernel above
+    (one partly filled workgroup up to one, two and four tokens per wave,
+    including partial last workgroups)."""
     from litemind_amd import workload as wl
 
     ctx, layers = v2_ctx
-    T = {"t1": 1, "t5": 5, "t32": 32, "t100_ragged": 100, "t512_uniform": 512, "t2048_skewed": 2048,
-         "t4096": 4096, "t4100_ragged": 4100}[case]
+    T = {"t1": 1, "t5": 5, "t32": 32, "t48_bias": 48, "t64": 64, "t100_ragged": 100, "t512_uniform": 512,
+         "t2048_skewed": 2048, "t4096": 4096, "t4100_ragged": 4100}[case]
     layer_id = 1 if case == "t512_uniform" else 0
-    bias = wl.skew_bias() if case == "t2048_skewed" else None
+    bias = wl.skew_bias() if case in ("t2048_skewed", "t48_bias") else None
     x = wl.tokens(wl.MASTER_SEED + T, T, 2048)
     announce(f"router {case} T={T} layer={layer_id}")
     g_logits, g_idx, g_w = _gpu_route(ctx, layer_id, x, bias)
@@ -61,10 +63,11 @@ def test_router_bit_exact_v2lite(v2_ctx, case):
     assert np.array_equal(g_w.view(np.uint32), o_w.view(np.uint32)), "weights differ"
 
 
-@pytest.mark.parametrize("T", [2, 4, 37])
+@pytest.mark.parametrize("T", [2, 4, 37, 70])
 def test_router_bit_exact_32_experts(T):
-    """A 32-expert gate (H = 512) is outside the wide kernel's shape, so T <= 4
-    runs the 16-wave few-token kernel and larger batches the per-wave kernel."""
+    """A 32-expert gate (H = 512) is outside the wide kernel's shape: 2 to 64
+    tokens take the logits over 4 workgroups per token, more the per-wave
+    kernel."""
     from litemind_amd import Context
     from litemind_amd import workload as wl
 
@@ -82,6 +85,30 @@ def test_router_bit_exact_32_experts(T):
     o = _oracle_route(layer, x)
     for a, b in zip(g, o):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [3, 40])
+def test_router_bit_exact_60_experts(T):
+    """60 experts (not a multiple of 8): no per-token split, so few tokens take
+    the 16-wave few-token kernel and more the per-wave kernel; logits, experts
+    and weights bit for bit, with a logit bias."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = wl.Dims(hidden=512, inter=128, experts=60, top_k=6, n_shared=1, dense_inter=256, layers=1)
+    rng = np.random.default_rng(60 + T)
+    gate = (rng.standard_normal((60, 512)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(60) * 0.01).astype(np.float32)
+    x = rng.standard_normal((T, 512)).astype(np.float32)
+    layer = wl.MoeLayer(dims, gate, None, None, None, None, None, None)
+    announce(f"router 60 experts T={T}")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        ctx.upload_router(0, gate)
+        g_logits, g_idx, g_w = _gpu_route(ctx, 0, x, bias)
+    o_logits, o_idx, o_w = _oracle_route(layer, x, bias)
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32)), "logits differ"
+    assert np.array_equal(g_idx, o_idx), "selected experts differ"
+    assert np.array_equal(g_w.view(np.uint32), o_w.view(np.uint32)), "weights differ"
 
 
 def test_router_tiny_model(tiny_ctx):
