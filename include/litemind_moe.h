@@ -117,6 +117,13 @@ int lm_head_forward(lm_context* ctx, const float* hidden_dev, int64_t tokens, fl
 /* Finishes a layer's upload: builds the fp16 shadow copy the MFMA path reads.
  * Must be called after the layer's experts and shared expert are uploaded. */
 int lm_finalize_layer(lm_context* ctx, int32_t layer);
+/* After lm_finalize_layer: how many of the layer's BF16 weights its fp16 copy
+ * does not hold exactly (no counterpart in LiteMind, which has no fp16 copy).
+ * The copy is exact for magnitudes in [2^-17, 65504]; larger weights make
+ * lm_finalize_layer fail, smaller ones round to fp16 subnormals (absolute
+ * error <= 2^-25) in the MFMA path's operands only: the GEMV and single-token
+ * paths read the BF16 weights themselves. */
+int lm_layer_fp16_inexact(lm_context* ctx, int32_t layer, int64_t* out_count);
 /* ---- SafeTensors checkpoints: replaces WeightStore + SafeTensor ----
  * (src/WeightStore.cpp:52-185, src/SafeTensor.cpp:30-160).  lm_checkpoint_open maps
  * every *.safetensors file of a directory read-only (sorted by file name; a tensor

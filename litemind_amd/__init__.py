@@ -103,6 +103,7 @@ PROTOTYPES = {
     "lm_upload_dense": [_P, _I32, _P, _P, _P],
     "lm_upload_norm": [_P, _I32, _P],
     "lm_finalize_layer": [_P, _I32],
+    "lm_layer_fp16_inexact": [_P, _I32, _P],
     "lm_resident_bytes": [_P, _P],
     "lm_moe_forward": [_P, _I32, _P, _I64, _P, _P, _P, _P, _P, _I32],
     "lm_moe_forward_noalloc": [_P, _I32, _P, _I64, _P, _P, _P, _P, _P],
@@ -420,6 +421,13 @@ class Context:
 
     def finalize_layer(self, layer: int) -> None:
         self._check(self.lib.lm_finalize_layer(self.handle, layer))
+
+    def layer_fp16_inexact(self, layer: int) -> int:
+        """lm_layer_fp16_inexact: weights of a finalized layer whose fp16 copy
+        (the MFMA path's operands) rounds: BF16 magnitudes below 2^-17."""
+        n = C.c_int64()
+        self._check(self.lib.lm_layer_fp16_inexact(self.handle, layer, C.byref(n)))
+        return n.value
 
     def resident_bytes(self) -> int:
         out = C.c_uint64()

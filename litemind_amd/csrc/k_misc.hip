@@ -244,27 +244,36 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(CombineArgs a) {
 
 // BF16 -> fp16 re-encoding of resident weights for the MFMA path, written in
 // panel layout.  Exact for every BF16 value of magnitude in [2^-17, 65504];
-// smaller ones round to fp16 subnormals (absolute error <= 2^-25), larger ones
-// would overflow and are counted so the host can refuse the layer.  Thread i
-// produces destination element i (coalesced writes; reads within one panel
-// row are contiguous).
+// larger ones would overflow and are counted so the host can refuse the
+// layer; smaller ones round to fp16 subnormals (absolute error <= 2^-25) and
+// are counted into `inexact` (when not null) so the host can report them.
+// Thread i produces destination element i (coalesced writes; reads within one
+// panel row are contiguous).
 __global__ __launch_bounds__(256) void bf16_to_f16_panels_kernel(const uint16_t* __restrict__ src,
                                                                  _Float16* __restrict__ dst, int64_t rows,
-                                                                 int64_t cols, int* overflow) {
+                                                                 int64_t cols, int* overflow,
+                                                                 unsigned long long* inexact) {
     const int64_t n = rows * cols;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     int bad = 0;
+    unsigned lossy = 0;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
         const int64_t panel = i / (rows * kPanel);
         const int64_t rem = i - panel * rows * kPanel;
         const int64_t r = rem / kPanel;
         const int64_t c = panel * kPanel + (rem - r * kPanel);
         const float v = widen_bf16(src[r * cols + c]);
-        bad += (v > 65504.0f || v < -65504.0f) ? 1 : 0;
-        dst[i] = static_cast<_Float16>(v);
+        const bool big = v > 65504.0f || v < -65504.0f;
+        const _Float16 h = static_cast<_Float16>(v);
+        bad += big ? 1 : 0;
+        lossy += (!big && v == v && static_cast<float>(h) != v) ? 1u : 0u;
+        dst[i] = h;
     }
     if (bad != 0) {
         atomicAdd(overflow, bad);
+    }
+    if (inexact != nullptr && lossy != 0) {
+        atomicAdd(inexact, static_cast<unsigned long long>(lossy));
     }
 }
 
@@ -615,7 +624,7 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t rows, int64_t cols, int* overflow,
-                                     hipStream_t s) {
+                                     unsigned long long* inexact, hipStream_t s) {
     const int64_t n = rows * cols;
     if (n <= 0) {
         return hipSuccess;
@@ -628,7 +637,7 @@ hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t
         blocks = 65536;
     }
     hipLaunchKernelGGL(bf16_to_f16_panels_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, rows,
-                       cols, overflow);
+                       cols, overflow, inexact);
     return hipGetLastError();
 }
 

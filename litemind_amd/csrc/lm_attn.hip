@@ -881,7 +881,7 @@ int lm_upload_attention(lm_context* ctx, int32_t layer, const uint16_t* q_proj_h
             if (err == hipSuccess && pc.rows > 0) {
                 err = lm::launch_bf16_to_f16_panels(reinterpret_cast<const uint16_t*>(base + pc.off),
                                                     reinterpret_cast<_Float16*>(b16 + offs16[pc.proj]), pc.rows,
-                                                    pc.cols, d_overflow, info.stream);
+                                                    pc.cols, d_overflow, nullptr, info.stream);
             }
         }
         int overflow = 0;

@@ -69,6 +69,7 @@ struct Layer {
     bool allocated = false;
     bool dense = false;
     bool finalized = false;
+    int64_t fp16_inexact = 0;          // weights whose fp16 copy rounds (|w| < 2^-17), counted at finalize
     float* router_t = nullptr;         // [H, E], then [ceil(E/4)][H][4], then [ceil(H/4)][E][4]
     float* norm = nullptr;             // [H]
     void* slab = nullptr;              // all FFN matrices of the layer (bf16 then fp16 shadow)
@@ -170,6 +171,7 @@ struct lm_context {
     uint16_t* staging = nullptr;   // pinned host buffer for repacking uploads
     size_t staging_bytes = 0;
     int* d_overflow = nullptr;
+    unsigned long long* d_inexact = nullptr;  // lm_finalize_layer's count of rounded fp16 copies
     uint64_t resident = 0;
     // Per-pointer HBM residency (WeightView::prefetch / release and the per-call
     // gemm entry points), keyed by host pointer.
@@ -1024,6 +1026,9 @@ int lm_context_create(int32_t device, const lm_moe_config* config, lm_context** 
     if (rc == LM_OK && hipMalloc(reinterpret_cast<void**>(&ctx->d_overflow), sizeof(int)) != hipSuccess) {
         rc = fail(LM_ENOMEM, "hipMalloc failed");
     }
+    if (rc == LM_OK && hipMalloc(reinterpret_cast<void**>(&ctx->d_inexact), sizeof(unsigned long long)) != hipSuccess) {
+        rc = fail(LM_ENOMEM, "hipMalloc failed");
+    }
     if (rc == LM_OK) {
         rc = static_scratch_setup(ctx);
     }
@@ -1073,6 +1078,7 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->head_logits);
     (void)hipFree(ctx->head_partial);
     (void)hipFree(ctx->d_overflow);
+    (void)hipFree(ctx->d_inexact);
     (void)hipFree(w.decode_sync);
     (void)hipFree(w.decode_part);
     lm::attention_release(ctx->attention);
@@ -1389,6 +1395,7 @@ int lm_finalize_layer(lm_context* ctx, int32_t layer) {
     }
     // fp16 shadow of every matrix in panel layout (the MFMA path's operands).
     LM_HIP(hipMemsetAsync(ctx->d_overflow, 0, sizeof(int), ctx->stream));
+    LM_HIP(hipMemsetAsync(ctx->d_inexact, 0, sizeof(unsigned long long), ctx->stream));
     std::vector<const lm::FfnDev*> ffns;
     if (L.dense) {
         ffns.push_back(&L.dense_ffn);
@@ -1402,15 +1409,19 @@ int lm_finalize_layer(lm_context* ctx, int32_t layer) {
     }
     for (const lm::FfnDev* f : ffns) {
         LM_HIP(lm::launch_bf16_to_f16_panels(f->gu, f->gu_h, 2 * static_cast<int64_t>(f->inter_p), ctx->Hp,
-                                             ctx->d_overflow, ctx->stream));
-        LM_HIP(lm::launch_bf16_to_f16_panels(f->down, f->down_h, ctx->H, f->inter_p, ctx->d_overflow, ctx->stream));
+                                             ctx->d_overflow, ctx->d_inexact, ctx->stream));
+        LM_HIP(lm::launch_bf16_to_f16_panels(f->down, f->down_h, ctx->H, f->inter_p, ctx->d_overflow, ctx->d_inexact,
+                                             ctx->stream));
         if (f->down_t != nullptr) {
             LM_HIP(lm::launch_transpose_u16(f->down, f->down_t, ctx->H, f->inter_p, f->inter_p, ctx->Hp, ctx->stream));
         }
     }
     int overflow = 0;
+    unsigned long long inexact = 0;
     LM_HIP(hipMemcpyAsync(&overflow, ctx->d_overflow, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+    LM_HIP(hipMemcpyAsync(&inexact, ctx->d_inexact, sizeof(inexact), hipMemcpyDeviceToHost, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
+    L.fp16_inexact = static_cast<int64_t>(inexact);
     if (overflow != 0) {
         return fail(LM_EINVAL, "layer " + std::to_string(layer) + ": " + std::to_string(overflow) +
                                    " weights exceed the fp16 range of the MFMA path");
@@ -1434,6 +1445,24 @@ int lm_finalize_layer(lm_context* ctx, int32_t layer) {
     LM_HIP(hipMemcpyAsync(L.table, table.data(), sizeof(void*) * table.size(), hipMemcpyHostToDevice, ctx->stream));
     LM_HIP(hipStreamSynchronize(ctx->stream));
     L.finalized = true;
+    return LM_OK;
+    LM_GUARD_END
+}
+
+int lm_layer_fp16_inexact(lm_context* ctx, int32_t layer, int64_t* out_count) {
+    LM_GUARD_BEGIN
+    int rc = check_layer(ctx, layer);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (out_count == nullptr) {
+        return fail(LM_EINVAL, "null argument");
+    }
+    const Layer& L = ctx->layers[static_cast<size_t>(layer)];
+    if (!L.finalized) {
+        return fail(LM_ENOTRES, "layer " + std::to_string(layer) + " is not finalized (lm_finalize_layer)");
+    }
+    *out_count = L.fp16_inexact;
     return LM_OK;
     LM_GUARD_END
 }

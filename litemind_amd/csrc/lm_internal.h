@@ -572,7 +572,7 @@ bool combine_norm_supported(int32_t hidden, int32_t hidden_p);
 // dst = fp16 panels of the BF16 matrix src [rows, cols] (cols % kPanel == 0);
 // counts values outside the fp16 range into *overflow.
 hipError_t launch_bf16_to_f16_panels(const uint16_t* src, _Float16* dst, int64_t rows, int64_t cols, int* overflow,
-                                     hipStream_t s);
+                                     unsigned long long* inexact, hipStream_t s);
 // x16 = fp16 panels of x [rows, cols], zero-padded to cols_p columns.
 hipError_t launch_to_f16_rows(const float* x, _Float16* x16, int64_t rows, int32_t cols, int32_t cols_p,
                               hipStream_t s);
