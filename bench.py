@@ -49,8 +49,8 @@ ROUTER_BYTES = 64 * 2048 * 4                # 524,288
 # known size (profiles/decode_fused_kernel_decode_t1_hbm_traffic.md and
 # profiles/mfma_grouped_kernel_prefill_t2048_skewed.md).
 MEASURED_TRAFFIC = {("decode_t1", "decode_fused_kernel"): 142_380_838,
-                    ("prefill_t2048_skewed", "gate_up"): 1_261_088_451,
-                    ("prefill_t2048_skewed", "down"): 708_908_194}
+                    ("prefill_t2048_skewed", "gate_up"): 1_261_440_220,
+                    ("prefill_t2048_skewed", "down"): 705_484_080}
 
 
 class ClockSampler:
