@@ -332,6 +332,15 @@ int lm_decode_speculation_test(lm_context* ctx, int32_t mode);
  * check that path without a stalled GPU; mode 0 (the default) restores the
  * normal bound. */
 int lm_decode_wait_test(lm_context* ctx, int32_t mode);
+/* No counterpart in LiteMind.  One token through a layer of more than 64
+ * experts (the multi-launch path: DeepSeek-V2's 160) runs the router and the
+ * gate/up projections as one launch that streams the experts of a fast,
+ * reassociated ranking while the exact logits are summed, and recomputes the
+ * activations when the exact set of experts differs.  Outputs are the same
+ * bits either way.  mode 1 (the default): that launch; 0: the router, then the
+ * gate/up launch; 2 (testing): that launch with the speculated set made wrong,
+ * so that the recomputation runs.  Not used under stream capture. */
+int lm_router_speculation(lm_context* ctx, int32_t mode);
 
 /* ---- timing: hipEvents on the context stream ---- */
 int lm_event_create(lm_context* ctx, void** out_event);

@@ -126,6 +126,7 @@ PROTOTYPES = {
     "lm_weight_resident": [_P, _P, _P],
     "lm_decode_speculation_test": [_P, _I32],
     "lm_decode_wait_test": [_P, _I32],
+    "lm_router_speculation": [_P, _I32],
     "lm_event_create": [_P, _P],
     "lm_event_destroy": [_P, _P],
     "lm_event_record": [_P, _P],
@@ -535,6 +536,12 @@ class Context:
 
     def stack_forward(self, first, last, hidden, tokens, path=PATH_AUTO) -> None:
         self._check(self.lib.lm_stack_forward(self.handle, first, last, _ptr(hidden), tokens, path))
+
+    def router_speculation(self, mode: int) -> None:
+        """lm_router_speculation: one token over more than 64 experts runs the
+        router and gate/up as one speculative launch (1, the default), the router
+        then gate/up (0), or the speculative launch with its repair forced (2)."""
+        self._check(self.lib.lm_router_speculation(self.handle, mode))
 
     def stack_graph_create(self, first, last, hidden, tokens, path=PATH_AUTO) -> int:
         """lm_stack_graph_create: the stack pass recorded as a HIP graph (a handle for

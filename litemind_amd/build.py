@@ -27,7 +27,7 @@ REFERENCE = os.environ.get("LITEMIND_REFERENCE", "/root/reference")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 HIP_SOURCES = ["k_router.hip", "k_permute.hip", "k_gemv.hip", "k_decode.hip", "k_mfma.hip",
-               "k_misc.hip", "k_head.hip", "k_attn.hip", "lm_capi.hip", "lm_attn.hip"]
+               "k_misc.hip", "k_head.hip", "k_attn.hip", "k_spec.hip", "lm_capi.hip", "lm_attn.hip"]
 # Host-only parts of the same library (no device code), compiled by g++.
 HOST_SOURCES = ["lm_checkpoint.cpp"]
 # -ffp-contract=off: every fused multiply-add in the kernels is written out

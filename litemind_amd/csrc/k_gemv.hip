@@ -12,6 +12,7 @@ namespace lm {
 namespace {
 
 using gemv::dot_rows;
+using gemv::dot_rows_stream;
 using gemv::fma8;
 using gemv::load_act;
 using gemv::load_rows;
@@ -107,55 +108,6 @@ __device__ inline void dot_rows_lds(const uint4 (&w)[R][ITERS], const float* lds
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// acc[r + R k] += W[r] . x[k] streaming the rows (no register cache; any width).
-template <int R, int NTB>
-__device__ inline void dot_rows_stream(const uint16_t* const (&rows)[R], const float* lds, int width, int lane,
-                                       float (&acc)[R * NTB]) {
-    // Four steps' loads are issued before their products (the same order of
-    // additions): one step at a time left a lane with R loads in flight, and a
-    // long row (the dense layer's down, width 10944) waited on every one.
-    constexpr int U = 4;
-    int c = lane * 8;
-    for (; c + (U - 1) * 512 < width; c += U * 512) {
-        uint4 wu[U][R];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                wu[u][r] = load_stream16(rows[r] + c + u * 512);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int k = 0; k < NTB; ++k) {
-                const float4 x0 = *reinterpret_cast<const float4*>(lds + k * width + c + u * 512);
-                const float4 x1 = *reinterpret_cast<const float4*>(lds + k * width + c + u * 512 + 4);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    fma8(acc[r + R * k], wu[u][r], x0, x1);
-                }
-            }
-        }
-    }
-    for (; c < width; c += 512) {
-        uint4 w[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            w[r] = load_stream16(rows[r] + c);
-        }
-#pragma unroll
-        for (int k = 0; k < NTB; ++k) {
-            const float4 x0 = *reinterpret_cast<const float4*>(lds + k * width + c);
-            const float4 x1 = *reinterpret_cast<const float4*>(lds + k * width + c + 4);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                fma8(acc[r + R * k], w[r], x0, x1);
-            }
-        }
     }
 }
 

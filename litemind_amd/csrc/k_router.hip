@@ -10,6 +10,7 @@
 // stored transposed ([H, E]) so the 64 lanes read one 256-byte row per step;
 // the token's activations are wave-uniform scalar loads.
 #include "lm_select.h"
+#include "router_chunks.h"
 
 namespace lm {
 namespace {
@@ -1002,135 +1003,17 @@ __global__ __launch_bounds__(kSplitThreads) void router_single_kernel(RouterArgs
     }
 }
 
-// Raw logits (bias not added) of experts [e0, e0 + 8) for token blockIdx.y,
-// for any hidden width: the gate rows in chunks of kChunkRows, each chunk's
-// rounded products formed by all threads into one of two LDS buffers while
-// lanes 0..7 of wave 0 add the previous chunk's products to their expert's
-// chain, strictly left to right over the whole row (LiteMind's dot,
-// src/Gemm.cpp:183-189), as router_single_kernel does for a row that fits LDS
-// whole.  For more than 64 experts, where the per-token router gives one wave
-// every expert of a token (a chain per expert, one after another).  Grid
-// (E / 8, T); hidden % 4 == 0, E % 8 == 0.
-constexpr int kChunkRows = 512;
+// Raw logits (bias not added) of experts [e0, e0 + 8) for token blockIdx.y
+// (chunked_logit).  Grid (E / 8, T); hidden % 4 == 0, E % 8 == 0.
+static_assert(kChunkExperts == kSplitExperts && kChunkThreads == kSplitThreads, "router chunk shape");
 __global__ __launch_bounds__(kSplitThreads) void router_chunked_kernel(RouterArgs a, const float* __restrict__ x,
                                                                         const float* __restrict__ wt) {
-    __shared__ float4 prod[2][kChunkRows / 4 * kSplitExperts];
-    const int tid = threadIdx.x;
-    const int H = a.hidden;
-    const int E = a.experts;
+    __shared__ float4 prod[kChunkFloat4s];
     const int e0 = blockIdx.x * kSplitExperts;
     const int64_t t = blockIdx.y;
-    const float* xt = x + t * H;
-    const int nchunks = (H + kChunkRows - 1) / kChunkRows;
-    constexpr int kPer = kChunkRows * (kSplitExperts / 4) / kSplitThreads;  // float4 loads per thread per chunk
-    float4 w[kPer];
-    float xv[kPer];
-    auto fetch = [&](int c) {
-        const int i0 = c * kChunkRows;
-        const int nf = (H - i0 < kChunkRows ? H - i0 : kChunkRows) * (kSplitExperts / 4);
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int f = j * kSplitThreads + tid;
-            const int fl = f < nf ? f : nf - 1;
-            const int i = i0 + (fl >> 1);
-            w[j] = *reinterpret_cast<const float4*>(wt + static_cast<int64_t>(i) * E + e0 + 4 * (fl & 1));
-            xv[j] = xt[i];
-        }
-    };
-    auto store = [&](int c) {
-        const int i0 = c * kChunkRows;
-        const int nf = (H - i0 < kChunkRows ? H - i0 : kChunkRows) * (kSplitExperts / 4);
-        float4* buf = prod[c & 1];
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int f = j * kSplitThreads + tid;
-            if (f < nf) {
-                const int i = f >> 1;  // row within the chunk
-                const int el = 4 * (f & 1);
-                float* base = reinterpret_cast<float*>(&buf[(i >> 2) * kSplitExperts]);
-                base[(el + 0) * 4 + (i & 3)] = w[j].x * xv[j];
-                base[(el + 1) * 4 + (i & 3)] = w[j].y * xv[j];
-                base[(el + 2) * 4 + (i & 3)] = w[j].z * xv[j];
-                base[(el + 3) * 4 + (i & 3)] = w[j].w * xv[j];
-            }
-        }
-    };
-    fetch(0);
-    store(0);
-    lds_barrier();
-    float acc = 0.0f;
-    for (int c = 0; c < nchunks; ++c) {
-        if (c + 1 < nchunks) {
-            fetch(c + 1);  // in flight while the chains run
-        }
-        if (tid < kSplitExperts) {
-            const float4* buf = prod[c & 1];
-            const int quads = (H - c * kChunkRows < kChunkRows ? H - c * kChunkRows : kChunkRows) / 4;
-            auto add8 = [&](const float4 (&p)[8]) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    acc = acc + p[u].x;
-                    acc = acc + p[u].y;
-                    acc = acc + p[u].z;
-                    acc = acc + p[u].w;
-                }
-            };
-            int q = 0;
-            if (quads == kChunkRows / 4) {
-                // a whole chunk fully unrolled, two register sets in turn: one
-                // batch's reads are in flight while the other batch is added,
-                // so the chain (a dependent add every ~3.5 ns) never waits for
-                // LDS (a loop over the batches costs register copies and a
-                // full wait per batch)
-                constexpr int kBatches = kChunkRows / 32;
-                float4 p[2][8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    p[0][u] = buf[u * kSplitExperts + tid];
-                }
-#pragma unroll
-                for (int b = 0; b < kBatches; ++b) {
-                    if (b + 1 < kBatches) {
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            p[(b + 1) & 1][u] = buf[(8 * (b + 1) + u) * kSplitExperts + tid];
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the adds
-                    add8(p[b & 1]);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                q = quads;
-            }
-            for (; q + 8 <= quads; q += 8) {  // eight reads in flight, then their adds in order
-                float4 p[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    p[u] = buf[(q + u) * kSplitExperts + tid];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    acc = acc + p[u].x;
-                    acc = acc + p[u].y;
-                    acc = acc + p[u].z;
-                    acc = acc + p[u].w;
-                }
-            }
-            for (; q < quads; ++q) {
-                const float4 p = buf[q * kSplitExperts + tid];
-                acc = acc + p.x;
-                acc = acc + p.y;
-                acc = acc + p.z;
-                acc = acc + p.w;
-            }
-        }
-        if (c + 1 < nchunks) {
-            store(c + 1);  // the other buffer: its last readers passed the previous barrier
-        }
-        lds_barrier();
-    }
-    if (tid < kSplitExperts) {
-        a.logits_scratch[t * E + e0 + tid] = acc;
+    const float acc = chunked_logit(a.hidden, a.experts, x + t * a.hidden, wt, e0, prod);
+    if (threadIdx.x < kSplitExperts) {
+        a.logits_scratch[t * a.experts + e0 + threadIdx.x] = acc;
     }
 }
 

@@ -100,6 +100,7 @@ struct Workspace {
     float* logit_scratch = nullptr;  // [kRouterSplitTokens, E] router hand-off of the few-token launches
     uint32_t* decode_sync = nullptr;  // single-launch decode counters (zeroed once) + error word
     float* decode_part = nullptr;     // single-launch decode: the shared items' partial down projections
+    uint32_t* spec_sync = nullptr;   // speculative router + gate/up launches: counters, tags, partial logits (zeroed once)
     uint32_t* ticket = nullptr;      // single-token router arrival counter (kept at 0 between launches)
     int32_t* permute_scratch = nullptr;  // segment counts and arrival ticket of the permutation
 };
@@ -183,6 +184,9 @@ struct lm_context {
     int32_t decode_parity = 0;   // alternates between single-launch decodes
     uint32_t decode_seq = 0;     // tag of the single-launch decode's hand-off words (never 0 in a launch)
     int32_t decode_perturb = 0;  // testing: force the speculative selection to disagree
+    int32_t spec_mode = 1;       // one token over more than 64 experts: 0 router then gate/up, 1 speculative launch, 2 its repair forced
+    int32_t spec_parity = 0;     // alternates between speculative launches
+    uint32_t spec_seq = 0;       // tag of the last speculative launch
     uint32_t decode_max_spins = 0;  // testing: polls before a wait gives up (0: the kernel's default)
     bool decode_pending = false; // a single-launch decode ran since the last error check
     void* gemm_w = nullptr;      // per-call upload of a matrix that is not resident
@@ -493,7 +497,9 @@ lm::ExpertArgs expert_args(lm_context* ctx, const Layer& L, const float* x, cons
 
 // Gate/up then down of every group into ws.down_out (one row per slot, then
 // the shared rows), with stage marks 2 and 3 before each launch.
-int launch_expert_kernels(lm_context* ctx, const Layer& L, const lm::ExpertArgs& ea, int64_t T, bool mfma) {
+// gateup_done: the speculative launch already wrote the activations.
+int launch_expert_kernels(lm_context* ctx, const Layer& L, const lm::ExpertArgs& ea, int64_t T, bool mfma,
+                          bool gateup_done = false) {
     const int64_t max_active = L.dense ? 0 : std::min<int64_t>(ctx->E, T * ctx->K);
     stage_mark(ctx, 2);
     if (mfma) {
@@ -501,7 +507,9 @@ int launch_expert_kernels(lm_context* ctx, const Layer& L, const lm::ExpertArgs&
         stage_mark(ctx, 3);
         LM_HIP(lm::launch_mfma_down(ea, ctx->stream));
     } else {
-        LM_HIP(lm::launch_gemv_gateup(ea, max_active, ctx->stream));
+        if (!gateup_done) {
+            LM_HIP(lm::launch_gemv_gateup(ea, max_active, ctx->stream));
+        }
         stage_mark(ctx, 3);
         LM_HIP(lm::launch_gemv_down(ea, max_active, ctx->stream));
     }
@@ -512,9 +520,10 @@ int launch_expert_kernels(lm_context* ctx, const Layer& L, const lm::ExpertArgs&
 // next_norm: the next stack layer's RMSNorm weight; the combine then also
 // writes that layer's input (ws.xnorm, and ws.x16 when the MFMA path follows).
 int run_experts(lm_context* ctx, Layer& L, const float* x, const _Float16* x16, int64_t T, const lm::RouteBufs& rb,
-                float* y, const float* residual, bool mfma, const float* next_norm = nullptr) {
+                float* y, const float* residual, bool mfma, const float* next_norm = nullptr,
+                bool gateup_done = false) {
     const lm::ExpertArgs ea = expert_args(ctx, L, x, x16, T, rb);
-    const int rc = launch_expert_kernels(ctx, L, ea, T, mfma);
+    const int rc = launch_expert_kernels(ctx, L, ea, T, mfma, gateup_done);
     if (rc != LM_OK) {
         return rc;
     }
@@ -572,11 +581,19 @@ struct DecodeScratch {
 
 // The context's own decode scratch (the workspace; the hand-off words are
 // allocated and zeroed on first use).
-int context_decode_scratch(lm_context* ctx, DecodeScratch* out) {
+int ensure_decode_sync(lm_context* ctx) {
     if (ctx->ws.decode_sync == nullptr) {
         const size_t bytes = sizeof(uint32_t) * lm::kDecodeSyncWords;
         LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.decode_sync), bytes));
         LM_HIP(hipMemsetAsync(ctx->ws.decode_sync, 0, bytes, ctx->stream));
+    }
+    return LM_OK;
+}
+
+int context_decode_scratch(lm_context* ctx, DecodeScratch* out) {
+    const int rc = ensure_decode_sync(ctx);
+    if (rc != LM_OK) {
+        return rc;
     }
     if (ctx->ws.decode_part == nullptr) {
         const size_t floats = static_cast<size_t>(lm::decode_shared_part_floats(ctx->H, ctx->Sp));
@@ -636,6 +653,44 @@ int decode_layer(lm_context* ctx, Layer& L, const DecodeScratch& sc, const float
     stage_mark(ctx, 4);
     stage_mark(ctx, 5);
     return stage_finish(ctx);
+}
+
+// One token over more than 64 experts on the GEMV path: the router and the
+// gate/up projections in one launch that starts the routed experts from a
+// speculative selection (lm::launch_spec_gateup), unless it is off
+// (lm_router_speculation), the shape is outside it, or the stream is being
+// captured (its hand-off words carry a tag the host advances per launch, which
+// a replay would repeat).  Sets *speculated when it launched.
+int spec_router_gateup(lm_context* ctx, Layer& L, const lm::RouterArgs& ra, int64_t T, bool mfma, bool* speculated) {
+    *speculated = false;
+    if (T != 1 || mfma || ctx->spec_mode == 0 || ra.x16 != nullptr || ra.rb.counts == nullptr ||
+        !lm::spec_gateup_supported(ctx->E, ctx->H, ctx->K, ctx->cfg.n_group, ctx->cfg.group_limited, ctx->Ip,
+                                   L.shared_present ? ctx->Sp : 0)) {
+        return LM_OK;
+    }
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    LM_HIP(hipStreamIsCapturing(ctx->stream, &capture));
+    if (capture != hipStreamCaptureStatusNone) {
+        return LM_OK;
+    }
+    int rc = ensure_decode_sync(ctx);  // its error word
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (ctx->ws.spec_sync == nullptr) {
+        const size_t bytes = sizeof(uint32_t) * lm::kSpecSyncWords;
+        LM_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->ws.spec_sync), bytes));
+        LM_HIP(hipMemsetAsync(ctx->ws.spec_sync, 0, bytes, ctx->stream));
+    }
+    const lm::ExpertArgs ea = expert_args(ctx, L, ra.x, nullptr, 1, ra.rb);
+    ctx->spec_seq = ctx->spec_seq == 0xffffffffu ? 1u : ctx->spec_seq + 1u;
+    LM_HIP(lm::launch_spec_gateup(ra, ea, ctx->ws.spec_sync, ctx->ws.decode_sync + lm::kDecodeErrorWord,
+                                  ctx->spec_parity, ctx->spec_seq, ctx->spec_mode == 2 ? 1 : 0,
+                                  ctx->decode_max_spins, ctx->stream));
+    ctx->spec_parity ^= 1;
+    ctx->decode_pending = true;
+    *speculated = true;
+    return LM_OK;
 }
 
 // norm: when set, x is the hidden state and the block's input is rms_norm(x, norm).
@@ -711,7 +766,16 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
     ra.rb = route_bufs(ctx, idx, wts);
     stage_mark(ctx, 0);
     bool permuted = false;
-    LM_HIP(lm::launch_router(ra, ctx->stream, &permuted));
+    bool speculated = false;
+    rc = spec_router_gateup(ctx, L, ra, T, mfma, &speculated);
+    if (rc != LM_OK) {
+        return rc;
+    }
+    if (speculated) {
+        permuted = true;
+    } else {
+        LM_HIP(lm::launch_router(ra, ctx->stream, &permuted));
+    }
     stage_mark(ctx, 1);
 
     lm::PermuteArgs pa{};
@@ -725,7 +789,7 @@ int moe_layer(lm_context* ctx, int32_t layer, const float* x, int64_t T, float* 
         LM_HIP(lm::launch_permute(pa, ctx->stream));
     }
 
-    rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma, next_norm);
+    rc = run_experts(ctx, L, x, ctx->ws.x16, T, pa.rb, y, residual, mfma, next_norm, speculated);
     if (rc != LM_OK) {
         return rc;
     }
@@ -1081,6 +1145,7 @@ int lm_context_destroy(lm_context* ctx) {
     (void)hipFree(ctx->d_inexact);
     (void)hipFree(w.decode_sync);
     (void)hipFree(w.decode_part);
+    (void)hipFree(w.spec_sync);
     lm::attention_release(ctx->attention);
     ctx->attention = nullptr;
     if (ctx->staging != nullptr) {
@@ -2053,6 +2118,17 @@ int lm_decode_speculation_test(lm_context* ctx, int32_t mode) {
         return fail(LM_EINVAL, "null context");
     }
     ctx->decode_perturb = mode != 0 ? 1 : 0;
+    return LM_OK;
+}
+
+int lm_router_speculation(lm_context* ctx, int32_t mode) {
+    if (ctx == nullptr) {
+        return fail(LM_EINVAL, "null context");
+    }
+    if (mode < 0 || mode > 2) {
+        return fail(LM_EINVAL, "lm_router_speculation: mode must be 0, 1 or 2");
+    }
+    ctx->spec_mode = mode;
     return LM_OK;
 }
 

@@ -219,6 +219,24 @@ constexpr int kDecodeMaskWord = kDecodeSpecWord + 2 * kMaxTopK;
 constexpr int kDecodeXcdSpecWord = (kDecodeMaskWord + 16 + 31) / 32 * 32;
 constexpr int kDecodeXcdSlotWords = 32;
 constexpr int kDecodeSyncWords = kDecodeXcdSpecWord + 8 * kDecodeXcdSlotWords;
+// One token over more than 64 experts on the GEMV path (k_spec.hip): the
+// router (selection and permutation into r's outputs) and the gate/up
+// projections of the selected and the shared experts into e.act, in one
+// launch that starts the routed experts from a speculative selection.  The
+// down and combine launches follow as on the multi-launch path.  spec_sync:
+// kSpecSyncWords words, zeroed once (counters of the two launch parities,
+// tagged hand-off words, partial logits); error: a word that a bounded wait
+// which gave up sets; parity alternates and seq (nonzero) differs between
+// consecutive launches on spec_sync.  perturb (testing) makes the speculated
+// set of experts wrong, so the repair runs.
+constexpr int kSpecCounterWords = 2 * 3 * 16 * 16;
+constexpr int kSpecTagWord = kSpecCounterWords;
+constexpr int kSpecPartialWord = kSpecTagWord + 64;
+constexpr int kSpecSyncWords = kSpecPartialWord + 16 * kMaxExpertsWide;
+bool spec_gateup_supported(int experts, int hidden, int top_k, int n_group, int group_limited, int inter_p,
+                           int shared_inter_p);
+hipError_t launch_spec_gateup(const RouterArgs& r, const ExpertArgs& e, uint32_t* spec_sync, uint32_t* error,
+                              int parity, uint32_t seq, int perturb, uint32_t max_spins, hipStream_t s);
 hipError_t launch_permute(const PermuteArgs& a, hipStream_t s);
 // LM head (k_head.hip): logits [tokens, rows] = w [rows, in_dim] . x [tokens, in_dim]
 // with gemm::dot_bf16's association, tokens <= kHeadTokens, in_dim % 8 == 0; and

@@ -211,3 +211,67 @@ def test_wide_layer(wide_ctx, T, path):
         assert mean_rel < 1e-5
     for b in (dx, y, idx, w):
         b.free()
+
+
+# One token over more than 64 experts: the router and gate/up in one
+# speculative launch (lm_router_speculation 1, the default), with its repair
+# forced (2), and the router then gate/up as separate launches (0).
+# (E, k, grouped, n_group, topk_group, hidden, inter, bias)
+SPEC_CASES = {
+    "e160_g8": (160, 6, True, 8, 3, 1024, 256, False),
+    "e160_g8_bias": (160, 6, True, 8, 3, 1024, 256, True),
+    "e72_greedy_h2048": (72, 6, False, 1, 1, 2048, 128, False),
+    "e256_g8_k8": (256, 8, True, 8, 4, 512, 128, False),
+    "e512_greedy_k8": (512, 8, False, 1, 1, 256, 64, False),
+    "e100_h1040_ragged": (100, 5, True, 4, 2, 1040, 192, True),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SPEC_CASES))
+def test_speculative_router_gateup(name):
+    """The three modes give the same bits (logits, experts, weights, layer
+    output) on several tokens, and match the oracle: logits, experts and
+    weights bit-exact, the output within 1e-5 (the fp32 GEMV path).  The
+    ragged case has a last row slice of 16 rows and a logit bias."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    E, k, grouped, ng, tg, hidden, inter, with_bias = SPEC_CASES[name]
+    dims = _dims(E, k, grouped, ng, tg, hidden=hidden, inter=inter)
+    layer = wl.moe_layer(wl.MASTER_SEED + 2300 + E, 0, dims)
+    rng = np.random.default_rng(E + hidden)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32) if with_bias else None
+    announce(f"speculative router + gate/up, {name}")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        wl.upload_moe_layer(ctx, 0, layer)
+        db = ctx.to_device(bias) if with_bias else None
+        for t in range(3):
+            x = wl.tokens(wl.MASTER_SEED + 2400 + t, 1, hidden)
+            dx = ctx.to_device(x)
+            outs = {}
+            for mode in (1, 2, 0, 1):
+                ctx.router_speculation(mode)
+                y, idx, w, lg = ctx.empty((1, hidden)), ctx.empty((1, k), np.int32), ctx.empty((1, k)), \
+                    ctx.empty((1, E))
+                ctx.moe_forward(0, dx, 1, y, bias=db, idx=idx, w=w, logits=lg)
+                ctx.synchronize()
+                got = (y.download(), idx.download(), w.download(), lg.download())
+                if mode in outs:
+                    ref = outs[mode]
+                    assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(got, ref))
+                outs[mode] = got
+                for bb in (y, idx, w, lg):
+                    bb.free()
+            for mode in (1, 2):
+                assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(outs[mode], outs[0]))
+            ctx.router_speculation(1)
+            oy, oidx, ow, ologits = ol.oracle_moe_layer(layer, x, bias)
+            gy, gidx, gw, glg = outs[1]
+            assert np.array_equal(glg.view(np.uint32), np.asarray(ologits, np.float32).reshape(1, E).view(np.uint32))
+            assert np.array_equal(gidx, oidx)
+            assert np.array_equal(gw.view(np.uint32), ow.view(np.uint32))
+            _, mean_rel = layer_error(gy, oy)
+            assert mean_rel < 1e-5
+            dx.free()
+        with pytest.raises(RuntimeError):
+            ctx.router_speculation(3)
