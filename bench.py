@@ -621,10 +621,10 @@ def run_v2_decode(steps: int, warmup: int, rotate: int) -> dict:
     weights scaled by 16) at T = 1, `rotate` independently seeded layers
     resident (15.1 GB each with the fp16 shadow) and rotated per step.  Its
     shape is outside the single-token kernel's (more than 64 experts, hidden
-    above 4096), so LM_PATH_AUTO runs the multi-launch path: the router for
-    more than 64 experts with MoeRouter's group mask, the permutation, the
-    GEMV experts and the combine.  Per-stage times from a second pass with
-    events between the stages."""
+    above 4096), so LM_PATH_AUTO runs the router (MoeRouter's group mask) and
+    the gate/up projections as one speculative launch, then the GEMV down
+    launch and the combine.  Per-stage times from a second pass with events
+    between the stages (the speculative launch counts as the router stage)."""
     from litemind_amd import Context
     from litemind_amd import workload as wl
 
