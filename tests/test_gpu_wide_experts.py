@@ -275,3 +275,54 @@ def test_speculative_router_gateup(name):
             dx.free()
         with pytest.raises(RuntimeError):
             ctx.router_speculation(3)
+
+
+def test_speculative_stack_t1_and_graph():
+    """Two 160-expert layers as a stack at one token: the eager pass (the
+    speculative launch per layer) matches the oracle's chain within 1e-5 and
+    gives the same bits as the separate launches (lm_router_speculation 0) and
+    as three replays of a captured graph of the pass, which records the
+    separate launches (the speculative launch is not used under capture)."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = _dims()
+    layers = [("moe", wl.moe_layer(wl.MASTER_SEED + 2500 + l, 0, dims)) for l in range(2)]
+    rng = np.random.default_rng(2501)
+    norms = [(1.0 + 0.1 * rng.standard_normal(dims.hidden)).astype(np.float32) for _ in range(2)]
+    announce("160-expert stack at T=1: eager, separate launches, graph replays")
+    with Context(dims.moe_config(num_layers=2)) as ctx:
+        for l, (_, layer) in enumerate(layers):
+            wl.upload_moe_layer(ctx, l, layer)
+            ctx.upload_norm(l, norms[l])
+        h0 = wl.tokens(wl.MASTER_SEED + 2502, 1, dims.hidden)
+
+        def run(mode):
+            ctx.router_speculation(mode)
+            dh = ctx.to_device(h0)
+            ctx.stack_forward(0, 1, dh, 1)
+            ctx.synchronize()
+            out = dh.download()
+            dh.free()
+            return out
+
+        eager = run(1)
+        separate = run(0)
+        ctx.router_speculation(1)
+        assert np.array_equal(eager.view(np.uint32), separate.view(np.uint32))
+        oh = ol.oracle_stack(layers, h0, dims.rms_norm_eps, norms=norms)
+        _, mean_rel = layer_error(eager, oh)
+        assert mean_rel < 1e-5
+        dh = ctx.to_device(h0)
+        graph = ctx.stack_graph_create(0, 1, dh, 1)
+        try:
+            for rep in range(3):
+                dh.upload(h0)
+                ctx.synchronize()
+                ctx.stack_graph_launch(graph)
+                ctx.synchronize()
+                assert np.array_equal(dh.download().view(np.uint32), eager.view(np.uint32)), f"replay {rep}"
+                assert np.array_equal(run(1).view(np.uint32), eager.view(np.uint32))
+        finally:
+            ctx.stack_graph_destroy(graph)
+            dh.free()
