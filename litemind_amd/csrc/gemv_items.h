@@ -112,13 +112,12 @@ __device__ inline void dot_rows(const uint4 (&w)[R][ITERS], const float4 (&x)[NT
 }
 
 // acc[r + R k] += W[r] . x[k] streaming the rows (no register cache; any width).
-template <int R, int NTB>
+// U steps' loads are issued before their products (the same order of
+// additions): one step at a time left a lane with R loads in flight, and a
+// long row (the dense layer's down, width 10944) waited on every one.
+template <int R, int NTB, int U = 4>
 __device__ inline void dot_rows_stream(const uint16_t* const (&rows)[R], const float* lds, int width, int lane,
                                        float (&acc)[R * NTB]) {
-    // Four steps' loads are issued before their products (the same order of
-    // additions): one step at a time left a lane with R loads in flight, and a
-    // long row (the dense layer's down, width 10944) waited on every one.
-    constexpr int U = 4;
     int c = lane * 8;
     for (; c + (U - 1) * 512 < width; c += U * 512) {
         uint4 wu[U][R];

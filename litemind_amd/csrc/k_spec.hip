@@ -160,7 +160,9 @@ __device__ inline void gateup_item(const ExpertArgs& a, const uint16_t* gu, int 
     for (int i = 0; i < R; ++i) {
         acc[i] = 0.0f;
     }
-    dot_rows_stream<R, 1>(rows, xs, a.hidden, lane, acc);
+    // five steps per batch: DeepSeek-V2's ten 512-column steps in two round
+    // trips instead of four (4 + 4 + 1 + 1); 75.5 against 76.3 us per layer
+    dot_rows_stream<R, 1, 5>(rows, xs, a.hidden, lane, acc);
     const float sum = transpose_reduce<R>(acc, lane);
     constexpr int L = log2c<R>();
     const int vi = lane >> (6 - L);
