@@ -326,3 +326,42 @@ def test_speculative_stack_t1_and_graph():
         finally:
             ctx.stack_graph_destroy(graph)
             dh.free()
+
+
+def test_speculative_wait_timeout_reports_kernel_error(wide_ctx):
+    """Every hand-off wait of the speculative launch made to give up after its
+    first poll (a bound the host sets; every wave still runs to its end and
+    every index stays clamped): the next lm_synchronize returns LM_EKERNEL,
+    and the context then computes exact results again."""
+    from litemind_amd import LmError
+    from litemind_amd import workload as wl
+
+    ctx, layer = wide_ctx
+    H = layer.dims.hidden
+    x = wl.tokens(wl.MASTER_SEED + 2600, 1, H)
+    dx, y = ctx.to_device(x), ctx.empty((1, H))
+    idx, w = ctx.empty((1, 6), np.int32), ctx.empty((1, 6))
+    announce("160-expert speculative launch with every wait giving up at once")
+    reported = 0
+    ctx._check(ctx.lib.lm_decode_wait_test(ctx.handle, 1))
+    try:
+        for _ in range(4):
+            ctx.moe_forward(0, dx, 1, y, idx=idx, w=w)
+            try:
+                ctx.synchronize()
+            except LmError as error:
+                assert "status -5" in str(error)
+                reported += 1
+    finally:
+        ctx._check(ctx.lib.lm_decode_wait_test(ctx.handle, 0))
+    assert reported >= 1
+    ctx.synchronize()
+    ctx.moe_forward(0, dx, 1, y, idx=idx, w=w)
+    ctx.synchronize()
+    oy, oidx, ow, _ = ol.oracle_moe_layer(layer, x)
+    assert np.array_equal(idx.download(), oidx)
+    assert np.array_equal(w.download().view(np.uint32), ow.view(np.uint32))
+    _, mean_rel = layer_error(y.download(), oy)
+    assert mean_rel < 1e-5
+    for b in (dx, y, idx, w):
+        b.free()
