@@ -615,7 +615,7 @@ def run_head(steps: int, warmup: int) -> dict:
             "peak": HBM_PEAK_GBS, "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
 
 
-def run_v2_decode(steps: int, warmup: int, rotate: int) -> dict:
+def run_v2_decode(steps: int, warmup: int, rotate: int, prefill: bool = True) -> dict:
     """DeepSeek-V2's full MoE layer (hidden 5120, 160 routed experts in 8
     groups of which 3 are kept, top-6, two shared experts of 1536, routed
     weights scaled by 16) at T = 1, `rotate` independently seeded layers
@@ -659,6 +659,15 @@ def run_v2_decode(steps: int, warmup: int, rotate: int) -> dict:
     stages = {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in ctx.stage_times().items()}
     ctx.stage_timing(False)
     idx = didx.download()
+    H, I, S, E = dims.hidden, dims.inter, dims.shared_inter, dims.experts
+    by = 6 * 3 * I * H * 2 + 3 * S * H * 2 + E * H * 4 + H * 8
+    gbs = by / (us * 1e-6) / 1e9
+    out = {"us": round(us, 2), "tokens_per_s": round(1e6 / us, 1), "stage_us": stages,
+           "algorithmic_bytes": by, "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS,
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "experts_per_step": [sorted(map(int, r)) for r in idx]}
+    if not prefill:
+        ctx.close()
+        return out
     # a prefill batch of 2048 tokens on layer 0 (MFMA experts): stage times
     T = 2048
     dxp = ctx.to_device(wl.tokens(wl.MASTER_SEED + 302, T, dims.hidden))
@@ -678,13 +687,8 @@ def run_v2_decode(steps: int, warmup: int, rotate: int) -> dict:
     stages_p = {k: round(v[0] * 1e3 / v[1], 2) if v[1] else None for k, v in ctx.stage_times().items()}
     ctx.stage_timing(False)
     ctx.close()
-    H, I, S, E = dims.hidden, dims.inter, dims.shared_inter, dims.experts
-    by = 6 * 3 * I * H * 2 + 3 * S * H * 2 + E * H * 4 + H * 8
-    gbs = by / (us * 1e-6) / 1e9
-    return {"us": round(us, 2), "tokens_per_s": round(1e6 / us, 1), "stage_us": stages,
-            "algorithmic_bytes": by, "achieved": round(gbs, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS,
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "experts_per_step": [sorted(map(int, r)) for r in idx],
-            "t2048": {"us": round(us_p, 2), "tokens_per_s": round(T / (us_p * 1e-6), 1), "stage_us": stages_p}}
+    out["t2048"] = {"us": round(us_p, 2), "tokens_per_s": round(T / (us_p * 1e-6), 1), "stage_us": stages_p}
+    return out
 
 
 def main() -> int:
@@ -698,6 +702,8 @@ def main() -> int:
     ap.add_argument("--path", type=int, default=0, help="0 auto, 1 GEMV, 2 MFMA")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-v2", action="store_true",
+                    help="skip the default run's DeepSeek-V2 T=1 leg (160 experts: the speculative launch)")
     args = ap.parse_args()
     if args.workload == "stack":
         if args.gpus != 1:
@@ -864,6 +870,19 @@ def main() -> int:
                                what=f"{args.second}: distinct rows of the workload's {w2.tokens} tokens")
             if cb2 is not None:
                 line["t2048" if w2.tokens == 2048 else args.second]["cpu_baseline"] = cb2
+    if not args.no_v2 and args.workload == "decode_t1":
+        # DeepSeek-V2's MoE layer (160 experts in 8 groups, hidden 5120) at T = 1:
+        # more experts than the single-token kernel's lanes, so the router and
+        # gate/up run as one speculative launch, then down and the combine
+        log("decode_t1_v2 leg: DeepSeek-V2 layers at T=1 (4 rotated)")
+        v2 = run_v2_decode(args.steps, args.warmup, 4, prefill=False)
+        line["deepseek_v2_t1"] = {
+            "workload": "decode_t1_v2", "tokens": 1, "hidden": 5120, "experts": 160, "top_k": 6, "n_group": 8,
+            "topk_group": 3, "layers_rotated": 4, "us": v2["us"], "value": v2["tokens_per_s"],
+            "unit": "tokens/s", "steps": args.steps,
+            "roofline": {"bound": "hbm", "achieved": v2["achieved"], "peak": v2["peak"], "unit": "GB/s",
+                         "frac": v2["frac"], "algorithmic_bytes": v2["algorithmic_bytes"]},
+            "stage_us": v2["stage_us"]}
     print(json.dumps(line), flush=True)
     return 0
 
