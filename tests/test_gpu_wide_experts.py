@@ -224,6 +224,7 @@ SPEC_CASES = {
     "e256_g8_k8": (256, 8, True, 8, 4, 512, 128, False),
     "e512_greedy_k8": (512, 8, False, 1, 1, 256, 64, False),
     "e100_h1040_ragged": (100, 5, True, 4, 2, 1040, 192, True),
+    "e256_h7168_k8": (256, 8, True, 8, 4, 7168, 64, False),
 }
 
 
@@ -232,7 +233,9 @@ def test_speculative_router_gateup(name):
     """The three modes give the same bits (logits, experts, weights, layer
     output) on several tokens, and match the oracle: logits, experts and
     weights bit-exact, the output within 1e-5 (the fp32 GEMV path).  The
-    ragged case has a last row slice of 16 rows and a logit bias."""
+    ragged case has a last row slice of 16 rows and a logit bias; the widest
+    has DeepSeek-V3's routing and hidden size (256 experts, top-8, 7168: seven
+    row slices, rows of fourteen 512-column steps)."""
     from litemind_amd import Context
     from litemind_amd import workload as wl
 
