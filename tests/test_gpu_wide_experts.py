@@ -368,3 +368,38 @@ def test_speculative_wait_timeout_reports_kernel_error(wide_ctx):
     assert mean_rel < 1e-5
     for b in (dx, y, idx, w):
         b.free()
+
+
+@pytest.mark.parametrize("grouped", [True, False])
+def test_speculative_router_all_ties(grouped):
+    """Every expert's gate row the same: all logits tie exactly, in the exact
+    chains and in the reassociated sums alike, so MoeRouter::select's lower
+    index rule alone decides (the lowest groups, then the lowest experts).
+    The speculative launch and the separate launches give the oracle's
+    experts, weights and output."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    dims = _dims(160, 6, grouped, 8 if grouped else 1, 3 if grouped else 1, hidden=1024, inter=128)
+    layer = wl.moe_layer(wl.MASTER_SEED + 2700, 0, dims)
+    layer.router[:] = layer.router[0]
+    announce(f"160-expert layer with tied logits, grouped={grouped}")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        wl.upload_moe_layer(ctx, 0, layer)
+        x = wl.tokens(wl.MASTER_SEED + 2701, 1, dims.hidden)
+        oy, oidx, ow, _ = ol.oracle_moe_layer(layer, x)
+        assert list(oidx[0]) == list(range(6))
+        dx = ctx.to_device(x)
+        for mode in (1, 0):
+            ctx.router_speculation(mode)
+            y, idx, w = ctx.empty((1, dims.hidden)), ctx.empty((1, 6), np.int32), ctx.empty((1, 6))
+            ctx.moe_forward(0, dx, 1, y, idx=idx, w=w)
+            ctx.synchronize()
+            assert np.array_equal(idx.download(), oidx)
+            assert np.array_equal(w.download().view(np.uint32), ow.view(np.uint32))
+            _, mean_rel = layer_error(y.download(), oy)
+            assert mean_rel < 1e-5
+            for b in (y, idx, w):
+                b.free()
+        ctx.router_speculation(1)
+        dx.free()
