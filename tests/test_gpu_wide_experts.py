@@ -403,3 +403,54 @@ def test_speculative_router_all_ties(grouped):
                 b.free()
         ctx.router_speculation(1)
         dx.free()
+
+
+@pytest.mark.parametrize("grouped", [True, False])
+def test_speculative_router_real_misprediction(grouped):
+    """A gate whose exact and reassociated logits order two experts
+    differently at the top-k boundary.  Expert 6's products are 1e8, 1 and
+    -1e8 in rows 0, 4 and 8: LiteMind's left-to-right sum loses the 1
+    (1e8 + 1 rounds to 1e8), so its logit is 0; the partial-sum workgroups add
+    the row quads in a tree, (1e8 + -1e8) + 1 = 1.  Expert 5's logit is 0.5
+    either way and experts 0-4 lead with 10..6, so the speculation takes
+    expert 6 and the exact selection expert 5: the repair runs without the
+    testing switch, and the outputs still match the oracle."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    E, H = 160, 1024
+    dims = _dims(E, 6, grouped, 8 if grouped else 1, 3 if grouped else 1, hidden=H, inter=128)
+    layer = wl.moe_layer(wl.MASTER_SEED + 2800, 0, dims)
+    gate = np.zeros((E, H), np.float32)
+    gate[:, 12] = -5.0
+    for e, v in enumerate((10.0, 9.0, 8.0, 7.0, 6.0)):
+        gate[e, 12] = v
+    gate[5, 12] = 0.5
+    gate[6, 12] = 0.0
+    gate[6, 0], gate[6, 4], gate[6, 8] = 1e8, 1.0, -1e8
+    layer.router[:] = gate
+    x = np.zeros((1, H), np.float32)
+    x[0, [0, 4, 8, 12]] = 1.0
+    announce(f"160-expert layer whose speculation is wrong, grouped={grouped}")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        wl.upload_moe_layer(ctx, 0, layer)
+        oy, oidx, ow, ologits = ol.oracle_moe_layer(layer, x)
+        assert ologits[0, 6] == 0.0 and 5 in oidx[0] and 6 not in oidx[0]
+        dx = ctx.to_device(x)
+        outs = []
+        for mode in (1, 0):
+            ctx.router_speculation(mode)
+            y, idx, w = ctx.empty((1, H)), ctx.empty((1, 6), np.int32), ctx.empty((1, 6))
+            ctx.moe_forward(0, dx, 1, y, idx=idx, w=w)
+            ctx.synchronize()
+            got = (y.download(), idx.download(), w.download())
+            assert np.array_equal(got[1], oidx)
+            assert np.array_equal(got[2].view(np.uint32), ow.view(np.uint32))
+            _, mean_rel = layer_error(got[0], oy)
+            assert mean_rel < 1e-5
+            outs.append(got)
+            for b in (y, idx, w):
+                b.free()
+        assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+        ctx.router_speculation(1)
+        dx.free()
