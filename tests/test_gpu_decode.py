@@ -133,3 +133,35 @@ def test_decode_wait_timeout_reports_kernel_error(v2_ctx):
     _check(out, layers[0], x)
     for b in (dx, y, idx, w):
         b.free()
+
+
+def test_decode_real_misprediction(v2_layer):
+    """The single-token kernel's speculation wrong without the testing switch:
+    a gate whose expert 6 has products 1e8, 1 and -1e8 in rows 0, 4 and 8.
+    LiteMind's left-to-right chain loses the 1 (its logit is 0); the
+    approximate logit, each lane adding its row quads and the wave's butterfly
+    adding the lanes, keeps it (1).  Expert 5 sits at 0.5 and experts 0-4 lead,
+    so rank 5 is speculated as expert 6 and is expert 5 exactly: the down
+    workgroups recompute it, and the outputs match the oracle."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    E, H = 64, 2048
+    gate = np.zeros((E, H), np.float32)
+    gate[:, 12] = -5.0
+    for e, v in enumerate((10.0, 9.0, 8.0, 7.0, 6.0)):
+        gate[e, 12] = v
+    gate[5, 12] = 0.5
+    gate[6, 12] = 0.0
+    gate[6, 0], gate[6, 4], gate[6, 8] = 1e8, 1.0, -1e8
+    layer = wl.MoeLayer(v2_layer.dims, gate, v2_layer.gate, v2_layer.up, v2_layer.down, v2_layer.shared_gate,
+                        v2_layer.shared_up, v2_layer.shared_down)
+    x = np.zeros((1, H), np.float32)
+    x[0, [0, 4, 8, 12]] = 1.0
+    announce("decode V2-Lite with a speculation the exact selection overturns")
+    with Context(wl.V2_LITE.moe_config(num_layers=1)) as ctx:
+        wl.upload_moe_layer(ctx, 0, layer)
+        out = _one_token_calls(ctx, 0, x)
+    oy, oidx, ow, olg = ol.oracle_moe_layer(layer, x)
+    assert olg[0, 6] == 0.0 and oidx[0, 5] == 5
+    _check(out, layer, x)
