@@ -310,3 +310,52 @@ def test_stack_graph_lifetime(stack_ctx):
         ctx.stack_graph_destroy(graph)
         dh.free()
     assert lm.LM_OK == 0
+
+
+def test_stack_t1_real_misprediction(stack_ctx):
+    """With the norm fused, the single-token kernel speculates from the
+    unnormalised products, each thread adding its elements and the wave's
+    butterfly adding the threads.  A layer whose expert 6 has products 1e8, 1
+    and -1e8 in rows 0, 1 and 2 (threads 0, 1 and 2 of wave 0) keeps the 1
+    there (the butterfly adds threads 0 and 2 first) and loses it in LiteMind's
+    left-to-right chain over the normalised token (logit 0).  Expert 5 sits at
+    0.5 and experts 0-4 lead, so rank 5 is speculated as expert 6 and is expert
+    5 exactly; the pass still matches the oracle."""
+    from litemind_amd import Context
+    from litemind_amd import workload as wl
+
+    _, layers, dims = stack_ctx
+    base = layers[1][1]
+    E, H = dims.experts, dims.hidden
+    gate = np.zeros((E, H), np.float32)
+    gate[:, 12] = -5.0
+    for e, v in enumerate((10.0, 9.0, 8.0, 7.0, 6.0)):
+        gate[e, 12] = v
+    gate[5, 12] = 0.5
+    gate[6, 12] = 0.0
+    gate[6, 0], gate[6, 1], gate[6, 2] = 1e8, 1.0, -1e8
+    layer = wl.MoeLayer(base.dims, gate, base.gate, base.up, base.down, base.shared_gate, base.shared_up,
+                        base.shared_down)
+    h0 = np.zeros((1, H), np.float32)
+    h0[0, [0, 1, 2, 12]] = 1.0
+    # the butterfly's order (threads 0 + 2, then + 1) keeps the 1; the exact
+    # logit over the normalised token loses it, and rank 5 is expert 5
+    f = np.float32
+    assert (f(1e8) + f(-1e8)) + f(1.0) == f(1.0) > f(0.5)
+    xn = h0.copy()
+    ol.oracle().orc_rms_norm(ol.p(xn[0]), ol.p(np.ones(H, np.float32)), H, dims.rms_norm_eps)
+    _, oidx, _, olg = ol.oracle_moe_layer(layer, xn)
+    assert olg[0, 6] == 0.0 and oidx[0, 5] == 5
+    announce("stack T=1 with a speculation the exact selection overturns")
+    with Context(dims.moe_config(num_layers=1)) as ctx:
+        wl.upload_moe_layer(ctx, 0, layer)
+        ctx.upload_norm(0, np.ones(H, np.float32))
+        dh = ctx.to_device(h0)
+        ctx.stack_forward(0, 0, dh, 1)
+        ctx.synchronize()
+        h = dh.download()
+        dh.free()
+    oh = ol.oracle_stack([("moe", layer)], h0, dims.rms_norm_eps)
+    max_abs, mean_rel = layer_error(h, oh)
+    print(f"stack T=1 misprediction max_abs={max_abs:.3e} mean_rel={mean_rel:.3e}")
+    assert max_abs <= MAX_ABS and mean_rel < 1e-5
