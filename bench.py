@@ -796,7 +796,7 @@ def main() -> int:
         print(json.dumps(line), flush=True)
         return 0
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
+        print(f"bench.py measures one GPU: the library has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)
         return 2
 

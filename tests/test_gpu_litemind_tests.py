@@ -2,7 +2,7 @@
 
 oracle/_ref/KernelTest_gpu and MoeRouterSamplerTest_gpu are LiteMind's
 tests/KernelTest.cpp and tests/MoeRouterSamplerTest.cpp compiled unchanged from
-its sources (`make -C oracle ref-tests`), linked with this build's Gemm,
+its sources (`make -C oracle ref-tests`), linked with this library's Gemm,
 MoeRouter and ExpertCache sources and liblitemind_moe.so in place of LiteMind's
 CPU kernels.  Every gemm:: and MoeRouter call they make runs on the GPU, and
 every check they contain must pass.

@@ -2,7 +2,7 @@
 
 oracle/_ref/AttentionTest_gpu and RopeTest_gpu are LiteMind's
 tests/AttentionTest.cpp and tests/RopeTest.cpp compiled unchanged from its
-sources (`make -C oracle ref-tests`) with this build's Attention, KvCache and
+sources (`make -C oracle ref-tests`) with this library's Attention, KvCache and
 Rope sources and liblitemind_moe.so in place of LiteMind's: the KvCache checks
 run on the drop-in's cache, the RotaryEmbedding checks on tables built by the
 library (lm_rope_tables).  Neither reaches the GPU (the drop-in touches it only
