@@ -486,13 +486,23 @@ constexpr int kWideDepth = 4;
 constexpr int kWideWaves = 4;
 constexpr int64_t kWideTpw2Tokens = 2048;  // above this, two tokens per wave
 constexpr int64_t kWideTpw4Tokens = 4096;  // above this, four
+#ifndef LM_WIDE8_TOKENS
+#define LM_WIDE8_TOKENS 2048
+#endif
+constexpr int64_t kWide8Tokens = LM_WIDE8_TOKENS;  // from this on, 8-wave workgroups (one token per wave)
 
-template <int TPW>
+// NW waves per workgroup.  With 4 waves a lane's token values come in one
+// 16-byte load (1 KB per wave, TPW * 256 B used); with 8 (one token per wave,
+// one workgroup per CU) in one 4-byte load per lane (256 B per wave), which
+// leaves LDS for an 8-deep ring.
+template <int TPW, int NW>
 struct WideShape {
-    static constexpr int kWBytes = kWideRows * 64 * 4;                   // 16 KB of gate rows
-    static constexpr int kXBytes = kWideWaves * 1024;  // activations: 1 KB per wave (TPW * 256 B used)
+    static constexpr int kWBytes = kWideRows * 64 * 4;                    // 16 KB of gate rows
+    static constexpr int kXWave = NW == 4 ? 1024 : 256 * TPW;             // activation bytes per wave
+    static constexpr int kXBytes = NW * kXWave;
     static constexpr int kStage = kWBytes + kXBytes;
-    static constexpr int kLoads = kWBytes / 1024 / kWideWaves + 1;       // wave instructions per chunk
+    static constexpr int kWLoads = kWBytes / 1024 / NW;                   // gate wave instructions per chunk
+    static constexpr int kLoads = kWLoads + (NW == 4 ? 1 : TPW);          // wave instructions per chunk
 };
 
 __device__ inline void route_token_lds(float logit, bool valid, int lane, int64_t t, const RouterArgs& a,
@@ -508,39 +518,53 @@ __device__ inline void route_token_lds(float logit, bool valid, int lane, int64_
     }
 }
 
-template <int TPW>
-__global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs a, const float* __restrict__ x,
-                                                                       const float* __restrict__ wq4) {
-    using S = WideShape<TPW>;
-    constexpr int kS4 = kWideDepth > 4 ? S::kStage : 16;
+template <int TPW, int NW, int DEPTH>
+__global__ __launch_bounds__(NW * 64) void router_wide_kernel(RouterArgs a, const float* __restrict__ x,
+                                                               const float* __restrict__ wq4) {
+    using S = WideShape<TPW, NW>;
+    static_assert(DEPTH == 4 || DEPTH == 8, "ring depth");
+    static_assert(DEPTH * S::kStage <= 160 * 1024, "LDS");
+    constexpr int kS4 = DEPTH > 4 ? S::kStage : 16;
     __shared__ __attribute__((aligned(1024))) char r0[S::kStage], r1[S::kStage], r2[S::kStage], r3[S::kStage];
     __shared__ __attribute__((aligned(1024))) char r4[kS4], r5[kS4], r6[kS4], r7[kS4];
     char* const ring[8] = {r0, r1, r2, r3, r4, r5, r6, r7};
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int H = a.hidden;
-    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * kWideWaves * TPW;
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * NW * TPW;
     const int nchunks = H / kWideRows;
 
-    // This lane's activation row segment: token wave * TPW + (lane / 16) % TPW
-    // of the workgroup (clamped to the last token), rows 4 (lane % 16) .. +3.
-    // Every lane loads (lanes past TPW * 16 repeat a token into the unused part
-    // of the wave's slot), so the issue has no divergent branch.
-    int64_t xt = tb0 + wave * TPW + ((lane >> 4) % TPW);
+    // With 4 waves, this lane's activation row segment: token wave * TPW +
+    // (lane / 16) % TPW of the workgroup (clamped to the last token), rows
+    // 4 (lane % 16) .. +3.  Every lane loads (lanes past TPW * 16 repeat a token
+    // into the unused part of the wave's slot), so the issue has no divergent
+    // branch.  With 8 waves, row lane of each of the wave's tokens.
+    int64_t xt = tb0 + wave * TPW + (NW == 4 ? ((lane >> 4) % TPW) : 0);
     xt = xt < a.tokens ? xt : a.tokens - 1;
-    const float* xsrc = x + xt * H + 4 * (lane & 15);
+    const float* xsrc = x + xt * H + (NW == 4 ? 4 * (lane & 15) : lane);
     const float* wsrc = wq4 + static_cast<int64_t>(wave) * 256 + 4 * lane;
     auto issue = [&](int c, char* buf) {
         c = c < nchunks ? c : nchunks - 1;
         const int64_t i0 = static_cast<int64_t>(c) * kWideRows;
 #pragma unroll
-        for (int j = 0; j < S::kLoads - 1; ++j) {
-            const int n = j * kWideWaves + wave;  // 1 KB block n of the chunk's gate rows
-            __builtin_amdgcn_global_load_lds((router_global_void*)(wsrc + i0 * 64 + j * kWideWaves * 256),
+        for (int j = 0; j < S::kWLoads; ++j) {
+            const int n = j * NW + wave;  // 1 KB block n of the chunk's gate rows
+            __builtin_amdgcn_global_load_lds((router_global_void*)(wsrc + i0 * 64 + j * NW * 256),
                                              (router_lds_void*)(buf + n * 1024), 16, 0, 0);
         }
-        __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + i0), (router_lds_void*)(buf + S::kWBytes + wave * 1024),
-                                         16, 0, 0);
+        if constexpr (NW == 4) {
+            __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + i0),
+                                             (router_lds_void*)(buf + S::kWBytes + wave * S::kXWave), 16, 0, 0);
+        } else {
+            // token k of the wave: tokens past the batch end repeat the last one
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) {
+                const int64_t step = tb0 + wave * TPW + k < a.tokens ? static_cast<int64_t>(k) * H : 0;
+                __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + step + i0),
+                                                 (router_lds_void*)(buf + S::kWBytes + wave * S::kXWave + k * 256), 4,
+                                                 0, 0);
+            }
+        }
     };
 
     float acc[TPW];
@@ -557,7 +581,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs
     constexpr int kBatch = 32;
     auto compute = [&](const char* buf) {
         const float4* wb = reinterpret_cast<const float4*>(buf);
-        const float* xb = reinterpret_cast<const float*>(buf + S::kWBytes + wave * 1024);
+        const float* xb = reinterpret_cast<const float*>(buf + S::kWBytes + wave * S::kXWave);
 #pragma unroll
         for (int r0 = 0; r0 < kWideRows; r0 += kBatch) {
             float4 w[kBatch / 4];
@@ -597,19 +621,19 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_kernel(RouterArgs
     // most the depth - 2 chunks issued after it are in flight (and this wave's
     // LDS reads of the previous chunk are done); the barrier then also frees the
     // buffer consumed in the previous step for chunk c + depth - 1.
-    constexpr int kVm = (kWideDepth - 2) * S::kLoads;
+    constexpr int kVm = (DEPTH - 2) * S::kLoads;
     static_assert(kVm < 64, "vmcnt immediate");
     constexpr int kWait = 0x0070 | (kVm & 15) | ((kVm >> 4) << 14);  // vmcnt(kVm) lgkmcnt(0)
 #pragma unroll
-    for (int d = 0; d < kWideDepth - 1; ++d) {
+    for (int d = 0; d < DEPTH - 1; ++d) {
         issue(d, ring[d]);
     }
-    for (int c0 = 0; c0 < nchunks; c0 += kWideDepth) {
+    for (int c0 = 0; c0 < nchunks; c0 += DEPTH) {
 #pragma unroll
-        for (int j = 0; j < kWideDepth; ++j) {
+        for (int j = 0; j < DEPTH; ++j) {
             __builtin_amdgcn_s_waitcnt(kWait);
             __builtin_amdgcn_s_barrier();
-            issue(c0 + j + kWideDepth - 1, ring[(j + kWideDepth - 1) % kWideDepth]);
+            issue(c0 + j + DEPTH - 1, ring[(j + DEPTH - 1) % DEPTH]);
             compute(ring[j]);
         }
     }
@@ -1266,7 +1290,11 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
     // decode router; T = 16: 241 against 273 us with router_kernel).
     if (a.do_matvec && a.wq4 != nullptr && a.experts == 64 && a.hidden % (kWideRows * kWideDepth) == 0) {
         const int tpw = a.tokens > kWideTpw4Tokens ? 4 : (a.tokens > kWideTpw2Tokens ? 2 : 1);
-        const int64_t per_block = static_cast<int64_t>(kWideWaves) * tpw;
+        // From kWide8Tokens on, one or two tokens per wave in workgroups of 8
+        // waves (one per CU) with an 8-deep ring: each gate chunk serves 8 or 16
+        // tokens.
+        const bool eight = tpw <= 2 && a.tokens >= kWide8Tokens && a.hidden % (kWideRows * 8) == 0;
+        const int64_t per_block = static_cast<int64_t>(eight ? 8 : kWideWaves) * tpw;
         const dim3 grid(static_cast<unsigned>((a.tokens + per_block - 1) / per_block));
         // the kernel writes the fp16 copy itself when it covers every column
         RouterArgs k = a;
@@ -1274,10 +1302,16 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         if (separate_x16) {
             k.x16 = nullptr;
         }
-        switch (tpw) {
-            case 4: hipLaunchKernelGGL(router_wide_kernel<4>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
-            case 2: hipLaunchKernelGGL(router_wide_kernel<2>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
-            default: hipLaunchKernelGGL(router_wide_kernel<1>, grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+        if (eight && tpw == 2) {
+            hipLaunchKernelGGL((router_wide_kernel<2, 8, 8>), grid, dim3(8 * 64), 0, s, k, a.x, a.wq4);
+        } else if (eight) {
+            hipLaunchKernelGGL((router_wide_kernel<1, 8, 8>), grid, dim3(8 * 64), 0, s, k, a.x, a.wq4);
+        } else {
+            switch (tpw) {
+                case 4: hipLaunchKernelGGL((router_wide_kernel<4, 4, 4>), grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+                case 2: hipLaunchKernelGGL((router_wide_kernel<2, 4, 4>), grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+                default: hipLaunchKernelGGL((router_wide_kernel<1, 4, 4>), grid, dim3(kWideWaves * 64), 0, s, k, a.x, a.wq4); break;
+            }
         }
         hipError_t err = hipGetLastError();
         if (err == hipSuccess && separate_x16) {
