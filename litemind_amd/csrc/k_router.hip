@@ -699,14 +699,24 @@ __global__ __launch_bounds__(NW * 64) void router_wide_kernel(RouterArgs a, cons
 template <int EPL>
 constexpr int wide_multi_rows() { return EPL <= 2 ? 32 : (EPL <= 4 ? 16 : 8); }
 constexpr int kWideMultiGate = 16 * 1024;  // gate bytes per ring slot
-constexpr int kWideMultiSlot = kWideMultiGate + kWideWaves * 1024;
 
-template <int EPL, int TPW, int DEPTH>
-__global__ __launch_bounds__(kWideWaves * 64) void router_wide_multi_kernel(RouterArgs a, const float* __restrict__ x,
-                                                                             const float* __restrict__ wq4) {
+// NW waves per workgroup.  With 8 (one token per wave, one workgroup per CU, an
+// 8-deep ring) each lane loads one 4-byte token value per chunk (256 B per
+// wave), so each gate chunk serves 8 tokens in 144 KB of LDS.
+template <int NW>
+constexpr int wide_multi_slot() {
+    return kWideMultiGate + NW * (NW == 4 ? 1024 : 256);
+}
+
+template <int EPL, int TPW, int DEPTH, int NW = kWideWaves>
+__global__ __launch_bounds__(NW * 64) void router_wide_multi_kernel(RouterArgs a, const float* __restrict__ x,
+                                                                     const float* __restrict__ wq4) {
     static_assert(DEPTH == 4 || DEPTH == 8, "ring depth");
+    static_assert(NW == 4 || (NW == 8 && TPW == 1 && DEPTH == 8), "8 waves: one token per wave, 8-deep ring");
+    constexpr int kWideMultiSlot = wide_multi_slot<NW>();
+    constexpr int kXWave = NW == 4 ? 1024 : 256;
     constexpr int R = wide_multi_rows<EPL>();
-    constexpr int kGateLoads = kWideMultiGate / 1024 / kWideWaves;  // 4 per wave
+    constexpr int kGateLoads = kWideMultiGate / 1024 / NW;  // 4 (2) per wave
     constexpr int kLoads = kGateLoads + 1;
     constexpr int kHi = DEPTH > 4 ? kWideMultiSlot : 16;
     __shared__ __attribute__((aligned(1024))) char r0[kWideMultiSlot], r1[kWideMultiSlot], r2[kWideMultiSlot],
@@ -717,27 +727,35 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_multi_kernel(Rout
     const int wave = threadIdx.x >> 6;
     const int H = a.hidden;
     const int E = a.experts;
-    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * kWideWaves * TPW;
+    const int64_t tb0 = static_cast<int64_t>(blockIdx.x) * NW * TPW;
     const int nchunks = H / R;
     const int chunk_bytes = R / 4 * E * 16;
 
-    // activations: lane -> token (lane / (R / 4)) % TPW of the wave, rows 4 (lane % (R / 4)) .. + 3
-    int64_t xt = tb0 + wave * TPW + ((lane / (R / 4)) % TPW);
+    // activations, 4 waves: lane -> token (lane / (R / 4)) % TPW of the wave,
+    // rows 4 (lane % (R / 4)) .. + 3; 8 waves: the wave's token, row lane of
+    // the chunk (lanes past R read rows of later chunks, clamped to the last row)
+    int64_t xt = tb0 + wave * TPW + (NW == 4 ? ((lane / (R / 4)) % TPW) : 0);
     xt = xt < a.tokens ? xt : a.tokens - 1;
-    const float* xsrc = x + xt * H + 4 * (lane % (R / 4));
+    const float* xsrc = x + xt * H + (NW == 4 ? 4 * (lane % (R / 4)) : 0);
     const char* wbase = reinterpret_cast<const char*>(wq4);
     auto issue = [&](int c, char* buf) {
         c = c < nchunks ? c : nchunks - 1;
         const char* chunk = wbase + static_cast<int64_t>(c) * chunk_bytes;
 #pragma unroll
         for (int j = 0; j < kGateLoads; ++j) {
-            const int n = j * kWideWaves + wave;  // 1 KB block n of the slot
+            const int n = j * NW + wave;  // 1 KB block n of the slot
             const int off = n * 1024 + lane * 16;
             __builtin_amdgcn_global_load_lds((router_global_void*)(chunk + (off < chunk_bytes ? off : 0)),
                                              (router_lds_void*)(buf + n * 1024), 16, 0, 0);
         }
-        __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + static_cast<int64_t>(c) * R),
-                                         (router_lds_void*)(buf + kWideMultiGate + wave * 1024), 16, 0, 0);
+        if constexpr (NW == 4) {
+            __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + static_cast<int64_t>(c) * R),
+                                             (router_lds_void*)(buf + kWideMultiGate + wave * kXWave), 16, 0, 0);
+        } else {
+            const int row = c * R + lane;
+            __builtin_amdgcn_global_load_lds((router_global_void*)(xsrc + (row < H ? row : H - 1)),
+                                             (router_lds_void*)(buf + kWideMultiGate + wave * kXWave), 4, 0, 0);
+        }
     };
 
     float acc[TPW][EPL];
@@ -755,7 +773,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_multi_kernel(Rout
     }
     auto compute = [&](const char* buf) {
         const float4* wb = reinterpret_cast<const float4*>(buf);
-        const float* xb = reinterpret_cast<const float*>(buf + kWideMultiGate + wave * 1024);
+        const float* xb = reinterpret_cast<const float*>(buf + kWideMultiGate + wave * kXWave);
 #pragma unroll
         for (int q = 0; q < R / 4; ++q) {
             float4 w[EPL];
@@ -810,8 +828,12 @@ __global__ __launch_bounds__(kWideWaves * 64) void router_wide_multi_kernel(Rout
     const SelectPolicy p{a.experts, a.top_k, a.normalize, a.group_limited, a.n_group, a.topk_group, a.scale};
     const int K = a.top_k < E ? a.top_k : E;
     // one slot per wave (selected, not indexed: ring[] is only ever indexed by constants)
-    float* sh = reinterpret_cast<float*>(wave == 0 ? r0 : (wave == 1 ? r1 : (wave == 2 ? r2 : r3)));
-    static_assert(kWideWaves <= 4 && select_multi_words(EPL) * 4 <= kWideMultiSlot, "selection scratch in the ring");
+    char* slot = wave == 0 ? r0 : (wave == 1 ? r1 : (wave == 2 ? r2 : r3));
+    if constexpr (NW == 8) {
+        slot = wave < 4 ? slot : (wave == 4 ? r4 : (wave == 5 ? r5 : (wave == 6 ? r6 : r7)));
+    }
+    float* sh = reinterpret_cast<float*>(slot);
+    static_assert(select_multi_words(EPL) * 4 <= kWideMultiSlot, "selection scratch in the ring");
 #pragma unroll
     for (int k = 0; k < TPW; ++k) {
         const int64_t t = tb0 + wave * TPW + k;
@@ -858,6 +880,11 @@ constexpr int64_t kRingTpw4Tokens = LM_RING_TPW4_TOKENS;
 #endif
 // Grids of up to this many workgroups (one per CU) take the 8-deep ring.
 constexpr int64_t kRingDeepBlocks = LM_RING_DEEP_BLOCKS;
+#ifndef LM_RING_WIDE8
+#define LM_RING_WIDE8 1
+#endif
+// Above that, one token per wave in workgroups of 8 waves (0: of 4, 4-deep).
+constexpr bool kRingWide8 = LM_RING_WIDE8 != 0;
 #ifndef LM_SMALL_SPLIT_TOKENS
 #define LM_SMALL_SPLIT_TOKENS 64
 #endif
@@ -875,6 +902,13 @@ void launch_wide_multi_tpw(const RouterArgs& a, hipStream_t s) {
         if (blocks <= kRingDeepBlocks) {
             hipLaunchKernelGGL((router_wide_multi_kernel<EPL, 1, 8>), grid, dim3(kWideWaves * 64), 0, s, a, a.x,
                                a.wq4);
+            return;
+        }
+        // more workgroups than CUs: 8 waves per workgroup instead, so each gate
+        // chunk serves 8 tokens (at most one workgroup per CU either way)
+        if (kRingWide8) {
+            const dim3 grid8(static_cast<unsigned>((a.tokens + 7) / 8));
+            hipLaunchKernelGGL((router_wide_multi_kernel<EPL, 1, 8, 8>), grid8, dim3(8 * 64), 0, s, a, a.x, a.wq4);
             return;
         }
     }

@@ -109,7 +109,8 @@ def test_wide_router_bit_exact(wide_ctx, T):
 # experts, top-k, group-limited, groups, kept, hidden, tokens, bias.  Above 256
 # tokens (or with E % 8 != 0) the batched ring router: every lane-ownership
 # width (two to eight experts per lane), the 8-deep ring (up to 256
-# workgroups) and the 4-deep one, one, two and four tokens per wave, expert
+# workgroups; above that with one token per wave, workgroups of 8 waves) and
+# the 4-deep one, one, two and four tokens per wave, expert
 # counts off multiples of 4 and 8, and a hidden size the ring's chunks do not
 # divide (the per-token kernel).  Up to 256 tokens with E % 8 == 0: logits
 # over E / 8 workgroups per token, then the selection.
@@ -126,6 +127,8 @@ RING_CASES = {
     "e384_epl6_tpw2": (384, 8, True, 8, 4, 320, 2060, True),
     "e448_split": (448, 8, False, 1, 1, 256, 77, False),
     "e160_split_256": (160, 6, True, 8, 3, 512, 256, True),
+    "e100_epl2_wide8": (100, 6, False, 1, 1, 512, 2048, True),
+    "e512_epl8_wide8": (512, 8, True, 16, 4, 256, 1100, False),
 }
 
 
