@@ -490,6 +490,9 @@ constexpr int64_t kWideTpw4Tokens = 4096;  // above this, four
 #define LM_WIDE8_TOKENS 2048
 #endif
 constexpr int64_t kWide8Tokens = LM_WIDE8_TOKENS;  // from this on, 8-wave workgroups (one token per wave)
+// ... and with two tokens per wave from this on (224 or more workgroups of 16
+// tokens; with fewer, more CUs stay busy with 4-wave workgroups)
+constexpr int64_t kWide8Tpw2Tokens = 3584;
 
 // NW waves per workgroup.  With 4 waves a lane's token values come in one
 // 16-byte load (1 KB per wave, TPW * 256 B used); with 8 (one token per wave,
@@ -1327,7 +1330,8 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s, bool* permuted) {
         // From kWide8Tokens on, one or two tokens per wave in workgroups of 8
         // waves (one per CU) with an 8-deep ring: each gate chunk serves 8 or 16
         // tokens.
-        const bool eight = tpw <= 2 && a.tokens >= kWide8Tokens && a.hidden % (kWideRows * 8) == 0;
+        const bool eight = ((tpw == 1 && a.tokens >= kWide8Tokens) || (tpw == 2 && a.tokens >= kWide8Tpw2Tokens)) &&
+                           a.hidden % (kWideRows * 8) == 0;
         const int64_t per_block = static_cast<int64_t>(eight ? 8 : kWideWaves) * tpw;
         const dim3 grid(static_cast<unsigned>((a.tokens + per_block - 1) / per_block));
         // the kernel writes the fp16 copy itself when it covers every column
